@@ -1,0 +1,13 @@
+"""MI355X (gfx950) PKDA recurrence: hand-written HIP kernels behind a C ABI.
+
+A drop-in for the PKDA recurrence path of a9lim/delta-feedback-experiment
+(``delta_feedback_experiment/pkda.py:412-475`` and
+``delta_feedback_experiment/fla_ops.py:252-569``).  The compute lives in
+``libpkda_gfx950.so`` (``csrc/*.hip``, C ABI in ``include/pkda_gfx950.h``);
+this package is the PyTorch-facing host side.  Nothing here falls back to the
+CPU: without a HIP device and the built library every operator raises.
+"""
+
+from .pkda import fused_recurrent_pkda, pkda_decode_step_
+
+__all__ = ["fused_recurrent_pkda", "pkda_decode_step_"]

@@ -1,0 +1,104 @@
+// Shared device and host helpers for the gfx950 PKDA kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "pkda_gfx950.h"
+
+namespace pkda {
+
+// ----------------------------------------------------------------------------
+// Error reporting (host).  One message per calling thread.
+// ----------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+
+#define PKDA_REQUIRE(cond, code, ...)          \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::pkda::set_error(__VA_ARGS__);          \
+      return (code);                           \
+    }                                          \
+  } while (0)
+
+inline int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return 0;
+}
+
+// ----------------------------------------------------------------------------
+// bf16 <-> f32 (round to nearest even, NaN preserved), on raw 16-bit storage.
+// ----------------------------------------------------------------------------
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<bf16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+template <typename T> struct io;
+template <> struct io<float> {
+  static constexpr int dtype = PKDA_F32;
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+};
+template <> struct io<bf16_t> {
+  static constexpr int dtype = PKDA_BF16;
+  __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
+  __device__ __forceinline__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+
+// Load four consecutive elements as floats (16-byte or 8-byte vector loads).
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const bf16_t* p) {
+  uint2 r = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                     __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+}
+__device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void store4(bf16_t* p, float4 v) {
+  uint2 r;
+  r.x = static_cast<uint32_t>(f32_to_bf16(v.x)) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+  r.y = static_cast<uint32_t>(f32_to_bf16(v.z)) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+  *reinterpret_cast<uint2*>(p) = r;
+}
+
+// Scalar load of a runtime-typed element.
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  return dtype == PKDA_BF16 ? bf16_to_f32(static_cast<const bf16_t*>(p)[i])
+                            : static_cast<const float*>(p)[i];
+}
+
+// torch.nn.functional.softplus with beta = 1, threshold = 20.
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Sequence bounds for flat token tensors: packed documents or equal rows.
+struct SeqBounds {
+  int64_t start;
+  int32_t len;
+};
+__device__ __forceinline__ SeqBounds seq_bounds(const int32_t* cu, int n, int seqlen) {
+  SeqBounds b;
+  if (cu) {
+    b.start = cu[n];
+    b.len = cu[n + 1] - cu[n];
+  } else {
+    b.start = static_cast<int64_t>(n) * seqlen;
+    b.len = seqlen;
+  }
+  return b;
+}
+
+}  // namespace pkda

@@ -1,0 +1,282 @@
+// Token-recurrent PKDA forward and the slot-pool decode step (gfx950).
+//
+// One 256-thread workgroup owns one (sequence, head).  The FP32 state
+// S [D x D] lives in registers for the whole sequence: thread (rg, cg) holds
+// columns 4cg..4cg+3 of rows rg, rg+NRG, rg+2NRG, ...  Every token costs two
+// column reductions of the *old* state, since
+//
+//   e_v = v_v - sum_k (alpha_k k_k) S[k,v]
+//   o_v = sum_k (alpha_k qs_k) S[k,v] + beta e_v (qs . kw)
+//
+// (o reads the updated state, pkda.py:406; expanding S_t gives the second
+// line), followed by the in-register rank-1 update
+// S[k,v] <- alpha_k S[k,v] + beta kw_k e_v.  The state is read from HBM once
+// and written once per sequence, which is what makes the decode step
+// bandwidth-bound on the 64 KiB-per-head FP32 state.
+#include "pkda_common.h"
+
+namespace pkda {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct RecParams {
+  int num_seqs, seqlen, heads;
+  const int32_t* cu_seqlens;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  int gate_kind, g_dtype;
+  const float* A_log;
+  const float* dt_bias;
+  const float* beta;
+  float scale;
+  const float* g_atk;
+  const float* beta_atk;
+  const float* center;
+  float log_x, squash_eps;
+  float* state_pool;
+  float* a_pool;
+  const int32_t* slot_idx;
+  const float* initial_state;
+  const float* initial_A_state;
+  float* final_state;
+  float* final_A_state;
+  void* o;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void recurrent_kernel(RecParams p) {
+  constexpr int NCG = D / 4;            // column groups of 4
+  constexpr int NRG = kThreads / NCG;   // row groups
+  constexpr int RPT = D / NRG;          // rows per thread
+  static_assert(RPT >= 1 && NRG * RPT == D, "bad head dim");
+
+  __shared__ float s_ak[2][D];   // alpha_k * k_k            (prediction read)
+  __shared__ float s_aq[2][D];   // alpha_k * scale * q_k    (output read)
+  __shared__ float s_al[2][D];   // alpha_k
+  __shared__ float s_bw[2][D];   // beta * kw_k               (write)
+  __shared__ float s_v[2][D];
+  __shared__ float s_qk[2][kThreads / 64];
+  __shared__ float4 s_pe[NRG][NCG];
+  __shared__ float4 s_po[NRG][NCG];
+
+  const int n = blockIdx.x;
+  const int h = blockIdx.y;
+  const int H = p.heads;
+  const int tid = threadIdx.x;
+  const int cg = tid % NCG;
+  const int rg = tid / NCG;
+  const SeqBounds sb = seq_bounds(p.cu_seqlens, n, p.seqlen);
+
+  // ---- state source --------------------------------------------------------
+  const float* s_src = nullptr;
+  float* s_dst = nullptr;
+  const float* a_src = nullptr;
+  float* a_dst = nullptr;
+  if (p.state_pool) {
+    const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
+    s_src = s_dst = p.state_pool + (slot * H + h) * (int64_t)D * D;
+    if (p.a_pool) a_src = a_dst = p.a_pool + (slot * H + h) * (int64_t)D;
+  } else {
+    if (p.initial_state) s_src = p.initial_state + ((int64_t)n * H + h) * D * D;
+    if (p.final_state) s_dst = p.final_state + ((int64_t)n * H + h) * D * D;
+    if (p.initial_A_state) a_src = p.initial_A_state + ((int64_t)n * H + h) * D;
+    if (p.final_A_state) a_dst = p.final_A_state + ((int64_t)n * H + h) * D;
+  }
+
+  float4 S[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int row = rg + NRG * j;
+    S[j] = s_src ? load4(s_src + row * D + 4 * cg) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const bool precond = p.g_atk != nullptr;
+  float a_c = 0.f;  // preconditioner state of channel tid (tid < D)
+  if (precond && tid < D && a_src) a_c = a_src[tid];
+
+  const float A_scale = (p.gate_kind == PKDA_GATE_RAW_CHANNEL) ? -expf(p.A_log[h]) : 0.f;
+  const float center = precond ? p.center[h] : 0.f;
+
+  for (int t = 0; t < sb.len; ++t) {
+    const int buf = t & 1;
+    const int64_t tok = sb.start + t;
+    const int64_t th = tok * H + h;
+    // ---- channel phase: gate, preconditioner, operands to LDS -------------
+    float qk_part = 0.f;
+    if (tid < D) {
+      const int c = tid;
+      const float qc = io<T>::load(static_cast<const T*>(p.q) + th * D + c) * p.scale;
+      const float kc = io<T>::load(static_cast<const T*>(p.k) + th * D + c);
+      const float vc = io<T>::load(static_cast<const T*>(p.v) + th * D + c);
+      float gl;
+      if (p.gate_kind == PKDA_GATE_LOG_HEAD) {
+        gl = load_any(p.g, th, p.g_dtype);
+      } else if (p.gate_kind == PKDA_GATE_LOG_CHANNEL) {
+        gl = load_any(p.g, th * D + c, p.g_dtype);
+      } else {
+        gl = A_scale * softplus_f(load_any(p.g, th * D + c, p.g_dtype) + p.dt_bias[h * D + c]);
+      }
+      const float al = expf(gl);
+      float kw = kc;
+      if (precond) {
+        a_c = expf(p.g_atk[th]) * a_c + p.beta_atk[th] * (kc * kc);
+        const float r = logf(a_c + p.squash_eps) - center;
+        kw = kc * expf(-p.log_x * (r / (1.f + fabsf(r))));
+      }
+      const float bt = p.beta[th];
+      s_ak[buf][c] = al * kc;
+      s_aq[buf][c] = al * qc;
+      s_al[buf][c] = al;
+      s_bw[buf][c] = bt * kw;
+      s_v[buf][c] = vc;
+      qk_part = qc * kw * bt;
+    }
+    // wave reduction of beta * (qs . kw)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) qk_part += __shfl_xor(qk_part, off);
+    if ((tid & 63) == 0) s_qk[buf][tid >> 6] = qk_part;
+    __syncthreads();
+
+    // ---- reduction phase: partial column sums of the old state -------------
+    float4 pe = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rg + NRG * j;
+      const float ak = s_ak[buf][row];
+      const float aq = s_aq[buf][row];
+      pe.x += ak * S[j].x; pe.y += ak * S[j].y; pe.z += ak * S[j].z; pe.w += ak * S[j].w;
+      po.x += aq * S[j].x; po.y += aq * S[j].y; po.z += aq * S[j].z; po.w += aq * S[j].w;
+    }
+    s_pe[rg][cg] = pe;
+    s_po[rg][cg] = po;
+    __syncthreads();
+
+    // ---- finish: residual, output, rank-1 update ----------------------------
+    float4 e = *reinterpret_cast<const float4*>(&s_v[buf][4 * cg]);
+    float4 out = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < NRG; ++r) {
+      const float4 a = s_pe[r][cg];
+      const float4 b = s_po[r][cg];
+      e.x -= a.x; e.y -= a.y; e.z -= a.z; e.w -= a.w;
+      out.x += b.x; out.y += b.y; out.z += b.z; out.w += b.w;
+    }
+    float bqk = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) bqk += s_qk[buf][w];
+    out.x += bqk * e.x; out.y += bqk * e.y; out.z += bqk * e.z; out.w += bqk * e.w;
+    if (rg == 0) store4(static_cast<T*>(p.o) + th * D + 4 * cg, out);
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rg + NRG * j;
+      const float al = s_al[buf][row];
+      const float bw = s_bw[buf][row];
+      S[j].x = al * S[j].x + bw * e.x;
+      S[j].y = al * S[j].y + bw * e.y;
+      S[j].z = al * S[j].z + bw * e.z;
+      S[j].w = al * S[j].w + bw * e.w;
+    }
+  }
+
+  if (s_dst) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rg + NRG * j;
+      store4(s_dst + row * D + 4 * cg, S[j]);
+    }
+  }
+  if (precond && tid < D && a_dst) a_dst[tid] = a_c;
+}
+
+template <typename T>
+int launch_recurrent(const RecParams& rp, int D, hipStream_t stream) {
+  dim3 grid(rp.num_seqs, rp.heads);
+  switch (D) {
+    case 32: hipLaunchKernelGGL((recurrent_kernel<T, 32>), grid, dim3(kThreads), 0, stream, rp); break;
+    case 64: hipLaunchKernelGGL((recurrent_kernel<T, 64>), grid, dim3(kThreads), 0, stream, rp); break;
+    case 128: hipLaunchKernelGGL((recurrent_kernel<T, 128>), grid, dim3(kThreads), 0, stream, rp); break;
+    default: set_error("head_dim %d not built (32, 64, 128)", D); return PKDA_EUNSUPPORTED;
+  }
+  return launch_status("pkda_recurrent");
+}
+
+int recurrent_entry(const pkda_recurrent_args* a, void* stream, bool decode) {
+  PKDA_REQUIRE(a != nullptr, PKDA_EINVAL, "null args");
+  PKDA_REQUIRE(a->struct_size == (int32_t)sizeof(pkda_recurrent_args), PKDA_EINVAL,
+               "pkda_recurrent_args size %d, library expects %d", a->struct_size, (int)sizeof(pkda_recurrent_args));
+  PKDA_REQUIRE(a->dtype == PKDA_F32 || a->dtype == PKDA_BF16, PKDA_EUNSUPPORTED, "dtype %d", a->dtype);
+  PKDA_REQUIRE(a->g_dtype == PKDA_F32 || a->g_dtype == PKDA_BF16, PKDA_EUNSUPPORTED, "g dtype %d", a->g_dtype);
+  PKDA_REQUIRE(a->num_seqs >= 0 && a->heads > 0 && a->seqlen >= 0, PKDA_EINVAL, "bad sizes");
+  PKDA_REQUIRE(a->head_dim == 32 || a->head_dim == 64 || a->head_dim == 128, PKDA_EUNSUPPORTED,
+               "head_dim %d not built (32, 64, 128)", a->head_dim);
+  PKDA_REQUIRE(a->gate_kind >= PKDA_GATE_LOG_HEAD && a->gate_kind <= PKDA_GATE_RAW_CHANNEL, PKDA_EINVAL,
+               "gate_kind %d", a->gate_kind);
+  PKDA_REQUIRE(a->gate_kind != PKDA_GATE_RAW_CHANNEL || (a->A_log && a->dt_bias), PKDA_EINVAL,
+               "raw gate needs A_log and dt_bias");
+  PKDA_REQUIRE(!a->g_atk || (a->beta_atk && a->center), PKDA_EINVAL, "preconditioner needs beta_atk and center");
+  PKDA_REQUIRE(!a->g_atk || a->squash_x > 0.f, PKDA_EINVAL, "squash_x must be positive");
+  PKDA_REQUIRE(!a->cu_seqlens || !decode, PKDA_EINVAL, "decode takes no cu_seqlens");
+  if (decode) {
+    PKDA_REQUIRE(a->seqlen == 1, PKDA_EINVAL, "decode step needs seqlen == 1");
+    PKDA_REQUIRE(a->state_pool != nullptr, PKDA_EINVAL, "decode step needs a state pool");
+  }
+  if (a->state_pool) {
+    PKDA_REQUIRE(a->pool_size >= 0, PKDA_EINVAL, "pool_size");
+    PKDA_REQUIRE(a->slot_idx || a->num_seqs <= a->pool_size, PKDA_ERANGE, "identity slots exceed the pool");
+    PKDA_REQUIRE(!a->g_atk || a->a_pool, PKDA_EINVAL, "preconditioned pool step needs a_pool");
+    if (a->check_slots && a->slot_idx_host && a->num_seqs > 0) {
+      // Range and uniqueness: duplicate slots would race on the in-place write.
+      const int64_t P = a->pool_size;
+      if (P <= (int64_t)1 << 26) {
+        uint8_t* seen = static_cast<uint8_t*>(calloc((size_t)P + 1, 1));
+        PKDA_REQUIRE(seen != nullptr, PKDA_EINVAL, "out of host memory");
+        for (int i = 0; i < a->num_seqs; ++i) {
+          const int32_t s = a->slot_idx_host[i];
+          if (s < 0 || s >= P || seen[s]) {
+            free(seen);
+            set_error("slot_idx[%d] = %d is out of range [0, %lld) or repeated", i, s, (long long)P);
+            return PKDA_ERANGE;
+          }
+          seen[s] = 1;
+        }
+        free(seen);
+      }
+    }
+  }
+  if (a->num_seqs == 0) return PKDA_OK;
+  PKDA_REQUIRE(a->q && a->k && a->v && a->g && a->beta && a->o, PKDA_EINVAL, "null token tensor");
+
+  RecParams rp;
+  rp.num_seqs = a->num_seqs;
+  rp.seqlen = a->seqlen;
+  rp.heads = a->heads;
+  rp.cu_seqlens = a->cu_seqlens;
+  rp.q = a->q; rp.k = a->k; rp.v = a->v; rp.g = a->g;
+  rp.gate_kind = a->gate_kind; rp.g_dtype = a->g_dtype;
+  rp.A_log = a->A_log; rp.dt_bias = a->dt_bias;
+  rp.beta = a->beta; rp.scale = a->scale;
+  rp.g_atk = a->g_atk; rp.beta_atk = a->beta_atk; rp.center = a->center;
+  rp.log_x = a->g_atk ? logf(a->squash_x) : 0.f;
+  rp.squash_eps = a->squash_eps;
+  rp.state_pool = a->state_pool; rp.a_pool = a->a_pool; rp.slot_idx = a->slot_idx;
+  rp.initial_state = a->initial_state; rp.initial_A_state = a->initial_A_state;
+  rp.final_state = a->final_state; rp.final_A_state = a->final_A_state;
+  rp.o = a->o;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return a->dtype == PKDA_F32 ? launch_recurrent<float>(rp, a->head_dim, s)
+                              : launch_recurrent<bf16_t>(rp, a->head_dim, s);
+}
+
+}  // namespace
+}  // namespace pkda
+
+extern "C" int pkda_recurrent_fwd(const pkda_recurrent_args* args, void* stream) {
+  return pkda::recurrent_entry(args, stream, false);
+}
+
+extern "C" int pkda_decode_step(const pkda_recurrent_args* args, void* stream) {
+  return pkda::recurrent_entry(args, stream, true);
+}

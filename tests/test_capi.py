@@ -1,0 +1,68 @@
+"""The C ABI library loads, exports every declared entry point and agrees
+with its ctypes mirror -- no compute, so this runs without a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "pkda_gfx950.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(pkda_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = _declared_functions()
+    for required in ("pkda_abi_version", "pkda_last_error", "pkda_recurrent_fwd", "pkda_decode_step"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from delta_feedback_experiment_amd import _lib
+
+    path = _lib.library_path()
+    if not path.exists():
+        pytest.fail(f"{path} missing: build it with python -m delta_feedback_experiment_amd.build")
+    handle = ctypes.CDLL(str(path))
+    for name in _declared_functions():
+        assert hasattr(handle, name), name
+
+
+def test_binding_structs_match_library():
+    from delta_feedback_experiment_amd import _lib
+
+    handle = _lib.lib()  # checks ABI version and every struct size it knows
+    assert handle.pkda_abi_version() == _lib.ABI_VERSION
+    assert handle.pkda_args_size(0) == ctypes.sizeof(_lib.RecurrentArgs)
+
+
+def test_rejected_arguments_raise_before_any_launch():
+    from delta_feedback_experiment_amd import _lib
+
+    args = _lib.RecurrentArgs(dtype=0, num_seqs=1, seqlen=1, heads=1, head_dim=48)
+    with pytest.raises(ValueError, match="head_dim 48"):
+        _lib.call("pkda_recurrent_fwd", args, 0)
+    args = _lib.RecurrentArgs(dtype=7, num_seqs=1, seqlen=1, heads=1, head_dim=64)
+    with pytest.raises(ValueError, match="dtype"):
+        _lib.call("pkda_recurrent_fwd", args, 0)
+    args = _lib.RecurrentArgs(dtype=0, num_seqs=1, seqlen=2, heads=1, head_dim=64)
+    with pytest.raises(ValueError, match="seqlen == 1"):
+        _lib.call("pkda_decode_step", args, 0)
+
+
+def test_operators_refuse_cpu_tensors():
+    import torch
+
+    from delta_feedback_experiment_amd import fused_recurrent_pkda
+
+    q = torch.randn(1, 4, 1, 64)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fused_recurrent_pkda(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1))
