@@ -47,7 +47,7 @@ class GateArgs(ctypes.Structure):
         ("cu_seqlens", c_void_p), ("g", c_void_p), ("A_log", c_void_p), ("dt_bias", c_void_p),
         ("gcum", c_void_p), ("dgcum", c_void_p), ("dg", c_void_p), ("dA_log_part", c_void_p),
         ("ddt_bias_part", c_void_p), ("dA_log", c_void_p), ("ddt_bias", c_void_p),
-        ("num_chunks", c_int32),
+        ("num_chunks", c_int32), ("table", c_void_p),
     ]
 
 
@@ -64,28 +64,28 @@ class PrecondArgs(ctypes.Structure):
     ]
 
 
+_CHUNK_COMMON = [
+    ("struct_size", c_int32), ("dtype", c_int32), ("num_seqs", c_int32), ("seqlen", c_int32),
+    ("heads", c_int32), ("head_dim", c_int32), ("cu_seqlens", c_void_p), ("num_chunks", c_int32),
+    ("table", c_void_p),
+    ("q", c_void_p), ("k", c_void_p), ("kw", c_void_p), ("v", c_void_p),
+    ("gcum", c_void_p), ("gate_per_channel", c_int32), ("beta", c_void_p), ("scale", c_float),
+    ("initial_state", c_void_p),
+]
+
+
 class ChunkFwdArgs(ctypes.Structure):
-    _fields_ = [
-        ("struct_size", c_int32), ("dtype", c_int32), ("num_seqs", c_int32), ("seqlen", c_int32),
-        ("heads", c_int32), ("head_dim", c_int32), ("cu_seqlens", c_void_p), ("num_chunks", c_int32),
-        ("chunk_table", c_void_p),
-        ("q", c_void_p), ("k", c_void_p), ("kw", c_void_p), ("v", c_void_p),
-        ("gcum", c_void_p), ("gate_per_channel", c_int32), ("beta", c_void_p), ("scale", c_float),
-        ("initial_state", c_void_p), ("final_state", c_void_p), ("o", c_void_p),
-        ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("h", c_void_p),
+    _fields_ = _CHUNK_COMMON + [
+        ("final_state", c_void_p), ("o", c_void_p),
+        ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
     ]
 
 
 class ChunkBwdArgs(ctypes.Structure):
-    _fields_ = [
-        ("struct_size", c_int32), ("dtype", c_int32), ("num_seqs", c_int32), ("seqlen", c_int32),
-        ("heads", c_int32), ("head_dim", c_int32), ("cu_seqlens", c_void_p), ("num_chunks", c_int32),
-        ("chunk_table", c_void_p),
-        ("q", c_void_p), ("k", c_void_p), ("kw", c_void_p), ("v", c_void_p),
-        ("gcum", c_void_p), ("gate_per_channel", c_int32), ("beta", c_void_p), ("scale", c_float),
-        ("initial_state", c_void_p), ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("h", c_void_p),
-        ("do", c_void_p), ("dht", c_void_p),
-        ("dh", c_void_p), ("du", c_void_p),
+    _fields_ = _CHUNK_COMMON + [
+        ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
+        ("do", c_void_p), ("dht", c_void_p), ("dh", c_void_p),
+        ("du", c_void_p), ("dw", c_void_p), ("daqk", c_void_p), ("da", c_void_p),
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
     ]
@@ -146,6 +146,8 @@ def lib() -> ctypes.CDLL:
         if fn is not None:
             fn.restype = c_int32
             fn.argtypes = [POINTER(struct), c_void_p]
+    handle.pkda_chunk_table.restype = c_int32
+    handle.pkda_chunk_table.argtypes = [c_void_p, c_int32, c_int32, c_void_p, c_void_p]
     if handle.pkda_abi_version() != ABI_VERSION:
         raise RuntimeError(f"libpkda ABI {handle.pkda_abi_version()} != binding ABI {ABI_VERSION}")
     for kind, struct in _ARG_KINDS.items():

@@ -24,12 +24,10 @@ extern "C" const char* pkda_last_error(void) { return pkda::g_last_error; }
 extern "C" int64_t pkda_args_size(int which) {
   switch (which) {
     case PKDA_ARGS_RECURRENT: return sizeof(pkda_recurrent_args);
-#ifdef PKDA_HAVE_CHUNK_ARGS
     case PKDA_ARGS_GATE: return sizeof(pkda_gate_args);
     case PKDA_ARGS_PRECOND: return sizeof(pkda_precond_args);
     case PKDA_ARGS_CHUNK_FWD: return sizeof(pkda_chunk_fwd_args);
     case PKDA_ARGS_CHUNK_BWD: return sizeof(pkda_chunk_bwd_args);
-#endif
     default: return -1;
   }
 }

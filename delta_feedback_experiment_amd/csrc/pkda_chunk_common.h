@@ -1,0 +1,245 @@
+// Chunk geometry, LDS tile movement and wave64 MFMA tiles for the chunked
+// PKDA kernels (gfx950).
+//
+// Token tensors are flat [N_tok, H, D].  A "document" is either one of
+// `num_seqs` equal rows of `seqlen` tokens or a cu_seqlens span; chunks of
+// C = 64 tokens start at each document's first token, so the last chunk of a
+// document may be partial.  Per-chunk kernels see a chunk as
+// (document n, first token, length, chunk id); per-document kernels walk the
+// chunk ids of their document in order.
+#pragma once
+
+#include "pkda_common.h"
+
+namespace pkda {
+
+constexpr int C = PKDA_CHUNK;  // 64
+constexpr int kWG = 256;       // 4 waves
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ----------------------------------------------------------------------------
+// Chunk geometry
+// ----------------------------------------------------------------------------
+struct ChunkGeom {
+  int num_seqs;
+  int seqlen;          // equal rows (cu == nullptr)
+  int nt;              // chunks per row, equal rows
+  const int32_t* cu;   // [num_seqs+1] or nullptr
+  const int4* table;   // [num_chunks] {n, start, len, -} (varlen)
+  const int32_t* offsets;  // [num_seqs+1] first chunk id of each document (varlen)
+  int num_chunks;      // launch bound
+};
+
+struct ChunkInfo {
+  int n;
+  int start;
+  int len;  // 0: empty slot of the varlen launch bound
+};
+
+// Host: fill a ChunkGeom from the entry-point arguments (validates them).
+int chunk_geom_from(const int32_t* cu, int num_seqs, int seqlen, int num_chunks, const int32_t* table, ChunkGeom& g);
+
+__device__ __forceinline__ ChunkInfo chunk_info(const ChunkGeom& g, int c) {
+  ChunkInfo ci;
+  if (g.cu) {
+    const int4 e = g.table[c];
+    ci.n = e.x;
+    ci.start = e.y;
+    ci.len = e.z;
+  } else {
+    ci.n = c / g.nt;
+    const int j = c - ci.n * g.nt;
+    ci.start = ci.n * g.seqlen + j * C;
+    ci.len = min(C, g.seqlen - j * C);
+  }
+  return ci;
+}
+
+// First chunk id, chunk count and first token of document n.
+__device__ __forceinline__ void doc_chunks(const ChunkGeom& g, int n, int& first, int& count, int& start, int& len) {
+  if (g.cu) {
+    first = g.offsets[n];
+    count = g.offsets[n + 1] - first;
+    start = g.cu[n];
+    len = g.cu[n + 1] - start;
+  } else {
+    first = n * g.nt;
+    count = g.nt;
+    start = n * g.seqlen;
+    len = g.seqlen;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// MFMA 16x16 tiles.  C layout (both types): lane l holds
+//   acc[j] = C[4*(l>>4) + j][l & 15],  j = 0..3.
+// Operand views in LDS:
+//   A (M x K): ROW -> A[m*lda + k];  COL -> A[k*lda + m]
+//   B (K x N): ROW -> B[k*ldb + n];  COL -> B[n*ldb + k]
+// bf16 tiles are fastest as A=ROW, B=COL (8 contiguous k per lane, one
+// 16-byte LDS read); the other views gather 8 scalars.  FP32 tiles read one
+// element per lane and are cheap in every view.
+// ----------------------------------------------------------------------------
+enum { ROW = 0, COL = 1 };
+
+template <typename E> struct Mma;
+
+template <> struct Mma<bf16_t> {
+  static constexpr int KS = 32;
+  template <int LA, int LB>
+  __device__ __forceinline__ static void step(f32x4& acc, const bf16_t* A, int lda, const bf16_t* B, int ldb,
+                                              int k0, int lane) {
+    const int r = lane & 15;
+    const int kq = (lane >> 4) * 8;
+    s16x8_t a, b;
+    if constexpr (LA == ROW) {
+      a = *reinterpret_cast<const s16x8_t*>(A + r * lda + k0 + kq);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = static_cast<short>(A[(k0 + kq + j) * lda + r]);
+    }
+    if constexpr (LB == COL) {
+      b = *reinterpret_cast<const s16x8_t*>(B + r * ldb + k0 + kq);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = static_cast<short>(B[(k0 + kq + j) * ldb + r]);
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                  acc, 0, 0, 0);
+  }
+};
+
+template <> struct Mma<float> {
+  static constexpr int KS = 4;
+  template <int LA, int LB>
+  __device__ __forceinline__ static void step(f32x4& acc, const float* A, int lda, const float* B, int ldb, int k0,
+                                              int lane) {
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+    const float a = (LA == ROW) ? A[r * lda + k0 + kq] : A[(k0 + kq) * lda + r];
+    const float b = (LB == COL) ? B[r * ldb + k0 + kq] : B[(k0 + kq) * ldb + r];
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+  }
+};
+
+// acc += A[m0:m0+16, 0:K] * B[0:K, n0:n0+16]
+template <typename E, int LA, int LB>
+__device__ __forceinline__ void mma_tile(f32x4& acc, const E* A, int lda, int m0, const E* B, int ldb, int n0, int K,
+                                         int lane) {
+  const E* a = (LA == ROW) ? A + m0 * lda : A + m0;
+  const E* b = (LB == COL) ? B + n0 * ldb : B + n0;
+  for (int k0 = 0; k0 < K; k0 += Mma<E>::KS) Mma<E>::template step<LA, LB>(acc, a, lda, b, ldb, k0, lane);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ int acc_row(int lane, int j) { return 4 * (lane >> 4) + j; }
+__device__ __forceinline__ int acc_col(int lane) { return lane & 15; }
+
+template <typename E> __device__ __forceinline__ E to_e(float x);
+template <> __device__ __forceinline__ float to_e<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t to_e<bf16_t>(float x) { return f32_to_bf16(x); }
+template <typename E> __device__ __forceinline__ float from_e(E x);
+template <> __device__ __forceinline__ float from_e<float>(float x) { return x; }
+template <> __device__ __forceinline__ float from_e<bf16_t>(bf16_t x) { return bf16_to_f32(x); }
+
+// Row padding of LDS tiles: keeps 16-byte alignment and spreads rows over banks.
+template <typename E> struct Pad;
+template <> struct Pad<bf16_t> { static constexpr int v = 8; };
+template <> struct Pad<float> { static constexpr int v = 4; };
+
+// ----------------------------------------------------------------------------
+// Cooperative tile loads (256 threads).  Rows r >= nvalid load as zero, so a
+// partial chunk never touches the next document's tokens.
+// f(r, c, x) maps the loaded value (as float) before it is stored.
+// ----------------------------------------------------------------------------
+template <typename T, typename E, int NC, typename F>
+__device__ __forceinline__ void load_rows(E* lds, int ld, const T* g, int64_t gstride, int nrows, int nvalid, F f) {
+  constexpr int V = 4;  // elements per thread per step
+  constexpr int PER_ROW = NC / V;
+  for (int idx = threadIdx.x; idx < nrows * PER_ROW; idx += kWG) {
+    const int r = idx / PER_ROW;
+    const int c = (idx - r * PER_ROW) * V;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < nvalid) x = load4(g + r * gstride + c);
+    E* dst = lds + r * ld + c;
+    dst[0] = to_e<E>(f(r, c + 0, x.x));
+    dst[1] = to_e<E>(f(r, c + 1, x.y));
+    dst[2] = to_e<E>(f(r, c + 2, x.z));
+    dst[3] = to_e<E>(f(r, c + 3, x.w));
+  }
+}
+
+// Same, stored transposed: lds[c*ld + r].
+template <typename T, typename E, int NC, typename F>
+__device__ __forceinline__ void load_rows_t(E* lds, int ld, const T* g, int64_t gstride, int nrows, int nvalid, F f) {
+  constexpr int V = 4;
+  constexpr int PER_ROW = NC / V;
+  for (int idx = threadIdx.x; idx < nrows * PER_ROW; idx += kWG) {
+    const int r = idx % nrows;  // consecutive threads walk rows: contiguous LDS writes
+    const int c = (idx / nrows) * V;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < nvalid) x = load4(g + r * gstride + c);
+    lds[(c + 0) * ld + r] = to_e<E>(f(r, c + 0, x.x));
+    lds[(c + 1) * ld + r] = to_e<E>(f(r, c + 1, x.y));
+    lds[(c + 2) * ld + r] = to_e<E>(f(r, c + 2, x.z));
+    lds[(c + 3) * ld + r] = to_e<E>(f(r, c + 3, x.w));
+  }
+}
+
+struct Ident {
+  __device__ __forceinline__ float operator()(int, int, float x) const { return x; }
+};
+
+// Store a [nrows x NC] row-major LDS/register-free tile back to global rows < nvalid.
+template <typename T, typename E, int NC>
+__device__ __forceinline__ void store_rows(T* g, int64_t gstride, const E* lds, int ld, int nvalid) {
+  constexpr int V = 4;
+  constexpr int PER_ROW = NC / V;
+  for (int idx = threadIdx.x; idx < nvalid * PER_ROW; idx += kWG) {
+    const int r = idx / PER_ROW;
+    const int c = (idx - r * PER_ROW) * V;
+    const E* src = lds + r * ld + c;
+    store4(g + r * gstride + c, make_float4(from_e<E>(src[0]), from_e<E>(src[1]), from_e<E>(src[2]), from_e<E>(src[3])));
+  }
+}
+
+// Store an accumulator tile (origin m0, n0) to global with row mask.
+template <typename T>
+__device__ __forceinline__ void store_acc_global(T* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
+                                                 int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = m0 + acc_row(lane, j);
+    if (r < nvalid) io<T>::store(g + r * gstride + n0 + acc_col(lane), acc[j]);
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ void store_acc_lds(E* lds, int ld, const f32x4& acc, int m0, int n0, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lds[(m0 + acc_row(lane, j)) * ld + n0 + acc_col(lane)] = to_e<E>(acc[j]);
+}
+
+// Transposed: lds[(n0+col)*ld + m0+row]; the four rows of a lane are contiguous.
+template <typename E>
+__device__ __forceinline__ void store_acc_lds_t(E* lds, int ld, const f32x4& acc, int m0, int n0, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lds[(n0 + acc_col(lane)) * ld + m0 + acc_row(lane, j)] = to_e<E>(acc[j]);
+}
+
+// Deterministic row sums of an fp32 [64 x ncols] LDS tile into out[64]
+// (fixed summation order; one wave per 16 rows).
+__device__ __forceinline__ void row_sums_64(const float* lds, int ld, int ncols, float* out) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    float s = 0.f;
+    for (int c = 0; c < ncols; ++c) s += lds[tid * ld + c];
+    out[tid] = s;
+  }
+}
+
+}  // namespace pkda

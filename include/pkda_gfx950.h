@@ -131,6 +131,167 @@ int pkda_recurrent_fwd(const pkda_recurrent_args* args, void* stream);
 /* Same kernel; requires seqlen == 1 and state_pool != NULL. */
 int pkda_decode_step(const pkda_recurrent_args* args, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Chunk geometry for packed documents.
+ *
+ * Chunks of PKDA_CHUNK tokens start at every document's first token.  With
+ * cu_seqlens the chunk list depends on the data, so it is built on the device
+ * into a caller-provided int32 workspace `table` of
+ *   4 * num_chunks_max + num_seqs + 1 elements,
+ * num_chunks_max = ceil(N_tok / 64) + num_seqs (an upper bound the host knows
+ * without reading cu_seqlens).  Every chunked entry point below takes the same
+ * table; launches sized by num_chunks_max skip the unused tail.  Equal-length
+ * rows need no table (pass NULL).  cu_seqlens must be nondecreasing from 0.
+ * ------------------------------------------------------------------------- */
+int pkda_chunk_table(const int32_t* cu_seqlens, int32_t num_seqs, int32_t num_chunks_max, int32_t* table,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Gate: chunk-local cumulative log-decay, and its backward.
+ *
+ * Replaces FLA's kda_gate_chunk_cumsum / kda_gate_bwd as driven by
+ * delta_feedback_experiment/fla_ops.py:290-299,423-432,480-487 (FLA works in
+ * log2; this library keeps natural log throughout).
+ *   forward:  gcum[t] = sum_{s in chunk, s <= t} glog[s], glog per gate_kind;
+ *             gcum is [N_tok, H] (PKDA_GATE_LOG_HEAD) or [N_tok, H, K] FP32.
+ *   backward: from dgcum (same shape as gcum) writes dg (same shape as g,
+ *             FP32), and for PKDA_GATE_RAW_CHANNEL dA_log [H] and
+ *             ddt_bias [H*K] through per-chunk partials dA_log_part
+ *             [num_chunks, H] and ddt_bias_part [num_chunks, H*K]
+ *             (caller workspace; summed in a fixed order -> deterministic).
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_gate_args {
+  int32_t struct_size;
+  int32_t num_seqs, seqlen, heads, head_dim, gate_kind, g_dtype;
+  const int32_t* cu_seqlens;
+  const void* g;
+  const float* A_log;
+  const float* dt_bias;
+  float* gcum;              /* forward output */
+  const float* dgcum;       /* backward input */
+  float* dg;                /* backward output, FP32, shape of g */
+  float* dA_log_part;       /* [num_chunks, H]   workspace (raw gate) */
+  float* ddt_bias_part;     /* [num_chunks, H*K] workspace (raw gate) */
+  float* dA_log;            /* [H]   (raw gate) */
+  float* ddt_bias;          /* [H*K] (raw gate) */
+  int32_t num_chunks;       /* chunks (equal rows) or num_chunks_max (packed) */
+  const int32_t* table;     /* pkda_chunk_table output or NULL */
+} pkda_gate_args;
+
+int pkda_gate_fwd(const pkda_gate_args* args, void* stream);
+int pkda_gate_bwd(const pkda_gate_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Preconditioner scan (forward) and its reverse scan (backward).
+ *
+ * Replaces FLA's ATK scans (chunk_atk_fwd / its backward) run inside
+ * chunk_precond_kda_fwd/_bwd (delta_feedback_experiment/fla_ops.py:300-339,
+ * 441-479); math of delta_feedback_experiment/pkda.py:392-398.
+ *   forward:  kw [N_tok,H,K] (dtype), A at every chunk start a_chunk
+ *             [num_chunks, H, K] FP32 (backward checkpoint), final A.
+ *   backward: dkw (FP32 [N_tok,H,K]) -> dk (FP32, accumulated: dk += ...),
+ *             dg_atk, dbeta_atk [N_tok,H] FP32, dcenter [H] (per-chunk
+ *             partials dcenter_part [num_chunks, H]), dA0 [N,H,K] when
+ *             dA0 != NULL; dA_T optional gradient of the final A.
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_precond_args {
+  int32_t struct_size;
+  int32_t dtype;            /* of k and kw */
+  int32_t num_seqs, seqlen, heads, head_dim;
+  const int32_t* cu_seqlens;
+  const void* k;
+  const float* g_atk;
+  const float* beta_atk;
+  const float* center;
+  float squash_x, squash_eps;
+  const float* initial_A_state;  /* [N,H,K] or NULL */
+  float* final_A_state;          /* [N,H,K] or NULL */
+  void* kw;                      /* forward output [N_tok,H,K] dtype */
+  float* a_chunk;                /* [num_chunks, H, K] */
+  int32_t num_chunks;
+  const float* dkw;              /* backward input */
+  float* dk;                     /* backward: accumulated into */
+  float* dg_atk;
+  float* dbeta_atk;
+  float* dcenter_part;           /* [num_chunks, H] workspace */
+  float* dcenter;                /* [H] */
+  float* dA0;                    /* [N,H,K] or NULL */
+  const float* dA_T;             /* [N,H,K] or NULL */
+} pkda_precond_args;
+
+int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
+int pkda_precond_bwd(const pkda_precond_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Chunked forward (training / prefill).
+ *
+ * Replaces chunk_precond_kda_fwd as called by the pkda_recurrence custom op
+ * (delta_feedback_experiment/fla_ops.py:316-339) and by chunk_precond_kda
+ * (delta_feedback_experiment/pkda.py:475).  Inputs are the gate's gcum and the
+ * preconditioner's kw (kw == k when there is no preconditioner).
+ * Per chunk: Akk (strictly lower, row = read key, col = write key),
+ * T = (I + Akk)^-1, w = T diag(beta) (exp(gcum) * k), u = T diag(beta) v,
+ * Aqk (inclusive, with `scale`); per document, sequentially over chunks:
+ * U = u - w S, o = (exp(gcum) * scale q) S + Aqk U, S <- exp(gcum_last) S + kg^T U.
+ * Saved for the backward (all [N_tok, H, *] in dtype unless stated):
+ * w, u (overwritten with U), aqk [.., 64], akk (= T) [.., 64],
+ * h [num_chunks, H, K, V] (state entering each chunk; NULL when not training).
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_chunk_fwd_args {
+  int32_t struct_size;
+  int32_t dtype;
+  int32_t num_seqs, seqlen, heads, head_dim;
+  const int32_t* cu_seqlens;
+  int32_t num_chunks;
+  const int32_t* table;
+  const void *q, *k, *kw, *v;
+  const float* gcum;
+  int32_t gate_per_channel;
+  const float* beta;
+  float scale;
+  const float* initial_state;  /* [N,H,K,V] or NULL */
+  float* final_state;          /* [N,H,K,V] or NULL */
+  void* o;
+  void *w, *u, *aqk, *akk, *h;
+} pkda_chunk_fwd_args;
+
+int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Chunked backward.
+ *
+ * Replaces chunk_precond_kda_bwd (delta_feedback_experiment/fla_ops.py:441-479)
+ * for the recurrence proper (the gate and preconditioner backward are the
+ * entry points above).  Consumes the forward's saved tensors and do
+ * (and dht, the final-state gradient, or NULL).  Workspace (caller):
+ * dh [num_chunks, H, K, V] (dtype), du, dw [N_tok,H,K] FP32, daqk, da
+ * [N_tok,H,64] FP32.  Outputs (FP32): dq, dk (read key), dkw (write key;
+ * when kw == k it is added into dk and may be NULL), dv, dbeta [N_tok,H],
+ * dgcum (shape of gcum), dh0 [N,H,K,V] (NULL if not wanted).
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_chunk_bwd_args {
+  int32_t struct_size;
+  int32_t dtype;
+  int32_t num_seqs, seqlen, heads, head_dim;
+  const int32_t* cu_seqlens;
+  int32_t num_chunks;
+  const int32_t* table;
+  const void *q, *k, *kw, *v;
+  const float* gcum;
+  int32_t gate_per_channel;
+  const float* beta;
+  float scale;
+  const float* initial_state;
+  const void *w, *u, *aqk, *akk, *h;
+  const void* do_;
+  const float* dht;
+  void* dh;
+  float *du, *dw, *daqk, *da;
+  float *dq, *dk, *dkw, *dv, *dbeta, *dgcum, *dh0;
+} pkda_chunk_bwd_args;
+
+int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,108 @@
+"""Chunked PKDA kernels on the GPU vs the CPU oracle.
+
+Relative L2 bars: FP32 inputs <= 1e-5 against the FP32 oracle; BF16 inputs
+<= 2e-2 against the FP32 oracle on the same BF16-rounded inputs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import rel_l2
+from oracle import pkda_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+    from delta_feedback_experiment_amd import _lib
+
+    _lib.lib()
+    return torch.device("cuda:0")
+
+
+def make_inputs(B, T, H, D, dtype, seed=0, strong=False, per_channel=False):
+    gen = torch.Generator().manual_seed(seed)
+
+    def randn(*s):
+        return torch.randn(*s, generator=gen)
+
+    q = oracle.l2norm(randn(B, T, H, D)).to(dtype)
+    k = oracle.l2norm(randn(B, T, H, D)).to(dtype)
+    v = randn(B, T, H, D).to(dtype)
+    beta = torch.sigmoid(randn(B, T, H))
+    g = -F.softplus(randn(B, T, H, D) if per_channel else randn(B, T, H))
+    if strong:
+        mask = torch.rand(B, T, generator=gen) < 0.1
+        m = mask[:, :, None] if g.dim() == 3 else mask[:, :, None, None]
+        g = torch.where(m, torch.full_like(g, -8.0), g)
+    return q, k, v, g, beta
+
+
+def run_chunk_forward(dev, q, k, v, g, beta, S0=None, cu=None):
+    from delta_feedback_experiment_amd import _lib
+    from delta_feedback_experiment_amd.chunk import ChunkPlan, chunk_forward, gate_forward
+
+    qd, kd, vd = (t.to(dev).contiguous() for t in (q, k, v))
+    plan = ChunkPlan.make(qd, None if cu is None else cu.to(dev))
+    kind = _lib.GATE_LOG_HEAD if g.dim() == 3 else _lib.GATE_LOG_CHANNEL
+    gcum = gate_forward(plan, g.to(dev).float().contiguous(), kind, None, None)
+    flat = lambda t: t.reshape(plan.num_tokens, plan.heads, plan.head_dim)  # noqa: E731
+    o, S, saved = chunk_forward(
+        plan, flat(qd), flat(kd), flat(kd), flat(vd), gcum, beta.to(dev).float().contiguous(),
+        q.shape[-1] ** -0.5, None if S0 is None else S0.to(dev).contiguous(), True, True,
+    )
+    torch.cuda.synchronize()
+    return o.reshape(q.shape), S, saved
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_chunk_forward_matches_oracle(dev, D, dtype):
+    print(f"[gpu] chunk fwd D={D} {dtype}", flush=True)
+    B, T, H = 2, 200, 3  # 200 = 3 full chunks + a partial one
+    q, k, v, g, beta = make_inputs(B, T, H, D, dtype, seed=D, strong=True)
+    S0 = 0.02 * torch.randn(B, H, D, D)
+    o_ref, S_ref, _ = oracle.pkda_reference(q, k, v, g, beta, initial_state=S0, output_final_state=True,
+                                            out_dtype=torch.float32)
+    o, S, _ = run_chunk_forward(dev, q, k, v, g, beta, S0)
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    print(f"  rel o {rel_l2(o.float(), o_ref):.3e} S {rel_l2(S, S_ref):.3e}", flush=True)
+    assert rel_l2(o.float(), o_ref) < tol
+    assert rel_l2(S, S_ref) < tol
+
+
+def test_chunk_forward_c1_fp32(dev):
+    """B1 T256 H4 d64 FP32, zero initial state."""
+    print("[gpu] chunk fwd c1", flush=True)
+    q, k, v, g, beta = make_inputs(1, 256, 4, 64, torch.float32, seed=1)
+    o_ref, S_ref, _ = oracle.pkda_reference(q, k, v, g, beta, output_final_state=True)
+    o, S, _ = run_chunk_forward(dev, q, k, v, g, beta)
+    print(f"  rel o {rel_l2(o, o_ref):.3e} S {rel_l2(S, S_ref):.3e}", flush=True)
+    assert rel_l2(o, o_ref) < FP32_TOL
+    assert rel_l2(S, S_ref) < FP32_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_chunk_forward_varlen(dev, dtype):
+    print(f"[gpu] chunk fwd varlen {dtype}", flush=True)
+    D, H = 64, 2
+    cu = torch.tensor([0, 17, 17, 100, 164, 300, 301], dtype=torch.int32)
+    q, k, v, g, beta = make_inputs(1, 301, H, D, dtype, seed=5)
+    S0 = 0.02 * torch.randn(6, H, D, D)
+    o_ref, S_ref, _ = oracle.pkda_reference(q, k, v, g, beta, initial_state=S0, output_final_state=True,
+                                            cu_seqlens=cu, out_dtype=torch.float32)
+    o, S, _ = run_chunk_forward(dev, q, k, v, g, beta, S0, cu)
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    print(f"  rel o {rel_l2(o.float(), o_ref):.3e} S {rel_l2(S, S_ref):.3e}", flush=True)
+    assert rel_l2(o.float(), o_ref) < tol
+    assert rel_l2(S, S_ref) < tol
+    assert torch.equal(S[1].cpu(), S0[1])
