@@ -112,3 +112,231 @@ def chunk_forward(
     )
     _lib.call("pkda_chunk_fwd", args, _stream(dev))
     return o, S_T, FwdSaved(w, u, aqk, akk, h)
+
+
+@dataclass
+class BwdGrads:
+    dq: Tensor
+    dk: Tensor
+    dkw: Tensor | None
+    dv: Tensor
+    dbeta: Tensor
+    dgcum: Tensor
+    dh0: Tensor | None
+
+
+def chunk_backward(
+    plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor, scale: float,
+    initial_state: Tensor | None, saved: FwdSaved, do: Tensor, dht: Tensor | None, want_dh0: bool,
+) -> BwdGrads:
+    """Chunk backward on flat operands; gradients are FP32."""
+    dev = q.device
+    N, H, D = plan.num_seqs, plan.heads, plan.head_dim
+    ntok = plan.num_tokens
+    f32 = dict(device=dev, dtype=torch.float32)
+    kw_is_k = kw.data_ptr() == k.data_ptr()
+    dq = torch.empty(ntok, H, D, **f32)
+    dk = torch.empty(ntok, H, D, **f32)
+    dkw = None if kw_is_k else torch.empty(ntok, H, D, **f32)
+    dv = torch.empty(ntok, H, D, **f32)
+    dbeta = torch.empty(ntok, H, **f32)
+    dgcum = torch.empty_like(gcum)
+    dh0 = torch.empty(N, H, D, D, **f32) if want_dh0 else None
+    dh = torch.empty(plan.num_chunks, H, D, D, device=dev, dtype=q.dtype)
+    du = torch.empty(ntok, H, D, **f32)
+    dw = torch.empty(ntok, H, D, **f32)
+    daqk = torch.empty(ntok, H, CHUNK_SIZE, **f32)
+    da = torch.empty(ntok, H, CHUNK_SIZE, **f32)
+    args = _lib.ChunkBwdArgs(
+        dtype=_dtype_code(q), **plan.common(),
+        q=_ptr(q), k=_ptr(k), kw=_ptr(kw), v=_ptr(v), gcum=_ptr(gcum),
+        gate_per_channel=int(gcum.dim() == 3), beta=_ptr(beta32), scale=float(scale),
+        initial_state=_ptr(initial_state),
+        w=_ptr(saved.w), u=_ptr(saved.u), aqk=_ptr(saved.aqk), akk=_ptr(saved.akk), h=_ptr(saved.h),
+        do=_ptr(do), dht=_ptr(dht), dh=_ptr(dh), du=_ptr(du), dw=_ptr(dw), daqk=_ptr(daqk), da=_ptr(da),
+        dq=_ptr(dq), dk=_ptr(dk), dkw=_ptr(dkw), dv=_ptr(dv), dbeta=_ptr(dbeta), dgcum=_ptr(dgcum),
+        dh0=_ptr(dh0),
+    )
+    _lib.call("pkda_chunk_bwd", args, _stream(dev))
+    return BwdGrads(dq, dk, dkw, dv, dbeta, dgcum, dh0)
+
+
+def gate_backward(
+    plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt_bias: Tensor | None, dgcum: Tensor,
+) -> tuple[Tensor, Tensor | None, Tensor | None]:
+    """``dg`` (FP32, shape of ``g``) and, for the raw gate, ``dA_log``, ``ddt_bias``."""
+    dev = dgcum.device
+    dg = torch.empty(dgcum.shape, device=dev, dtype=torch.float32)
+    raw = kind == _lib.GATE_RAW_CHANNEL
+    dA_part = ddt_part = dA_log = ddt_bias = None
+    if raw:
+        H, D = plan.heads, plan.head_dim
+        dA_part = torch.empty(plan.num_chunks, H, device=dev, dtype=torch.float32)
+        ddt_part = torch.empty(plan.num_chunks, H, D, device=dev, dtype=torch.float32)
+        dA_log = torch.empty(H, device=dev, dtype=torch.float32)
+        ddt_bias = torch.empty(H * D, device=dev, dtype=torch.float32)
+    args = _lib.GateArgs(
+        num_seqs=plan.num_seqs, seqlen=plan.seqlen, heads=plan.heads, head_dim=plan.head_dim,
+        gate_kind=kind, g_dtype=_dtype_code(g), cu_seqlens=_ptr(plan.cu_seqlens), g=_ptr(g),
+        A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), dgcum=_ptr(dgcum), dg=_ptr(dg),
+        dA_log_part=_ptr(dA_part), ddt_bias_part=_ptr(ddt_part), dA_log=_ptr(dA_log), ddt_bias=_ptr(ddt_bias),
+        num_chunks=plan.num_chunks, table=_ptr(plan.table),
+    )
+    _lib.call("pkda_gate_bwd", args, _stream(dev))
+    return dg, dA_log, ddt_bias
+
+
+def _flat(t: Tensor, plan: ChunkPlan) -> Tensor:
+    return t.reshape(plan.num_tokens, plan.heads, *t.shape[3:]) if t.dim() >= 3 else t
+
+
+class _ChunkPKDA(torch.autograd.Function):
+    """Differentiable chunked PKDA over the gfx950 kernels.
+
+    Saving: ``lean`` keeps only the inputs and rebuilds the chunk quantities
+    (WY factors, chunk states) with a second forward inside the backward;
+    otherwise they are kept from the forward.  Either way the gradients are
+    those of the same kernels on the same inputs.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, g_atk, beta_atk, A_log, dt_bias, log_atk_scale,
+                initial_state, initial_A_state, cu_seqlens, opts):
+        from .pkda import gate_form
+        from . import precond as pre
+
+        use_gate, scale, output_final_state, x, eps, lean = opts
+        plan = ChunkPlan.make(q, cu_seqlens)
+        kind, g_used = gate_form(g, q.shape[:-1], q.shape[-1], use_gate, A_log, dt_bias)
+        g_used = g_used.contiguous()
+        if g_used.dtype not in (torch.float32, torch.bfloat16):
+            g_used = g_used.float()
+        A_log32, dt32 = _f32(A_log), _f32(dt_bias)
+        qf, kf, vf = (_flat(t.contiguous(), plan) for t in (q, k, v))
+        beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
+        s0 = _f32(initial_state)
+        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32)
+        precond = g_atk is not None
+        if precond:
+            pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, x, eps, initial_A_state)
+            kwf, A_T = pstate.kw, pstate.final_A
+        else:
+            pstate, kwf, A_T = None, kf, None
+        needs_grad = any(ctx.needs_input_grad)
+        o, S_T, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, scale, s0,
+                                      output_final_state, save_states=needs_grad and not lean)
+        if needs_grad:
+            ctx.plan, ctx.kind, ctx.scale, ctx.lean, ctx.x, ctx.eps = plan, kind, scale, lean, x, eps
+            ctx.per_head_raw = use_gate and g.dim() == q.dim() - 1
+            ctx.dtypes = tuple(None if t is None else t.dtype for t in (q, k, v, g, beta, g_atk, beta_atk,
+                                                                          A_log, dt_bias, log_atk_scale,
+                                                                          initial_state, initial_A_state))
+            ctx.saved_fwd = None if lean else saved
+            ctx.pstate = pstate
+            ctx.save_for_backward(qf, kf, kwf, vf, gcum, beta32, s0, g_used, A_log32, dt32,
+                                  None if g_atk is None else _f32(g_atk),
+                                  None if beta_atk is None else _f32(beta_atk),
+                                  None if log_atk_scale is None else _f32(log_atk_scale))
+        o = o.reshape(v.shape)
+        return o, S_T, A_T
+
+    @staticmethod
+    def backward(ctx, do, dS_T, dA_T):
+        from . import precond as pre
+
+        (qf, kf, kwf, vf, gcum, beta32, s0, g_used, A_log32, dt32,
+         g_atk32, beta_atk32, center32) = ctx.saved_tensors
+        plan = ctx.plan
+        saved = ctx.saved_fwd
+        if saved is None:  # lean: rebuild the chunk quantities
+            _, _, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, False, True)
+        dof = _flat(do.to(qf.dtype).contiguous(), plan)
+        dht = None if dS_T is None else dS_T.float().contiguous()
+        want_dh0 = ctx.needs_input_grad[10]
+        gr = chunk_backward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, saved, dof, dht, want_dh0)
+        dk = gr.dk
+        dg_atk = dbeta_atk = dcenter = dA0 = None
+        if ctx.pstate is not None:
+            pg = pre.precond_backward(plan, kf, g_atk32, beta_atk32, center32, ctx.x, ctx.eps, ctx.pstate,
+                                      gr.dkw, dk, None if dA_T is None else dA_T.float().contiguous(),
+                                      want_dA0=ctx.needs_input_grad[11])
+            dg_atk, dbeta_atk, dcenter, dA0 = pg
+        dg, dA_log, ddt_bias = gate_backward(plan, _flat(g_used, plan), ctx.kind, A_log32, dt32, gr.dgcum)
+        shape = tuple(do.shape)
+        dt = ctx.dtypes
+
+        def cast(x, i, shp=None):
+            if x is None or dt[i] is None or not ctx.needs_input_grad[i]:
+                return None
+            x = x if shp is None else x.reshape(shp)
+            return x.to(dt[i])
+
+        dg = dg.reshape(*shape[:-1], *dg.shape[2:])
+        if ctx.per_head_raw:
+            dg = dg.sum(-1)
+        return (
+            cast(gr.dq, 0, shape), cast(dk, 1, shape), cast(gr.dv, 2, shape), cast(dg, 3),
+            cast(gr.dbeta, 4, shape[:-1]),
+            cast(dg_atk, 5, shape[:-1]), cast(dbeta_atk, 6, shape[:-1]),
+            cast(dA_log, 7), cast(ddt_bias, 8), cast(dcenter, 9),
+            cast(gr.dh0, 10), cast(dA0, 11), None, None,
+        )
+
+
+def chunk_pkda(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    g: Tensor,
+    beta: Tensor,
+    *,
+    g_atk: Tensor | None = None,
+    beta_atk: Tensor | None = None,
+    A_log: Tensor | None = None,
+    dt_bias: Tensor | None = None,
+    use_gate_in_kernel: bool = False,
+    scale: float | None = None,
+    initial_state: Tensor | None = None,
+    initial_A_state: Tensor | None = None,
+    output_final_state: bool = False,
+    cu_seqlens: Tensor | None = None,
+    x: float = 1.0,
+    eps: float = 1e-6,
+    log_atk_scale: Tensor | None = None,
+    lean: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    **_ignored,
+) -> tuple[Tensor, Tensor | None, Tensor | None]:
+    """Stateful, differentiable chunked PKDA: ``(o, S_T, A_T)``.
+
+    The call surface of FLA's ``chunk_precond_kda`` as
+    ``PreconditionedKDA._cuda_recurrence`` uses it (pkda.py:450-475).  ``g`` is
+    the raw gate (``use_gate_in_kernel``, with ``A_log``/``dt_bias``) or the
+    natural-log decay, per head ``[B,T,H]`` or per channel ``[B,T,H,K]``.
+    The preconditioner (``g_atk``, ``beta_atk``, ``log_atk_scale``, ``x``,
+    ``eps``) runs when ``g_atk`` is given.  ``scale`` defaults to ``K**-0.5``.
+    Gradients flow to every tensor input including ``initial_state`` and
+    ``initial_A_state``.
+    """
+    from .pkda import _check_common, _require_cuda
+
+    if use_qk_l2norm_in_kernel:
+        raise ValueError("q and k arrive L2-normalised (pkda.py:464-465); in-kernel norm is not provided")
+    _check_common(q, k, v, beta)
+    _require_cuda(q, k, v, g, beta, g_atk, beta_atk, initial_state, initial_A_state, cu_seqlens, A_log, dt_bias,
+                  log_atk_scale)
+    if g_atk is not None and (beta_atk is None or log_atk_scale is None):
+        raise ValueError("the preconditioner needs g_atk, beta_atk and log_atk_scale")
+    D = q.shape[-1]
+    if scale is None:
+        scale = D ** -0.5
+    N = q.shape[0] if cu_seqlens is None else cu_seqlens.numel() - 1
+    if initial_state is not None and tuple(initial_state.shape) != (N, q.shape[2], D, D):
+        raise ValueError(f"initial_state must be {(N, q.shape[2], D, D)}")
+    opts = (use_gate_in_kernel, float(scale), output_final_state, float(x), float(eps), lean)
+    with torch.cuda.device(q.device):
+        o, S_T, A_T = _ChunkPKDA.apply(q, k, v, g, beta, g_atk, beta_atk, A_log, dt_bias, log_atk_scale,
+                                      initial_state, initial_A_state, cu_seqlens, opts)
+    if not output_final_state:
+        return o, None, None
+    return o, S_T, A_T

@@ -106,3 +106,47 @@ def test_chunk_forward_varlen(dev, dtype):
     assert rel_l2(o.float(), o_ref) < tol
     assert rel_l2(S, S_ref) < tol
     assert torch.equal(S[1].cpu(), S0[1])
+
+
+def _grad_case(dev, B, T, H, D, dtype, seed, cu=None, S0_scale=0.02):
+    from delta_feedback_experiment_amd.chunk import chunk_pkda
+
+    q, k, v, g, beta = make_inputs(B, T, H, D, dtype, seed=seed, strong=True)
+    N = B if cu is None else cu.numel() - 1
+    gen = torch.Generator().manual_seed(seed + 100)
+    S0 = S0_scale * torch.randn(N, H, D, D, generator=gen)
+    do = torch.randn(B, T, H, D, generator=gen).to(dtype)
+    dS = torch.randn(N, H, D, D, generator=gen)
+    # CPU oracle in FP32 on the same (rounded) inputs
+    leaves = [t.float().clone().requires_grad_() for t in (q, k, v, g, beta, S0)]
+    o_r, S_r, _ = oracle.pkda_reference(*leaves[:5], initial_state=leaves[5], output_final_state=True,
+                                        cu_seqlens=cu, out_dtype=torch.float32)
+    ref = torch.autograd.grad((o_r * do.float()).sum() + (S_r * dS).sum(), leaves)
+    # GPU
+    dl = [t.to(dev).clone().requires_grad_() for t in (q, k, v, g, beta, S0)]
+    o, S, _ = chunk_pkda(*dl[:5], initial_state=dl[5], output_final_state=True,
+                         cu_seqlens=None if cu is None else cu.to(dev))
+    got = torch.autograd.grad((o.float() * do.to(dev).float()).sum() + (S * dS.to(dev)).sum(), dl)
+    torch.cuda.synchronize()
+    res = {"o": rel_l2(o.float(), o_r), "S": rel_l2(S, S_r)}
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "dS0"), got, ref):
+        res[name] = rel_l2(a.float(), b)
+    print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
+    return res
+
+
+@pytest.mark.parametrize("D,dtype", [(64, torch.float32), (64, torch.bfloat16), (128, torch.bfloat16)])
+def test_chunk_gradients_match_oracle(dev, D, dtype):
+    print(f"[gpu] chunk grads D={D} {dtype}", flush=True)
+    res = _grad_case(dev, 2, 200, 3, D, dtype, seed=7 + D)
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    for name, val in res.items():
+        assert val < tol, (name, val)
+
+
+def test_chunk_gradients_varlen(dev):
+    print("[gpu] chunk grads varlen", flush=True)
+    cu = torch.tensor([0, 17, 17, 100, 164, 300, 301], dtype=torch.int32)
+    res = _grad_case(dev, 1, 301, 2, 64, torch.bfloat16, seed=3, cu=cu)
+    for name, val in res.items():
+        assert val < BF16_TOL, (name, val)
