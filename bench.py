@@ -1,0 +1,379 @@
+"""PKDA recurrence benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c5]
+                    [--decode-steps 1000] [--no-decode] [--no-cpu]
+
+Mirrors the structure of the reference's ``scripts/pkda_bench.py`` (seeded
+synthetic inputs, warm-up, event-timed repeats): one *step* is one forward +
+backward of the chunked PKDA recurrence over one batch of the workload
+(default ``c2``: B=8, T=4096, H=16, d=128, chunk 64, BF16 q/k/v, FP32 state,
+per-head log-decay, returning dq, dk, dv, dbeta, dg).  Inputs are resident in
+HBM before the timed region starts.
+
+Printed as ONE JSON line:
+  value           tokens/s of the whole fwd+bwd step (K steps between two
+                  synchronised events);
+  roofline        the dominant kernel of the step, timed with HIP events on
+                  the stream it runs on, against bf16 dense MFMA peak, with its
+                  algorithmic flops per launch (per token-head figures below);
+  cpu_baseline    the CPU oracle (a restatement of the reference's portable
+                  recurrence) timed on this host over a bounded sample;
+  decode          the batched slot-pool decode step (B=256 live sequences in
+                  a 512-slot [512, 32, 128, 128] FP32 pool, 1000 steps),
+                  achieved HBM GB/s against 8 TB/s.
+
+Algorithmic work per token-head (C = 64, dk = dv = d; the triangular solve,
+gate scans and elementwise work are not counted):
+  fwd intra   8Cd           (Akk, Aqk, W, Uu)
+  fwd state   6d^2 + 2Cd    (W S, Q S, Kg^T U; Aqk U)
+  bwd state   6d^2 + 2Cd    (Kg dS, Qg^T dO, W^T dU; Aqk^T dO)
+  bwd dqkw    6d^2 + 2Cd    (dO S^T, dU S^T, U dS^T; dO U^T)
+  bwd wy      8Cd           (T^T dW, T^T dU, dW Bw^T, dU Bv^T)
+  bwd intra   8Cd           (pairwise dq, dk, dkw products)
+  total       18d^2 + 30Cd = 540,672 flop at d = 128
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
+
+MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA, flop/s (MI355X published figure)
+HBM_PEAK = 8.0e12        # bytes/s
+CHUNK = 64
+
+WORKLOADS = {
+    "c2": dict(B=8, T=4096, H=16, D=128, strong=False, s0=False, varlen=False),
+    "c3": dict(B=1, T=32768, H=16, D=128, strong=False, s0=False, varlen=True),
+    "c5": dict(B=2, T=16384, H=32, D=128, strong=True, s0=True, varlen=False),
+}
+
+
+def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
+    """Algorithmic flops per token-head of each kernel of the step."""
+    return {
+        "fwd_intra": 8 * C * D,
+        "fwd_state": 6 * D * D + 2 * C * D,
+        "bwd_state": 6 * D * D + 2 * C * D,
+        "bwd_dqkw": 6 * D * D + 2 * C * D,
+        "bwd_wy": 8 * C * D,
+        "bwd_intra": 8 * C * D,
+    }
+
+
+def l2norm(t: torch.Tensor) -> torch.Tensor:
+    f = t.float()
+    return f * torch.rsqrt(f.square().sum(-1, keepdim=True) + 1e-6)
+
+
+def geometric_cu_seqlens(total: int, gen: torch.Generator) -> torch.Tensor:
+    """Document lengths 16 + Geometric(p = 1/1009) (mean 1024), truncated to ``total``."""
+    p = 1.0 / 1009.0
+    lens = []
+    acc = 0
+    while acc < total:
+        u = torch.rand((), generator=gen, dtype=torch.float64).item()
+        n = 16 + int(math.floor(math.log1p(-u) / math.log1p(-p)))
+        n = min(n, total - acc)
+        lens.append(n)
+        acc += n
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    return torch.tensor(cu, dtype=torch.int32)
+
+
+def make_chunk_inputs(w: dict, dev: torch.device, seed: int = 42):
+    B, T, H, D = w["B"], w["T"], w["H"], w["D"]
+    gen = torch.Generator(device=dev).manual_seed(seed)
+
+    def randn(*s):
+        return torch.randn(*s, generator=gen, device=dev)
+
+    q = l2norm(randn(B, T, H, D)).to(torch.bfloat16)
+    k = l2norm(randn(B, T, H, D)).to(torch.bfloat16)
+    v = randn(B, T, H, D).to(torch.bfloat16)
+    beta = torch.sigmoid(randn(B, T, H))
+    g = -F.softplus(randn(B, T, H))
+    if w["strong"]:
+        mask = torch.rand(B, T, generator=gen, device=dev) < 0.1
+        g = torch.where(mask[:, :, None], torch.full_like(g, -8.0), g)
+    do = randn(B, T, H, D).to(torch.bfloat16)
+    cu = None
+    N = B
+    if w["varlen"]:
+        cu = geometric_cu_seqlens(T, torch.Generator().manual_seed(seed)).to(dev)
+        N = cu.numel() - 1
+    s0 = 0.02 * randn(N, H, D, D) if w["s0"] else None
+    return dict(q=q, k=k, v=v, g=g, beta=beta, do=do, cu=cu, s0=s0)
+
+
+def fwd_bwd(inp: dict, leaves: list[torch.Tensor]):
+    from delta_feedback_experiment_amd import chunk_pkda
+
+    q, k, v, g, beta = leaves[:5]
+    s0 = leaves[5] if len(leaves) > 5 else None
+    o, S, _ = chunk_pkda(q, k, v, g, beta, initial_state=s0, output_final_state=s0 is not None,
+                         cu_seqlens=inp["cu"])
+    outs = [o] if S is None else [o, S]
+    grads = [inp["do"]] if S is None else [inp["do"], torch.zeros_like(S)]
+    return torch.autograd.grad(outs, leaves, grads)
+
+
+def time_step(inp: dict, steps: int, warmup: int) -> float:
+    names = ["q", "k", "v", "g", "beta"] + (["s0"] if inp["s0"] is not None else [])
+    leaves = [inp[n].detach().requires_grad_() for n in names]
+    for _ in range(warmup):
+        fwd_bwd(inp, leaves)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fwd_bwd(inp, leaves)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
+    """Average duration (ms) of each kernel of the step, launched one stage at a
+    time on the current stream with events around each launch."""
+    from delta_feedback_experiment_amd import _lib
+    from delta_feedback_experiment_amd.chunk import ChunkPlan, gate_forward
+    from delta_feedback_experiment_amd.pkda import _ptr, _stream
+
+    dev = inp["q"].device
+    plan = ChunkPlan.make(inp["q"], inp["cu"])
+    ntok, H, D = plan.num_tokens, plan.heads, plan.head_dim
+    flat = lambda t: t.reshape(ntok, H, D)  # noqa: E731
+    q, k, v, do = (flat(inp[n].contiguous()) for n in ("q", "k", "v", "do"))
+    beta = inp["beta"].float().reshape(ntok, H).contiguous()
+    gcum = gate_forward(plan, inp["g"].reshape(ntok, H).contiguous(), _lib.GATE_LOG_HEAD, None, None)
+    bf = dict(device=dev, dtype=torch.bfloat16)
+    f32 = dict(device=dev, dtype=torch.float32)
+    o, wbuf, ubuf = torch.empty(ntok, H, D, **bf), torch.empty(ntok, H, D, **bf), torch.empty(ntok, H, D, **bf)
+    aqk, akk = torch.empty(ntok, H, CHUNK, **bf), torch.empty(ntok, H, CHUNK, **bf)
+    h = torch.empty(plan.num_chunks, H, D, D, **bf)
+    dh = torch.empty(plan.num_chunks, H, D, D, **bf)
+    du, dw = torch.empty(ntok, H, D, **f32), torch.empty(ntok, H, D, **f32)
+    daqk, da = torch.empty(ntok, H, CHUNK, **f32), torch.empty(ntok, H, CHUNK, **f32)
+    dq, dk, dv = (torch.empty(ntok, H, D, **f32) for _ in range(3))
+    dbeta, dgcum = torch.empty(ntok, H, **f32), torch.empty(ntok, H, **f32)
+    s0 = inp["s0"]
+    scale = D ** -0.5
+    fa = _lib.ChunkFwdArgs(
+        dtype=_lib.PKDA_BF16, **plan.common(), q=_ptr(q), k=_ptr(k), kw=_ptr(k), v=_ptr(v), gcum=_ptr(gcum),
+        gate_per_channel=0, beta=_ptr(beta), scale=scale, initial_state=_ptr(s0), final_state=None, o=_ptr(o),
+        w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h),
+    )
+    ba = _lib.ChunkBwdArgs(
+        dtype=_lib.PKDA_BF16, **plan.common(), q=_ptr(q), k=_ptr(k), kw=_ptr(k), v=_ptr(v), gcum=_ptr(gcum),
+        gate_per_channel=0, beta=_ptr(beta), scale=scale, initial_state=_ptr(s0),
+        w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), do=_ptr(do), dht=None, dh=_ptr(dh),
+        du=_ptr(du), dw=_ptr(dw), daqk=_ptr(daqk), da=_ptr(da), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
+        dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None,
+    )
+    stages = [
+        ("fwd_intra", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_INTRA),
+        ("fwd_state", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_STATE),
+        ("bwd_state", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_STATE),
+        ("bwd_dqkw", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_DQKW),
+        ("bwd_wy", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_WY),
+        ("bwd_intra", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_INTRA),
+    ]
+    stream = _stream(dev)
+    events = {name: [] for name, *_ in stages}
+
+    def run(record: bool):
+        for name, fn, args, mask in stages:
+            args.stages = mask
+            if record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            _lib.call(fn, args, stream)
+            if record:
+                e1.record()
+                events[name].append((e0, e1))
+
+    run(False)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        run(True)
+    torch.cuda.synchronize()
+    return {name: sum(a.elapsed_time(b) for a, b in ev) / len(ev) for name, ev in events.items()}
+
+
+def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7) -> dict:
+    """B=256 live sequences in a 512-slot FP32 pool [512, 32, 128, 128]."""
+    from delta_feedback_experiment_amd import pkda_decode_step_
+
+    P, N, H, D = 512, 256, 32, 128
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    pool = 0.02 * torch.randn(P, H, D, D, generator=gen, device=dev)
+    cpu_gen = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(P, generator=cpu_gen)[:N] for _ in range(steps)]).to(torch.int32).to(dev)
+    sets = []
+    for _ in range(4):
+        q = l2norm(torch.randn(N, H, D, generator=gen, device=dev)).to(torch.bfloat16)
+        k = l2norm(torch.randn(N, H, D, generator=gen, device=dev)).to(torch.bfloat16)
+        v = torch.randn(N, H, D, generator=gen, device=dev).to(torch.bfloat16)
+        beta = torch.sigmoid(torch.randn(N, H, generator=gen, device=dev))
+        g = -F.softplus(torch.randn(N, H, generator=gen, device=dev))
+        sets.append((q, k, v, g, beta))
+    out = torch.empty(N, H, D, device=dev, dtype=torch.bfloat16)
+    for i in range(warmup):
+        pkda_decode_step_(*sets[i % 4], pool, idx[i % steps], out=out)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        ev[i][0].record()
+        pkda_decode_step_(*sets[i % 4], pool, idx[i], out=out)
+        ev[i][1].record()
+    t1.record()
+    torch.cuda.synchronize()
+    wall_ms = t0.elapsed_time(t1)
+    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    nbytes = 2 * N * H * D * D * 4 + N * H * (2 * (2 * D + D) + 2 * 2) + N * H * D * 2 + 4 * N
+    return {
+        "workload": "c4 decode: 256 live of 512 slots, H32 d128, fp32 state, bf16 q/k/v",
+        "steps": steps,
+        "ms_per_step": wall_ms / steps,
+        "tokens_per_s": N * steps / (wall_ms / 1e3),
+        "kernel_us": kern_ms * 1e3,
+        "bytes_per_step": nbytes,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": nbytes / (kern_ms / 1e3) / 1e9,
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": nbytes / (kern_ms / 1e3) / HBM_PEAK,
+            "traffic": None,
+        },
+    }
+
+
+def cpu_baseline(D: int = 128, H: int = 16, T: int = 192, seed: int = 3) -> dict:
+    """The CPU oracle's fwd+bwd on a B=1 slice of the workload (FP32, all host cores)."""
+    from oracle import pkda_oracle as oracle
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(seed)
+    q = l2norm(torch.randn(1, T, H, D, generator=gen)).to(torch.bfloat16).float()
+    k = l2norm(torch.randn(1, T, H, D, generator=gen)).to(torch.bfloat16).float()
+    v = torch.randn(1, T, H, D, generator=gen).to(torch.bfloat16).float()
+    beta = torch.sigmoid(torch.randn(1, T, H, generator=gen))
+    g = -F.softplus(torch.randn(1, T, H, generator=gen))
+    do = torch.randn(1, T, H, D, generator=gen)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v, g, beta)]
+    t0 = time.perf_counter()
+    o, _, _ = oracle.pkda_reference(*leaves)
+    torch.autograd.grad(o, leaves, do)
+    dt = time.perf_counter() - t0
+    return {
+        "value": T / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle fwd+bwd (token-recurrent FP32 torch CPU), B=1 T={T} H={H} d={D}, "
+                  f"{dt:.1f} s; same per-token work as one row of the GPU workload",
+        "seconds": dt,
+        "token_heads_per_s": T * H / dt,
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=512)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the recurrence never communicates; every (sequence, head) shards with no exchange).",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    from delta_feedback_experiment_amd import _lib
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = WORKLOADS[args.workload]
+    print(f"[bench] workload {args.workload} {w}", file=sys.stderr, flush=True)
+    inp = make_chunk_inputs(w, dev)
+    ntok = w["B"] * w["T"]
+    ms = time_step(inp, args.steps, args.warmup)
+    print(f"[bench] fwd+bwd {ms:.3f} ms/step", file=sys.stderr, flush=True)
+    per_th = stage_flops(w["D"])
+    token_heads = ntok * w["H"]
+    step_flops = token_heads * sum(per_th.values())
+    stage_ms = time_stages(inp, w, args.steps)
+    print(f"[bench] stages (ms): {json.dumps({k: round(v, 4) for k, v in stage_ms.items()})}",
+          file=sys.stderr, flush=True)
+    dom = max(stage_ms, key=stage_ms.get)
+    dom_flops = token_heads * per_th[dom]
+    achieved = dom_flops / (stage_ms[dom] / 1e3)
+    result = {
+        "metric": "PKDA fwd+bwd tokens/s & %MFMA peak; decode state-update GB/s & %HBM peak",
+        "value": ntok / (ms / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload} chunked PKDA fwd+bwd",
+            "batch": w["B"], "seq_len": w["T"], "heads": w["H"], "head_dim": w["D"], "chunk": CHUNK,
+            "state": "fp32", "gate": "per-head log-decay", "varlen": w["varlen"],
+        },
+        "mfma_frac_step": step_flops / (ms / 1e3) / MFMA_BF16_PEAK,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dom,
+            "achieved": achieved / 1e12,
+            "peak": MFMA_BF16_PEAK / 1e12,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_BF16_PEAK,
+            "traffic": None,
+        },
+        "stage_ms": stage_ms,
+    }
+    if not args.no_decode:
+        del inp
+        torch.cuda.empty_cache()
+        result["decode"] = bench_decode(dev, args.decode_steps)
+        print(f"[bench] decode {result['decode']['kernel_us']:.1f} us/step", file=sys.stderr, flush=True)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(D=w["D"], H=w["H"], T=args.cpu_tokens)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -8,6 +8,7 @@ this package is the PyTorch-facing host side.  Nothing here falls back to the
 CPU: without a HIP device and the built library every operator raises.
 """
 
+from .chunk import chunk_pkda
 from .pkda import fused_recurrent_pkda, pkda_decode_step_
 
-__all__ = ["fused_recurrent_pkda", "pkda_decode_step_"]
+__all__ = ["chunk_pkda", "fused_recurrent_pkda", "pkda_decode_step_"]

@@ -18,6 +18,12 @@ PKDA_BF16 = 1
 GATE_LOG_HEAD = 0
 GATE_LOG_CHANNEL = 1
 GATE_RAW_CHANNEL = 2
+STAGE_FWD_INTRA = 1
+STAGE_FWD_STATE = 2
+STAGE_BWD_STATE = 1
+STAGE_BWD_DQKW = 2
+STAGE_BWD_WY = 4
+STAGE_BWD_INTRA = 8
 ABI_VERSION = 1
 
 
@@ -61,6 +67,7 @@ class PrecondArgs(ctypes.Structure):
         ("kw", c_void_p), ("a_chunk", c_void_p), ("num_chunks", c_int32),
         ("dkw", c_void_p), ("dk", c_void_p), ("dg_atk", c_void_p), ("dbeta_atk", c_void_p),
         ("dcenter_part", c_void_p), ("dcenter", c_void_p), ("dA0", c_void_p), ("dA_T", c_void_p),
+        ("table", c_void_p),
     ]
 
 
@@ -78,6 +85,7 @@ class ChunkFwdArgs(ctypes.Structure):
     _fields_ = _CHUNK_COMMON + [
         ("final_state", c_void_p), ("o", c_void_p),
         ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
+        ("stages", c_int32),
     ]
 
 
@@ -88,6 +96,7 @@ class ChunkBwdArgs(ctypes.Structure):
         ("du", c_void_p), ("dw", c_void_p), ("daqk", c_void_p), ("da", c_void_p),
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
+        ("stages", c_int32),
     ]
 
 

@@ -629,9 +629,10 @@ int set_smem(K kernel, int bytes) {
 }
 
 template <typename T, int D, int BV>
-int launch_bwd(const BwdParams& p, int num_chunks, hipStream_t s) {
+int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const int N = p.geom.num_seqs;
-  {
+  const bool all = stages == 0;
+  if (all || (stages & PKDA_STAGE_BWD_STATE)) {
     auto kern = chunk_state_bwd_kernel<T, D, BV>;
     const int bytes = StateBwdLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
@@ -639,27 +640,28 @@ int launch_bwd(const BwdParams& p, int num_chunks, hipStream_t s) {
     if (int st = launch_status("pkda_chunk_bwd(state)")) return st;
   }
   if (num_chunks == 0) return 0;
-  {
+  if (all || (stages & PKDA_STAGE_BWD_DQKW)) {
     auto kern = chunk_dqkw_kernel<T, D>;
     const int bytes = DqkwLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kWG), bytes, s, p);
     if (int st = launch_status("pkda_chunk_bwd(dqkw)")) return st;
   }
-  {
+  if (all || (stages & PKDA_STAGE_BWD_WY)) {
     auto kern = chunk_wy_bwd_kernel<T, D>;
     const int bytes = WyLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kWG), bytes, s, p);
     if (int st = launch_status("pkda_chunk_bwd(wy)")) return st;
   }
-  {
+  if (all || (stages & PKDA_STAGE_BWD_INTRA)) {
     auto kern = chunk_intra_bwd_kernel<T, D>;
     const int bytes = IntraBwdLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kWG), bytes, s, p);
-    return launch_status("pkda_chunk_bwd(intra)");
+    if (int st = launch_status("pkda_chunk_bwd(intra)")) return st;
   }
+  return 0;
 }
 
 }  // namespace
@@ -694,8 +696,10 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   p.kw_is_k = kw_is_k;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
+  const int st = a->stages;
+  PKDA_REQUIRE(st >= 0 && st <= 15, PKDA_EINVAL, "stages %d", st);
   if (a->dtype == PKDA_BF16) {
-    return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64>(p, nc, s) : launch_bwd<bf16_t, 64, 64>(p, nc, s);
+    return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64>(p, nc, st, s) : launch_bwd<bf16_t, 64, 64>(p, nc, st, s);
   }
-  return launch_bwd<float, 64, 64>(p, nc, s);
+  return launch_bwd<float, 64, 64>(p, nc, st, s);
 }

@@ -375,21 +375,23 @@ int set_smem(K kernel, int bytes) {
 }
 
 template <typename T, int D, int BV>
-int launch_fwd(const FwdParams& p, int num_chunks, hipStream_t s) {
-  {
+int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
+  const bool all = stages == 0;
+  if (all || (stages & PKDA_STAGE_FWD_INTRA)) {
     auto kern = chunk_intra_fwd_kernel<T, D>;
     const int bytes = IntraLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kWG), bytes, s, p);
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
   }
-  {
+  if (all || (stages & PKDA_STAGE_FWD_STATE)) {
     auto kern = chunk_state_fwd_kernel<T, D, BV>;
     const int bytes = StateLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     if (p.geom.num_seqs > 0) hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(kWG), bytes, s, p);
-    return launch_status("pkda_chunk_fwd(state)");
+    if (int st = launch_status("pkda_chunk_fwd(state)")) return st;
   }
+  return 0;
 }
 
 }  // namespace
@@ -432,8 +434,10 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   p.w = a->w; p.u = a->u; p.aqk = a->aqk; p.akk = a->akk; p.h = a->h;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
+  const int st = a->stages;
+  PKDA_REQUIRE(st >= 0 && st <= (PKDA_STAGE_FWD_INTRA | PKDA_STAGE_FWD_STATE), PKDA_EINVAL, "stages %d", st);
   if (a->dtype == PKDA_BF16) {
-    return a->head_dim == 128 ? launch_fwd<bf16_t, 128, 64>(p, nc, s) : launch_fwd<bf16_t, 64, 64>(p, nc, s);
+    return a->head_dim == 128 ? launch_fwd<bf16_t, 128, 64>(p, nc, st, s) : launch_fwd<bf16_t, 64, 64>(p, nc, st, s);
   }
-  return a->head_dim == 128 ? launch_fwd<float, 128, 32>(p, nc, s) : launch_fwd<float, 64, 64>(p, nc, s);
+  return a->head_dim == 128 ? launch_fwd<float, 128, 32>(p, nc, st, s) : launch_fwd<float, 64, 64>(p, nc, st, s);
 }

@@ -1,11 +1,82 @@
-"""Preconditioner scan host side (kernels pending in this build)."""
+"""Host side of the diagonal write-key preconditioner scans.
+
+The forward turns the raw key into the write key
+``kw = k * exp(-ln(x) r / (1 + |r|))``, ``r = log(A + eps) - center`` with
+``A_t = exp(g_atk_t) A_{t-1} + beta_atk_t k_t^2``
+(``delta_feedback_experiment/pkda.py:392-398``), checkpointing ``A`` at every
+chunk start; the backward is its reverse scan.  Both run in
+``libpkda_gfx950.so`` (``pkda_precond_fwd`` / ``pkda_precond_bwd``).
+"""
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 
-def precond_forward(*args, **kwargs):
-    raise NotImplementedError("the preconditioner scan is not built yet")
+import torch
+from torch import Tensor
+
+from . import _lib
+from .pkda import _dtype_code, _f32, _ptr, _stream
 
 
-def precond_backward(*args, **kwargs):
-    raise NotImplementedError("the preconditioner scan is not built yet")
+@dataclass
+class PrecondState:
+    kw: Tensor            # [N_tok, H, K], dtype of k
+    a_chunk: Tensor       # [num_chunks, H, K] FP32, A entering each chunk
+    final_A: Tensor       # [N, H, K] FP32
+    initial_A: Tensor | None
+
+
+def _flat2(t: Tensor, plan) -> Tensor:
+    return _f32(t).reshape(plan.num_tokens, plan.heads)
+
+
+def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
+                    initial_A_state: Tensor | None) -> PrecondState:
+    """Write keys for flat ``kf [N_tok, H, K]``; returns the scan's state."""
+    dev = kf.device
+    H, K, N = plan.heads, plan.head_dim, plan.num_seqs
+    ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
+    if cen.shape != (H,):
+        raise ValueError(f"log_atk_scale must be [{H}]")
+    a0 = _f32(initial_A_state)
+    if a0 is not None and tuple(a0.shape) != (N, H, K):
+        raise ValueError(f"initial_A_state must be {(N, H, K)}")
+    kw = torch.empty_like(kf)
+    a_chunk = torch.empty(plan.num_chunks, H, K, device=dev, dtype=torch.float32)
+    final_A = torch.empty(N, H, K, device=dev, dtype=torch.float32)
+    args = _lib.PrecondArgs(
+        dtype=_dtype_code(kf), num_seqs=N, seqlen=plan.seqlen, heads=H, head_dim=K,
+        cu_seqlens=_ptr(plan.cu_seqlens), k=_ptr(kf), g_atk=_ptr(ga), beta_atk=_ptr(ba), center=_ptr(cen),
+        squash_x=float(x), squash_eps=float(eps), initial_A_state=_ptr(a0), final_A_state=_ptr(final_A),
+        kw=_ptr(kw), a_chunk=_ptr(a_chunk), num_chunks=plan.num_chunks, table=_ptr(plan.table),
+    )
+    _lib.call("pkda_precond_fwd", args, _stream(dev))
+    return PrecondState(kw, a_chunk, final_A, a0)
+
+
+def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
+                     state: PrecondState, dkw: Tensor, dk: Tensor, dA_T: Tensor | None, want_dA0: bool):
+    """Reverse scan: adds the preconditioner's terms into ``dk`` (FP32, in
+    place) and returns ``(dg_atk [N_tok,H], dbeta_atk [N_tok,H], dcenter [H],
+    dA0 [N,H,K] or None)``, all FP32."""
+    dev = kf.device
+    H, K, N = plan.heads, plan.head_dim, plan.num_seqs
+    ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dg_atk = torch.empty(plan.num_tokens, H, **f32)
+    dbeta_atk = torch.empty(plan.num_tokens, H, **f32)
+    dcenter_part = torch.empty(max(N, 1), H, **f32)
+    dcenter = torch.empty(H, **f32)
+    dA0 = torch.empty(N, H, K, **f32) if want_dA0 else None
+    dAT = None if dA_T is None else _f32(dA_T)
+    args = _lib.PrecondArgs(
+        dtype=_dtype_code(kf), num_seqs=N, seqlen=plan.seqlen, heads=H, head_dim=K,
+        cu_seqlens=_ptr(plan.cu_seqlens), k=_ptr(kf), g_atk=_ptr(ga), beta_atk=_ptr(ba), center=_ptr(cen),
+        squash_x=float(x), squash_eps=float(eps), a_chunk=_ptr(state.a_chunk), num_chunks=plan.num_chunks,
+        dkw=_ptr(dkw), dk=_ptr(dk), dg_atk=_ptr(dg_atk), dbeta_atk=_ptr(dbeta_atk),
+        dcenter_part=_ptr(dcenter_part), dcenter=_ptr(dcenter), dA0=_ptr(dA0), dA_T=_ptr(dAT),
+        table=_ptr(plan.table),
+    )
+    _lib.call("pkda_precond_bwd", args, _stream(dev))
+    return dg_atk, dbeta_atk, dcenter, dA0

@@ -190,9 +190,13 @@ int pkda_gate_bwd(const pkda_gate_args* args, void* stream);
  *   forward:  kw [N_tok,H,K] (dtype), A at every chunk start a_chunk
  *             [num_chunks, H, K] FP32 (backward checkpoint), final A.
  *   backward: dkw (FP32 [N_tok,H,K]) -> dk (FP32, accumulated: dk += ...),
- *             dg_atk, dbeta_atk [N_tok,H] FP32, dcenter [H] (per-chunk
- *             partials dcenter_part [num_chunks, H]), dA0 [N,H,K] when
- *             dA0 != NULL; dA_T optional gradient of the final A.
+ *             dg_atk, dbeta_atk [N_tok,H] FP32, dcenter [H] (through
+ *             per-document partials dcenter_part [num_seqs, H], summed in a
+ *             fixed order), dA0 [N,H,K] when dA0 != NULL; dA_T optional
+ *             gradient of the final A.
+ * One workgroup per (document, head) scans its key channels in parallel; the
+ * backward recomputes A inside each chunk from a_chunk.  Packed documents
+ * take the pkda_chunk_table `table` (NULL for equal rows).
  * ------------------------------------------------------------------------- */
 typedef struct pkda_precond_args {
   int32_t struct_size;
@@ -213,14 +217,31 @@ typedef struct pkda_precond_args {
   float* dk;                     /* backward: accumulated into */
   float* dg_atk;
   float* dbeta_atk;
-  float* dcenter_part;           /* [num_chunks, H] workspace */
+  float* dcenter_part;           /* [num_seqs, H] workspace */
   float* dcenter;                /* [H] */
   float* dA0;                    /* [N,H,K] or NULL */
   const float* dA_T;             /* [N,H,K] or NULL */
+  const int32_t* table;          /* pkda_chunk_table output or NULL */
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
 int pkda_precond_bwd(const pkda_precond_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Kernel stages of the chunked entry points.  `stages` selects which of an
+ * entry point's kernels one call enqueues (0 = all, in order).  A caller that
+ * splits a call into stages must issue them in the listed order on one stream;
+ * the split exists so that each kernel can be timed or placed on its own.
+ * ------------------------------------------------------------------------- */
+enum pkda_chunk_stage {
+  PKDA_STAGE_ALL = 0,
+  PKDA_STAGE_FWD_INTRA = 1, /* per chunk: Akk, T = (I + Akk)^-1, w, u, Aqk     */
+  PKDA_STAGE_FWD_STATE = 2, /* per document: U, o, the chunk states h, S_T     */
+  PKDA_STAGE_BWD_STATE = 1, /* per document, reverse: dh, dU, dS0            */
+  PKDA_STAGE_BWD_DQKW = 2,  /* per chunk: state-path terms of dq, dk, dkw, dw */
+  PKDA_STAGE_BWD_WY = 4,    /* per chunk: WY / triangular-solve backward      */
+  PKDA_STAGE_BWD_INTRA = 8  /* per chunk: pairwise terms; final dq, dk, dv... */
+};
 
 /* ---------------------------------------------------------------------------
  * Chunked forward (training / prefill).
@@ -253,6 +274,7 @@ typedef struct pkda_chunk_fwd_args {
   float* final_state;          /* [N,H,K,V] or NULL */
   void* o;
   void *w, *u, *aqk, *akk, *h;
+  int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
 } pkda_chunk_fwd_args;
 
 int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
@@ -288,6 +310,7 @@ typedef struct pkda_chunk_bwd_args {
   void* dh;
   float *du, *dw, *daqk, *da;
   float *dq, *dk, *dkw, *dv, *dbeta, *dgcum, *dh0;
+  int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);

@@ -150,3 +150,63 @@ def test_chunk_gradients_varlen(dev):
     res = _grad_case(dev, 1, 301, 2, 64, torch.bfloat16, seed=3, cu=cu)
     for name, val in res.items():
         assert val < BF16_TOL, (name, val)
+
+
+def _precond_inputs(B, T, H, gen):
+    """Preconditioner controls drawn as the reference's bench draws them
+    (scripts/pkda_bench.py:162-187): g_atk = -A softplus(0.2 n + bias)."""
+    pA = torch.empty(H).uniform_(1, 16, generator=gen)
+    pdt = torch.empty(H).uniform_(-6.9, -2.3, generator=gen).exp()
+    pbias = pdt + torch.log(-torch.expm1(-pdt))
+    g_atk = -pA * F.softplus(0.2 * torch.randn(B, T, H, generator=gen) + pbias)
+    beta_atk = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    center = -0.2 + 0.1 * torch.randn(H, generator=gen)
+    return g_atk, beta_atk, center
+
+
+@pytest.mark.parametrize("D,dtype,cu", [(64, torch.float32, None), (128, torch.bfloat16, None),
+                                         (64, torch.bfloat16, "varlen")])
+def test_chunk_preconditioned_matches_oracle(dev, D, dtype, cu):
+    """Production write-key preconditioner (x = 1.5) through the chunked path:
+    outputs, final S and A, and every gradient including the preconditioner's
+    controls, the initial states and the log-space center."""
+    from delta_feedback_experiment_amd.chunk import chunk_pkda
+
+    print(f"[gpu] chunk precond D={D} {dtype} {cu}", flush=True)
+    B, T, H = (2, 150, 2) if cu is None else (1, 301, 2)
+    cu_t = None if cu is None else torch.tensor([0, 17, 17, 100, 164, 300, 301], dtype=torch.int32)
+    N = B if cu_t is None else cu_t.numel() - 1
+    q, k, v, g, beta = make_inputs(B, T, H, D, dtype, seed=11 + D, strong=True)
+    gen = torch.Generator().manual_seed(99)
+    g_atk, beta_atk, center = _precond_inputs(B, T, H, gen)
+    S0 = 0.02 * torch.randn(N, H, D, D, generator=gen)
+    A0 = 0.1 * torch.randn(N, H, D, generator=gen).abs()
+    do = torch.randn(B, T, H, D, generator=gen).to(dtype)
+    dS = torch.randn(N, H, D, D, generator=gen)
+    dA = torch.randn(N, H, D, generator=gen)
+    names = ("q", "k", "v", "g", "beta", "g_atk", "beta_atk", "center", "S0", "A0")
+    base = (q, k, v, g, beta, g_atk, beta_atk, center, S0, A0)
+
+    def run(t, device):
+        o, S, A = (oracle.pkda_reference if device is None else chunk_pkda)(
+            t[0], t[1], t[2], t[3], t[4], g_atk=t[5], beta_atk=t[6], log_atk_scale=t[7],
+            initial_state=t[8], initial_A_state=t[9], output_final_state=True, x=1.5, eps=1e-6,
+            cu_seqlens=None if cu_t is None else (cu_t if device is None else cu_t.to(device)),
+            **({"out_dtype": torch.float32} if device is None else {}),
+        )
+        dev_ = o.device
+        loss = (o.float() * do.to(dev_).float()).sum() + (S * dS.to(dev_)).sum() + (A * dA.to(dev_)).sum()
+        return o, S, A, torch.autograd.grad(loss, t)
+
+    ref_leaves = [x.float().clone().requires_grad_() for x in base]
+    o_r, S_r, A_r, g_r = run(ref_leaves, None)
+    leaves = [x.to(dev).clone().requires_grad_() for x in base]
+    o, S, A, g_d = run(leaves, dev)
+    torch.cuda.synchronize()
+    res = {"o": rel_l2(o.float(), o_r), "S": rel_l2(S, S_r), "A": rel_l2(A, A_r)}
+    for n, a, b in zip(names, g_d, g_r):
+        res["d" + n] = rel_l2(a.float(), b)
+    print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    for n, val in res.items():
+        assert val < tol, (n, val)
