@@ -266,33 +266,58 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
     }
 
 
-def cpu_baseline(D: int = 128, H: int = 16, T: int = 192, seed: int = 3) -> dict:
-    """The CPU oracle's fwd+bwd on a B=1 slice of the workload (FP32, all host cores)."""
+def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
+    """A plain device copy of ``nbytes`` (read + write), the practical HBM
+    ceiling beside the kernels' rates and the scale for the byte counters."""
+    src = torch.empty(nbytes // 4, device=dev, dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": ms * 1e3,
+            "GBps": 2 * nbytes / (ms / 1e3) / 1e9}
+
+
+def cpu_baseline(D: int = 128, H: int = 16, T: int = 512, seed: int = 3, budget_s: float = 12.0,
+                 max_rows: int = 8) -> dict:
+    """The CPU oracle's fwd+bwd over B=1 row slices of the workload (FP32, all
+    host cores): rows of T tokens are run one after another until ``budget_s``
+    seconds or ``max_rows`` rows, and the token rate is over all of them."""
     from oracle import pkda_oracle as oracle
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(seed)
-    q = l2norm(torch.randn(1, T, H, D, generator=gen)).to(torch.bfloat16).float()
-    k = l2norm(torch.randn(1, T, H, D, generator=gen)).to(torch.bfloat16).float()
-    v = torch.randn(1, T, H, D, generator=gen).to(torch.bfloat16).float()
-    beta = torch.sigmoid(torch.randn(1, T, H, generator=gen))
-    g = -F.softplus(torch.randn(1, T, H, generator=gen))
-    do = torch.randn(1, T, H, D, generator=gen)
-    leaves = [t.clone().requires_grad_() for t in (q, k, v, g, beta)]
-    t0 = time.perf_counter()
-    o, _, _ = oracle.pkda_reference(*leaves)
-    torch.autograd.grad(o, leaves, do)
-    dt = time.perf_counter() - t0
+    total = 0.0
+    rows = 0
+    while rows < max_rows and total < budget_s:
+        q = l2norm(torch.randn(1, T, H, D, generator=gen)).to(torch.bfloat16).float()
+        k = l2norm(torch.randn(1, T, H, D, generator=gen)).to(torch.bfloat16).float()
+        v = torch.randn(1, T, H, D, generator=gen).to(torch.bfloat16).float()
+        beta = torch.sigmoid(torch.randn(1, T, H, generator=gen))
+        g = -F.softplus(torch.randn(1, T, H, generator=gen))
+        do = torch.randn(1, T, H, D, generator=gen)
+        leaves = [t.clone().requires_grad_() for t in (q, k, v, g, beta)]
+        t0 = time.perf_counter()
+        o, _, _ = oracle.pkda_reference(*leaves)
+        torch.autograd.grad(o, leaves, do)
+        total += time.perf_counter() - t0
+        rows += 1
     return {
-        "value": T / dt,
+        "value": rows * T / total,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle fwd+bwd (token-recurrent FP32 torch CPU), B=1 T={T} H={H} d={D}, "
-                  f"{dt:.1f} s; same per-token work as one row of the GPU workload",
-        "seconds": dt,
-        "token_heads_per_s": T * H / dt,
+        "sample": f"oracle fwd+bwd (token-recurrent FP32 torch CPU) over {rows} row(s) of B=1 T={T} H={H} "
+                  f"d={D} ({total:.1f} s); same per-token work as one row of the GPU workload",
+        "seconds": total,
+        "token_heads_per_s": rows * T * H / total,
     }
 
 
@@ -306,6 +331,7 @@ def main() -> None:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=512)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -365,13 +391,15 @@ def main() -> None:
         },
         "stage_ms": stage_ms,
     }
+    result["copy"] = copy_bandwidth(dev)
+    print(f"[bench] copy {result['copy']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
     if not args.no_decode:
         del inp
         torch.cuda.empty_cache()
         result["decode"] = bench_decode(dev, args.decode_steps)
         print(f"[bench] decode {result['decode']['kernel_us']:.1f} us/step", file=sys.stderr, flush=True)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(D=w["D"], H=w["H"], T=args.cpu_tokens)
+        result["cpu_baseline"] = cpu_baseline(D=w["D"], H=w["H"], T=args.cpu_tokens, budget_s=args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

@@ -9,6 +9,7 @@ CPU: without a HIP device and the built library every operator raises.
 """
 
 from .chunk import chunk_pkda
+from .ops import pkda_recurrence
 from .pkda import fused_recurrent_pkda, pkda_decode_step_
 
-__all__ = ["chunk_pkda", "fused_recurrent_pkda", "pkda_decode_step_"]
+__all__ = ["chunk_pkda", "fused_recurrent_pkda", "pkda_decode_step_", "pkda_recurrence"]

@@ -79,13 +79,34 @@ __device__ __forceinline__ void doc_chunks(const ChunkGeom& g, int n, int& first
 // Operand views in LDS:
 //   A (M x K): ROW -> A[m*lda + k];  COL -> A[k*lda + m]
 //   B (K x N): ROW -> B[k*ldb + n];  COL -> B[n*ldb + k]
-// bf16 tiles are fastest as A=ROW, B=COL (8 contiguous k per lane, one
-// 16-byte LDS read); the other views gather 8 scalars.  FP32 tiles read one
-// element per lane and are cheap in every view.
+// bf16 tiles read as A=ROW, B=COL take one 16-byte LDS read per lane; the
+// k-major views (A=COL, B=ROW) take two transposing 8-byte reads, so every
+// tile can stay in its natural row-major layout.  FP32 tiles read one element
+// per lane and are cheap in every view.  k-major bf16 tiles need ld % 4 == 0
+// and 8-byte aligned tile origins.
 // ----------------------------------------------------------------------------
 enum { ROW = 0, COL = 1 };
 
 template <typename E> struct Mma;
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+// Eight k-consecutive bf16 of one column of a k-major LDS tile (element
+// (k, n) at p[k * ld + n], p already offset to the tile's column 0), as the
+// MFMA 16x16x32 operand of this lane: lane 16q + i receives column i, rows
+// k0 + 8q .. k0 + 8q + 7.  Two ds_read_b64_tr_b16: inside each 16-lane group
+// lane 4r + c addresses row r, columns 4c .. 4c + 3 of a 4 x 16 block and
+// lane i receives column i of the four rows.
+__device__ __forceinline__ s16x8_t lds_read_kmajor(const bf16_t* p, int ld, int k0, int lane) {
+  const int i = lane & 15, q = lane >> 4;
+  const bf16_t* src = p + (k0 + 8 * q + (i >> 2)) * ld + 4 * (i & 3);
+  const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(src));
+  const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(src + 4 * ld));
+  const s16x4_t l = __builtin_bit_cast(s16x4_t, lo), h = __builtin_bit_cast(s16x4_t, hi);
+  return s16x8_t{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
+}
 
 template <> struct Mma<bf16_t> {
   static constexpr int KS = 32;
@@ -98,14 +119,12 @@ template <> struct Mma<bf16_t> {
     if constexpr (LA == ROW) {
       a = *reinterpret_cast<const s16x8_t*>(A + r * lda + k0 + kq);
     } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a[j] = static_cast<short>(A[(k0 + kq + j) * lda + r]);
+      a = lds_read_kmajor(A, lda, k0, lane);
     }
     if constexpr (LB == COL) {
       b = *reinterpret_cast<const s16x8_t*>(B + r * ldb + k0 + kq);
     } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) b[j] = static_cast<short>(B[(k0 + kq + j) * ldb + r]);
+      b = lds_read_kmajor(B, ldb, k0, lane);
     }
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                   acc, 0, 0, 0);

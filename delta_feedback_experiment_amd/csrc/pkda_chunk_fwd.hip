@@ -217,19 +217,19 @@ __global__ __launch_bounds__(kWG) void chunk_intra_fwd_kernel(FwdParams p) {
     if (r < ci.len) io<T>::store(akk_out + (int64_t)r * H * C + c, x);
   }
   // ---- W = T diag(beta e^G) K,  Uu = T diag(beta) V ---------------------------
-  E* sBwT = reinterpret_cast<E*>(smem);
-  E* sBvT = sBwT + D * L::LDC;
-  load_rows_t<T, E, D>(sBwT, L::LDC, k, gs, C, ci.len,
-                       [&](int r, int, float x) { return sBeta[r] * expf(sGam[r]) * x; });
-  load_rows_t<T, E, D>(sBvT, L::LDC, v, gs, C, ci.len, [&](int r, int, float x) { return sBeta[r] * x; });
+  E* sBw = reinterpret_cast<E*>(smem);
+  E* sBv = sBw + C * L::LD;
+  load_rows<T, E, D>(sBw, L::LD, k, gs, C, ci.len,
+                     [&](int r, int, float x) { return sBeta[r] * expf(sGam[r]) * x; });
+  load_rows<T, E, D>(sBv, L::LD, v, gs, C, ci.len, [&](int r, int, float x) { return sBeta[r] * x; });
   __syncthreads();
   const int kdim = ((16 * (wave + 1) + Mma<E>::KS - 1) / Mma<E>::KS) * Mma<E>::KS;  // T is lower triangular
   T* w_out = static_cast<T*>(p.w) + row0 * D;
   T* u_out = static_cast<T*>(p.u) + row0 * D;
   for (int ct = 0; ct < D / 16; ++ct) {
     f32x4 aw = zero4(), au = zero4();
-    mma_tile<E, ROW, COL>(aw, sTe, L::LDC, 16 * wave, sBwT, L::LDC, 16 * ct, kdim, lane);
-    mma_tile<E, ROW, COL>(au, sTe, L::LDC, 16 * wave, sBvT, L::LDC, 16 * ct, kdim, lane);
+    mma_tile<E, ROW, ROW>(aw, sTe, L::LDC, 16 * wave, sBw, L::LD, 16 * ct, kdim, lane);
+    mma_tile<E, ROW, ROW>(au, sTe, L::LDC, 16 * wave, sBv, L::LD, 16 * ct, kdim, lane);
     store_acc_global<T>(w_out, gs, aw, 16 * wave, 16 * ct, ci.len, lane);
     store_acc_global<T>(u_out, gs, au, 16 * wave, 16 * ct, ci.len, lane);
   }

@@ -1,0 +1,197 @@
+"""The stateless training/prefill PKDA operator, as a graph-friendly custom op.
+
+Mirrors ``delta_feedback::pkda_recurrence`` and its backward op
+(``delta_feedback_experiment/fla_ops.py:252-569``): same argument list and
+meaning, the gate computed inside from the raw decay projection, the
+preconditioner always applied, no cache state, no final state, no packing.
+``PreconditionedKDA._cuda_recurrence`` calls it for dense training and prefill
+(``delta_feedback_experiment/pkda.py:429-449``).
+
+The saved list is this library's own (the caller treats it as opaque,
+``pkda.py:433``): the write keys and the preconditioner's chunk checkpoints
+always; the WY factors, corrected values, intra-chunk products and chunk
+states as well unless ``lean``, in which case the backward rebuilds them with
+the same kernels the forward ran.  The gate cumsum is relaunched in the
+backward either way, as the reference does.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .chunk import CHUNK_SIZE, ChunkPlan, chunk_backward, chunk_forward, gate_backward, gate_forward
+from .pkda import _f32
+from . import precond as pre
+
+SAVED_ALWAYS = ("k_write", "a_chunk")
+"""Saved by every forward: the preconditioned write keys and the
+preconditioner state entering each chunk."""
+
+SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h")
+"""Saved as well unless ``lean``: W, the corrected values U, the intra-chunk
+query-key products, the inverted WY matrix and the chunk-entry states."""
+
+
+def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int, ...], torch.dtype], ...]:
+    """Shape and dtype of every saved intermediate, from the input geometry."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    chunks = -(-T // CHUNK_SIZE)
+    act = q.dtype
+    ntok = B * T
+    meta = [
+        ((ntok, H, K), act),                      # k_write
+        ((B * chunks, H, K), torch.float32),      # a_chunk
+    ]
+    if not lean:
+        meta += [
+            ((ntok, H, K), act),                  # w
+            ((ntok, H, V), act),                  # v_new
+            ((ntok, H, CHUNK_SIZE), act),         # Aqk
+            ((ntok, H, CHUNK_SIZE), act),         # T
+            ((B * chunks, H, K, V), act),         # h
+        ]
+    return tuple(meta)
+
+
+def _check_saved(saved: list[Tensor], q: Tensor, v: Tensor, lean: bool) -> None:
+    expected = intermediate_meta(q, v, lean)
+    names = SAVED_ALWAYS + (() if lean else SAVED_RETAINED)
+    if len(saved) != len(expected):
+        raise RuntimeError(f"pkda_recurrence saved {len(saved)} tensors, not {len(expected)}")
+    for name, t, (shape, dtype) in zip(names, saved, expected):
+        if tuple(t.shape) != shape or t.dtype != dtype or t.device != q.device or not t.is_contiguous():
+            raise RuntimeError(
+                f"pkda_recurrence intermediate {name} is {(tuple(t.shape), t.dtype, t.device)}, "
+                f"not {(shape, dtype, q.device)}; the fake implementation is stale"
+            )
+
+
+def _check_inputs(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale) -> None:
+    B, T, H, K = q.shape
+    if k.shape != q.shape or v.shape[:3] != q.shape[:3] or v.shape[-1] != K:
+        raise ValueError("pkda_recurrence needs q, k, v [B, T, H, D] with one D")
+    if g.shape != q.shape:
+        raise ValueError(f"g (raw decay) must be {tuple(q.shape)}, got {tuple(g.shape)}")
+    for name, t in (("g_atk", g_atk), ("beta_atk", beta_atk), ("beta", beta)):
+        if tuple(t.shape) != (B, T, H):
+            raise ValueError(f"{name} must be {(B, T, H)}, got {tuple(t.shape)}")
+    if A_log.numel() != H or dt_bias.numel() != H * K or log_atk_scale.numel() != H:
+        raise ValueError("A_log [H], dt_bias [H*D] and log_atk_scale [H] expected")
+    if not q.is_cuda:
+        raise RuntimeError("pkda_recurrence needs tensors on a HIP device; there is no CPU fallback")
+
+
+def _forward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, scale, squash_x, squash_eps,
+             save_all: bool):
+    plan = ChunkPlan.make(q, None)
+    flat = lambda t: t.contiguous().reshape(plan.num_tokens, plan.heads, *t.shape[3:])  # noqa: E731
+    qf, kf, vf, gf = flat(q), flat(k), flat(v), flat(g)
+    if gf.dtype not in (torch.float32, torch.bfloat16):
+        gf = gf.float()
+    A32, dt32 = _f32(A_log), _f32(dt_bias)
+    gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)
+    pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, None)
+    beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
+    o, _, fs = chunk_forward(plan, qf, kf, pstate.kw, vf, gcum, beta32, scale, None, False, save_states=save_all)
+    return plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs
+
+
+@torch.library.custom_op("pkda_mi355x::pkda_recurrence", mutates_args=(), device_types="cuda")
+def pkda_recurrence(
+    q: Tensor, k: Tensor, v: Tensor, g: Tensor, g_atk: Tensor, beta_atk: Tensor, beta: Tensor,
+    A_log: Tensor, dt_bias: Tensor, log_atk_scale: Tensor,
+    scale: float, squash_x: float, squash_eps: float, lean: bool,
+) -> tuple[Tensor, list[Tensor]]:
+    """Chunked PKDA forward over the gfx950 kernels: ``(o, saved)``.
+
+    ``g`` is the raw decay projection ``[B,T,H,D]``; the log gate
+    ``-exp(A_log) softplus(g + dt_bias)`` and its chunk-local cumsum are
+    computed on the device.  ``o`` is in ``q.dtype``.
+    """
+    _check_inputs(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale)
+    with torch.cuda.device(q.device):
+        (plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs) = _forward(
+            q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, scale, squash_x, squash_eps,
+            save_all=not lean)
+    saved = [pstate.kw, pstate.a_chunk]
+    if not lean:
+        saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h]
+    _check_saved(saved, q, v, lean)
+    return o.reshape(*q.shape[:3], v.shape[-1]).to(q.dtype), saved
+
+
+@pkda_recurrence.register_fake
+def _pkda_recurrence_fake(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale,
+                          scale, squash_x, squash_eps, lean):
+    out = torch.empty((*q.shape[:3], v.shape[-1]), device=q.device, dtype=q.dtype)
+    saved = [torch.empty(shape, device=q.device, dtype=dtype) for shape, dtype in intermediate_meta(q, v, lean)]
+    return out, saved
+
+
+@torch.library.custom_op("pkda_mi355x::pkda_recurrence_backward", mutates_args=(), device_types="cuda")
+def pkda_recurrence_backward(
+    q: Tensor, k: Tensor, v: Tensor, g: Tensor, g_atk: Tensor, beta_atk: Tensor, beta: Tensor,
+    A_log: Tensor, dt_bias: Tensor, log_atk_scale: Tensor, saved: list[Tensor], do: Tensor,
+    scale: float, squash_x: float, squash_eps: float, lean: bool,
+) -> list[Tensor]:
+    """Gradients of :func:`pkda_recurrence` for its ten tensor inputs, each in
+    that input's dtype (``delta_feedback_experiment/fla_ops.py:488-499``)."""
+    from .chunk import FwdSaved
+
+    with torch.cuda.device(q.device):
+        plan = ChunkPlan.make(q, None)
+        flat = lambda t: t.contiguous().reshape(plan.num_tokens, plan.heads, *t.shape[3:])  # noqa: E731
+        qf, kf, vf, gf = flat(q), flat(k), flat(v), flat(g)
+        if gf.dtype not in (torch.float32, torch.bfloat16):
+            gf = gf.float()
+        A32, dt32 = _f32(A_log), _f32(dt_bias)
+        beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
+        gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)  # relaunched, as the forward ran it
+        kw, a_chunk = saved[0], saved[1]
+        if lean:
+            _, _, fs = chunk_forward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, False, save_states=True)
+        else:
+            fs = FwdSaved(*saved[2:7])
+        dof = flat(do.to(q.dtype))
+        gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False)
+        pstate = pre.PrecondState(kw, a_chunk, None, None)
+        dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(
+            plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, pstate, gr.dkw, gr.dk, None, False)
+        dg, dA_log, ddt_bias = gate_backward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gr.dgcum)
+    shape = tuple(q.shape)
+    lead = shape[:3]
+    return [
+        gr.dq.reshape(shape).to(q.dtype), gr.dk.reshape(shape).to(k.dtype), gr.dv.reshape(v.shape).to(v.dtype),
+        dg.reshape(g.shape).to(g.dtype), dg_atk.reshape(lead).to(g_atk.dtype),
+        dbeta_atk.reshape(lead).to(beta_atk.dtype), gr.dbeta.reshape(lead).to(beta.dtype),
+        dA_log.reshape(A_log.shape).to(A_log.dtype), ddt_bias.reshape(dt_bias.shape).to(dt_bias.dtype),
+        dcenter.reshape(log_atk_scale.shape).to(log_atk_scale.dtype),
+    ]
+
+
+@pkda_recurrence_backward.register_fake
+def _pkda_recurrence_backward_fake(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, saved, do,
+                                   scale, squash_x, squash_eps, lean):
+    return [torch.empty_like(t) for t in (q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale)]
+
+
+def _setup_context(ctx, inputs, output) -> None:
+    q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, *scalars = inputs
+    _o, saved = output
+    ctx.save_for_backward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, *saved)
+    ctx.scalars = tuple(scalars)
+    ctx.mark_non_differentiable(*saved)
+
+
+def _backward(ctx, do, _dsaved):
+    tensors = ctx.saved_tensors
+    inputs, saved = tensors[:10], list(tensors[10:])
+    scale, squash_x, squash_eps, lean = ctx.scalars
+    grads = pkda_recurrence_backward(*inputs, saved, do, scale, squash_x, squash_eps, lean)
+    return (*grads, None, None, None, None)
+
+
+pkda_recurrence.register_autograd(_backward, setup_context=_setup_context)
