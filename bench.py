@@ -27,9 +27,8 @@ gate scans and elementwise work are not counted):
   fwd intra   8Cd           (Akk, Aqk, W, Uu)
   fwd state   6d^2 + 2Cd    (W S, Q S, Kg^T U; Aqk U)
   bwd state   6d^2 + 2Cd    (Kg dS, Qg^T dO, W^T dU; Aqk^T dO)
-  bwd dqkw    6d^2 + 2Cd    (dO S^T, dU S^T, U dS^T; dO U^T)
-  bwd wy      8Cd           (T^T dW, T^T dU, dW Bw^T, dU Bv^T)
-  bwd intra   8Cd           (pairwise dq, dk, dkw products)
+  bwd chunk   6d^2 + 18Cd   (dO S^T, dU S^T, U dS^T; dO U^T; T^T dW, T^T dU,
+                             dW Bw^T, dU Bv^T; pairwise dq, dk, dkw products)
   total       18d^2 + 30Cd = 540,672 flop at d = 128
 """
 
@@ -67,9 +66,7 @@ def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
         "fwd_intra": 8 * C * D,
         "fwd_state": 6 * D * D + 2 * C * D,
         "bwd_state": 6 * D * D + 2 * C * D,
-        "bwd_dqkw": 6 * D * D + 2 * C * D,
-        "bwd_wy": 8 * C * D,
-        "bwd_intra": 8 * C * D,
+        "bwd_chunk": 6 * D * D + 2 * C * D + 8 * C * D + 8 * C * D,
     }
 
 
@@ -167,8 +164,7 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
     aqk, akk = torch.empty(ntok, H, CHUNK, **bf), torch.empty(ntok, H, CHUNK, **bf)
     h = torch.empty(plan.num_chunks, H, D, D, **bf)
     dh = torch.empty(plan.num_chunks, H, D, D, **bf)
-    du, dw = torch.empty(ntok, H, D, **f32), torch.empty(ntok, H, D, **f32)
-    daqk, da = torch.empty(ntok, H, CHUNK, **f32), torch.empty(ntok, H, CHUNK, **f32)
+    du = torch.empty(ntok, H, D, **bf)
     dq, dk, dv = (torch.empty(ntok, H, D, **f32) for _ in range(3))
     dbeta, dgcum = torch.empty(ntok, H, **f32), torch.empty(ntok, H, **f32)
     s0 = inp["s0"]
@@ -182,16 +178,14 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
         dtype=_lib.PKDA_BF16, **plan.common(), q=_ptr(q), k=_ptr(k), kw=_ptr(k), v=_ptr(v), gcum=_ptr(gcum),
         gate_per_channel=0, beta=_ptr(beta), scale=scale, initial_state=_ptr(s0),
         w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), do=_ptr(do), dht=None, dh=_ptr(dh),
-        du=_ptr(du), dw=_ptr(dw), daqk=_ptr(daqk), da=_ptr(da), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
+        du=_ptr(du), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
         dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None,
     )
     stages = [
         ("fwd_intra", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_INTRA),
         ("fwd_state", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_STATE),
         ("bwd_state", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_STATE),
-        ("bwd_dqkw", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_DQKW),
-        ("bwd_wy", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_WY),
-        ("bwd_intra", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_INTRA),
+        ("bwd_chunk", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_CHUNK),
     ]
     stream = _stream(dev)
     events = {name: [] for name, *_ in stages}

@@ -21,9 +21,7 @@ GATE_RAW_CHANNEL = 2
 STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
-STAGE_BWD_DQKW = 2
-STAGE_BWD_WY = 4
-STAGE_BWD_INTRA = 8
+STAGE_BWD_CHUNK = 2
 ABI_VERSION = 1
 
 
@@ -92,8 +90,7 @@ class ChunkFwdArgs(ctypes.Structure):
 class ChunkBwdArgs(ctypes.Structure):
     _fields_ = _CHUNK_COMMON + [
         ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
-        ("do", c_void_p), ("dht", c_void_p), ("dh", c_void_p),
-        ("du", c_void_p), ("dw", c_void_p), ("daqk", c_void_p), ("da", c_void_p),
+        ("do", c_void_p), ("dht", c_void_p), ("dh", c_void_p), ("du", c_void_p),
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
         ("stages", c_int32),

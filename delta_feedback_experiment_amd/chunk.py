@@ -143,17 +143,14 @@ def chunk_backward(
     dgcum = torch.empty_like(gcum)
     dh0 = torch.empty(N, H, D, D, **f32) if want_dh0 else None
     dh = torch.empty(plan.num_chunks, H, D, D, device=dev, dtype=q.dtype)
-    du = torch.empty(ntok, H, D, **f32)
-    dw = torch.empty(ntok, H, D, **f32)
-    daqk = torch.empty(ntok, H, CHUNK_SIZE, **f32)
-    da = torch.empty(ntok, H, CHUNK_SIZE, **f32)
+    du = torch.empty(ntok, H, D, device=dev, dtype=q.dtype)
     args = _lib.ChunkBwdArgs(
         dtype=_dtype_code(q), **plan.common(),
         q=_ptr(q), k=_ptr(k), kw=_ptr(kw), v=_ptr(v), gcum=_ptr(gcum),
         gate_per_channel=int(gcum.dim() == 3), beta=_ptr(beta32), scale=float(scale),
         initial_state=_ptr(initial_state),
         w=_ptr(saved.w), u=_ptr(saved.u), aqk=_ptr(saved.aqk), akk=_ptr(saved.akk), h=_ptr(saved.h),
-        do=_ptr(do), dht=_ptr(dht), dh=_ptr(dh), du=_ptr(du), dw=_ptr(dw), daqk=_ptr(daqk), da=_ptr(da),
+        do=_ptr(do), dht=_ptr(dht), dh=_ptr(dh), du=_ptr(du),
         dq=_ptr(dq), dk=_ptr(dk), dkw=_ptr(dkw), dv=_ptr(dv), dbeta=_ptr(dbeta), dgcum=_ptr(dgcum),
         dh0=_ptr(dh0),
     )

@@ -153,6 +153,21 @@ __device__ __forceinline__ void mma_tile(f32x4& acc, const E* A, int lda, int m0
   for (int k0 = 0; k0 < K; k0 += Mma<E>::KS) Mma<E>::template step<LA, LB>(acc, a, lda, b, ldb, k0, lane);
 }
 
+// acc += A[m0:m0+16, kb:ke] * B[kb:ke, n0:n0+16]; kb, ke multiples of Mma<E>::KS.
+template <typename E, int LA, int LB>
+__device__ __forceinline__ void mma_tile_range(f32x4& acc, const E* A, int lda, int m0, const E* B, int ldb, int n0,
+                                               int kb, int ke, int lane) {
+  const E* a = (LA == ROW) ? A + m0 * lda : A + m0;
+  const E* b = (LB == COL) ? B + n0 * ldb : B + n0;
+  for (int k0 = kb; k0 < ke; k0 += Mma<E>::KS) Mma<E>::template step<LA, LB>(acc, a, lda, b, ldb, k0, lane);
+}
+
+// Round x down / up to a multiple of the MFMA k-step of E.
+template <typename E> __device__ __forceinline__ int kfloor(int x) { return x / Mma<E>::KS * Mma<E>::KS; }
+template <typename E> __device__ __forceinline__ int kceil(int x) {
+  return (x + Mma<E>::KS - 1) / Mma<E>::KS * Mma<E>::KS;
+}
+
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 __device__ __forceinline__ int acc_row(int lane, int j) { return 4 * (lane >> 4) + j; }
@@ -211,6 +226,101 @@ __device__ __forceinline__ void load_rows_t(E* lds, int ld, const T* g, int64_t 
 
 struct Ident {
   __device__ __forceinline__ float operator()(int, int, float x) const { return x; }
+};
+
+// ----------------------------------------------------------------------------
+// Vectorised tile loads: 16-byte global accesses, every load of a thread
+// issued before its LDS stores.  Rows r >= nvalid read as zero.  NT threads
+// (the whole workgroup) share the tile; f(r, c, x) maps each value.
+// ----------------------------------------------------------------------------
+template <typename T> struct Vec16;
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void load(const float* p, float* x) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  }
+};
+template <> struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void load(const bf16_t* p, float* x) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+
+// Store n (4 or 8) consecutive floats to LDS as E with one 8- or 16-byte write.
+template <int N> __device__ __forceinline__ void store_vec(float* dst, const float* x) {
+  if constexpr (N == 4) {
+    *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
+  } else {
+    *reinterpret_cast<float4*>(dst) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(x[4], x[5], x[6], x[7]);
+  }
+}
+template <int N> __device__ __forceinline__ void store_vec(bf16_t* dst, const float* x) {
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i)
+    w[i] = static_cast<uint32_t>(f32_to_bf16(x[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(x[2 * i + 1])) << 16);
+  if constexpr (N == 4) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+  } else {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <int NT, int ROWS, int NC, typename T, typename E, typename F>
+__device__ __forceinline__ void load_tile(E* lds, int ld, const T* g, int64_t gstride, int nvalid, F f) {
+  constexpr int V = Vec16<T>::N;
+  constexpr int PER_ROW = NC / V;
+  constexpr int TOTAL = ROWS * PER_ROW;
+  constexpr int ITER = (TOTAL + NT - 1) / NT;
+  static_assert(NC % V == 0, "tile width");
+  float x[ITER][V];
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int idx = threadIdx.x + i * NT;
+    const int r = idx / PER_ROW;
+    const int c = (idx - r * PER_ROW) * V;
+    if (idx < TOTAL && r < nvalid) {
+      Vec16<T>::load(g + r * gstride + c, x[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) x[i][j] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int idx = threadIdx.x + i * NT;
+    if (TOTAL % NT != 0 && idx >= TOTAL) break;
+    const int r = idx / PER_ROW;
+    const int c = (idx - r * PER_ROW) * V;
+#pragma unroll
+    for (int j = 0; j < V; ++j) x[i][j] = f(r, c + j, x[i][j]);
+    store_vec<V>(lds + r * ld + c, x[i]);
+  }
+}
+
+// V consecutive LDS elements as floats.
+template <int V> __device__ __forceinline__ void lds_vec(const float* p, float* x) {
+#pragma unroll
+  for (int j = 0; j < V; ++j) x[j] = p[j];
+}
+template <int V> __device__ __forceinline__ void lds_vec(const bf16_t* p, float* x) {
+#pragma unroll
+  for (int j = 0; j < V; ++j) x[j] = bf16_to_f32(p[j]);
+}
+
+// Row-scaled variant helper: f(r, c, x) = s[r] * x.
+struct RowScale {
+  const float* s;
+  __device__ __forceinline__ float operator()(int r, int, float x) const { return s[r] * x; }
 };
 
 // Store a [nrows x NC] row-major LDS/register-free tile back to global rows < nvalid.

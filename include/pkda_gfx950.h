@@ -238,9 +238,7 @@ enum pkda_chunk_stage {
   PKDA_STAGE_FWD_INTRA = 1, /* per chunk: Akk, T = (I + Akk)^-1, w, u, Aqk     */
   PKDA_STAGE_FWD_STATE = 2, /* per document: U, o, the chunk states h, S_T     */
   PKDA_STAGE_BWD_STATE = 1, /* per document, reverse: dh, dU, dS0            */
-  PKDA_STAGE_BWD_DQKW = 2,  /* per chunk: state-path terms of dq, dk, dkw, dw */
-  PKDA_STAGE_BWD_WY = 4,    /* per chunk: WY / triangular-solve backward      */
-  PKDA_STAGE_BWD_INTRA = 8  /* per chunk: pairwise terms; final dq, dk, dv... */
+  PKDA_STAGE_BWD_CHUNK = 2  /* per chunk: every gradient of the chunk          */
 };
 
 /* ---------------------------------------------------------------------------
@@ -286,10 +284,10 @@ int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
  * for the recurrence proper (the gate and preconditioner backward are the
  * entry points above).  Consumes the forward's saved tensors and do
  * (and dht, the final-state gradient, or NULL).  Workspace (caller):
- * dh [num_chunks, H, K, V] (dtype), du, dw [N_tok,H,K] FP32, daqk, da
- * [N_tok,H,64] FP32.  Outputs (FP32): dq, dk (read key), dkw (write key;
- * when kw == k it is added into dk and may be NULL), dv, dbeta [N_tok,H],
- * dgcum (shape of gcum), dh0 [N,H,K,V] (NULL if not wanted).
+ * dh [num_chunks, H, K, V] and du [N_tok, H, V], both in dtype.  Outputs
+ * (FP32): dq, dk (read key), dkw (write key; when kw == k it is added into dk
+ * and may be NULL), dv, dbeta [N_tok,H], dgcum (shape of gcum), dh0
+ * [N,H,K,V] (NULL if not wanted).
  * ------------------------------------------------------------------------- */
 typedef struct pkda_chunk_bwd_args {
   int32_t struct_size;
@@ -308,7 +306,7 @@ typedef struct pkda_chunk_bwd_args {
   const void* do_;
   const float* dht;
   void* dh;
-  float *du, *dw, *daqk, *da;
+  void* du;
   float *dq, *dk, *dkw, *dv, *dbeta, *dgcum, *dh0;
   int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
 } pkda_chunk_bwd_args;
