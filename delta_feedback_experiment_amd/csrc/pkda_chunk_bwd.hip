@@ -86,6 +86,13 @@ __device__ __forceinline__ float group16_sum(float x) {
 
 // ---------------------------------------------------------------------------
 // reverse state pass
+//
+// One workgroup per (document, head, BV value columns), chunks in reverse;
+// dS [D x BV] in MFMA accumulators.  The previous chunk's tiles (KW, Q, W,
+// Aqk, dO, G) are loaded into registers while the current chunk computes.
+// Per chunk (decays on accumulator rows or on dO, never on loaded tiles):
+//   dU = Aqk^T dO + diag(e^{G_C - G}) (KW dS)      -> du (activation dtype)
+//   dS <- e^{G_C} dS + Q^T diag(s e^G) dO - W^T dU
 // ---------------------------------------------------------------------------
 template <typename T, int D, int BV>
 struct StateBwdLayout {
@@ -93,13 +100,14 @@ struct StateBwdLayout {
   static constexpr int LDV = BV + Pad<T>::v;
   static constexpr int LDC = C + Pad<T>::v;
   static constexpr int off_dS = 0;                                    // [D][LDV]  dS_C slice
-  static constexpr int off_Kg = off_dS + D * LDV * (int)sizeof(T);    // [64][LD]
-  static constexpr int off_Qg = off_Kg + C * LD * (int)sizeof(T);     // [64][LD]
-  static constexpr int off_W = off_Qg + C * LD * (int)sizeof(T);      // [64][LD]  -W
+  static constexpr int off_KW = off_dS + D * LDV * (int)sizeof(T);    // [64][LD]
+  static constexpr int off_Q = off_KW + C * LD * (int)sizeof(T);      // [64][LD]
+  static constexpr int off_W = off_Q + C * LD * (int)sizeof(T);       // [64][LD]
   static constexpr int off_Aqk = off_W + C * LD * (int)sizeof(T);     // [64][LDC]
   static constexpr int off_dO = off_Aqk + C * LDC * (int)sizeof(T);   // [64][LDV]
-  static constexpr int off_dU = off_dO + C * LDV * (int)sizeof(T);    // [64][LDV]
-  static constexpr int off_gam = off_dU + C * LDV * (int)sizeof(T);
+  static constexpr int off_dOg = off_dO + C * LDV * (int)sizeof(T);   // [64][LDV]  s e^G dO
+  static constexpr int off_dUn = off_dOg + C * LDV * (int)sizeof(T);  // [64][LDV]  -dU
+  static constexpr int off_gam = off_dUn + C * LDV * (int)sizeof(T);
   static constexpr int bytes = off_gam + C * 4;
 };
 
@@ -111,12 +119,13 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
   constexpr int NS = (D / 16) * NCT / 4;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   E* sdS = reinterpret_cast<E*>(smem + L::off_dS);
-  E* sKg = reinterpret_cast<E*>(smem + L::off_Kg);
-  E* sQg = reinterpret_cast<E*>(smem + L::off_Qg);
+  E* sKW = reinterpret_cast<E*>(smem + L::off_KW);
+  E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
   E* sW = reinterpret_cast<E*>(smem + L::off_W);
   E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
   E* sdO = reinterpret_cast<E*>(smem + L::off_dO);
-  E* sdU = reinterpret_cast<E*>(smem + L::off_dU);
+  E* sdOg = reinterpret_cast<E*>(smem + L::off_dOg);
+  E* sdUn = reinterpret_cast<E*>(smem + L::off_dUn);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
 
   const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
@@ -137,13 +146,36 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
       dS[i][j] = p.dht ? p.dht[((int64_t)n * H + h) * D * D + r * D + c] : 0.f;
     }
   }
+  RegTile<kWG, C, D, T> rKW, rQ, rW;
+  RegTile<kWG, C, C, T> rA;
+  RegTile<kWG, C, BV, T> rdO;
+  float rg = 0.f;
+  auto prefetch = [&](int jc) {
+    const int cstart = dstart + jc * C;
+    const int clen = min(C, dlen - jc * C);
+    const int64_t row0 = (int64_t)cstart * H + h;
+    rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, clen);
+    rW.load(static_cast<const T*>(p.w) + row0 * D, gs, clen);
+    rA.load(static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+    rdO.load(static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen);
+    if (tid < C) rg = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
+  };
+  if (count > 0) prefetch(count - 1);
   const float scale = p.scale;
+  const int r0 = 16 * wave;
   for (int jc = count - 1; jc >= 0; --jc) {
     const int cid = first + jc;
     const int cstart = dstart + jc * C;
     const int clen = min(C, dlen - jc * C);
     const int64_t row0 = (int64_t)cstart * H + h;
-    // (a) checkpoint dS_C and publish it (natural [c][v] layout)
+    // publish this chunk's operands and dS_C; checkpoint dS_C
+    rKW.store(sKW, L::LD);
+    rQ.store(sQ, L::LD);
+    rW.store(sW, L::LD);
+    rA.store(sAqk, L::LDC);
+    rdO.store(sdO, L::LDV);
+    if (tid < C) sGam[tid] = rg;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
@@ -152,38 +184,42 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
       T* hb = static_cast<T*>(p.dh) + ((int64_t)cid * H + h) * D * D + v0;
       store_acc_global<T>(hb, D, dS[i], 16 * rt, 16 * ct, D, lane);
     }
-    if (tid < C) sGam[tid] = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
     __syncthreads();
+    if (jc > 0) prefetch(jc - 1);
     const float gC = sGam[C - 1];
-    load_tile<kWG, C, D>(sKg, L::LD, static_cast<const T*>(p.kw) + row0 * D, gs, clen,
-                         [&](int r, int, float x) { return expf(gC - sGam[r]) * x; });
-    load_tile<kWG, C, D>(sQg, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, clen,
-                         [&](int r, int, float x) { return scale * expf(sGam[r]) * x; });
-    load_tile<kWG, C, D>(sW, L::LD, static_cast<const T*>(p.w) + row0 * D, gs, clen,
-                         [&](int, int, float x) { return -x; });
-    load_tile<kWG, C, C>(sAqk, L::LDC, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen, Ident());
-    load_tile<kWG, C, BV>(sdO, L::LDV, static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen, Ident());
-    __syncthreads();
-    // (b) dU = Aqk^T dO + Kg dS_C     wave w: rows 16w..16w+15
+    // s e^G dO (elementwise, for Q^T diag(s e^G) dO)
+    for (int i = tid; i < C * BV; i += kWG) {
+      const int r = i / BV, c = i - r * BV;
+      sdOg[r * L::LDV + c] = to_e<E>(scale * expf(sGam[r]) * from_e<E>(sdO[r * L::LDV + c]));
+    }
+    // dU = Aqk^T dO + diag(e^{G_C - G}) KW dS     wave w: rows 16w..16w+15
+    float egc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) egc[e] = expf(gC - sGam[r0 + acc_row(lane, e)]);
     T* du_out = static_cast<T*>(p.du) + row0 * D + v0;
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
-      f32x4 acc = zero4();
-      mma_tile_range<E, COL, ROW>(acc, sAqk, L::LDC, 16 * wave, sdO, L::LDV, 16 * ct, kfloor<E>(16 * wave), C, lane);
-      mma_tile<E, ROW, ROW>(acc, sKg, L::LD, 16 * wave, sdS, L::LDV, 16 * ct, D, lane);
-      store_acc_global<T>(du_out, gs, acc, 16 * wave, 16 * ct, clen, lane);
-      store_acc_lds(sdU, L::LDV, acc, 16 * wave, 16 * ct, lane);
+      f32x4 a1 = zero4(), a2 = zero4();
+      mma_tile_range<E, COL, ROW>(a1, sAqk, L::LDC, r0, sdO, L::LDV, 16 * ct, kfloor<E>(r0), C, lane);
+      mma_tile<E, ROW, ROW>(a2, sKW, L::LD, r0, sdS, L::LDV, 16 * ct, D, lane);
+      f32x4 du;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        du[e] = a1[e] + egc[e] * a2[e];
+        sdUn[(r0 + acc_row(lane, e)) * L::LDV + 16 * ct + acc_col(lane)] = to_e<E>(-du[e]);
+      }
+      store_acc_global<T>(du_out, gs, du, r0, 16 * ct, clen, lane);
     }
     __syncthreads();
-    // (c) dS <- e^{G_C} dS + Qg^T dO - W^T dU
+    // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU
     const float decay = expf(gC);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
       dS[i] = dS[i] * decay;
-      mma_tile<E, COL, ROW>(dS[i], sQg, L::LD, 16 * rt, sdO, L::LDV, 16 * ct, C, lane);
-      mma_tile<E, COL, ROW>(dS[i], sW, L::LD, 16 * rt, sdU, L::LDV, 16 * ct, C, lane);
+      mma_tile<E, COL, ROW>(dS[i], sQ, L::LD, 16 * rt, sdOg, L::LDV, 16 * ct, C, lane);
+      mma_tile<E, COL, ROW>(dS[i], sW, L::LD, 16 * rt, sdUn, L::LDV, 16 * ct, C, lane);
     }
     __syncthreads();
   }
@@ -196,7 +232,6 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
     }
   }
 }
-
 // ---------------------------------------------------------------------------
 // fused per-chunk backward
 // ---------------------------------------------------------------------------

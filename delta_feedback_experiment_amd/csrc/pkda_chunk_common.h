@@ -317,6 +317,39 @@ template <int V> __device__ __forceinline__ void lds_vec(const bf16_t* p, float*
   for (int j = 0; j < V; ++j) x[j] = bf16_to_f32(p[j]);
 }
 
+// A [ROWS x NC] global tile held in registers as raw 16-byte pieces, so the
+// next chunk's operands can be in flight while the current chunk computes.
+// Rows r >= nvalid hold zeros.  store() copies the pieces to an LDS tile of
+// the same element type.
+template <int NT, int ROWS, int NC, typename T>
+struct RegTile {
+  static constexpr int V = Vec16<T>::N;
+  static constexpr int PER_ROW = NC / V;
+  static constexpr int TOTAL = ROWS * PER_ROW;
+  static constexpr int ITER = (TOTAL + NT - 1) / NT;
+  uint4 r[ITER];
+  __device__ __forceinline__ void load(const T* g, int64_t gstride, int nvalid) {
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      const int row = idx / PER_ROW;
+      const int c = (idx - row * PER_ROW) * V;
+      r[i] = (idx < TOTAL && row < nvalid) ? *reinterpret_cast<const uint4*>(g + row * gstride + c)
+                                           : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  __device__ __forceinline__ void store(T* lds, int ld) const {
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (TOTAL % NT != 0 && idx >= TOTAL) break;
+      const int row = idx / PER_ROW;
+      const int c = (idx - row * PER_ROW) * V;
+      *reinterpret_cast<uint4*>(lds + row * ld + c) = r[i];
+    }
+  }
+};
+
 // Row-scaled variant helper: f(r, c, x) = s[r] * x.
 struct RowScale {
   const float* s;

@@ -237,17 +237,33 @@ __global__ __launch_bounds__(kWG) void chunk_intra_fwd_kernel(FwdParams p) {
 
 // ---------------------------------------------------------------------------
 // per-document state pass
+//
+// One workgroup per (document, head, BV value columns).  The FP32 state slice
+// S [D x BV] lives in MFMA accumulators; each chunk it is published to LDS
+// (bf16/fp32, natural [c][v] layout) as the B operand of W S and Q S.  The
+// next chunk's tiles (W, Q, KW, Aqk, u, G) are loaded into registers while the
+// current chunk computes, so the chain of chunks is not serialised on HBM
+// latency.  Per chunk:
+//   U = u - W S                     (written back over u: the backward's U)
+//   O = diag(s e^G) (Q S) + Aqk U
+//   S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U
+// with the decays applied to accumulator rows or to U, never to the loaded
+// tiles.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int BV>
 struct StateLayout {
   static constexpr int LD = D + Pad<T>::v;
+  static constexpr int LDV = BV + Pad<T>::v;
   static constexpr int LDC = C + Pad<T>::v;
-  static constexpr int off_ST = 0;                                     // [BV][LD]  S^T
-  static constexpr int off_Y = off_ST + BV * LD * (int)sizeof(T);      // [64][LD]  W, then scale e^G Q
-  static constexpr int off_Aqk = off_Y + C * LD * (int)sizeof(T);      // [64][LDC]
-  static constexpr int off_UT = off_Aqk + C * LDC * (int)sizeof(T);    // [BV][LDC] U^T
-  static constexpr int off_KwT = off_UT + BV * LDC * (int)sizeof(T);   // [D][LDC]  (e^(G_C-G) kw)^T
-  static constexpr int off_gam = off_KwT + D * LDC * (int)sizeof(T);
+  static constexpr int off_S = 0;                                     // [D][LDV]
+  static constexpr int off_W = off_S + D * LDV * (int)sizeof(T);      // [64][LD]
+  static constexpr int off_Q = off_W + C * LD * (int)sizeof(T);       // [64][LD]
+  static constexpr int off_KW = off_Q + C * LD * (int)sizeof(T);      // [64][LD]
+  static constexpr int off_Aqk = off_KW + C * LD * (int)sizeof(T);    // [64][LDC]
+  static constexpr int off_Uin = off_Aqk + C * LDC * (int)sizeof(T);  // [64][LDV]  u
+  static constexpr int off_U = off_Uin + C * LDV * (int)sizeof(T);    // [64][LDV]  U
+  static constexpr int off_Ug = off_U + C * LDV * (int)sizeof(T);     // [64][LDV]  e^{G_C-G} U
+  static constexpr int off_gam = off_Ug + C * LDV * (int)sizeof(T);
   static constexpr int bytes = off_gam + C * 4;
 };
 
@@ -258,11 +274,14 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
   constexpr int NCT = BV / 16;              // column tiles of the slice
   constexpr int NS = (D / 16) * NCT / 4;    // state tiles per wave
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  E* sST = reinterpret_cast<E*>(smem + L::off_ST);
-  E* sY = reinterpret_cast<E*>(smem + L::off_Y);
+  E* sS = reinterpret_cast<E*>(smem + L::off_S);
+  E* sW = reinterpret_cast<E*>(smem + L::off_W);
+  E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
+  E* sKW = reinterpret_cast<E*>(smem + L::off_KW);
   E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
-  E* sUT = reinterpret_cast<E*>(smem + L::off_UT);
-  E* sKwT = reinterpret_cast<E*>(smem + L::off_KwT);
+  E* sUin = reinterpret_cast<E*>(smem + L::off_Uin);
+  E* sU = reinterpret_cast<E*>(smem + L::off_U);
+  E* sUg = reinterpret_cast<E*>(smem + L::off_Ug);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
 
   const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
@@ -284,71 +303,95 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
     }
   }
 
+  RegTile<kWG, C, D, T> rW, rQ, rKW;
+  RegTile<kWG, C, C, T> rA;
+  RegTile<kWG, C, BV, T> rU;
+  float rg = 0.f;
+  auto prefetch = [&](int jc) {
+    const int cstart = dstart + jc * C;
+    const int clen = min(C, dlen - jc * C);
+    const int64_t row0 = (int64_t)cstart * H + h;
+    rW.load(static_cast<const T*>(p.w) + row0 * D, gs, clen);
+    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, clen);
+    rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+    rA.load(static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+    rU.load(static_cast<const T*>(p.u) + row0 * D + v0, gs, clen);
+    if (tid < C) rg = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
+  };
+  if (count > 0) prefetch(0);
+  const float scale = p.scale;
+  const int r0 = 16 * wave;
+
   for (int jc = 0; jc < count; ++jc) {
     const int cid = first + jc;
     const int cstart = dstart + jc * C;
     const int clen = min(C, dlen - jc * C);
     const int64_t row0 = (int64_t)cstart * H + h;
-    // (a) publish S (B operand, transposed) and checkpoint it
+    // publish this chunk's operands and the entering state; checkpoint it
+    rW.store(sW, L::LD);
+    rQ.store(sQ, L::LD);
+    rKW.store(sKW, L::LD);
+    rA.store(sAqk, L::LDC);
+    rU.store(sUin, L::LDV);
+    if (tid < C) sGam[tid] = rg;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
-      store_acc_lds_t(sST, L::LD, S[i], 16 * rt, 16 * ct, lane);
+      store_acc_lds(sS, L::LDV, S[i], 16 * rt, 16 * ct, lane);
       if (p.h) {
         T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D + v0;
         store_acc_global<T>(hb, D, S[i], 16 * rt, 16 * ct, D, lane);
       }
     }
-    load_chunk_scalars(nullptr, sGam, nullptr, p.gcum, cstart, clen, H, h);
-    load_rows<T, E, D>(sY, L::LD, static_cast<const T*>(p.w) + row0 * D, gs, C, clen, Ident());
     __syncthreads();
+    if (jc + 1 < count) prefetch(jc + 1);
     const float gC = sGam[C - 1];  // padded rows repeat the last valid gate
-    // (b) U = Uu - W S      wave w: row tile w
+    float eg[4], egc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g = sGam[r0 + acc_row(lane, e)];
+      eg[e] = scale * expf(g);
+      egc[e] = expf(gC - g);
+    }
+    // U = u - W S
     T* u_io = static_cast<T*>(p.u) + row0 * D + v0;
-    f32x4 U[NCT];
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
       f32x4 acc = zero4();
-      mma_tile<E, ROW, COL>(acc, sY, L::LD, 16 * wave, sST, L::LD, 16 * ct, D, lane);
+      mma_tile<E, ROW, ROW>(acc, sW, L::LD, r0, sS, L::LDV, 16 * ct, D, lane);
+      f32x4 U;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 16 * wave + acc_row(lane, j);
-        const float uu = r < clen ? io<T>::load(u_io + r * gs + 16 * ct + acc_col(lane)) : 0.f;
-        U[ct][j] = uu - acc[j];
+      for (int e = 0; e < 4; ++e) {
+        const int r = r0 + acc_row(lane, e), c = 16 * ct + acc_col(lane);
+        U[e] = from_e<E>(sUin[r * L::LDV + c]) - acc[e];
+        sU[r * L::LDV + c] = to_e<E>(U[e]);
+        sUg[r * L::LDV + c] = to_e<E>(egc[e] * U[e]);
       }
+      store_acc_global<T>(u_io, gs, U, r0, 16 * ct, clen, lane);
     }
     __syncthreads();
-    // (c) publish U; stage Q (scaled), Aqk, KW^T (gated)
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      store_acc_lds_t(sUT, L::LDC, U[ct], 16 * wave, 16 * ct, lane);
-      store_acc_global<T>(u_io, gs, U[ct], 16 * wave, 16 * ct, clen, lane);
-    }
-    const float scale = p.scale;
-    load_rows<T, E, D>(sY, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, C, clen,
-                       [&](int r, int, float x) { return scale * expf(sGam[r]) * x; });
-    load_rows<T, E, C>(sAqk, L::LDC, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, C, clen, Ident());
-    load_rows_t<T, E, D>(sKwT, L::LDC, static_cast<const T*>(p.kw) + row0 * D, gs, C, clen,
-                         [&](int r, int, float x) { return expf(gC - sGam[r]) * x; });
-    __syncthreads();
-    // O = (scale e^G Q) S + Aqk U
+    // O = diag(s e^G) Q S + Aqk U
     T* o_out = static_cast<T*>(p.o) + row0 * D + v0;
+    const int kend = kceil<E>(r0 + 16);  // Aqk is lower triangular
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
-      f32x4 acc = zero4();
-      mma_tile<E, ROW, COL>(acc, sY, L::LD, 16 * wave, sST, L::LD, 16 * ct, D, lane);
-      mma_tile<E, ROW, COL>(acc, sAqk, L::LDC, 16 * wave, sUT, L::LDC, 16 * ct, C, lane);
-      store_acc_global<T>(o_out, gs, acc, 16 * wave, 16 * ct, clen, lane);
+      f32x4 a1 = zero4(), a2 = zero4();
+      mma_tile<E, ROW, ROW>(a1, sQ, L::LD, r0, sS, L::LDV, 16 * ct, D, lane);
+      mma_tile_range<E, ROW, ROW>(a2, sAqk, L::LDC, r0, sU, L::LDV, 16 * ct, 0, kend, lane);
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = eg[e] * a1[e] + a2[e];
+      store_acc_global<T>(o_out, gs, o, r0, 16 * ct, clen, lane);
     }
-    // S <- e^{G_C} S + KW_g^T U
+    // S <- e^{G_C} S + KW^T Ug
     const float decay = expf(gC);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
       S[i] = S[i] * decay;
-      mma_tile<E, ROW, COL>(S[i], sKwT, L::LDC, 16 * rt, sUT, L::LDC, 16 * ct, C, lane);
+      mma_tile<E, COL, ROW>(S[i], sKW, L::LD, 16 * rt, sUg, L::LDV, 16 * ct, C, lane);
     }
     __syncthreads();
   }
@@ -439,5 +482,5 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   if (a->dtype == PKDA_BF16) {
     return a->head_dim == 128 ? launch_fwd<bf16_t, 128, 64>(p, nc, st, s) : launch_fwd<bf16_t, 64, 64>(p, nc, st, s);
   }
-  return a->head_dim == 128 ? launch_fwd<float, 128, 32>(p, nc, st, s) : launch_fwd<float, 64, 64>(p, nc, st, s);
+  return a->head_dim == 128 ? launch_fwd<float, 128, 16>(p, nc, st, s) : launch_fwd<float, 64, 64>(p, nc, st, s);
 }
