@@ -48,129 +48,142 @@ struct FwdParams {
   void* h;
 };
 
-__device__ __forceinline__ float clamp_gate(const float* s_gam, int t) { return s_gam[t]; }
-
-// Load per-row beta and cumulative gate of a chunk into LDS.  Rows past the
-// chunk's end repeat the last cumulative gate (so exp(G_t - G_s) stays finite
-// where masks zero it) and get beta = 0.
-__device__ __forceinline__ void load_chunk_scalars(float* s_beta, float* s_gam, const float* beta, const float* gcum,
-                                                   int start, int len, int H, int h) {
-  const int t = threadIdx.x;
-  if (t < C) {
-    const int tt = t < len ? t : len - 1;
-    const int64_t idx = (int64_t)(start + tt) * H + h;
-    s_gam[t] = gcum[idx];
-    if (s_beta) s_beta[t] = t < len ? beta[idx] : 0.f;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Blocked inverse of (I + A), A strictly lower 64x64 FP32 in LDS (ld = ldf).
-// Result into s_t (same ld).  scratch: 4 waves x 3 x 16 x 17 floats.
+// Blocked inverse of (I + A) in place, A strictly lower 64x64 FP32 in LDS
+// (ld = ldf) whose blocks above the diagonal are zero.  Each 16x16 diagonal
+// block (I + N) is inverted as (I - N)(I + N^2)(I + N^4)(I + N^8) (N^16 = 0)
+// in three squarings, then the blocks below the diagonal follow by block
+// forward substitution T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, one block row at
+// a time; all products on FP32 MFMA.  Waves 0..3 work, every wave of the
+// workgroup reaches every barrier.  scratch: 4 x 3 x 16 x SLD floats.
 // ---------------------------------------------------------------------------
 constexpr int SLD = 17;
 
-__device__ __forceinline__ void solve_unit_lower_64(const float* s_a, float* s_t, int ldf, float* scratch) {
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  for (int i = tid; i < C * C; i += kWG) s_t[(i / C) * ldf + (i % C)] = 0.f;
-  float* M = scratch + wave * 3 * 16 * SLD;
+__device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* scratch) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const bool active = wave < 4;
+  const int b = wave & 3;  // diagonal block of this wave
+  float* M = scratch + b * 3 * 16 * SLD;
   float* P = M + 16 * SLD;
   float* X = P + 16 * SLD;
-  const int b = wave;  // diagonal block of this wave
-  const float* N = s_a + (16 * b) * ldf + 16 * b;
+  float* N = s + (16 * b) * ldf + 16 * b;
+  if (active) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = acc_row(lane, j), c = acc_col(lane);
-    const float n = N[r * ldf + c];
-    M[r * SLD + c] = n;
-    P[r * SLD + c] = (r == c ? 1.f : 0.f) - n;
+    for (int j = 0; j < 4; ++j) {
+      const int r = acc_row(lane, j), c = acc_col(lane);
+      const float n = N[r * ldf + c];
+      M[r * SLD + c] = n;
+      P[r * SLD + c] = (r == c ? 1.f : 0.f) - n;
+    }
   }
   __syncthreads();
   for (int step = 0; step < 3; ++step) {
-    f32x4 acc = zero4();
-    mma_tile<float, ROW, ROW>(acc, M, SLD, 0, M, SLD, 0, 16, lane);  // M <- M^2
-    __syncthreads();
-    store_acc_lds(M, SLD, acc, 0, 0, lane);
-    __syncthreads();
-    f32x4 pacc;
+    f32x4 acc = zero4(), pacc = zero4();
+    if (active) {
+      mma_tile<float, ROW, ROW>(acc, M, SLD, 0, M, SLD, 0, 16, lane);  // M <- M^2
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pacc[j] = P[acc_row(lane, j) * SLD + acc_col(lane)];
-    mma_tile<float, ROW, ROW>(pacc, P, SLD, 0, M, SLD, 0, 16, lane);  // P <- P (I + M)
+      for (int j = 0; j < 4; ++j) pacc[j] = P[acc_row(lane, j) * SLD + acc_col(lane)];
+    }
     __syncthreads();
-    store_acc_lds(P, SLD, pacc, 0, 0, lane);
+    if (active) store_acc_lds(M, SLD, acc, 0, 0, lane);
+    __syncthreads();
+    if (active) mma_tile<float, ROW, ROW>(pacc, P, SLD, 0, M, SLD, 0, 16, lane);  // P <- P (I + M)
+    __syncthreads();
+    if (active) store_acc_lds(P, SLD, pacc, 0, 0, lane);
     __syncthreads();
   }
-  // diagonal block inverse -> s_t
+  if (active) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = acc_row(lane, j), c = acc_col(lane);
-    s_t[(16 * b + r) * ldf + 16 * b + c] = P[r * SLD + c];
+    for (int j = 0; j < 4; ++j) N[acc_row(lane, j) * ldf + acc_col(lane)] = P[acc_row(lane, j) * SLD + acc_col(lane)];
   }
   __syncthreads();
-  // off-diagonal blocks, block row by block row: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj
   for (int i = 1; i < 4; ++i) {
-    const int j = wave;
-    const bool active = j < i;
-    f32x4 x = zero4();
-    if (active) {
+    const int j = b;
+    const bool on = active && j < i;
+    if (on) {
+      f32x4 x = zero4();
       for (int k = j; k < i; ++k)
-        mma_tile<float, ROW, ROW>(x, s_a + (16 * i) * ldf + 16 * k, ldf, 0, s_t + (16 * k) * ldf + 16 * j, ldf, 0, 16,
+        mma_tile<float, ROW, ROW>(x, s + (16 * i) * ldf + 16 * k, ldf, 0, s + (16 * k) * ldf + 16 * j, ldf, 0, 16,
                                   lane);
       store_acc_lds(X, SLD, x, 0, 0, lane);
     }
     __syncthreads();
-    if (active) {
+    if (on) {
       f32x4 y = zero4();
-      mma_tile<float, ROW, ROW>(y, s_t + (16 * i) * ldf + 16 * i, ldf, 0, X, SLD, 0, 16, lane);
+      mma_tile<float, ROW, ROW>(y, s + (16 * i) * ldf + 16 * i, ldf, 0, X, SLD, 0, 16, lane);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        s_t[(16 * i + acc_row(lane, jj)) * ldf + 16 * j + acc_col(lane)] = -y[jj];
+      for (int jj = 0; jj < 4; ++jj) s[(16 * i + acc_row(lane, jj)) * ldf + 16 * j + acc_col(lane)] = -y[jj];
     }
     __syncthreads();
   }
 }
 
+// Coalesced store of rows [0, nvalid) of an LDS tile [ROWS][NC] (element type
+// T) to global memory with 16-byte accesses.
+template <int NT, int ROWS, int NC, typename T>
+__device__ __forceinline__ void store_tile(T* g, int64_t gstride, const T* lds, int ld, int nvalid) {
+  constexpr int V = Vec16<T>::N;
+  constexpr int PER_ROW = NC / V;
+  constexpr int TOTAL = ROWS * PER_ROW;
+  for (int idx = threadIdx.x; idx < TOTAL; idx += NT) {
+    const int r = idx / PER_ROW;
+    const int c = (idx - r * PER_ROW) * V;
+    if (r < nvalid) *reinterpret_cast<uint4*>(g + r * gstride + c) = *reinterpret_cast<const uint4*>(lds + r * ld + c);
+  }
+}
+
 // ---------------------------------------------------------------------------
-// intra-chunk forward
+// intra-chunk forward: one 8-wave workgroup per (chunk, head).
+//   Akk, Aqk   the ten 16x16 blocks on or below the diagonal, one or two per
+//              wave (raw k.kw and q.kw products, then the pairwise decay);
+//   T          in place over Akk (waves 0..3);
+//   W, u       T (diag(beta e^G) K), T (diag(beta) V): wave w owns row block
+//              w % 4 and column half w / 4.
+// All outputs leave through LDS with 16-byte stores.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+constexpr int kIW = 512;
+
+template <typename T, int D, bool ALIAS>
 struct IntraLayout {
   static constexpr int LD = D + Pad<T>::v;
   static constexpr int LDC = C + Pad<T>::v;
   static constexpr int LDF = C + 4;
-  static constexpr int X12 = 3 * C * LD * (int)sizeof(T);
-  static constexpr int X4 = 2 * D * LDC * (int)sizeof(T);
-  static constexpr int XS = 4 * 3 * 16 * SLD * (int)sizeof(float);
-  static constexpr int XB = (X12 > X4 ? (X12 > XS ? X12 : XS) : (X4 > XS ? X4 : XS));
-  static constexpr int off_A = (XB + 15) / 16 * 16;
-  static constexpr int off_T = off_A + C * LDF * 4;
-  static constexpr int off_Te = off_T + C * LDF * 4;
-  static constexpr int off_beta = off_Te + C * LDC * (int)sizeof(T) + 16;
+  static constexpr int RT = C * LD * (int)sizeof(T);
+  static constexpr int SCR = 4 * 3 * 16 * SLD * 4;      // solve scratch
+  static constexpr int QR = RT > SCR ? RT : SCR;
+  static constexpr int off_K = 0;                       // K, then Bw, then W
+  static constexpr int off_Q = off_K + RT;              // Q, then solve scratch, then Bv, then u
+  static constexpr int off_KW = off_Q + QR;             // KW (when not aliased to K)
+  static constexpr int off_A = off_KW + (ALIAS ? 0 : RT);  // fp32 [64][LDF]: Akk, then T
+  static constexpr int off_Te = off_A + C * LDF * 4;    // [64][LDC] T in the operand type
+  static constexpr int off_Aqk = off_Te + C * LDC * (int)sizeof(T);
+  static constexpr int off_beta = off_Aqk + C * LDC * (int)sizeof(T);
   static constexpr int off_gam = off_beta + C * 4;
   static constexpr int bytes = off_gam + C * 4;
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(kWG) void chunk_intra_fwd_kernel(FwdParams p) {
-  using L = IntraLayout<T, D>;
+template <typename T, int D, bool ALIAS>
+__global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
+  using L = IntraLayout<T, D, ALIAS>;
   using E = T;
+  constexpr int HCT = D / 32;  // column tiles per wave of W / u
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
   if (ci.len <= 0) return;
   const int h = blockIdx.y;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int len = ci.len;
   const int64_t row0 = (int64_t)ci.start * H + h;  // token-row index of the chunk's first token
   const int64_t gs = (int64_t)H * D;               // token stride in elements
 
-  E* sK = reinterpret_cast<E*>(smem);
-  E* sKW = sK + C * L::LD;
-  E* sQ = sKW + C * L::LD;
+  E* sK = reinterpret_cast<E*>(smem + L::off_K);
+  E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
+  E* sKW = ALIAS ? sK : reinterpret_cast<E*>(smem + L::off_KW);
   float* sA = reinterpret_cast<float*>(smem + L::off_A);
-  float* sTf = reinterpret_cast<float*>(smem + L::off_T);
   E* sTe = reinterpret_cast<E*>(smem + L::off_Te);
+  E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
 
@@ -178,63 +191,83 @@ __global__ __launch_bounds__(kWG) void chunk_intra_fwd_kernel(FwdParams p) {
   const T* k = static_cast<const T*>(p.k) + row0 * D;
   const T* kw = static_cast<const T*>(p.kw) + row0 * D;
   const T* v = static_cast<const T*>(p.v) + row0 * D;
-  const bool alias = p.kw == p.k;
 
-  load_chunk_scalars(sBeta, sGam, p.beta, p.gcum, ci.start, ci.len, H, h);
-  load_rows<T, E, D>(sK, L::LD, k, gs, C, ci.len, Ident());
-  if (!alias) load_rows<T, E, D>(sKW, L::LD, kw, gs, C, ci.len, Ident());
-  load_rows<T, E, D>(sQ, L::LD, q, gs, C, ci.len, Ident());
+  if (tid < C) {
+    const int64_t idx = (int64_t)(ci.start + min(tid, len - 1)) * H + h;
+    sGam[tid] = p.gcum[idx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
+    sBeta[tid] = tid < len ? p.beta[idx] : 0.f;
+  }
+  load_tile<kIW, C, D>(sK, L::LD, k, gs, len, Ident());
+  load_tile<kIW, C, D>(sQ, L::LD, q, gs, len, Ident());
+  if (!ALIAS) load_tile<kIW, C, D>(sKW, L::LD, kw, gs, len, Ident());
+  // blocks above the diagonal of Akk / T are zero
+  for (int i = tid; i < C * C; i += kIW) {
+    const int r = i / C, c = i - r * C;
+    if ((c >> 4) > (r >> 4)) sA[r * L::LDF + c] = 0.f;
+  }
   __syncthreads();
-  const E* sKWr = alias ? sK : sKW;
 
-  // ---- Akk, Aqk: wave w owns row tile w ------------------------------------
-  T* aqk_out = static_cast<T*>(p.aqk) + row0 * C;
-  for (int ct = 0; ct < 4; ++ct) {
+  // ---- Akk, Aqk on the ten blocks (tb >= sb) --------------------------------
+  for (int blk = wave; blk < 10; blk += 8) {
+    const int tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
+    const int sb = blk - tb * (tb + 1) / 2;
     f32x4 akk = zero4(), aqk = zero4();
-    if (ct <= wave) {
-      mma_tile<E, ROW, COL>(akk, sK, L::LD, 16 * wave, sKWr, L::LD, 16 * ct, D, lane);
-      mma_tile<E, ROW, COL>(aqk, sQ, L::LD, 16 * wave, sKWr, L::LD, 16 * ct, D, lane);
-    }
+    mma_tile<E, ROW, COL>(akk, sK, L::LD, 16 * tb, sKW, L::LD, 16 * sb, D, lane);
+    mma_tile<E, ROW, COL>(aqk, sQ, L::LD, 16 * tb, sKW, L::LD, 16 * sb, D, lane);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = 16 * wave + acc_row(lane, j);
-      const int s = 16 * ct + acc_col(lane);
-      const bool valid_t = t < ci.len;
-      const float dec = (s <= t && valid_t) ? expf(sGam[t] - sGam[s]) : 0.f;
+      const int t = 16 * tb + acc_row(lane, j);
+      const int s = 16 * sb + acc_col(lane);
+      const float dec = (s <= t && t < len) ? expf(sGam[t] - sGam[s]) : 0.f;
       sA[t * L::LDF + s] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
-      if (valid_t) io<T>::store(aqk_out + (int64_t)t * H * C + s, p.scale * dec * aqk[j]);
+      sAqk[t * L::LDC + s] = to_e<E>(p.scale * dec * aqk[j]);
     }
   }
+  for (int i = tid; i < C * C; i += kIW) {  // Aqk blocks above the diagonal
+    const int r = i / C, c = i - r * C;
+    if ((c >> 4) > (r >> 4)) sAqk[r * L::LDC + c] = to_e<E>(0.f);
+  }
   __syncthreads();
 
-  // ---- T = (I + Akk)^-1 ------------------------------------------------------
-  solve_unit_lower_64(sA, sTf, L::LDF, reinterpret_cast<float*>(smem));
-  T* akk_out = static_cast<T*>(p.akk) + row0 * C;
-  for (int i = tid; i < C * C; i += kWG) {
-    const int r = i / C, c = i % C;
-    const float x = sTf[r * L::LDF + c];
-    sTe[r * L::LDC + c] = to_e<E>(x);
-    if (r < ci.len) io<T>::store(akk_out + (int64_t)r * H * C + c, x);
+  // ---- T = (I + Akk)^-1 in place; Aqk leaves meanwhile ------------------------
+  store_tile<kIW, C, C>(static_cast<T*>(p.aqk) + row0 * C, (int64_t)H * C, sAqk, L::LDC, len);
+  solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
+  for (int i = tid; i < C * C; i += kIW) {
+    const int r = i / C, c = i - r * C;
+    sTe[r * L::LDC + c] = to_e<E>(sA[r * L::LDF + c]);
   }
-  // ---- W = T diag(beta e^G) K,  Uu = T diag(beta) V ---------------------------
-  E* sBw = reinterpret_cast<E*>(smem);
-  E* sBv = sBw + C * L::LD;
-  load_rows<T, E, D>(sBw, L::LD, k, gs, C, ci.len,
-                     [&](int r, int, float x) { return sBeta[r] * expf(sGam[r]) * x; });
-  load_rows<T, E, D>(sBv, L::LD, v, gs, C, ci.len, [&](int r, int, float x) { return sBeta[r] * x; });
+  // Bw = diag(beta e^G) K in place over K; Bv = diag(beta) V over Q
+  for (int i = tid; i < C * D; i += kIW) {
+    const int r = i / D, c = i - r * D;
+    sK[r * L::LD + c] = to_e<E>(sBeta[r] * expf(sGam[r]) * from_e<E>(sK[r * L::LD + c]));
+  }
+  load_tile<kIW, C, D>(sQ, L::LD, v, gs, len, RowScale{sBeta});
   __syncthreads();
-  const int kdim = ((16 * (wave + 1) + Mma<E>::KS - 1) / Mma<E>::KS) * Mma<E>::KS;  // T is lower triangular
-  T* w_out = static_cast<T*>(p.w) + row0 * D;
-  T* u_out = static_cast<T*>(p.u) + row0 * D;
-  for (int ct = 0; ct < D / 16; ++ct) {
-    f32x4 aw = zero4(), au = zero4();
-    mma_tile<E, ROW, ROW>(aw, sTe, L::LDC, 16 * wave, sBw, L::LD, 16 * ct, kdim, lane);
-    mma_tile<E, ROW, ROW>(au, sTe, L::LDC, 16 * wave, sBv, L::LD, 16 * ct, kdim, lane);
-    store_acc_global<T>(w_out, gs, aw, 16 * wave, 16 * ct, ci.len, lane);
-    store_acc_global<T>(u_out, gs, au, 16 * wave, 16 * ct, ci.len, lane);
+  store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
+
+  // ---- W = T Bw, u = T Bv ------------------------------------------------------
+  const int rb = wave & 3, ch = wave >> 2;
+  const int kend = kceil<E>(16 * rb + 16);  // T is lower triangular
+  f32x4 aw[HCT], au[HCT];
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    aw[j] = zero4();
+    au[j] = zero4();
+    mma_tile_range<E, ROW, ROW>(aw[j], sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
+    mma_tile_range<E, ROW, ROW>(au[j], sTe, L::LDC, 16 * rb, sQ, L::LD, 16 * ct, 0, kend, lane);
   }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    store_acc_lds(sK, L::LD, aw[j], 16 * rb, 16 * ct, lane);
+    store_acc_lds(sQ, L::LD, au[j], 16 * rb, 16 * ct, lane);
+  }
+  __syncthreads();
+  store_tile<kIW, C, D>(static_cast<T*>(p.w) + row0 * D, gs, sK, L::LD, len);
+  store_tile<kIW, C, D>(static_cast<T*>(p.u) + row0 * D, gs, sQ, L::LD, len);
 }
-
 // ---------------------------------------------------------------------------
 // per-document state pass
 //
@@ -421,10 +454,11 @@ template <typename T, int D, int BV>
 int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const bool all = stages == 0;
   if (all || (stages & PKDA_STAGE_FWD_INTRA)) {
-    auto kern = chunk_intra_fwd_kernel<T, D>;
-    const int bytes = IntraLayout<T, D>::bytes;
+    const bool alias = p.kw == p.k;
+    auto kern = alias ? chunk_intra_fwd_kernel<T, D, true> : chunk_intra_fwd_kernel<T, D, false>;
+    const int bytes = alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
-    if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kWG), bytes, s, p);
+    if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kIW), bytes, s, p);
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
   }
   if (all || (stages & PKDA_STAGE_FWD_STATE)) {
