@@ -279,7 +279,7 @@ def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> 
 
 
 def cpu_baseline(D: int = 128, H: int = 16, T: int = 512, seed: int = 3, budget_s: float = 12.0,
-                 max_rows: int = 8) -> dict:
+                 max_rows: int = 32) -> dict:
     """The CPU oracle's fwd+bwd over B=1 row slices of the workload (FP32, all
     host cores): rows of T tokens are run one after another until ``budget_s``
     seconds or ``max_rows`` rows, and the token rate is over all of them."""

@@ -83,7 +83,7 @@ class ChunkFwdArgs(ctypes.Structure):
     _fields_ = _CHUNK_COMMON + [
         ("final_state", c_void_p), ("o", c_void_p),
         ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
-        ("stages", c_int32),
+        ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p),
     ]
 
 
@@ -93,7 +93,7 @@ class ChunkBwdArgs(ctypes.Structure):
         ("do", c_void_p), ("dht", c_void_p), ("dh", c_void_p), ("du", c_void_p),
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
-        ("stages", c_int32),
+        ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p),
     ]
 
 

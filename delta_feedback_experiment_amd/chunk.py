@@ -87,6 +87,8 @@ class FwdSaved:
     aqk: Tensor
     akk: Tensor
     h: Tensor | None
+    qg: Tensor | None = None   # per-channel gates: scale e^G q
+    kg: Tensor | None = None   # per-channel gates: e^{G_last - G} kw
 
 
 def chunk_forward(
@@ -103,15 +105,18 @@ def chunk_forward(
     akk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
     h = torch.empty(plan.num_chunks, H, D, D, device=dev, dtype=q.dtype) if save_states else None
     S_T = torch.empty(N, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
+    per_channel = gcum.dim() == 3
+    qg = torch.empty_like(q) if per_channel else None
+    kg = torch.empty_like(k) if per_channel else None
     args = _lib.ChunkFwdArgs(
         dtype=_dtype_code(q), **plan.common(),
         q=_ptr(q), k=_ptr(k), kw=_ptr(kw), v=_ptr(v), gcum=_ptr(gcum),
-        gate_per_channel=int(gcum.dim() == 3), beta=_ptr(beta32), scale=float(scale),
+        gate_per_channel=int(per_channel), beta=_ptr(beta32), scale=float(scale),
         initial_state=_ptr(initial_state), final_state=_ptr(S_T), o=_ptr(o),
-        w=_ptr(w), u=_ptr(u), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h),
+        w=_ptr(w), u=_ptr(u), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), qg=_ptr(qg), kg=_ptr(kg),
     )
     _lib.call("pkda_chunk_fwd", args, _stream(dev))
-    return o, S_T, FwdSaved(w, u, aqk, akk, h)
+    return o, S_T, FwdSaved(w, u, aqk, akk, h, qg, kg)
 
 
 @dataclass
@@ -152,7 +157,7 @@ def chunk_backward(
         w=_ptr(saved.w), u=_ptr(saved.u), aqk=_ptr(saved.aqk), akk=_ptr(saved.akk), h=_ptr(saved.h),
         do=_ptr(do), dht=_ptr(dht), dh=_ptr(dh), du=_ptr(du),
         dq=_ptr(dq), dk=_ptr(dk), dkw=_ptr(dkw), dv=_ptr(dv), dbeta=_ptr(dbeta), dgcum=_ptr(dgcum),
-        dh0=_ptr(dh0),
+        dh0=_ptr(dh0), qg=_ptr(saved.qg), kg=_ptr(saved.kg),
     )
     _lib.call("pkda_chunk_bwd", args, _stream(dev))
     return BwdGrads(dq, dk, dkw, dv, dbeta, dgcum, dh0)

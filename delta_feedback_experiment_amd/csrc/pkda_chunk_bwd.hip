@@ -59,6 +59,8 @@ struct BwdParams {
   float* dgcum;
   float* dh0;
   bool kw_is_k;
+  const void* qg;  // per-channel gates: s e^G q
+  const void* kg;  // per-channel gates: e^{G_last - G} kw
 };
 
 // Deterministic sum of one value per thread over an NT-thread workgroup.
@@ -108,10 +110,13 @@ struct StateBwdLayout {
   static constexpr int off_dOg = off_dO + C * LDV * (int)sizeof(T);   // [64][LDV]  s e^G dO
   static constexpr int off_dUn = off_dOg + C * LDV * (int)sizeof(T);  // [64][LDV]  -dU
   static constexpr int off_gam = off_dUn + C * LDV * (int)sizeof(T);
-  static constexpr int bytes = off_gam + C * 4;
+  static constexpr int off_gc = off_gam + C * 4;                       // [D] last-row G (per channel)
+  static constexpr int bytes = off_gc + D * 4;
 };
 
-template <typename T, int D, int BV>
+// PC: per-channel gate -- kg and qg come precomputed from the forward, no row
+// scaling applies and dS decays row by row.
+template <typename T, int D, int BV, bool PC>
 __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
   using L = StateBwdLayout<T, D, BV>;
   using E = T;
@@ -127,6 +132,7 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
   E* sdOg = reinterpret_cast<E*>(smem + L::off_dOg);
   E* sdUn = reinterpret_cast<E*>(smem + L::off_dUn);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
+  float* sGC = reinterpret_cast<float*>(smem + L::off_gc);
 
   const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
   const int H = p.H;
@@ -154,12 +160,16 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
     const int cstart = dstart + jc * C;
     const int clen = min(C, dlen - jc * C);
     const int64_t row0 = (int64_t)cstart * H + h;
-    rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, clen);
-    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, clen);
+    rKW.load(static_cast<const T*>(PC ? p.kg : p.kw) + row0 * D, gs, clen);
+    rQ.load(static_cast<const T*>(PC ? p.qg : p.q) + row0 * D, gs, clen);
     rW.load(static_cast<const T*>(p.w) + row0 * D, gs, clen);
     rA.load(static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
     rdO.load(static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen);
-    if (tid < C) rg = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
+    if (PC) {
+      if (tid < D) rg = p.gcum[((int64_t)(cstart + clen - 1) * H + h) * D + tid];
+    } else if (tid < C) {
+      rg = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
+    }
   };
   if (count > 0) prefetch(count - 1);
   const float scale = p.scale;
@@ -175,7 +185,11 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
     rW.store(sW, L::LD);
     rA.store(sAqk, L::LDC);
     rdO.store(sdO, L::LDV);
-    if (tid < C) sGam[tid] = rg;
+    if (PC) {
+      if (tid < D) sGC[tid] = rg;
+    } else if (tid < C) {
+      sGam[tid] = rg;
+    }
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
@@ -186,16 +200,18 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
     }
     __syncthreads();
     if (jc > 0) prefetch(jc - 1);
-    const float gC = sGam[C - 1];
+    const float gC = PC ? 0.f : sGam[C - 1];
     // s e^G dO (elementwise, for Q^T diag(s e^G) dO)
-    for (int i = tid; i < C * BV; i += kWG) {
-      const int r = i / BV, c = i - r * BV;
-      sdOg[r * L::LDV + c] = to_e<E>(scale * expf(sGam[r]) * from_e<E>(sdO[r * L::LDV + c]));
+    if (!PC) {
+      for (int i = tid; i < C * BV; i += kWG) {
+        const int r = i / BV, c = i - r * BV;
+        sdOg[r * L::LDV + c] = to_e<E>(scale * expf(sGam[r]) * from_e<E>(sdO[r * L::LDV + c]));
+      }
     }
     // dU = Aqk^T dO + diag(e^{G_C - G}) KW dS     wave w: rows 16w..16w+15
     float egc[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) egc[e] = expf(gC - sGam[r0 + acc_row(lane, e)]);
+    for (int e = 0; e < 4; ++e) egc[e] = PC ? 1.f : expf(gC - sGam[r0 + acc_row(lane, e)]);
     T* du_out = static_cast<T*>(p.du) + row0 * D + v0;
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
@@ -211,14 +227,19 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
       store_acc_global<T>(du_out, gs, du, r0, 16 * ct, clen, lane);
     }
     __syncthreads();
-    // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU
+    // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU   (per-channel: diag(e^{G_C}) dS + qg^T dO - W^T dU)
     const float decay = expf(gC);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
-      dS[i] = dS[i] * decay;
-      mma_tile<E, COL, ROW>(dS[i], sQ, L::LD, 16 * rt, sdOg, L::LDV, 16 * ct, C, lane);
+      if (PC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dS[i][j] *= expf(sGC[16 * rt + acc_row(lane, j)]);
+      } else {
+        dS[i] = dS[i] * decay;
+      }
+      mma_tile<E, COL, ROW>(dS[i], sQ, L::LD, 16 * rt, PC ? sdO : sdOg, L::LDV, 16 * ct, C, lane);
       mma_tile<E, COL, ROW>(dS[i], sW, L::LD, 16 * rt, sdUn, L::LDV, 16 * ct, C, lane);
     }
     __syncthreads();
@@ -512,6 +533,379 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// fused per-chunk backward, per-channel gate (G [64][D] per chunk).
+//
+// Same phases as the per-head kernel, with the decay inside every key
+// contraction:
+//   dq  = s e^G (dO S0^T) + sum_{x<=t} s dAqk[t,x] kw[x] e^{G[t]-G[x]}
+//   dk  = beta e^G (T^T dW) + beta_t sum_{x<t} dAkk[t,x] kw[x] e^{G[t]-G[x]}
+//   dkw = e^{G_C-G} (U dS_C^T) + sum_{t>x} beta_t dAkk[t,x] k[t] e^{G[t]-G[x]}
+//                              + sum_{t>=x} s dAqk[t,x] q[t] e^{G[t]-G[x]}
+// (channel by channel).  Pairs in different 16-row blocks go through MFMA
+// with the decay split at the block boundary -- every factor <= 1 -- and
+// pairs inside a block are summed exactly.  dG[t,c] = q dq + k dk - kw dkw
+// per element, plus e^{G_C[c]} sum_v S0[c,v] dS_C[c,v] + sum_t kg dkg on the
+// last row.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+struct FusedBwdPcLayout {
+  static constexpr int LD = D + Pad<T>::v;
+  static constexpr int LDC = C + Pad<T>::v;
+  static constexpr int LDG = D + 4;
+  static constexpr int RT = C * LD * (int)sizeof(T);
+  static constexpr int CT = C * LDC * (int)sizeof(T);
+  static constexpr int off_U = 0;                       // U, then V          } phase 4: G [64][LDG]
+  static constexpr int off_T = off_U + RT;              // T                  }   (then KW when D = 64)
+  static constexpr int off_dT = off_T + CT;             //                    }
+  static constexpr int off_X = off_dT + CT;             //                    }
+  static constexpr int off_dO = off_X + CT;             // dO, then Bw, then K
+  static constexpr int off_dU = off_dO + RT;            // dU
+  static constexpr int off_dW = off_dU + RT;            // dW, then P1r
+  static constexpr int off_H = off_dW + RT;             // h, dH; then Q (| KW at D = 128)
+  static constexpr int off_P2 = off_H + D * LD * (int)sizeof(T);
+  static constexpr int off_beta = off_P2 + CT;
+  static constexpr int off_hd = off_beta + C * 4;       // [D]
+  static constexpr int off_kg = off_hd + D * 4;         // [4][D]
+  static constexpr int off_red = off_kg + 4 * D * 4;    // [kFW]
+  static constexpr int bytes = off_red + kFW * 4;
+  static constexpr int G_BYTES = C * LDG * 4;
+  static constexpr int off_KW = D == 2 * C ? off_H + C * LD * (int)sizeof(T) : off_U + G_BYTES;
+  static_assert(G_BYTES <= off_dO, "G fits the U..X region");
+  static_assert(D == 2 * C || G_BYTES + RT <= off_dO, "KW fits after G");
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
+  using L = FusedBwdPcLayout<T, D>;
+  using E = T;
+  using F = FragK<E>;
+  constexpr int HCT = D / 32;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len <= 0) return;
+  const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int rb = wave & 3, ch = wave >> 2;
+  const int r0 = 16 * rb;
+  const int len = ci.len;
+  const int64_t gs = (int64_t)H * D;
+  const int64_t row0 = (int64_t)ci.start * H + hh;
+
+  E* sU = reinterpret_cast<E*>(smem + L::off_U);
+  E* sV = sU;
+  float* sG = reinterpret_cast<float*>(smem + L::off_U);
+  E* sT = reinterpret_cast<E*>(smem + L::off_T);
+  E* sdT = reinterpret_cast<E*>(smem + L::off_dT);
+  E* sX = reinterpret_cast<E*>(smem + L::off_X);
+  E* sdO = reinterpret_cast<E*>(smem + L::off_dO);
+  E* sK = sdO;  // Bw in phase 3, raw K in phase 4
+  E* sdU = reinterpret_cast<E*>(smem + L::off_dU);
+  E* sdW = reinterpret_cast<E*>(smem + L::off_dW);
+  E* sP1r = sdW;
+  E* sH = reinterpret_cast<E*>(smem + L::off_H);
+  E* sQ = sH;
+  E* sKW = reinterpret_cast<E*>(smem + L::off_KW);
+  E* sP2 = reinterpret_cast<E*>(smem + L::off_P2);
+  float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+  float* sHD = reinterpret_cast<float*>(smem + L::off_hd);
+  float* sKG = reinterpret_cast<float*>(smem + L::off_kg);
+  float* sRed = reinterpret_cast<float*>(smem + L::off_red);
+
+  const T* hsrc = static_cast<const T*>(p.h) + ((int64_t)cid * H + hh) * D * D;
+  const T* dhsrc = static_cast<const T*>(p.dh) + ((int64_t)cid * H + hh) * D * D;
+  const T* kg_ = static_cast<const T*>(p.k) + row0 * D;
+  const T* kwg = static_cast<const T*>(p.kw) + row0 * D;
+  const float* gg = p.gcum + row0 * D;        // G rows, stride gs
+  const float* gC = gg + (int64_t)(len - 1) * gs;
+  auto G = [&](int r, int c) { return gg[(int64_t)min(r, len - 1) * gs + c]; };
+  const float scale = p.scale;
+
+  if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
+  load_tile<kFW, C, D>(sU, L::LD, static_cast<const T*>(p.u) + row0 * D, gs, len, Ident());
+  load_tile<kFW, C, D>(sdO, L::LD, static_cast<const T*>(p.dO) + row0 * D, gs, len, Ident());
+  load_tile<kFW, C, D>(sdU, L::LD, static_cast<const T*>(p.du) + row0 * D, gs, len, Ident());
+  load_tile<kFW, D, D>(sH, L::LD, hsrc, D, D, Ident());
+  __syncthreads();
+
+  f32x4 dq[HCT], dk[HCT], dkw[HCT], dv[HCT], dkws[HCT];
+  // ---- phase 1: dQg, dW, dAqk ---------------------------------------------------
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    f32x4 acc = zero4();
+    mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dq[j][e] = scale * expf(G(r0 + acc_row(lane, e), c)) * acc[e];
+    f32x4 acw = zero4();
+    mma_tile<E, ROW, COL>(acw, sdU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
+    store_acc_lds(sdW, L::LD, -acw, r0, 16 * ct, lane);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ct = 2 * ch + j;
+    f32x4 acc = zero4();
+    if (ct <= rb) mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sU, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
+      sP2[t * L::LDC + s] = to_e<E>((s <= t && t < len) ? scale * acc[e] : 0.f);
+    }
+  }
+  __syncthreads();
+  // ---- phase 2: dH replaces h; per-row sum(h * dH) ----------------------------
+  {
+    constexpr int V = Vec16<T>::N;
+    constexpr int PER_ROW = D / V;  // consecutive threads of one row
+    static_assert(PER_ROW == 8 || PER_ROW == 16, "row of 8 or 16 vectors");
+    constexpr int TOTAL = D * PER_ROW;
+#pragma unroll
+    for (int i = 0; i < (TOTAL + kFW - 1) / kFW; ++i) {
+      const int idx = tid + i * kFW;
+      const int r = idx / PER_ROW, c = (idx - r * PER_ROW) * V;
+      float part = 0.f;
+      if (idx < TOTAL) {
+        float x[V], hv[V];
+        Vec16<T>::load(dhsrc + r * D + c, x);
+        lds_vec<V>(sH + r * L::LD + c, hv);
+#pragma unroll
+        for (int j = 0; j < V; ++j) part += hv[j] * x[j];
+        store_vec<V>(sH + r * L::LD + c, x);
+      }
+#pragma unroll
+      for (int off = 1; off < PER_ROW; off <<= 1) part += __shfl_xor(part, off);
+      if (idx < TOTAL && (lane & (PER_ROW - 1)) == 0) sHD[r] = part;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    f32x4 acc = zero4();
+    mma_tile<E, ROW, COL>(acc, sU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
+    float col = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = r0 + acc_row(lane, e);
+      dkws[j][e] = expf(gC[c] - G(s, c)) * acc[e];
+      if (s < len) col += io<T>::load(kwg + s * gs + c) * dkws[j][e];
+    }
+    col += __shfl_xor(col, 16);
+    col += __shfl_xor(col, 32);
+    if (lane < 16) sKG[rb * D + 16 * ct + lane] = col;
+  }
+  __syncthreads();
+  // ---- phase 3: WY backward ----------------------------------------------------
+  load_tile<kFW, C, D>(sV, L::LD, static_cast<const T*>(p.v) + row0 * D, gs, len, Ident());
+  load_tile<kFW, C, D>(sK, L::LD, kg_, gs, len,
+                       [&](int r, int c, float x) { return sBeta[r] * expf(G(r, c)) * x; });  // Bw
+  load_tile<kFW, C, C>(sT, L::LDC, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len, Ident());
+  load_tile<kFW, C, D>(sQ, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, len, Ident());
+  if (!p.kw_is_k && D == 2 * C) load_tile<kFW, C, D>(sKW, L::LD, kwg, gs, len, Ident());
+  __syncthreads();
+  const int kbeg = kfloor<E>(r0);
+  float db[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    f32x4 acc = zero4();
+    mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdW, L::LD, 16 * ct, kbeg, C, lane);  // dBw = T^T dW
+    f32x4 acv = zero4();
+    mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = r0 + acc_row(lane, e);
+      const float eg = expf(G(s, c));
+      const float kv = s < len ? io<T>::load(kg_ + s * gs + c) : 0.f;
+      const float vv = from_e<E>(sV[s * L::LD + c]);
+      dk[j][e] = sBeta[s] * eg * acc[e];
+      dv[j][e] = sBeta[s] * acv[e];
+      db[e] += acc[e] * eg * kv + acv[e] * vv;
+    }
+  }
+  // dT = dW Bw^T + (dU V^T) diag(beta)
+  f32x4 dTacc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ct = 2 * ch + j;
+    f32x4 a1 = zero4(), a2 = zero4();
+    mma_tile<E, ROW, COL>(a1, sdW, L::LD, r0, sK, L::LD, 16 * ct, D, lane);
+    mma_tile<E, ROW, COL>(a2, sdU, L::LD, r0, sV, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dTacc[j][e] = a1[e] + sBeta[16 * ct + acc_col(lane)] * a2[e];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) store_acc_lds(sdT, L::LDC, dTacc[j], r0, 16 * (2 * ch + j), lane);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ct = 2 * ch + j;
+    f32x4 acc = zero4();
+    mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdT, L::LDC, 16 * ct, kbeg, C, lane);  // X = T^T dT
+    store_acc_lds(sX, L::LDC, acc, r0, 16 * ct, lane);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ct = 2 * ch + j;
+    f32x4 acc = zero4();
+    if (ct <= rb) mma_tile_range<E, ROW, COL>(acc, sX, L::LDC, r0, sT, L::LDC, 16 * ct, 0, kceil<E>(16 * ct + 16), lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
+      const float raw = (s < t && t < len) ? -acc[e] : 0.f;  // dAkk
+      sP1r[t * L::LDC + s] = to_e<E>(raw);
+    }
+  }
+  __syncthreads();
+  // ---- phase 4: pairwise terms with the decay inside the contraction ----------
+  // dAkk is held once (unscaled); beta_t multiplies the other factor, so the
+  // two halves of each (t, x) pair's gate term see the same rounded value.
+  load_tile<kFW, C, D>(sK, L::LD, kg_, gs, len, Ident());
+  for (int i = tid; i < C * (D / 4); i += kFW) {
+    const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
+    *reinterpret_cast<float4*>(sG + r * L::LDG + c) =
+        *reinterpret_cast<const float4*>(gg + (int64_t)min(r, len - 1) * gs + c);
+  }
+  if (!p.kw_is_k && D != 2 * C) load_tile<kFW, C, D>(sKW, L::LD, kwg, gs, len, Ident());
+  __syncthreads();
+  const E* sKWr = p.kw_is_k ? sK : sKW;
+  const int rlo = r0 - 1;   // last row before this row block (G[-1] = 0)
+  const int rhi = r0 + 15;  // last row of this row block
+  float gsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    const int nn = 16 * ct + (lane & 15);  // this lane's B column
+    // (a) rows t of this block, x in earlier blocks: split at rlo
+    f32x4 akA = zero4(), aqP = zero4();
+    if (rb > 0) {
+      const float grlo = sG[rlo * L::LDG + nn];
+      for (int k0 = 0; k0 < kceil<E>(r0); k0 += Mma<E>::KS) {
+        const int kk = k0 + F::off(lane);
+        float a1[F::N], a2[F::N], bx[F::N];
+#pragma unroll
+        for (int jj = 0; jj < F::N; ++jj) {
+          const int x = kk + jj;
+          a1[jj] = from_e<E>(sP1r[(r0 + (lane & 15)) * L::LDC + x]);
+          a2[jj] = from_e<E>(sP2[(r0 + (lane & 15)) * L::LDC + x]);
+          bx[jj] = x <= rlo ? from_e<E>(sKWr[x * L::LD + nn]) * expf(grlo - sG[x * L::LDG + nn]) : 0.f;
+        }
+        F::mfma(akA, a1, bx);
+        F::mfma(aqP, a2, bx);
+      }
+    }
+    // (c) rows x of this block, t in later blocks: split at rhi
+    f32x4 awA = zero4(), awP = zero4();
+    if (rb < 3) {
+      const float grhi = sG[rhi * L::LDG + nn];
+      for (int k0 = kfloor<E>(r0 + 16); k0 < C; k0 += Mma<E>::KS) {
+        const int kk = k0 + F::off(lane);
+        float a1[F::N], a2[F::N], b1[F::N], b2[F::N];
+#pragma unroll
+        for (int jj = 0; jj < F::N; ++jj) {
+          const int t = kk + jj;
+          a1[jj] = from_e<E>(sP1r[t * L::LDC + r0 + (lane & 15)]);
+          a2[jj] = from_e<E>(sP2[t * L::LDC + r0 + (lane & 15)]);
+          const float f = t > rhi ? expf(sG[t * L::LDG + nn] - grhi) : 0.f;
+          b1[jj] = sBeta[t] * from_e<E>(sK[t * L::LD + nn]) * f;  // beta_t on the key, dAkk unscaled
+          b2[jj] = from_e<E>(sQ[t * L::LD + nn]) * f;
+        }
+        F::mfma(awA, a1, b1);
+        F::mfma(awP, a2, b2);
+      }
+    }
+    // split factors back onto the output rows, plus the in-block pairs exactly
+    const float grlo_c = rb > 0 ? sG[rlo * L::LDG + c] : 0.f;
+    const float grhi_c = sG[rhi * L::LDG + c];
+    float gr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gr[e] = sG[(r0 + acc_row(lane, e)) * L::LDG + c];
+      akA[e] *= expf(gr[e] - grlo_c);
+      aqP[e] *= expf(gr[e] - grlo_c);
+      awA[e] *= expf(grhi_c - gr[e]);
+      awP[e] *= expf(grhi_c - gr[e]);
+    }
+    for (int xo = 0; xo < 16; ++xo) {
+      const int x = r0 + xo;
+      const float gx = sG[x * L::LDG + c];
+      const float kwx = from_e<E>(sKWr[x * L::LD + c]);
+      const float kx = from_e<E>(sK[x * L::LD + c]);
+      const float qx = from_e<E>(sQ[x * L::LD + c]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r0 + acc_row(lane, e);
+        if (x <= r) {  // x as the column of row r
+          const float ex = expf(gr[e] - gx);
+          if (x < r) akA[e] += from_e<E>(sP1r[r * L::LDC + x]) * kwx * ex;
+          aqP[e] += from_e<E>(sP2[r * L::LDC + x]) * kwx * ex;
+        }
+        if (x >= r) {  // x as the row, r as the column
+          const float ex = expf(gx - gr[e]);
+          if (x > r) awA[e] += sBeta[x] * from_e<E>(sP1r[x * L::LDC + r]) * kx * ex;
+          awP[e] += from_e<E>(sP2[x * L::LDC + r]) * qx * ex;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + acc_row(lane, e);
+      const float kv = from_e<E>(sK[r * L::LD + c]);
+      const float qv = from_e<E>(sQ[r * L::LD + c]);
+      const float wv = from_e<E>(sKWr[r * L::LD + c]);
+      dk[j][e] += sBeta[r] * akA[e];
+      db[e] += kv * akA[e];
+      dq[j][e] += aqP[e];
+      dkw[j][e] = dkws[j][e] + awA[e] + awP[e];
+    }
+  }
+  // ---- outputs -------------------------------------------------------------
+  float* dqo = p.dq + row0 * D;
+  float* dko = p.dk + row0 * D;
+  float* dvo = p.dv + row0 * D;
+  float* dgo = p.dgcum + row0 * D;
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    float kgc = 0.f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) kgc += sKG[b * D + c];
+    f32x4 dg;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + acc_row(lane, e);
+      const float kv = from_e<E>(sK[r * L::LD + c]);
+      const float qv = from_e<E>(sQ[r * L::LD + c]);
+      const float wv = from_e<E>(sKWr[r * L::LD + c]);
+      dg[e] = qv * dq[j][e] + kv * dk[j][e] - wv * dkw[j][e];
+      if (r == len - 1) dg[e] += expf(gC[c]) * sHD[c] + kgc;
+    }
+    store_acc_global<float>(dgo, gs, dg, r0, 16 * ct, len, lane);
+    store_acc_global<float>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
+    store_acc_global<float>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
+    if (p.kw_is_k) {
+      store_acc_global<float>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
+    } else {
+      store_acc_global<float>(dko, gs, dk[j], r0, 16 * ct, len, lane);
+      store_acc_global<float>(p.dkw + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
+    }
+  }
+  float* sRowB = sRed;  // [2][64]
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float b = group16_sum(db[e]);
+    if ((lane & 15) == 0) sRowB[ch * C + r0 + acc_row(lane, e)] = b;
+  }
+  __syncthreads();
+  if (tid < len) p.dbeta[(int64_t)(ci.start + tid) * H + hh] = sRowB[tid] + sRowB[C + tid];
+}
+
 template <typename K>
 int set_smem(K kernel, int bytes) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -528,7 +922,7 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const int N = p.geom.num_seqs;
   const bool all = stages == 0;
   if (all || (stages & PKDA_STAGE_BWD_STATE)) {
-    auto kern = chunk_state_bwd_kernel<T, D, BV>;
+    auto kern = p.qg ? chunk_state_bwd_kernel<T, D, BV, true> : chunk_state_bwd_kernel<T, D, BV, false>;
     const int bytes = StateBwdLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     if (N > 0) hipLaunchKernelGGL(kern, dim3(N, p.H, D / BV), dim3(kWG), bytes, s, p);
@@ -536,8 +930,8 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   }
   if (num_chunks == 0) return 0;
   if (all || (stages & PKDA_STAGE_BWD_CHUNK)) {
-    auto kern = chunk_fused_bwd_kernel<T, D>;
-    const int bytes = FusedBwdLayout<T, D>::bytes;
+    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D> : chunk_fused_bwd_kernel<T, D>;
+    const int bytes = p.qg ? FusedBwdPcLayout<T, D>::bytes : FusedBwdLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kFW), bytes, s, p);
     if (int st = launch_status("pkda_chunk_bwd(chunk)")) return st;
@@ -558,7 +952,7 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   PKDA_REQUIRE(!(a->dtype == PKDA_F32 && a->head_dim == 128), PKDA_EUNSUPPORTED,
                "the FP32 chunked backward is built for head_dim 64 only");
   PKDA_REQUIRE(a->heads > 0, PKDA_EINVAL, "heads");
-  PKDA_REQUIRE(!a->gate_per_channel, PKDA_EUNSUPPORTED, "per-channel gates are not in this chunked build");
+  PKDA_REQUIRE(!a->gate_per_channel || (a->qg && a->kg), PKDA_EINVAL, "per-channel gates need the forward's qg and kg");
   BwdParams p;
   if (int st = chunk_geom_from(a->cu_seqlens, a->num_seqs, a->seqlen, a->num_chunks, a->table, p.geom)) return st;
   if (a->num_seqs == 0) return 0;
@@ -576,6 +970,8 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   p.dO = a->do_; p.dht = a->dht; p.dh = a->dh; p.du = a->du;
   p.dq = a->dq; p.dk = a->dk; p.dkw = a->dkw; p.dv = a->dv; p.dbeta = a->dbeta; p.dgcum = a->dgcum; p.dh0 = a->dh0;
   p.kw_is_k = kw_is_k;
+  p.qg = a->gate_per_channel ? a->qg : nullptr;
+  p.kg = a->gate_per_channel ? a->kg : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   if (a->dtype == PKDA_BF16) {

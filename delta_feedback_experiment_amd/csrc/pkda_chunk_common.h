@@ -162,6 +162,32 @@ __device__ __forceinline__ void mma_tile_range(f32x4& acc, const E* A, int lda, 
   for (int k0 = kb; k0 < ke; k0 += Mma<E>::KS) Mma<E>::template step<LA, LB>(acc, a, lda, b, ldb, k0, lane);
 }
 
+// One lane's operand elements of a 16x16 MFMA k-step whose k index is
+// contiguous in memory (N consecutive k from off(lane)), and the MFMA on
+// operands given as floats.
+template <typename E> struct FragK;
+template <> struct FragK<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static int off(int lane) { return 8 * (lane >> 4); }
+  __device__ __forceinline__ static void mfma(f32x4& acc, const float* a, const float* b) {
+    s16x8_t av, bv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      av[j] = static_cast<short>(f32_to_bf16(a[j]));
+      bv[j] = static_cast<short>(f32_to_bf16(b[j]));
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                  acc, 0, 0, 0);
+  }
+};
+template <> struct FragK<float> {
+  static constexpr int N = 1;
+  __device__ __forceinline__ static int off(int lane) { return lane >> 4; }
+  __device__ __forceinline__ static void mfma(f32x4& acc, const float* a, const float* b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+  }
+};
+
 // Round x down / up to a multiple of the MFMA k-step of E.
 template <typename E> __device__ __forceinline__ int kfloor(int x) { return x / Mma<E>::KS * Mma<E>::KS; }
 template <typename E> __device__ __forceinline__ int kceil(int x) {

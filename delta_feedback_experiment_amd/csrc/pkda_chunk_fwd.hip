@@ -46,6 +46,8 @@ struct FwdParams {
   void* aqk;
   void* akk;
   void* h;
+  void* qg;   // per-channel gates: s e^G q
+  void* kg;   // per-channel gates: e^{G_last - G} kw
 };
 
 // ---------------------------------------------------------------------------
@@ -269,6 +271,203 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   store_tile<kIW, C, D>(static_cast<T*>(p.u) + row0 * D, gs, sQ, L::LD, len);
 }
 // ---------------------------------------------------------------------------
+// intra-chunk forward, per-channel gate (G [64][D] per chunk).
+//   Akk[t,s] = beta_t sum_c k[t,c] kw[s,c] e^{G[t,c]-G[s,c]},  Aqk likewise
+//   with s q.  For a block of rows tb and columns sb < tb the decay is split
+//   at r = 16 tb - 1, the last row before the row block:
+//     e^{G[t]-G[s]} = e^{G[t]-G[r]} e^{G[r]-G[s]},  both factors <= 1,
+//   applied to the MFMA operands as they are read (no overflow for any gate).
+//   The four diagonal blocks are summed exactly, one (t, s) pair per lane.
+//   Also writes qg = s e^G q and kg = e^{G_last - G} kw for the state pass.
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool ALIAS>
+struct IntraPcLayout {
+  static constexpr int LD = D + Pad<T>::v;
+  static constexpr int LDC = C + Pad<T>::v;
+  static constexpr int LDF = C + 4;
+  static constexpr int LDG = D + 4;
+  static constexpr int RT = C * LD * (int)sizeof(T);
+  static constexpr int SCR = 4 * 3 * 16 * SLD * 4;
+  static constexpr int QR = RT > SCR ? RT : SCR;
+  static constexpr int off_K = 0;                          // K, then Bw, then W
+  static constexpr int off_Q = off_K + RT;                 // Q, then solve scratch, then Bv, then u
+  static constexpr int off_KW = off_Q + QR;                // KW (when not aliased to K)
+  static constexpr int off_G = off_KW + (ALIAS ? 0 : RT);  // fp32 [64][LDG]
+  static constexpr int off_A = off_G + C * LDG * 4;        // fp32 [64][LDF]: Akk, then T
+  static constexpr int off_Te = off_A + C * LDF * 4;
+  static constexpr int off_Aqk = off_Te + C * LDC * (int)sizeof(T);
+  static constexpr int off_beta = off_Aqk + C * LDC * (int)sizeof(T);
+  static constexpr int bytes = off_beta + C * 4;
+};
+
+template <typename T, int D, bool ALIAS>
+__global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
+  using L = IntraPcLayout<T, D, ALIAS>;
+  using E = T;
+  using F = FragK<E>;
+  constexpr int HCT = D / 32;
+  constexpr int V = Vec16<T>::N;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len <= 0) return;
+  const int h = blockIdx.y;
+  const int H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int len = ci.len;
+  const int64_t row0 = (int64_t)ci.start * H + h;
+  const int64_t gs = (int64_t)H * D;
+
+  E* sK = reinterpret_cast<E*>(smem + L::off_K);
+  E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
+  E* sKW = ALIAS ? sK : reinterpret_cast<E*>(smem + L::off_KW);
+  float* sG = reinterpret_cast<float*>(smem + L::off_G);
+  float* sA = reinterpret_cast<float*>(smem + L::off_A);
+  E* sTe = reinterpret_cast<E*>(smem + L::off_Te);
+  E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
+  float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+
+  const T* q = static_cast<const T*>(p.q) + row0 * D;
+  const T* k = static_cast<const T*>(p.k) + row0 * D;
+  const T* kw = static_cast<const T*>(p.kw) + row0 * D;
+  const T* v = static_cast<const T*>(p.v) + row0 * D;
+  const float* g = p.gcum + row0 * D;
+
+  if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + h] : 0.f;
+  load_tile<kIW, C, D>(sK, L::LD, k, gs, len, Ident());
+  load_tile<kIW, C, D>(sQ, L::LD, q, gs, len, Ident());
+  if (!ALIAS) load_tile<kIW, C, D>(sKW, L::LD, kw, gs, len, Ident());
+  // G rows past the end repeat the last row (G is non-increasing in t, so
+  // every split factor stays <= 1 there too)
+  for (int i = tid; i < C * (D / 4); i += kIW) {
+    const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
+    *reinterpret_cast<float4*>(sG + r * L::LDG + c) =
+        *reinterpret_cast<const float4*>(g + (int64_t)min(r, len - 1) * gs + c);
+  }
+  for (int i = tid; i < C * C; i += kIW) {
+    const int r = i / C, c = i - r * C;
+    sA[r * L::LDF + c] = 0.f;
+    sAqk[r * L::LDC + c] = to_e<E>(0.f);
+  }
+  __syncthreads();
+
+  if (wave < 4) {
+    // ---- diagonal block tb = wave, exactly: one (t, s) pair, s <= t, per lane --
+    const int tb = wave;
+    for (int pr = lane; pr < 136; pr += 64) {
+      int tl = 0, rest = pr;
+      while (rest > tl) {
+        rest -= tl + 1;
+        ++tl;
+      }
+      const int t = 16 * tb + tl, s = 16 * tb + rest;
+      float akk = 0.f, aqk = 0.f;
+      for (int c = 0; c < D; c += V) {
+        float kx[V], qx[V], wx[V];
+        lds_vec<V>(sK + t * L::LD + c, kx);
+        lds_vec<V>(sQ + t * L::LD + c, qx);
+        lds_vec<V>(sKW + s * L::LD + c, wx);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const float e = expf(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
+          akk += kx[j] * wx[j] * e;
+          aqk += qx[j] * wx[j] * e;
+        }
+      }
+      sA[t * L::LDF + s] = (s < t && t < len) ? sBeta[t] * akk : 0.f;
+      sAqk[t * L::LDC + s] = to_e<E>(t < len ? p.scale * aqk : 0.f);
+    }
+  } else {
+    // ---- off-diagonal blocks (tb > sb) with the split decay --------------------
+    for (int blk = wave - 4; blk < 6; blk += 4) {
+      const int tb = blk < 1 ? 1 : blk < 3 ? 2 : 3;
+      const int sb = blk - (tb - 1) * tb / 2;
+      const int r = 16 * tb - 1;
+      const int t = 16 * tb + (lane & 15), s = 16 * sb + (lane & 15);
+      f32x4 akk = zero4(), aqk = zero4();
+      for (int k0 = 0; k0 < D; k0 += Mma<E>::KS) {
+        const int kk = k0 + F::off(lane);
+        float ak[F::N], aq[F::N], bw[F::N];
+#pragma unroll
+        for (int j = 0; j < F::N; ++j) {
+          const float gr = sG[r * L::LDG + kk + j];
+          const float fa = expf(sG[t * L::LDG + kk + j] - gr);
+          const float fb = expf(gr - sG[s * L::LDG + kk + j]);
+          ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
+          aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
+          bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
+        }
+        F::mfma(akk, ak, bw);
+        F::mfma(aqk, aq, bw);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tt = 16 * tb + acc_row(lane, e), ss = 16 * sb + acc_col(lane);
+        sA[tt * L::LDF + ss] = tt < len ? sBeta[tt] * akk[e] : 0.f;
+        sAqk[tt * L::LDC + ss] = to_e<E>(tt < len ? p.scale * aqk[e] : 0.f);
+      }
+    }
+  }
+  // ---- qg = s e^G q and kg = e^{G_last - G} kw, straight to global -----------
+  T* qg_out = static_cast<T*>(p.qg) + row0 * D;
+  T* kg_out = static_cast<T*>(p.kg) + row0 * D;
+  for (int i = tid; i < C * (D / V); i += kIW) {
+    const int r = i / (D / V), c = (i - r * (D / V)) * V;
+    if (r < len) {
+      float qx[V], wx[V];
+      lds_vec<V>(sQ + r * L::LD + c, qx);
+      lds_vec<V>(sKW + r * L::LD + c, wx);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float gv = sG[r * L::LDG + c + j];
+        qx[j] *= p.scale * expf(gv);
+        wx[j] *= expf(sG[(C - 1) * L::LDG + c + j] - gv);
+      }
+      store_vec<V>(qg_out + r * gs + c, qx);
+      store_vec<V>(kg_out + r * gs + c, wx);
+    }
+  }
+  __syncthreads();
+
+  // ---- T = (I + Akk)^-1 in place; Aqk leaves meanwhile ------------------------
+  store_tile<kIW, C, C>(static_cast<T*>(p.aqk) + row0 * C, (int64_t)H * C, sAqk, L::LDC, len);
+  solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
+  for (int i = tid; i < C * C; i += kIW) {
+    const int r = i / C, c = i - r * C;
+    sTe[r * L::LDC + c] = to_e<E>(sA[r * L::LDF + c]);
+  }
+  // Bw = diag(beta) (e^G * K) in place over K; Bv = diag(beta) V over Q
+  for (int i = tid; i < C * D; i += kIW) {
+    const int r = i / D, c = i - r * D;
+    sK[r * L::LD + c] = to_e<E>(sBeta[r] * expf(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+  }
+  load_tile<kIW, C, D>(sQ, L::LD, v, gs, len, RowScale{sBeta});
+  __syncthreads();
+  store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
+
+  const int rb = wave & 3, ch = wave >> 2;
+  const int kend = kceil<E>(16 * rb + 16);
+  f32x4 aw[HCT], au[HCT];
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    aw[j] = zero4();
+    au[j] = zero4();
+    mma_tile_range<E, ROW, ROW>(aw[j], sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
+    mma_tile_range<E, ROW, ROW>(au[j], sTe, L::LDC, 16 * rb, sQ, L::LD, 16 * ct, 0, kend, lane);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    store_acc_lds(sK, L::LD, aw[j], 16 * rb, 16 * ct, lane);
+    store_acc_lds(sQ, L::LD, au[j], 16 * rb, 16 * ct, lane);
+  }
+  __syncthreads();
+  store_tile<kIW, C, D>(static_cast<T*>(p.w) + row0 * D, gs, sK, L::LD, len);
+  store_tile<kIW, C, D>(static_cast<T*>(p.u) + row0 * D, gs, sQ, L::LD, len);
+}
+
+// ---------------------------------------------------------------------------
 // per-document state pass
 //
 // One workgroup per (document, head, BV value columns).  The FP32 state slice
@@ -297,10 +496,13 @@ struct StateLayout {
   static constexpr int off_U = off_Uin + C * LDV * (int)sizeof(T);    // [64][LDV]  U
   static constexpr int off_Ug = off_U + C * LDV * (int)sizeof(T);     // [64][LDV]  e^{G_C-G} U
   static constexpr int off_gam = off_Ug + C * LDV * (int)sizeof(T);
-  static constexpr int bytes = off_gam + C * 4;
+  static constexpr int off_gc = off_gam + C * 4;                      // [D] last-row G (per channel)
+  static constexpr int bytes = off_gc + D * 4;
 };
 
-template <typename T, int D, int BV>
+// PC: per-channel gate.  The forward intra kernel wrote qg = s e^G q and
+// kg = e^{G_last - G} kw, so no row scaling applies and S decays row by row.
+template <typename T, int D, int BV, bool PC>
 __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
   using L = StateLayout<T, D, BV>;
   using E = T;
@@ -316,6 +518,7 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
   E* sU = reinterpret_cast<E*>(smem + L::off_U);
   E* sUg = reinterpret_cast<E*>(smem + L::off_Ug);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
+  float* sGC = reinterpret_cast<float*>(smem + L::off_gc);
 
   const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
   const int H = p.H;
@@ -345,11 +548,15 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
     const int clen = min(C, dlen - jc * C);
     const int64_t row0 = (int64_t)cstart * H + h;
     rW.load(static_cast<const T*>(p.w) + row0 * D, gs, clen);
-    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, clen);
-    rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+    rQ.load(static_cast<const T*>(PC ? p.qg : p.q) + row0 * D, gs, clen);
+    rKW.load(static_cast<const T*>(PC ? p.kg : p.kw) + row0 * D, gs, clen);
     rA.load(static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
     rU.load(static_cast<const T*>(p.u) + row0 * D + v0, gs, clen);
-    if (tid < C) rg = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
+    if (PC) {
+      if (tid < D) rg = p.gcum[((int64_t)(cstart + clen - 1) * H + h) * D + tid];
+    } else if (tid < C) {
+      rg = p.gcum[(int64_t)(cstart + min(tid, clen - 1)) * H + h];
+    }
   };
   if (count > 0) prefetch(0);
   const float scale = p.scale;
@@ -366,7 +573,11 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
     rKW.store(sKW, L::LD);
     rA.store(sAqk, L::LDC);
     rU.store(sUin, L::LDV);
-    if (tid < C) sGam[tid] = rg;
+    if (PC) {
+      if (tid < D) sGC[tid] = rg;
+    } else if (tid < C) {
+      sGam[tid] = rg;
+    }
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
@@ -379,13 +590,18 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
     }
     __syncthreads();
     if (jc + 1 < count) prefetch(jc + 1);
-    const float gC = sGam[C - 1];  // padded rows repeat the last valid gate
+    const float gC = PC ? 0.f : sGam[C - 1];  // padded rows repeat the last valid gate
     float eg[4], egc[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float g = sGam[r0 + acc_row(lane, e)];
-      eg[e] = scale * expf(g);
-      egc[e] = expf(gC - g);
+      if (PC) {
+        eg[e] = 1.f;
+        egc[e] = 1.f;
+      } else {
+        const float g = sGam[r0 + acc_row(lane, e)];
+        eg[e] = scale * expf(g);
+        egc[e] = expf(gC - g);
+      }
     }
     // U = u - W S
     T* u_io = static_cast<T*>(p.u) + row0 * D + v0;
@@ -399,7 +615,7 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
         const int r = r0 + acc_row(lane, e), c = 16 * ct + acc_col(lane);
         U[e] = from_e<E>(sUin[r * L::LDV + c]) - acc[e];
         sU[r * L::LDV + c] = to_e<E>(U[e]);
-        sUg[r * L::LDV + c] = to_e<E>(egc[e] * U[e]);
+        if (!PC) sUg[r * L::LDV + c] = to_e<E>(egc[e] * U[e]);
       }
       store_acc_global<T>(u_io, gs, U, r0, 16 * ct, clen, lane);
     }
@@ -417,14 +633,19 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
       for (int e = 0; e < 4; ++e) o[e] = eg[e] * a1[e] + a2[e];
       store_acc_global<T>(o_out, gs, o, r0, 16 * ct, clen, lane);
     }
-    // S <- e^{G_C} S + KW^T Ug
+    // S <- e^{G_C} S + KW^T Ug   (per-channel: diag(e^{G_C}) S + kg^T U)
     const float decay = expf(gC);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
-      S[i] = S[i] * decay;
-      mma_tile<E, COL, ROW>(S[i], sKW, L::LD, 16 * rt, sUg, L::LDV, 16 * ct, C, lane);
+      if (PC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S[i][j] *= expf(sGC[16 * rt + acc_row(lane, j)]);
+      } else {
+        S[i] = S[i] * decay;
+      }
+      mma_tile<E, COL, ROW>(S[i], sKW, L::LD, 16 * rt, PC ? sU : sUg, L::LDV, 16 * ct, C, lane);
     }
     __syncthreads();
   }
@@ -455,14 +676,16 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const bool all = stages == 0;
   if (all || (stages & PKDA_STAGE_FWD_INTRA)) {
     const bool alias = p.kw == p.k;
-    auto kern = alias ? chunk_intra_fwd_kernel<T, D, true> : chunk_intra_fwd_kernel<T, D, false>;
-    const int bytes = alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes;
+    auto kern = p.qg ? (alias ? chunk_intra_fwd_pc_kernel<T, D, true> : chunk_intra_fwd_pc_kernel<T, D, false>)
+                     : (alias ? chunk_intra_fwd_kernel<T, D, true> : chunk_intra_fwd_kernel<T, D, false>);
+    const int bytes = p.qg ? (alias ? IntraPcLayout<T, D, true>::bytes : IntraPcLayout<T, D, false>::bytes)
+                           : (alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes);
     if (int st = set_smem(kern, bytes)) return st;
     if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kIW), bytes, s, p);
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
   }
   if (all || (stages & PKDA_STAGE_FWD_STATE)) {
-    auto kern = chunk_state_fwd_kernel<T, D, BV>;
+    auto kern = p.qg ? chunk_state_fwd_kernel<T, D, BV, true> : chunk_state_fwd_kernel<T, D, BV, false>;
     const int bytes = StateLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     if (p.geom.num_seqs > 0) hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(kWG), bytes, s, p);
@@ -498,7 +721,9 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   PKDA_REQUIRE(a->dtype == PKDA_F32 || a->dtype == PKDA_BF16, PKDA_EUNSUPPORTED, "dtype %d", a->dtype);
   PKDA_REQUIRE(a->head_dim == 64 || a->head_dim == 128, PKDA_EUNSUPPORTED, "chunked head_dim %d (64, 128)", a->head_dim);
   PKDA_REQUIRE(a->heads > 0, PKDA_EINVAL, "heads");
-  PKDA_REQUIRE(!a->gate_per_channel, PKDA_EUNSUPPORTED, "per-channel gates are not in this chunked build");
+  PKDA_REQUIRE(!a->gate_per_channel || (a->qg && a->kg), PKDA_EINVAL, "per-channel gates need the qg and kg outputs");
+  PKDA_REQUIRE(!a->gate_per_channel || a->dtype == PKDA_BF16 || a->head_dim == 64, PKDA_EUNSUPPORTED,
+               "FP32 per-channel chunked forward is built for head_dim 64 only");
   FwdParams p;
   if (int st = chunk_geom_from(a->cu_seqlens, a->num_seqs, a->seqlen, a->num_chunks, a->table, p.geom)) return st;
   if (a->num_seqs == 0) return 0;
@@ -509,6 +734,8 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   p.gcum = a->gcum; p.beta = a->beta; p.scale = a->scale;
   p.s0 = a->initial_state; p.sT = a->final_state; p.o = a->o;
   p.w = a->w; p.u = a->u; p.aqk = a->aqk; p.akk = a->akk; p.h = a->h;
+  p.qg = a->gate_per_channel ? a->qg : nullptr;
+  p.kg = a->gate_per_channel ? a->kg : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   const int st = a->stages;

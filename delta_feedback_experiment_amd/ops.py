@@ -29,9 +29,10 @@ SAVED_ALWAYS = ("k_write", "a_chunk")
 """Saved by every forward: the preconditioned write keys and the
 preconditioner state entering each chunk."""
 
-SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h")
+SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h", "qg", "kg")
 """Saved as well unless ``lean``: W, the corrected values U, the intra-chunk
-query-key products, the inverted WY matrix and the chunk-entry states."""
+query-key products, the inverted WY matrix, the chunk-entry states and the
+gated query and write key."""
 
 
 def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int, ...], torch.dtype], ...]:
@@ -52,6 +53,8 @@ def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int
             ((ntok, H, CHUNK_SIZE), act),         # Aqk
             ((ntok, H, CHUNK_SIZE), act),         # T
             ((B * chunks, H, K, V), act),         # h
+            ((ntok, H, K), act),                  # qg
+            ((ntok, H, K), act),                  # kg
         ]
     return tuple(meta)
 
@@ -118,7 +121,7 @@ def pkda_recurrence(
             save_all=not lean)
     saved = [pstate.kw, pstate.a_chunk]
     if not lean:
-        saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h]
+        saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h, fs.qg, fs.kg]
     _check_saved(saved, q, v, lean)
     return o.reshape(*q.shape[:3], v.shape[-1]).to(q.dtype), saved
 
@@ -154,7 +157,7 @@ def pkda_recurrence_backward(
         if lean:
             _, _, fs = chunk_forward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, False, save_states=True)
         else:
-            fs = FwdSaved(*saved[2:7])
+            fs = FwdSaved(*saved[2:9])
         dof = flat(do.to(q.dtype))
         gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False)
         pstate = pre.PrecondState(kw, a_chunk, None, None)

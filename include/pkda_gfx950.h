@@ -255,6 +255,13 @@ enum pkda_chunk_stage {
  * Saved for the backward (all [N_tok, H, *] in dtype unless stated):
  * w, u (overwritten with U), aqk [.., 64], akk (= T) [.., 64],
  * h [num_chunks, H, K, V] (state entering each chunk; NULL when not training).
+ * Per-channel gates (gate_per_channel != 0, gcum [N_tok, H, K]): the decay
+ * sits inside every key contraction.  Pairs of tokens in different 16-token
+ * sub-blocks are products of operands each scaled by a decay <= 1 relative
+ * to the last token before the row's sub-block (no overflow for any gate);
+ * pairs inside one sub-block are summed exactly, channel by channel.  The
+ * gated operands qg = scale e^G q and kg = e^{G_last - G} kw [N_tok, H, K]
+ * (dtype) are written for the state pass and the backward.
  * ------------------------------------------------------------------------- */
 typedef struct pkda_chunk_fwd_args {
   int32_t struct_size;
@@ -273,6 +280,7 @@ typedef struct pkda_chunk_fwd_args {
   void* o;
   void *w, *u, *aqk, *akk, *h;
   int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
+  void *qg, *kg;               /* per-channel gates only, else NULL */
 } pkda_chunk_fwd_args;
 
 int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
@@ -309,6 +317,7 @@ typedef struct pkda_chunk_bwd_args {
   void* du;
   float *dq, *dk, *dkw, *dv, *dbeta, *dgcum, *dh0;
   int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
+  const void *qg, *kg;         /* per-channel gates only: the forward's qg, kg */
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);
