@@ -1,4 +1,6 @@
 // Token-recurrent PKDA forward and the slot-pool decode step (gfx950).
+// (recurrent_kernel: any sequence length; decode_kernel: the persistent
+// one-token step over a slot pool.)
 //
 // One 256-thread workgroup owns one (sequence, head).  The FP32 state
 // S [D x D] lives in registers for the whole sequence: thread (rg, cg) holds
@@ -191,6 +193,171 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(RecParams p) {
   if (precond && tid < D && a_dst) a_dst[tid] = a_c;
 }
 
+// ---------------------------------------------------------------------------
+// Slot-pool decode step (one token per live sequence), persistent and
+// software-pipelined.  Each workgroup walks (sequence, head) items
+// blockIdx.x, blockIdx.x + gridDim.x, ...; while it reduces and writes back
+// one item's state it already has the next item's 64 KiB (d = 128) in flight,
+// so the state stream never waits on the read-compute-write chain of a single
+// item.  The state is touched once per step: loaded and stored with
+// non-temporal hints (no reuse, so it is kept out of the caches' way).
+// Same arithmetic as recurrent_kernel at T = 1.
+// ---------------------------------------------------------------------------
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <typename T, int D, int NTH>
+__global__ __launch_bounds__(NTH) void decode_kernel(RecParams p) {
+  constexpr int NCG = D / 4;
+  constexpr int NRG = NTH / NCG;
+  constexpr int RPT = D / NRG;
+  static_assert(RPT >= 1 && NRG * RPT == D, "bad head dim");
+  __shared__ float s_ak[D], s_aq[D], s_al[D], s_bw[D], s_v[D];
+  __shared__ float s_qk[NTH / 64];
+  __shared__ float4 s_pe[NRG][NCG];
+  __shared__ float4 s_po[NRG][NCG];
+
+  const int H = p.heads;
+  const int tid = threadIdx.x;
+  const int cg = tid % NCG;
+  const int rg = tid / NCG;
+  const int total = p.num_seqs * H;
+  const bool precond = p.g_atk != nullptr;
+  auto state_of = [&](int it) {
+    const int n = it / H, h = it - n * H;
+    const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
+    return p.state_pool + (slot * H + h) * (int64_t)D * D;
+  };
+  // One item's per-channel inputs (thread c < D holds channel c).
+  struct ChanIn {
+    float q, k, v, g, beta, a, g_atk, beta_atk;
+  };
+  auto load_chan = [&](int it, ChanIn& x) {
+    if (tid >= D) return;
+    const int n = it / H, h = it - n * H;
+    const int64_t th = (int64_t)n * H + h;
+    const int c = tid;
+    x.q = io<T>::load(static_cast<const T*>(p.q) + th * D + c);
+    x.k = io<T>::load(static_cast<const T*>(p.k) + th * D + c);
+    x.v = io<T>::load(static_cast<const T*>(p.v) + th * D + c);
+    x.g = load_any(p.g, p.gate_kind == PKDA_GATE_LOG_HEAD ? th : th * D + c, p.g_dtype);
+    x.beta = p.beta[th];
+    if (precond) {
+      const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
+      x.a = p.a_pool[(slot * H + h) * (int64_t)D + c];
+      x.g_atk = p.g_atk[th];
+      x.beta_atk = p.beta_atk[th];
+    }
+  };
+  f4v S[RPT], Sn[RPT];
+  ChanIn cur{}, nxt_in{};
+  int item = blockIdx.x;
+  if (item < total) {
+    const float* src = state_of(item);
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      S[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src + (rg + NRG * j) * D + 4 * cg));
+    load_chan(item, cur);
+  }
+  for (; item < total; item += gridDim.x) {
+    const int nxt = item + gridDim.x;
+    if (nxt < total) {
+      const float* src = state_of(nxt);
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        Sn[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src + (rg + NRG * j) * D + 4 * cg));
+      load_chan(nxt, nxt_in);
+    }
+    const int n = item / H, h = item - n * H;
+    const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
+    const int64_t th = (int64_t)n * H + h;
+    // ---- channel phase ------------------------------------------------------
+    float qk_part = 0.f;
+    if (tid < D) {
+      const int c = tid;
+      const float qc = cur.q * p.scale;
+      const float kc = cur.k;
+      const float vc = cur.v;
+      float gl = cur.g;
+      if (p.gate_kind == PKDA_GATE_RAW_CHANNEL) gl = -expf(p.A_log[h]) * softplus_f(gl + p.dt_bias[h * D + c]);
+      const float al = expf(gl);
+      float kw = kc;
+      if (precond) {
+        const float a_c = expf(cur.g_atk) * cur.a + cur.beta_atk * (kc * kc);
+        p.a_pool[(slot * H + h) * (int64_t)D + c] = a_c;
+        const float r = logf(a_c + p.squash_eps) - p.center[h];
+        kw = kc * expf(-p.log_x * (r / (1.f + fabsf(r))));
+      }
+      const float bt = cur.beta;
+      s_ak[c] = al * kc;
+      s_aq[c] = al * qc;
+      s_al[c] = al;
+      s_bw[c] = bt * kw;
+      s_v[c] = vc;
+      qk_part = qc * kw * bt;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) qk_part += __shfl_xor(qk_part, off);
+    if ((tid & 63) == 0) s_qk[tid >> 6] = qk_part;
+    __syncthreads();
+    // ---- column reductions of the old state ---------------------------------
+    float4 pe = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rg + NRG * j;
+      const float ak = s_ak[row], aq = s_aq[row];
+      pe.x += ak * S[j][0]; pe.y += ak * S[j][1]; pe.z += ak * S[j][2]; pe.w += ak * S[j][3];
+      po.x += aq * S[j][0]; po.y += aq * S[j][1]; po.z += aq * S[j][2]; po.w += aq * S[j][3];
+    }
+    s_pe[rg][cg] = pe;
+    s_po[rg][cg] = po;
+    __syncthreads();
+    // ---- residual, output, rank-1 update, write-back -------------------------
+    float4 e = *reinterpret_cast<const float4*>(&s_v[4 * cg]);
+    float4 out = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < NRG; ++r) {
+      const float4 a = s_pe[r][cg];
+      const float4 b = s_po[r][cg];
+      e.x -= a.x; e.y -= a.y; e.z -= a.z; e.w -= a.w;
+      out.x += b.x; out.y += b.y; out.z += b.z; out.w += b.w;
+    }
+    float bqk = 0.f;
+#pragma unroll
+    for (int w = 0; w < NTH / 64; ++w) bqk += s_qk[w];
+    out.x += bqk * e.x; out.y += bqk * e.y; out.z += bqk * e.z; out.w += bqk * e.w;
+    if (rg == 0) store4(static_cast<T*>(p.o) + th * D + 4 * cg, out);
+    float* dst = p.state_pool + (slot * H + h) * (int64_t)D * D;
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int row = rg + NRG * j;
+      const float al = s_al[row], bw = s_bw[row];
+      const f4v x = {al * S[j][0] + bw * e.x, al * S[j][1] + bw * e.y, al * S[j][2] + bw * e.z,
+                     al * S[j][3] + bw * e.w};
+      __builtin_nontemporal_store(x, reinterpret_cast<f4v*>(dst + row * D + 4 * cg));
+    }
+    __syncthreads();  // LDS is reused by the next item
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) S[j] = Sn[j];
+    cur = nxt_in;
+  }
+}
+
+template <typename T>
+int launch_decode(const RecParams& rp, int D, hipStream_t stream) {
+  const int total = rp.num_seqs * rp.heads;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int grid = total < 12 * cus ? total : 12 * cus;  // ~12 items in flight per CU measured best at d = 128
+  switch (D) {
+    case 32: hipLaunchKernelGGL((decode_kernel<T, 32, 256>), dim3(grid), dim3(256), 0, stream, rp); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<T, 64, 512>), dim3(grid), dim3(512), 0, stream, rp); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<T, 128, 512>), dim3(grid), dim3(512), 0, stream, rp); break;
+    default: set_error("head_dim %d not built (32, 64, 128)", D); return PKDA_EUNSUPPORTED;
+  }
+  return launch_status("pkda_decode_step");
+}
+
 template <typename T>
 int launch_recurrent(const RecParams& rp, int D, hipStream_t stream) {
   dim3 grid(rp.num_seqs, rp.heads);
@@ -266,6 +433,9 @@ int recurrent_entry(const pkda_recurrent_args* a, void* stream, bool decode) {
   rp.final_state = a->final_state; rp.final_A_state = a->final_A_state;
   rp.o = a->o;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (decode) {
+    return a->dtype == PKDA_F32 ? launch_decode<float>(rp, a->head_dim, s) : launch_decode<bf16_t>(rp, a->head_dim, s);
+  }
   return a->dtype == PKDA_F32 ? launch_recurrent<float>(rp, a->head_dim, s)
                               : launch_recurrent<bf16_t>(rp, a->head_dim, s);
 }
