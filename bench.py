@@ -130,6 +130,7 @@ def fwd_bwd(inp: dict, leaves: list[torch.Tensor]):
 
 
 def time_step(inp: dict, steps: int, warmup: int) -> float:
+    """Eager: K fwd+bwd steps between two events on the stream; ms per step."""
     names = ["q", "k", "v", "g", "beta"] + (["s0"] if inp["s0"] is not None else [])
     leaves = [inp[n].detach().requires_grad_() for n in names]
     for _ in range(warmup):
@@ -142,6 +143,41 @@ def time_step(inp: dict, steps: int, warmup: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def time_step_graph(inp: dict, steps: int, warmup: int) -> tuple[float, bool]:
+    """Captured: one fwd+bwd step recorded into a HIP graph after warm-up on a
+    side stream, replayed K times between two events (the reference's
+    ``captured_run``, scripts/pkda_bench.py:239-285).  Every replay's
+    gradients are checked bitwise against the eager step first.
+    Returns (ms per step, replays agree)."""
+    names = ["q", "k", "v", "g", "beta"] + (["s0"] if inp["s0"] is not None else [])
+    leaves = [inp[n].detach().requires_grad_() for n in names]
+    eager = [gr.clone() for gr in fwd_bwd(inp, leaves)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 3)):
+            fwd_bwd(inp, leaves)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_grads = fwd_bwd(inp, leaves)
+    agree = True
+    for _ in range(3):  # replays interleaved with eager work and synchronisation
+        graph.replay()
+        torch.cuda.synchronize()
+        agree &= all(torch.equal(a, b) for a, b in zip(static_grads, eager))
+        fwd_bwd(inp, leaves)
+        torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    agree &= all(torch.equal(a, b) for a, b in zip(static_grads, eager))
+    return start.elapsed_time(end) / steps, agree
 
 
 def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
@@ -230,24 +266,44 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
     for i in range(warmup):
         pkda_decode_step_(*sets[i % 4], pool, idx[i % steps], out=out)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    # eager: one event pair around all steps
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for i in range(steps):
-        ev[i][0].record()
         pkda_decode_step_(*sets[i % 4], pool, idx[i], out=out)
-        ev[i][1].record()
     t1.record()
     torch.cuda.synchronize()
     wall_ms = t0.elapsed_time(t1)
-    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    # captured: G steps (each with its own slot indices) in one HIP graph,
+    # replayed until `steps` steps have run; one launch per step
+    G = min(100, steps)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        pkda_decode_step_(*sets[0], pool, idx[0], out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        for i in range(G):
+            pkda_decode_step_(*sets[i % 4], pool, idx[i], out=out)
+    reps = max(1, steps // G)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(reps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    kern_ms = t0.elapsed_time(t1) / (reps * G)
     nbytes = 2 * N * H * D * D * 4 + N * H * (2 * (2 * D + D) + 2 * 2) + N * H * D * 2 + 4 * N
     return {
         "workload": "c4 decode: 256 live of 512 slots, H32 d128, fp32 state, bf16 q/k/v",
         "steps": steps,
-        "ms_per_step": wall_ms / steps,
-        "tokens_per_s": N * steps / (wall_ms / 1e3),
+        "ms_per_step": kern_ms,
+        "ms_per_step_eager": wall_ms / steps,
+        "tokens_per_s": N / (kern_ms / 1e3),
         "kernel_us": kern_ms * 1e3,
+        "timing": "HIP graph of 100 steps replayed; kernel_us = replay time / steps (launch gaps included)",
         "bytes_per_step": nbytes,
         "roofline": {
             "bound": "hbm",
@@ -324,6 +380,7 @@ def main() -> None:
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time the eager step only")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -344,8 +401,18 @@ def main() -> None:
     print(f"[bench] workload {args.workload} {w}", file=sys.stderr, flush=True)
     inp = make_chunk_inputs(w, dev)
     ntok = w["B"] * w["T"]
-    ms = time_step(inp, args.steps, args.warmup)
-    print(f"[bench] fwd+bwd {ms:.3f} ms/step", file=sys.stderr, flush=True)
+    ms_eager = time_step(inp, args.steps, args.warmup)
+    print(f"[bench] fwd+bwd eager {ms_eager:.3f} ms/step", file=sys.stderr, flush=True)
+    ms, graph_ok, timing = ms_eager, None, "eager"
+    if not args.no_graph:
+        try:
+            ms_graph, graph_ok = time_step_graph(inp, args.steps, args.warmup)
+            print(f"[bench] fwd+bwd graph {ms_graph:.3f} ms/step (replays agree: {graph_ok})", file=sys.stderr,
+                  flush=True)
+            if graph_ok:
+                ms, timing = ms_graph, "HIP graph replay"
+        except RuntimeError as exc:  # capture unsupported here: report eager
+            print(f"[bench] graph capture failed ({exc}); reporting eager timing", file=sys.stderr, flush=True)
     per_th = stage_flops(w["D"])
     token_heads = ntok * w["H"]
     step_flops = token_heads * sum(per_th.values())
@@ -363,6 +430,9 @@ def main() -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_eager": ms_eager,
+        "timing": timing,
+        "graph_replays_agree": graph_ok,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
