@@ -201,7 +201,7 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
     h = torch.empty(plan.num_chunks, H, D, D, **bf)
     dh = torch.empty(plan.num_chunks, H, D, D, **bf)
     du = torch.empty(ntok, H, D, **bf)
-    dq, dk, dv = (torch.empty(ntok, H, D, **f32) for _ in range(3))
+    dq, dk, dv = (torch.empty(ntok, H, D, **bf) for _ in range(3))  # the step's own gradient dtype
     dbeta, dgcum = torch.empty(ntok, H, **f32), torch.empty(ntok, H, **f32)
     s0 = inp["s0"]
     scale = D ** -0.5
@@ -215,7 +215,7 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
         gate_per_channel=0, beta=_ptr(beta), scale=scale, initial_state=_ptr(s0),
         w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), do=_ptr(do), dht=None, dh=_ptr(dh),
         du=_ptr(du), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
-        dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None,
+        dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None, grad_dtype=_lib.PKDA_BF16,
     )
     stages = [
         ("fwd_intra", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_INTRA),

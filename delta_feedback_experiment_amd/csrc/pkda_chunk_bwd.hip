@@ -51,10 +51,10 @@ struct BwdParams {
   const float* dht;
   void* dh;
   void* du;
-  float* dq;
-  float* dk;
-  float* dkw;
-  float* dv;
+  void* dq;   // dq, dk, dkw, dv: FP32 or the activation dtype (kernel template OT)
+  void* dk;
+  void* dkw;
+  void* dv;
   float* dbeta;
   float* dgcum;
   float* dh0;
@@ -281,7 +281,7 @@ struct FusedBwdLayout {
   static constexpr int bytes = off_red + kFW * 4;
 };
 
-template <typename T, int D>
+template <typename T, int D, typename OT>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   using L = FusedBwdLayout<T, D>;
   using E = T;
@@ -325,14 +325,24 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     sGam[tid] = p.gcum[idx];
     sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
   }
-  load_tile<kFW, C, D>(sU, L::LD, static_cast<const T*>(p.u) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, D>(sdO, L::LD, static_cast<const T*>(p.dO) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, D>(sdU, L::LD, static_cast<const T*>(p.du) + row0 * D, gs, len, Ident());
-  load_tile<kFW, D, D>(sH, L::LD, hsrc, D, D, Ident());
+  // every global load of the phase is issued before the first LDS store, so
+  // the tiles share one memory round trip
+  {
+    RegTile<kFW, C, D, T> rU, rdO, rdU;
+    RegTile<kFW, D, D, T> rH;
+    rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
+    rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
+    rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
+    rH.load(hsrc, D, D);
+    rU.store(sU, L::LD);
+    rdO.store(sdO, L::LD);
+    rdU.store(sdU, L::LD);
+    rH.store(sH, L::LD);
+  }
   __syncthreads();
   const float gC = sGam[C - 1];
 
-  f32x4 dq[HCT], dk[HCT], dkw[HCT], dv[HCT], dkws[HCT];
+  f32x4 dq[HCT], dk[HCT], dkw[HCT], dkws[HCT];
   // ---- phase 1: dQg, dW (my column half), dAqk (two 16-column tiles) ----------
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
@@ -364,18 +374,19 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     constexpr int V = Vec16<T>::N;
     constexpr int PER_ROW = D / V;
     constexpr int TOTAL = D * PER_ROW;
+    static_assert(TOTAL % kFW == 0, "dH tile covers the workgroup");
+    RegTile<kFW, D, D, T> rdH;
+    rdH.load(dhsrc, D, D);
 #pragma unroll
-    for (int i = 0; i < (TOTAL + kFW - 1) / kFW; ++i) {
+    for (int i = 0; i < TOTAL / kFW; ++i) {
       const int idx = tid + i * kFW;
-      if (idx < TOTAL) {
-        const int r = idx / PER_ROW, c = (idx - r * PER_ROW) * V;
-        float x[V], hv[V];
-        Vec16<T>::load(dhsrc + r * D + c, x);
-        lds_vec<V>(sH + r * L::LD + c, hv);
+      const int r = idx / PER_ROW, c = (idx - r * PER_ROW) * V;
+      float x[V], hv[V];
+      Vec16<T>::unpack(rdH.r[i], x);
+      lds_vec<V>(sH + r * L::LD + c, hv);
 #pragma unroll
-        for (int j = 0; j < V; ++j) hd += hv[j] * x[j];
-        store_vec<V>(sH + r * L::LD + c, x);
-      }
+      for (int j = 0; j < V; ++j) hd += hv[j] * x[j];
+      *reinterpret_cast<uint4*>(sH + r * L::LD + c) = rdH.r[i];  // this thread's own slots
     }
   }
   __syncthreads();
@@ -390,10 +401,18 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   }
   __syncthreads();
   // ---- phase 3: WY backward ----------------------------------------------------
-  load_tile<kFW, C, D>(sV, L::LD, static_cast<const T*>(p.v) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, D>(sK, L::LD, static_cast<const T*>(p.k) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, C>(sT, L::LDC, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len, Ident());
-  load_tile<kFW, C, D>(sQ, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, len, Ident());
+  {
+    RegTile<kFW, C, D, T> rV, rK, rQ;
+    RegTile<kFW, C, C, T> rT;
+    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
+    rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);
+    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
+    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
+    rV.store(sV, L::LD);
+    rK.store(sK, L::LD);
+    rT.store(sT, L::LDC);
+    rQ.store(sQ, L::LD);
+  }
   if (!p.kw_is_k && D == 2 * C) load_tile<kFW, C, D>(sKW, L::LD, static_cast<const T*>(p.kw) + row0 * D, gs, len, Ident());
   __syncthreads();
   const E* sKWr = p.kw_is_k ? sK : sKW;
@@ -407,6 +426,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdW, L::LD, 16 * ct, kbeg, C, lane);  // dBw = T^T dW
     f32x4 acv = zero4();
     mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
+    f32x4 dv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int s = r0 + acc_row(lane, e);
@@ -414,9 +434,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
       const float kv = from_e<E>(sK[s * L::LD + c]);
       const float vv = from_e<E>(sV[s * L::LD + c]);
       dk[j][e] = sBeta[s] * eg * acc[e];
-      dv[j][e] = sBeta[s] * acv[e];
+      dv[e] = sBeta[s] * acv[e];
       db[e] += acc[e] * eg * kv + acv[e] * vv;
     }
+    store_acc_global<OT>(static_cast<OT*>(p.dv) + row0 * D, gs, dv, r0, 16 * ct, len, lane);  // final: leaves now
   }
   // dT = dW Bw^T + dU Bv^T (two 16-column tiles)
 #pragma unroll
@@ -488,19 +509,17 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     }
   }
   // ---- outputs -------------------------------------------------------------
-  float* dqo = p.dq + row0 * D;
-  float* dko = p.dk + row0 * D;
-  float* dvo = p.dv + row0 * D;
+  OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
+  OT* dko = static_cast<OT*>(p.dk) + row0 * D;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
-    store_acc_global<float>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
-    store_acc_global<float>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
+    store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
     if (p.kw_is_k) {
-      store_acc_global<float>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
     } else {
-      store_acc_global<float>(dko, gs, dk[j], r0, 16 * ct, len, lane);
-      store_acc_global<float>(p.dkw + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dko, gs, dk[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
     }
   }
   // row sums over the two column halves, then the last-row decay terms
@@ -575,7 +594,7 @@ struct FusedBwdPcLayout {
   static_assert(D == 2 * C || G_BYTES + RT <= off_dO, "KW fits after G");
 };
 
-template <typename T, int D>
+template <typename T, int D, typename OT>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   using L = FusedBwdPcLayout<T, D>;
   using E = T;
@@ -622,10 +641,18 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   const float scale = p.scale;
 
   if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
-  load_tile<kFW, C, D>(sU, L::LD, static_cast<const T*>(p.u) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, D>(sdO, L::LD, static_cast<const T*>(p.dO) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, D>(sdU, L::LD, static_cast<const T*>(p.du) + row0 * D, gs, len, Ident());
-  load_tile<kFW, D, D>(sH, L::LD, hsrc, D, D, Ident());
+  {
+    RegTile<kFW, C, D, T> rU, rdO, rdU;
+    RegTile<kFW, D, D, T> rH;
+    rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
+    rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
+    rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
+    rH.load(hsrc, D, D);
+    rU.store(sU, L::LD);
+    rdO.store(sdO, L::LD);
+    rdU.store(sdU, L::LD);
+    rH.store(sH, L::LD);
+  }
   __syncthreads();
 
   f32x4 dq[HCT], dk[HCT], dkw[HCT], dv[HCT], dkws[HCT];
@@ -698,11 +725,18 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   __syncthreads();
   // ---- phase 3: WY backward ----------------------------------------------------
-  load_tile<kFW, C, D>(sV, L::LD, static_cast<const T*>(p.v) + row0 * D, gs, len, Ident());
-  load_tile<kFW, C, D>(sK, L::LD, kg_, gs, len,
-                       [&](int r, int c, float x) { return sBeta[r] * expf(G(r, c)) * x; });  // Bw
-  load_tile<kFW, C, C>(sT, L::LDC, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len, Ident());
-  load_tile<kFW, C, D>(sQ, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, len, Ident());
+  {
+    RegTile<kFW, C, D, T> rV, rK, rQ;
+    RegTile<kFW, C, C, T> rT;
+    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
+    rK.load(kg_, gs, len);
+    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
+    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
+    rV.store(sV, L::LD);
+    rK.store(sK, L::LD, [&](int r, int c, float x) { return sBeta[r] * expf(G(r, c)) * x; });  // Bw
+    rT.store(sT, L::LDC);
+    rQ.store(sQ, L::LD);
+  }
   if (!p.kw_is_k && D == 2 * C) load_tile<kFW, C, D>(sKW, L::LD, kwg, gs, len, Ident());
   __syncthreads();
   const int kbeg = kfloor<E>(r0);
@@ -865,9 +899,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     }
   }
   // ---- outputs -------------------------------------------------------------
-  float* dqo = p.dq + row0 * D;
-  float* dko = p.dk + row0 * D;
-  float* dvo = p.dv + row0 * D;
+  OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
+  OT* dko = static_cast<OT*>(p.dk) + row0 * D;
+  OT* dvo = static_cast<OT*>(p.dv) + row0 * D;
   float* dgo = p.dgcum + row0 * D;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
@@ -887,13 +921,13 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       if (r == len - 1) dg[e] += expf(gC[c]) * sHD[c] + kgc;
     }
     store_acc_global<float>(dgo, gs, dg, r0, 16 * ct, len, lane);
-    store_acc_global<float>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
-    store_acc_global<float>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
+    store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
+    store_acc_global<OT>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
     if (p.kw_is_k) {
-      store_acc_global<float>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
     } else {
-      store_acc_global<float>(dko, gs, dk[j], r0, 16 * ct, len, lane);
-      store_acc_global<float>(p.dkw + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dko, gs, dk[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
     }
   }
   float* sRowB = sRed;  // [2][64]
@@ -917,7 +951,7 @@ int set_smem(K kernel, int bytes) {
   return 0;
 }
 
-template <typename T, int D, int BV>
+template <typename T, int D, int BV, typename OT>
 int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const int N = p.geom.num_seqs;
   const bool all = stages == 0;
@@ -930,7 +964,7 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   }
   if (num_chunks == 0) return 0;
   if (all || (stages & PKDA_STAGE_BWD_CHUNK)) {
-    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D> : chunk_fused_bwd_kernel<T, D>;
+    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D, OT> : chunk_fused_bwd_kernel<T, D, OT>;
     const int bytes = p.qg ? FusedBwdPcLayout<T, D>::bytes : FusedBwdLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kFW), bytes, s, p);
@@ -953,6 +987,8 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
                "the FP32 chunked backward is built for head_dim 64 only");
   PKDA_REQUIRE(a->heads > 0, PKDA_EINVAL, "heads");
   PKDA_REQUIRE(!a->gate_per_channel || (a->qg && a->kg), PKDA_EINVAL, "per-channel gates need the forward's qg and kg");
+  PKDA_REQUIRE(a->grad_dtype == PKDA_F32 || a->grad_dtype == a->dtype, PKDA_EUNSUPPORTED,
+               "grad_dtype %d (FP32 or the activation dtype)", a->grad_dtype);
   BwdParams p;
   if (int st = chunk_geom_from(a->cu_seqlens, a->num_seqs, a->seqlen, a->num_chunks, a->table, p.geom)) return st;
   if (a->num_seqs == 0) return 0;
@@ -975,7 +1011,12 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   if (a->dtype == PKDA_BF16) {
-    return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64>(p, nc, st, s) : launch_bwd<bf16_t, 64, 64>(p, nc, st, s);
+    if (a->grad_dtype == PKDA_BF16) {
+      return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, bf16_t>(p, nc, st, s)
+                                : launch_bwd<bf16_t, 64, 64, bf16_t>(p, nc, st, s);
+    }
+    return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, float>(p, nc, st, s)
+                              : launch_bwd<bf16_t, 64, 64, float>(p, nc, st, s);
   }
-  return launch_bwd<float, 64, 64>(p, nc, st, s);
+  return launch_bwd<float, 64, 64, float>(p, nc, st, s);
 }

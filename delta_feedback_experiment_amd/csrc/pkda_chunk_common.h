@@ -262,21 +262,26 @@ struct Ident {
 template <typename T> struct Vec16;
 template <> struct Vec16<float> {
   static constexpr int N = 4;
+  __device__ __forceinline__ static void unpack(const uint4& v, float* x) {
+    x[0] = __uint_as_float(v.x); x[1] = __uint_as_float(v.y);
+    x[2] = __uint_as_float(v.z); x[3] = __uint_as_float(v.w);
+  }
   __device__ __forceinline__ static void load(const float* p, float* x) {
-    const float4 v = *reinterpret_cast<const float4*>(p);
-    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    unpack(*reinterpret_cast<const uint4*>(p), x);
   }
 };
 template <> struct Vec16<bf16_t> {
   static constexpr int N = 8;
-  __device__ __forceinline__ static void load(const bf16_t* p, float* x) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
+  __device__ __forceinline__ static void unpack(const uint4& v, float* x) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       x[2 * i] = __uint_as_float(w[i] << 16);
       x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
+  }
+  __device__ __forceinline__ static void load(const bf16_t* p, float* x) {
+    unpack(*reinterpret_cast<const uint4*>(p), x);
   }
 };
 
@@ -364,6 +369,16 @@ struct RegTile {
                                            : make_uint4(0u, 0u, 0u, 0u);
     }
   }
+  // rows r >= nvalid (nvalid >= 1) repeat row nvalid - 1
+  __device__ __forceinline__ void load_clamped(const T* g, int64_t gstride, int nvalid) {
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      const int row = min(idx / PER_ROW, nvalid - 1);
+      const int c = (idx % PER_ROW) * V;
+      if (idx < TOTAL) r[i] = *reinterpret_cast<const uint4*>(g + row * gstride + c);
+    }
+  }
   __device__ __forceinline__ void store(T* lds, int ld) const {
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
@@ -372,6 +387,22 @@ struct RegTile {
       const int row = idx / PER_ROW;
       const int c = (idx - row * PER_ROW) * V;
       *reinterpret_cast<uint4*>(lds + row * ld + c) = r[i];
+    }
+  }
+  // store with f(r, c, x) applied to every value (rounded back to T)
+  template <typename F>
+  __device__ __forceinline__ void store(T* lds, int ld, F f) const {
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (TOTAL % NT != 0 && idx >= TOTAL) break;
+      const int row = idx / PER_ROW;
+      const int c = (idx - row * PER_ROW) * V;
+      float x[V];
+      Vec16<T>::unpack(r[i], x);
+#pragma unroll
+      for (int j = 0; j < V; ++j) x[j] = f(row, c + j, x[j]);
+      store_vec<V>(lds + row * ld + c, x);
     }
   }
 };

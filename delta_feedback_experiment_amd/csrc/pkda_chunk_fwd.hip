@@ -199,9 +199,18 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     sGam[tid] = p.gcum[idx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
     sBeta[tid] = tid < len ? p.beta[idx] : 0.f;
   }
-  load_tile<kIW, C, D>(sK, L::LD, k, gs, len, Ident());
-  load_tile<kIW, C, D>(sQ, L::LD, q, gs, len, Ident());
-  if (!ALIAS) load_tile<kIW, C, D>(sKW, L::LD, kw, gs, len, Ident());
+  // all tiles in one memory round trip; V waits in registers until Q's slot frees
+  RegTile<kIW, C, D, T> rV;
+  {
+    RegTile<kIW, C, D, T> rK, rQ, rKW;
+    rK.load(k, gs, len);
+    rQ.load(q, gs, len);
+    if (!ALIAS) rKW.load(kw, gs, len);
+    rV.load(v, gs, len);
+    rK.store(sK, L::LD);
+    rQ.store(sQ, L::LD);
+    if (!ALIAS) rKW.store(sKW, L::LD);
+  }
   // blocks above the diagonal of Akk / T are zero
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
@@ -243,7 +252,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     const int r = i / D, c = i - r * D;
     sK[r * L::LD + c] = to_e<E>(sBeta[r] * expf(sGam[r]) * from_e<E>(sK[r * L::LD + c]));
   }
-  load_tile<kIW, C, D>(sQ, L::LD, v, gs, len, RowScale{sBeta});
+  rV.store(sQ, L::LD, RowScale{sBeta});
   __syncthreads();
   store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
 
@@ -333,15 +342,22 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   const float* g = p.gcum + row0 * D;
 
   if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + h] : 0.f;
-  load_tile<kIW, C, D>(sK, L::LD, k, gs, len, Ident());
-  load_tile<kIW, C, D>(sQ, L::LD, q, gs, len, Ident());
-  if (!ALIAS) load_tile<kIW, C, D>(sKW, L::LD, kw, gs, len, Ident());
-  // G rows past the end repeat the last row (G is non-increasing in t, so
-  // every split factor stays <= 1 there too)
-  for (int i = tid; i < C * (D / 4); i += kIW) {
-    const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
-    *reinterpret_cast<float4*>(sG + r * L::LDG + c) =
-        *reinterpret_cast<const float4*>(g + (int64_t)min(r, len - 1) * gs + c);
+  // all tiles in one memory round trip; V waits in registers until Q's slot
+  // frees.  G rows past the end repeat the last row (G is non-increasing in
+  // t, so every split factor stays <= 1 there too).
+  RegTile<kIW, C, D, T> rV;
+  {
+    RegTile<kIW, C, D, T> rK, rQ, rKW;
+    RegTile<kIW, C, D, float> rG;
+    rK.load(k, gs, len);
+    rQ.load(q, gs, len);
+    if (!ALIAS) rKW.load(kw, gs, len);
+    rG.load_clamped(g, gs, len);
+    rV.load(v, gs, len);
+    rK.store(sK, L::LD);
+    rQ.store(sQ, L::LD);
+    if (!ALIAS) rKW.store(sKW, L::LD);
+    rG.store(sG, L::LDG);
   }
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
@@ -440,7 +456,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
     const int r = i / D, c = i - r * D;
     sK[r * L::LD + c] = to_e<E>(sBeta[r] * expf(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
   }
-  load_tile<kIW, C, D>(sQ, L::LD, v, gs, len, RowScale{sBeta});
+  rV.store(sQ, L::LD, RowScale{sBeta});
   __syncthreads();
   store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
 
