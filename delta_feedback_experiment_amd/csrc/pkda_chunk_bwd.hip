@@ -117,11 +117,15 @@ struct StateBwdLayout {
 // PC: per-channel gate -- kg and qg come precomputed from the forward, no row
 // scaling applies and dS decays row by row.
 template <typename T, int D, int BV, bool PC>
-__global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
+__global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(BwdParams p) {
   using L = StateBwdLayout<T, D, BV>;
   using E = T;
+  constexpr int kSW = state_threads(D, BV);
+  constexpr int NW = kSW / 64;
   constexpr int NCT = BV / 16;
-  constexpr int NS = (D / 16) * NCT / 4;
+  constexpr int NS = (D / 16) * NCT / NW;
+  constexpr int NRT = 4 * NCT;  // 16x16 tiles of a [64 x BV] chunk operand
+  static_assert(NS * NW == (D / 16) * NCT, "state tiles split evenly over the waves");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   E* sdS = reinterpret_cast<E*>(smem + L::off_dS);
   E* sKW = reinterpret_cast<E*>(smem + L::off_KW);
@@ -152,9 +156,9 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
       dS[i][j] = p.dht ? p.dht[((int64_t)n * H + h) * D * D + r * D + c] : 0.f;
     }
   }
-  RegTile<kWG, C, D, T> rKW, rQ, rW;
-  RegTile<kWG, C, C, T> rA;
-  RegTile<kWG, C, BV, T> rdO;
+  RegTile<kSW, C, D, T> rKW, rQ, rW;
+  RegTile<kSW, C, C, T> rA;
+  RegTile<kSW, C, BV, T> rdO;
   float rg = 0.f;
   auto prefetch = [&](int jc) {
     const int cstart = dstart + jc * C;
@@ -173,7 +177,6 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
   };
   if (count > 0) prefetch(count - 1);
   const float scale = p.scale;
-  const int r0 = 16 * wave;
   for (int jc = count - 1; jc >= 0; --jc) {
     const int cid = first + jc;
     const int cstart = dstart + jc * C;
@@ -203,18 +206,19 @@ __global__ __launch_bounds__(kWG) void chunk_state_bwd_kernel(BwdParams p) {
     const float gC = PC ? 0.f : sGam[C - 1];
     // s e^G dO (elementwise, for Q^T diag(s e^G) dO)
     if (!PC) {
-      for (int i = tid; i < C * BV; i += kWG) {
+      for (int i = tid; i < C * BV; i += kSW) {
         const int r = i / BV, c = i - r * BV;
         sdOg[r * L::LDV + c] = to_e<E>(scale * expf(sGam[r]) * from_e<E>(sdO[r * L::LDV + c]));
       }
     }
-    // dU = Aqk^T dO + diag(e^{G_C - G}) KW dS     wave w: rows 16w..16w+15
-    float egc[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) egc[e] = PC ? 1.f : expf(gC - sGam[r0 + acc_row(lane, e)]);
+    // dU = Aqk^T dO + diag(e^{G_C - G}) KW dS     (tile ti: row block ti % 4, column tile ti / 4)
     T* du_out = static_cast<T*>(p.du) + row0 * D + v0;
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int ti = wave; ti < NRT; ti += NW) {
+      const int r0 = 16 * (ti & 3), ct = ti >> 2;
+      float egc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) egc[e] = PC ? 1.f : expf(gC - sGam[r0 + acc_row(lane, e)]);
       f32x4 a1 = zero4(), a2 = zero4();
       mma_tile_range<E, COL, ROW>(a1, sAqk, L::LDC, r0, sdO, L::LDV, 16 * ct, kfloor<E>(r0), C, lane);
       mma_tile<E, ROW, ROW>(a2, sKW, L::LD, r0, sdS, L::LDV, 16 * ct, D, lane);
@@ -959,7 +963,7 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
     auto kern = p.qg ? chunk_state_bwd_kernel<T, D, BV, true> : chunk_state_bwd_kernel<T, D, BV, false>;
     const int bytes = StateBwdLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
-    if (N > 0) hipLaunchKernelGGL(kern, dim3(N, p.H, D / BV), dim3(kWG), bytes, s, p);
+    if (N > 0) hipLaunchKernelGGL(kern, dim3(N, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
     if (int st = launch_status("pkda_chunk_bwd(state)")) return st;
   }
   if (num_chunks == 0) return 0;

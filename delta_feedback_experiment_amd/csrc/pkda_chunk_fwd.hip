@@ -519,11 +519,15 @@ struct StateLayout {
 // PC: per-channel gate.  The forward intra kernel wrote qg = s e^G q and
 // kg = e^{G_last - G} kw, so no row scaling applies and S decays row by row.
 template <typename T, int D, int BV, bool PC>
-__global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(FwdParams p) {
   using L = StateLayout<T, D, BV>;
   using E = T;
+  constexpr int kSW = state_threads(D, BV);
+  constexpr int NW = kSW / 64;
   constexpr int NCT = BV / 16;              // column tiles of the slice
-  constexpr int NS = (D / 16) * NCT / 4;    // state tiles per wave
+  constexpr int NS = (D / 16) * NCT / NW;   // state tiles per wave
+  constexpr int NRT = 4 * NCT;              // 16x16 tiles of a [64 x BV] chunk operand
+  static_assert(NS * NW == (D / 16) * NCT, "state tiles split evenly over the waves");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   E* sS = reinterpret_cast<E*>(smem + L::off_S);
   E* sW = reinterpret_cast<E*>(smem + L::off_W);
@@ -555,9 +559,9 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
     }
   }
 
-  RegTile<kWG, C, D, T> rW, rQ, rKW;
-  RegTile<kWG, C, C, T> rA;
-  RegTile<kWG, C, BV, T> rU;
+  RegTile<kSW, C, D, T> rW, rQ, rKW;
+  RegTile<kSW, C, C, T> rA;
+  RegTile<kSW, C, BV, T> rU;
   float rg = 0.f;
   auto prefetch = [&](int jc) {
     const int cstart = dstart + jc * C;
@@ -576,7 +580,6 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
   };
   if (count > 0) prefetch(0);
   const float scale = p.scale;
-  const int r0 = 16 * wave;
 
   for (int jc = 0; jc < count; ++jc) {
     const int cid = first + jc;
@@ -607,22 +610,11 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
     __syncthreads();
     if (jc + 1 < count) prefetch(jc + 1);
     const float gC = PC ? 0.f : sGam[C - 1];  // padded rows repeat the last valid gate
-    float eg[4], egc[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (PC) {
-        eg[e] = 1.f;
-        egc[e] = 1.f;
-      } else {
-        const float g = sGam[r0 + acc_row(lane, e)];
-        eg[e] = scale * expf(g);
-        egc[e] = expf(gC - g);
-      }
-    }
-    // U = u - W S
+    // U = u - W S      (tile ti: row block ti % 4, column tile ti / 4)
     T* u_io = static_cast<T*>(p.u) + row0 * D + v0;
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int ti = wave; ti < NRT; ti += NW) {
+      const int r0 = 16 * (ti & 3), ct = ti >> 2;
       f32x4 acc = zero4();
       mma_tile<E, ROW, ROW>(acc, sW, L::LD, r0, sS, L::LDV, 16 * ct, D, lane);
       f32x4 U;
@@ -631,22 +623,23 @@ __global__ __launch_bounds__(kWG) void chunk_state_fwd_kernel(FwdParams p) {
         const int r = r0 + acc_row(lane, e), c = 16 * ct + acc_col(lane);
         U[e] = from_e<E>(sUin[r * L::LDV + c]) - acc[e];
         sU[r * L::LDV + c] = to_e<E>(U[e]);
-        if (!PC) sUg[r * L::LDV + c] = to_e<E>(egc[e] * U[e]);
+        if (!PC) sUg[r * L::LDV + c] = to_e<E>(expf(gC - sGam[r]) * U[e]);
       }
       store_acc_global<T>(u_io, gs, U, r0, 16 * ct, clen, lane);
     }
     __syncthreads();
     // O = diag(s e^G) Q S + Aqk U
     T* o_out = static_cast<T*>(p.o) + row0 * D + v0;
-    const int kend = kceil<E>(r0 + 16);  // Aqk is lower triangular
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int ti = wave; ti < NRT; ti += NW) {
+      const int r0 = 16 * (ti & 3), ct = ti >> 2;
+      const int kend = kceil<E>(r0 + 16);  // Aqk is lower triangular
       f32x4 a1 = zero4(), a2 = zero4();
       mma_tile<E, ROW, ROW>(a1, sQ, L::LD, r0, sS, L::LDV, 16 * ct, D, lane);
       mma_tile_range<E, ROW, ROW>(a2, sAqk, L::LDC, r0, sU, L::LDV, 16 * ct, 0, kend, lane);
       f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = eg[e] * a1[e] + a2[e];
+      for (int e = 0; e < 4; ++e) o[e] = (PC ? 1.f : scale * expf(sGam[r0 + acc_row(lane, e)])) * a1[e] + a2[e];
       store_acc_global<T>(o_out, gs, o, r0, 16 * ct, clen, lane);
     }
     // S <- e^{G_C} S + KW^T Ug   (per-channel: diag(e^{G_C}) S + kg^T U)
@@ -704,7 +697,7 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
     auto kern = p.qg ? chunk_state_fwd_kernel<T, D, BV, true> : chunk_state_fwd_kernel<T, D, BV, false>;
     const int bytes = StateLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
-    if (p.geom.num_seqs > 0) hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(kWG), bytes, s, p);
+    if (p.geom.num_seqs > 0) hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
     if (int st = launch_status("pkda_chunk_fwd(state)")) return st;
   }
   return 0;
