@@ -259,6 +259,18 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
 }
 // ---------------------------------------------------------------------------
 // fused per-chunk backward
+//
+// With dBv = T^T dU, the WY backward needs neither dW nor dT: since
+// dW = -dU S0^T and (Bv - Bw S0) = T^-1 U,
+//   dBw  = T^T dW = -dBv S0^T
+//   dT   = dW Bw^T + dU Bv^T = dU (T^-1 U)^T   so   dAkk = -T^T dT T^T = -dBv U^T.
+// Phases (8 waves, wave (rb, ch): row block rb, column half ch):
+//   1  dBv = T^T dU -> dv;  dQg = dO S0^T;  dAqk = dO U^T -> P2
+//   2  dBv to LDS over dU
+//   3  dBw = -dBv S0^T;  dAkk = -dBv U^T -> P1r = dAkk E, P1 = beta_t P1r
+//   4  dS_C replaces S0; sum(S0 * dS_C)
+//   5  dKg = U dS_C^T
+//   6  pairwise terms with K, Q, KW; outputs
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 struct FusedBwdLayout {
@@ -266,20 +278,15 @@ struct FusedBwdLayout {
   static constexpr int LDC = C + Pad<T>::v;
   static constexpr int RT = C * LD * (int)sizeof(T);    // one [64][LD] tile
   static constexpr int CT = C * LDC * (int)sizeof(T);   // one [64][LDC] tile
-  // h / dH region: D rows.  At D = 128 its second half later holds KW; at
-  // D = 64 (where LD == LDC) KW goes to the X tile, free by then.
-  static constexpr int HR = D;
-  static_assert(D == 2 * C || LD == LDC, "KW placement");
-  static constexpr int off_U = 0;                       // U, then V
-  static constexpr int off_dO = off_U + RT;             // dO, then K
-  static constexpr int off_dU = off_dO + RT;            // dU, then P1 = beta_t dAkk E
-  static constexpr int off_dW = off_dU + RT;            // dW, then P1r = dAkk E
-  static constexpr int off_H = off_dW + RT;             // h, dH [D][LD]; then Q | KW
-  static constexpr int off_T = off_H + HR * LD * (int)sizeof(T);
+  static constexpr int off_U = 0;                       // U, then K
+  static constexpr int off_dO = off_U + RT;             // dO, then Q
+  static constexpr int off_dU = off_dO + RT;            // dU, then dBv
+  static constexpr int off_V = off_dU + RT;             // V, then KW
+  static constexpr int off_H = off_V + RT;              // S0, then dS_C [D][LD]
+  static constexpr int off_T = off_H + D * LD * (int)sizeof(T);  // T, then P1r = dAkk E
   static constexpr int off_P2 = off_T + CT;             // s dAqk E
-  static constexpr int off_dT = off_P2 + CT;
-  static constexpr int off_X = off_dT + CT;
-  static constexpr int off_gam = off_X + CT;
+  static constexpr int off_P1 = off_P2 + CT;            // beta_t dAkk E
+  static constexpr int off_gam = off_P1 + CT;
   static constexpr int off_beta = off_gam + C * 4;
   static constexpr int off_red = off_beta + C * 4;      // [kFW] floats
   static constexpr int bytes = off_red + kFW * 4;
@@ -302,20 +309,18 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   const int64_t row0 = (int64_t)ci.start * H + hh;
 
   E* sU = reinterpret_cast<E*>(smem + L::off_U);
-  E* sV = sU;
+  E* sK = sU;
   E* sdO = reinterpret_cast<E*>(smem + L::off_dO);
-  E* sK = sdO;
+  E* sQ = sdO;
   E* sdU = reinterpret_cast<E*>(smem + L::off_dU);
-  E* sP1 = sdU;
-  E* sdW = reinterpret_cast<E*>(smem + L::off_dW);
-  E* sP1r = sdW;
+  E* sdBv = sdU;
+  E* sV = reinterpret_cast<E*>(smem + L::off_V);
+  E* sKW = sV;
   E* sH = reinterpret_cast<E*>(smem + L::off_H);
-  E* sQ = sH;
   E* sT = reinterpret_cast<E*>(smem + L::off_T);
+  E* sP1r = sT;
   E* sP2 = reinterpret_cast<E*>(smem + L::off_P2);
-  E* sdT = reinterpret_cast<E*>(smem + L::off_dT);
-  E* sX = reinterpret_cast<E*>(smem + L::off_X);
-  E* sKW = (D == 2 * C) ? sH + C * L::LD : sX;
+  E* sP1 = reinterpret_cast<E*>(smem + L::off_P1);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
   float* sRed = reinterpret_cast<float*>(smem + L::off_red);
@@ -332,32 +337,48 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   // every global load of the phase is issued before the first LDS store, so
   // the tiles share one memory round trip
   {
-    RegTile<kFW, C, D, T> rU, rdO, rdU;
+    RegTile<kFW, C, D, T> rU, rdO, rdU, rV;
+    RegTile<kFW, C, C, T> rT;
     RegTile<kFW, D, D, T> rH;
     rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
     rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
     rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
+    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
+    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rH.load(hsrc, D, D);
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
+    rV.store(sV, L::LD);
+    rT.store(sT, L::LDC);
     rH.store(sH, L::LD);
   }
   __syncthreads();
   const float gC = sGam[C - 1];
+  const int kbeg = kfloor<E>(r0);  // T, P1, P2 vanish above the diagonal
 
-  f32x4 dq[HCT], dk[HCT], dkw[HCT], dkws[HCT];
-  // ---- phase 1: dQg, dW (my column half), dAqk (two 16-column tiles) ----------
+  f32x4 dq[HCT], dkb[HCT], dkws[HCT], dBv[HCT];
+  float db[4] = {0.f, 0.f, 0.f, 0.f};
+  // ---- phase 1: dBv = T^T dU (-> dv), dQg = dO S0^T, dAqk = dO U^T ------------
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    f32x4 acv = zero4();
+    mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);
+    dBv[j] = acv;
+    f32x4 dv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = r0 + acc_row(lane, e);
+      dv[e] = sBeta[s] * acv[e];
+      db[e] += acv[e] * from_e<E>(sV[s * L::LD + c]);
+    }
+    store_acc_global<OT>(static_cast<OT*>(p.dv) + row0 * D, gs, dv, r0, 16 * ct, len, lane);  // final
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
     for (int e = 0; e < 4; ++e) dq[j][e] = scale * expf(sGam[r0 + acc_row(lane, e)]) * acc[e];
-    f32x4 acw = zero4();
-    mma_tile<E, ROW, COL>(acw, sdU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
-    store_acc_lds(sdW, L::LD, -acw, r0, 16 * ct, lane);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -372,15 +393,48 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     }
   }
   __syncthreads();
-  // ---- phase 2: dH replaces h; e^{G_C} sum(h * dH) ---------------------------
+  // ---- phase 2: dBv over dU; Q, KW and dS_C start their way in -------------
+  RegTile<kFW, C, D, T> rQ, rKW;
+  RegTile<kFW, D, D, T> rdH;
+  rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
+  if (!p.kw_is_k) rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, len);
+  rdH.load(dhsrc, D, D);
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
+  __syncthreads();
+  // ---- phase 3: dBw = -dBv S0^T, dAkk = -dBv U^T --------------------------------
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    f32x4 acc = zero4();
+    mma_tile<E, ROW, COL>(acc, sdBv, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dkb[j][e] = -expf(sGam[r0 + acc_row(lane, e)]) * acc[e];  // e^G dBw
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ct = 2 * ch + j;
+    f32x4 acc = zero4();
+    if (ct <= rb) mma_tile<E, ROW, COL>(acc, sdBv, L::LD, r0, sU, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
+      const float raw = (s < t && t < len) ? -acc[e] * expf(sGam[t] - sGam[s]) : 0.f;
+      sP1r[t * L::LDC + s] = to_e<E>(raw);
+      sP1[t * L::LDC + s] = to_e<E>(sBeta[t] * raw);
+    }
+  }
+  // Q and KW regions (dO, V) have been free since phase 1
+  rQ.store(sQ, L::LD);
+  if (!p.kw_is_k) rKW.store(sKW, L::LD);
+  __syncthreads();
+  // ---- phase 4: dS_C replaces S0; sum(S0 * dS_C) ------------------------------
   float hd = 0.f;
   {
     constexpr int V = Vec16<T>::N;
     constexpr int PER_ROW = D / V;
     constexpr int TOTAL = D * PER_ROW;
-    static_assert(TOTAL % kFW == 0, "dH tile covers the workgroup");
-    RegTile<kFW, D, D, T> rdH;
-    rdH.load(dhsrc, D, D);
+    static_assert(TOTAL % kFW == 0, "dS_C tile covers the workgroup");
 #pragma unroll
     for (int i = 0; i < TOTAL / kFW; ++i) {
       const int idx = tid + i * kFW;
@@ -394,7 +448,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     }
   }
   __syncthreads();
-  // dKg = U dH^T -> write-key gradient of the state path
+  // ---- phase 5: dKg = U dS_C^T (write-key gradient of the state path) ---------
+  RegTile<kFW, C, D, T> rK;
+  rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -404,91 +460,15 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     for (int e = 0; e < 4; ++e) dkws[j][e] = expf(gC - sGam[r0 + acc_row(lane, e)]) * acc[e];
   }
   __syncthreads();
-  // ---- phase 3: WY backward ----------------------------------------------------
-  {
-    RegTile<kFW, C, D, T> rV, rK, rQ;
-    RegTile<kFW, C, C, T> rT;
-    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
-    rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);
-    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
-    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
-    rV.store(sV, L::LD);
-    rK.store(sK, L::LD);
-    rT.store(sT, L::LDC);
-    rQ.store(sQ, L::LD);
-  }
-  if (!p.kw_is_k && D == 2 * C) load_tile<kFW, C, D>(sKW, L::LD, static_cast<const T*>(p.kw) + row0 * D, gs, len, Ident());
+  rK.store(sK, L::LD);
   __syncthreads();
   const E* sKWr = p.kw_is_k ? sK : sKW;
-  const int kbeg = kfloor<E>(r0);  // T, P1, P2 vanish above the diagonal
-  float db[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < HCT; ++j) {
-    const int ct = ch * HCT + j;
-    const int c = 16 * ct + acc_col(lane);
-    f32x4 acc = zero4();
-    mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdW, L::LD, 16 * ct, kbeg, C, lane);  // dBw = T^T dW
-    f32x4 acv = zero4();
-    mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
-    f32x4 dv;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int s = r0 + acc_row(lane, e);
-      const float eg = expf(sGam[s]);
-      const float kv = from_e<E>(sK[s * L::LD + c]);
-      const float vv = from_e<E>(sV[s * L::LD + c]);
-      dk[j][e] = sBeta[s] * eg * acc[e];
-      dv[e] = sBeta[s] * acv[e];
-      db[e] += acc[e] * eg * kv + acv[e] * vv;
-    }
-    store_acc_global<OT>(static_cast<OT*>(p.dv) + row0 * D, gs, dv, r0, 16 * ct, len, lane);  // final: leaves now
-  }
-  // dT = dW Bw^T + dU Bv^T (two 16-column tiles)
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ct = 2 * ch + j;
-    f32x4 a1 = zero4(), a2 = zero4();
-    mma_tile<E, ROW, COL>(a1, sdW, L::LD, r0, sK, L::LD, 16 * ct, D, lane);
-    mma_tile<E, ROW, COL>(a2, sdU, L::LD, r0, sV, L::LD, 16 * ct, D, lane);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int s = 16 * ct + acc_col(lane);
-      sdT[(r0 + acc_row(lane, e)) * L::LDC + s] = to_e<E>(sBeta[s] * (expf(sGam[s]) * a1[e] + a2[e]));
-    }
-  }
-  __syncthreads();
-  // X = T^T dT
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ct = 2 * ch + j;
-    f32x4 acc = zero4();
-    mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdT, L::LDC, 16 * ct, kbeg, C, lane);
-    store_acc_lds(sX, L::LDC, acc, r0, 16 * ct, lane);
-  }
-  __syncthreads();
-  // dAkk = -X T^T (strictly lower) -> P1r = dAkk E, P1 = beta_t P1r
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ct = 2 * ch + j;
-    f32x4 acc = zero4();
-    if (ct <= rb) mma_tile_range<E, ROW, COL>(acc, sX, L::LDC, r0, sT, L::LDC, 16 * ct, 0, kceil<E>(16 * ct + 16), lane);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
-      const float raw = (s < t && t < len) ? -acc[e] * expf(sGam[t] - sGam[s]) : 0.f;
-      sP1r[t * L::LDC + s] = to_e<E>(raw);
-      sP1[t * L::LDC + s] = to_e<E>(sBeta[t] * raw);
-    }
-  }
-  __syncthreads();
-  if (!p.kw_is_k && D != 2 * C) {  // KW into the X tile, now free
-    load_tile<kFW, C, D>(sKW, L::LD, static_cast<const T*>(p.kw) + row0 * D, gs, len, Ident());
-    __syncthreads();
-  }
-  // ---- phase 4: pairwise terms ------------------------------------------------
+  // ---- phase 6: pairwise terms ------------------------------------------------
   const int kend = kceil<E>(r0 + 16);
   float gsum[4] = {0.f, 0.f, 0.f, 0.f};
   float kgd = 0.f;
+  OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
+  OT* dko = static_cast<OT*>(p.dk) + row0 * D;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -498,32 +478,27 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     mma_tile_range<E, ROW, ROW>(aq, sP2, L::LDC, r0, sKWr, L::LD, 16 * ct, 0, kend, lane);     // sum_x P2 kw
     mma_tile_range<E, COL, ROW>(aw, sP1, L::LDC, r0, sK, L::LD, 16 * ct, kbeg, C, lane);       // sum_t P1 k
     mma_tile_range<E, COL, ROW>(aw, sP2, L::LDC, r0, sQ, L::LD, 16 * ct, kbeg, C, lane);       // sum_t P2 q
+    f32x4 dk, dkw;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = r0 + acc_row(lane, e);
       const float kv = from_e<E>(sK[r * L::LD + c]);
       const float qv = from_e<E>(sQ[r * L::LD + c]);
       const float wv = from_e<E>(sKWr[r * L::LD + c]);
-      dk[j][e] += sBeta[r] * ak[e];
-      db[e] += kv * ak[e];
+      const float tk = dkb[j][e] + ak[e];  // e^G dBw + sum_x P1r kw
+      dk[e] = sBeta[r] * tk;
+      db[e] += kv * tk;
       dq[j][e] += aq[e];
-      dkw[j][e] = dkws[j][e] + aw[e];
+      dkw[e] = dkws[j][e] + aw[e];
       kgd += wv * dkws[j][e];
-      gsum[e] += qv * dq[j][e] + kv * dk[j][e] - wv * dkw[j][e];
+      gsum[e] += qv * dq[j][e] + kv * dk[e] - wv * dkw[e];
     }
-  }
-  // ---- outputs -------------------------------------------------------------
-  OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
-  OT* dko = static_cast<OT*>(p.dk) + row0 * D;
-#pragma unroll
-  for (int j = 0; j < HCT; ++j) {
-    const int ct = ch * HCT + j;
     store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
     if (p.kw_is_k) {
-      store_acc_global<OT>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dko, gs, dk + dkw, r0, 16 * ct, len, lane);
     } else {
-      store_acc_global<OT>(dko, gs, dk[j], r0, 16 * ct, len, lane);
-      store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dko, gs, dk, r0, 16 * ct, len, lane);
+      store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw, r0, 16 * ct, len, lane);
     }
   }
   // row sums over the two column halves, then the last-row decay terms

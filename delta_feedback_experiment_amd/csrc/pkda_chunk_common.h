@@ -111,39 +111,54 @@ __device__ __forceinline__ s16x8_t lds_read_kmajor(const bf16_t* p, int ld, int 
   return s16x8_t{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
 }
 
+// Operand fragments of one MFMA k-step, loaded on their own (frag_a / frag_b
+// on tiles already offset to row m0 / column n0) so a phase can hold
+// operands that several products share, and mfma() on them.
 template <> struct Mma<bf16_t> {
   static constexpr int KS = 32;
+  using Frag = s16x8_t;
+  template <int LA>
+  __device__ __forceinline__ static Frag frag_a(const bf16_t* A, int lda, int k0, int lane) {
+    if constexpr (LA == ROW) {
+      return *reinterpret_cast<const s16x8_t*>(A + (lane & 15) * lda + k0 + (lane >> 4) * 8);
+    } else {
+      return lds_read_kmajor(A, lda, k0, lane);
+    }
+  }
+  template <int LB>
+  __device__ __forceinline__ static Frag frag_b(const bf16_t* B, int ldb, int k0, int lane) {
+    return frag_a<LB == COL ? ROW : COL>(B, ldb, k0, lane);
+  }
+  __device__ __forceinline__ static void mfma(f32x4& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                  acc, 0, 0, 0);
+  }
   template <int LA, int LB>
   __device__ __forceinline__ static void step(f32x4& acc, const bf16_t* A, int lda, const bf16_t* B, int ldb,
                                               int k0, int lane) {
-    const int r = lane & 15;
-    const int kq = (lane >> 4) * 8;
-    s16x8_t a, b;
-    if constexpr (LA == ROW) {
-      a = *reinterpret_cast<const s16x8_t*>(A + r * lda + k0 + kq);
-    } else {
-      a = lds_read_kmajor(A, lda, k0, lane);
-    }
-    if constexpr (LB == COL) {
-      b = *reinterpret_cast<const s16x8_t*>(B + r * ldb + k0 + kq);
-    } else {
-      b = lds_read_kmajor(B, ldb, k0, lane);
-    }
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                  acc, 0, 0, 0);
+    mfma(acc, frag_a<LA>(A, lda, k0, lane), frag_b<LB>(B, ldb, k0, lane));
   }
 };
 
 template <> struct Mma<float> {
   static constexpr int KS = 4;
+  using Frag = float;
+  template <int LA>
+  __device__ __forceinline__ static Frag frag_a(const float* A, int lda, int k0, int lane) {
+    const int r = lane & 15, kq = lane >> 4;
+    return (LA == ROW) ? A[r * lda + k0 + kq] : A[(k0 + kq) * lda + r];
+  }
+  template <int LB>
+  __device__ __forceinline__ static Frag frag_b(const float* B, int ldb, int k0, int lane) {
+    return frag_a<LB == COL ? ROW : COL>(B, ldb, k0, lane);
+  }
+  __device__ __forceinline__ static void mfma(f32x4& acc, const Frag& a, const Frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+  }
   template <int LA, int LB>
   __device__ __forceinline__ static void step(f32x4& acc, const float* A, int lda, const float* B, int ldb, int k0,
                                               int lane) {
-    const int r = lane & 15;
-    const int kq = lane >> 4;
-    const float a = (LA == ROW) ? A[r * lda + k0 + kq] : A[(k0 + kq) * lda + r];
-    const float b = (LB == COL) ? B[r * ldb + k0 + kq] : B[(k0 + kq) * ldb + r];
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+    mfma(acc, frag_a<LA>(A, lda, k0, lane), frag_b<LB>(B, ldb, k0, lane));
   }
 };
 
