@@ -86,6 +86,14 @@ __device__ __forceinline__ float group16_sum(float x) {
   return x;
 }
 
+// Sum over the 64 lanes of a wave, fixed order; every lane gets the result.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = group16_sum(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
 // ---------------------------------------------------------------------------
 // reverse state pass
 //
@@ -469,6 +477,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   float kgd = 0.f;
   OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
   OT* dko = static_cast<OT*>(p.dk) + row0 * D;
+  // outputs in the activation dtype with the write-key gradient folded into
+  // dk leave through LDS (16-byte stores)
+  const bool kStage = sizeof(OT) == sizeof(T) && p.kw_is_k;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -493,17 +504,23 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
       kgd += wv * dkws[j][e];
       gsum[e] += qv * dq[j][e] + kv * dk[e] - wv * dkw[e];
     }
-    store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
-    if (p.kw_is_k) {
-      store_acc_global<OT>(dko, gs, dk + dkw, r0, 16 * ct, len, lane);
+    if (kStage) {  // S0's and dBv's regions are free: stage for 16-byte stores
+      store_acc_lds(sH, L::LD, dq[j], r0, 16 * ct, lane);
+      store_acc_lds(sdBv, L::LD, dk + dkw, r0, 16 * ct, lane);
     } else {
-      store_acc_global<OT>(dko, gs, dk, r0, 16 * ct, len, lane);
-      store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw, r0, 16 * ct, len, lane);
+      store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
+      if (p.kw_is_k) {
+        store_acc_global<OT>(dko, gs, dk + dkw, r0, 16 * ct, len, lane);
+      } else {
+        store_acc_global<OT>(dko, gs, dk, r0, 16 * ct, len, lane);
+        store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw, r0, 16 * ct, len, lane);
+      }
     }
   }
-  // row sums over the two column halves, then the last-row decay terms
-  float* sRowG = sRed;           // [2][64]
-  float* sRowB = sRed + 2 * C;   // [2][64]
+  // row sums over the two column halves; wave sums of the last-row terms
+  float* sRowG = sRed;              // [2][64]
+  float* sRowB = sRed + 2 * C;      // [2][64]
+  float* sWave = sRed + 4 * C;      // [2][8]
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float g = group16_sum(gsum[e]);
@@ -513,21 +530,31 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
       sRowB[ch * C + r0 + acc_row(lane, e)] = b;
     }
   }
-  __syncthreads();
-  float rowg = 0.f, rowb = 0.f;
-  if (tid < C) {
-    rowg = sRowG[tid] + sRowG[C + tid];
-    rowb = sRowB[tid] + sRowB[C + tid];
+  hd = wave_sum(hd);
+  kgd = wave_sum(kgd);
+  if (lane == 0) {
+    sWave[wave] = hd;
+    sWave[kFW / 64 + wave] = kgd;
   }
   __syncthreads();
-  const float hd_sum = block_sum<kFW>(hd, sRed);
-  const float kg_sum = block_sum<kFW>(kgd, sRed);
+  if (kStage) {
+    store_tile<kFW, C, D>(dqo, gs, reinterpret_cast<const OT*>(sH), L::LD, len);
+    store_tile<kFW, C, D>(dko, gs, reinterpret_cast<const OT*>(sdBv), L::LD, len);
+  }
   if (tid < len) {
     const int64_t idx = (int64_t)(ci.start + tid) * H + hh;
-    float g = rowg;
-    if (tid == len - 1) g += expf(gC) * hd_sum + kg_sum;
+    float g = sRowG[tid] + sRowG[C + tid];
+    if (tid == len - 1) {
+      float hd_sum = 0.f, kg_sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kFW / 64; ++w) {
+        hd_sum += sWave[w];
+        kg_sum += sWave[kFW / 64 + w];
+      }
+      g += expf(gC) * hd_sum + kg_sum;
+    }
     p.dgcum[idx] = g;
-    p.dbeta[idx] = rowb;
+    p.dbeta[idx] = sRowB[tid] + sRowB[C + tid];
   }
 }
 

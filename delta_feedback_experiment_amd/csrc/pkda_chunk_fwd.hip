@@ -121,19 +121,6 @@ __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* sc
   }
 }
 
-// Coalesced store of rows [0, nvalid) of an LDS tile [ROWS][NC] (element type
-// T) to global memory with 16-byte accesses.
-template <int NT, int ROWS, int NC, typename T>
-__device__ __forceinline__ void store_tile(T* g, int64_t gstride, const T* lds, int ld, int nvalid) {
-  constexpr int V = Vec16<T>::N;
-  constexpr int PER_ROW = NC / V;
-  constexpr int TOTAL = ROWS * PER_ROW;
-  for (int idx = threadIdx.x; idx < TOTAL; idx += NT) {
-    const int r = idx / PER_ROW;
-    const int c = (idx - r * PER_ROW) * V;
-    if (r < nvalid) *reinterpret_cast<uint4*>(g + r * gstride + c) = *reinterpret_cast<const uint4*>(lds + r * ld + c);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // intra-chunk forward: one 8-wave workgroup per (chunk, head).
