@@ -363,7 +363,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   }
   __syncthreads();
   const float gC = sGam[C - 1];
-  const int kbeg = kfloor<E>(r0);  // T, P1, P2 vanish above the diagonal
+  // T, P1 and P2 hold exact zeros above the diagonal (and K, Q, KW, U zero
+  // rows past the chunk's end), so products over the chunk's tokens run over
+  // all 64: the extra k-steps add zeros and the loops unroll.
 
   f32x4 dq[HCT], dkb[HCT], dkws[HCT], dBv[HCT];
   float db[4] = {0.f, 0.f, 0.f, 0.f};
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     f32x4 acv = zero4();
-    mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);
+    mma_tile<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, C, lane);
     dBv[j] = acv;
     f32x4 dv;
 #pragma unroll
@@ -472,7 +474,6 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   __syncthreads();
   const E* sKWr = p.kw_is_k ? sK : sKW;
   // ---- phase 6: pairwise terms ------------------------------------------------
-  const int kend = kceil<E>(r0 + 16);
   float gsum[4] = {0.f, 0.f, 0.f, 0.f};
   float kgd = 0.f;
   OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
@@ -485,10 +486,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     f32x4 ak = zero4(), aq = zero4(), aw = zero4();
-    mma_tile_range<E, ROW, ROW>(ak, sP1r, L::LDC, r0, sKWr, L::LD, 16 * ct, 0, kend, lane);    // sum_x P1r kw
-    mma_tile_range<E, ROW, ROW>(aq, sP2, L::LDC, r0, sKWr, L::LD, 16 * ct, 0, kend, lane);     // sum_x P2 kw
-    mma_tile_range<E, COL, ROW>(aw, sP1, L::LDC, r0, sK, L::LD, 16 * ct, kbeg, C, lane);       // sum_t P1 k
-    mma_tile_range<E, COL, ROW>(aw, sP2, L::LDC, r0, sQ, L::LD, 16 * ct, kbeg, C, lane);       // sum_t P2 q
+    mma_tile<E, ROW, ROW>(ak, sP1r, L::LDC, r0, sKWr, L::LD, 16 * ct, C, lane);    // sum_x P1r kw
+    mma_tile<E, ROW, ROW>(aq, sP2, L::LDC, r0, sKWr, L::LD, 16 * ct, C, lane);     // sum_x P2 kw
+    mma_tile<E, COL, ROW>(aw, sP1, L::LDC, r0, sK, L::LD, 16 * ct, C, lane);       // sum_t P1 k
+    mma_tile<E, COL, ROW>(aw, sP2, L::LDC, r0, sQ, L::LD, 16 * ct, C, lane);       // sum_t P2 q
     f32x4 dk, dkw;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
