@@ -70,6 +70,33 @@ def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
     }
 
 
+# The kernel each timed stage launches for the default BF16, d = 128 workloads,
+# as rocprofv3 names it (template arguments with bf16 for unsigned short).
+STAGE_KERNEL = {
+    "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true>",
+    "fwd_state": "chunk_state_fwd_kernel<bf16, 128, 64, false>",
+    "bwd_state": "chunk_state_bwd_kernel<bf16, 128, 64, false>",
+    "bwd_chunk": "chunk_fused_bwd_kernel<bf16, 128, bf16>",
+    "decode": "decode_kernel<bf16, 128, 512>",
+}
+TRAFFIC_PROFILE = ROOT / "profiles" / "pkda_chunk_c2_decode_c4_hbm_traffic.md"
+
+
+def profiled_traffic(kernel: str) -> dict | None:
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE passes, scaled by the counters of a 1 GiB copy),
+    or None when the summary has no row for this kernel."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 4 and cells[0].strip("`").startswith(kernel + "("):
+            read_mib, write_mib = float(cells[2]), float(cells[3])
+            return {"bytes": (read_mib + write_mib) * 2**20, "read_MiB": read_mib, "written_MiB": write_mib,
+                    "source": TRAFFIC_PROFILE.name}
+    return None
+
+
 def l2norm(t: torch.Tensor) -> torch.Tensor:
     f = t.float()
     return f * torch.rsqrt(f.square().sum(-1, keepdim=True) + 1e-6)
@@ -296,6 +323,7 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
     torch.cuda.synchronize()
     kern_ms = t0.elapsed_time(t1) / (reps * G)
     nbytes = 2 * N * H * D * D * 4 + N * H * (2 * (2 * D + D) + 2 * 2) + N * H * D * 2 + 4 * N
+    traffic = profiled_traffic(STAGE_KERNEL["decode"])
     return {
         "workload": "c4 decode: 256 live of 512 slots, H32 d128, fp32 state, bf16 q/k/v",
         "steps": steps,
@@ -307,11 +335,13 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
         "bytes_per_step": nbytes,
         "roofline": {
             "bound": "hbm",
+            "kernel": STAGE_KERNEL["decode"],
             "achieved": nbytes / (kern_ms / 1e3) / 1e9,
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": nbytes / (kern_ms / 1e3) / HBM_PEAK,
-            "traffic": None,
+            "traffic": None if traffic is None else traffic["bytes"],
+            "traffic_detail": traffic,
         },
     }
 
@@ -422,6 +452,8 @@ def main() -> None:
     dom = max(stage_ms, key=stage_ms.get)
     dom_flops = token_heads * per_th[dom]
     achieved = dom_flops / (stage_ms[dom] / 1e3)
+    # the committed PMC summary is of the c2 workload
+    dom_traffic = profiled_traffic(STAGE_KERNEL[dom]) if args.workload == "c2" else None
     result = {
         "metric": "PKDA fwd+bwd tokens/s & %MFMA peak; decode state-update GB/s & %HBM peak",
         "value": ntok / (ms / 1e3),
@@ -451,7 +483,9 @@ def main() -> None:
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK,
-            "traffic": None,
+            "traffic": None if dom_traffic is None else dom_traffic["bytes"],
+            "traffic_detail": dom_traffic,
+            "hbm_GBps": None if dom_traffic is None else dom_traffic["bytes"] / (stage_ms[dom] / 1e3) / 1e9,
         },
         "stage_ms": stage_ms,
     }
