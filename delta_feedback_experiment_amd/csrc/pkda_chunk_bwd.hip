@@ -206,8 +206,8 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
       store_acc_lds(sdS, L::LDV, dS[i], 16 * rt, 16 * ct, lane);
-      T* hb = static_cast<T*>(p.dh) + ((int64_t)cid * H + h) * D * D + v0;
-      store_acc_global<T>(hb, D, dS[i], 16 * rt, 16 * ct, D, lane);
+      T* hb = static_cast<T*>(p.dh) + ((int64_t)cid * H + h) * D * D;
+      store_acc_tile(hb + tile_offset(D, rt, v0 / 16 + ct), dS[i], lane);
     }
     __syncthreads();
     if (jc > 0) prefetch(jc - 1);
@@ -347,13 +347,13 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   {
     RegTile<kFW, C, D, T> rU, rdO, rdU, rV;
     RegTile<kFW, C, C, T> rT;
-    RegTile<kFW, D, D, T> rH;
+    TiledTile<kFW, D, T> rH;
     rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
     rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
     rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
     rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
     rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
-    rH.load(hsrc, D, D);
+    rH.load(hsrc);
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
@@ -405,10 +405,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   __syncthreads();
   // ---- phase 2: dBv over dU; Q, KW and dS_C start their way in -------------
   RegTile<kFW, C, D, T> rQ, rKW;
-  RegTile<kFW, D, D, T> rdH;
+  TiledTile<kFW, D, T> rdH;
   rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
   if (!p.kw_is_k) rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, len);
-  rdH.load(dhsrc, D, D);
+  rdH.load(dhsrc);
 #pragma unroll
   for (int j = 0; j < HCT; ++j) store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
   __syncthreads();
@@ -442,13 +442,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   float hd = 0.f;
   {
     constexpr int V = Vec16<T>::N;
-    constexpr int PER_ROW = D / V;
-    constexpr int TOTAL = D * PER_ROW;
-    static_assert(TOTAL % kFW == 0, "dS_C tile covers the workgroup");
 #pragma unroll
-    for (int i = 0; i < TOTAL / kFW; ++i) {
-      const int idx = tid + i * kFW;
-      const int r = idx / PER_ROW, c = (idx - r * PER_ROW) * V;
+    for (int i = 0; i < TiledTile<kFW, D, T>::ITER; ++i) {
+      int r, c;
+      rdH.pos(i, r, c);
       float x[V], hv[V];
       Vec16<T>::unpack(rdH.r[i], x);
       lds_vec<V>(sH + r * L::LD + c, hv);
@@ -650,11 +647,11 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
   {
     RegTile<kFW, C, D, T> rU, rdO, rdU;
-    RegTile<kFW, D, D, T> rH;
+    TiledTile<kFW, D, T> rH;
     rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
     rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
     rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
-    rH.load(hsrc, D, D);
+    rH.load(hsrc);
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
@@ -689,27 +686,33 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   __syncthreads();
   // ---- phase 2: dH replaces h; per-row sum(h * dH) ----------------------------
+  // (dH arrives tile-major: per-piece partial sums go through the dT region,
+  // which phase 3 fills only later, and are summed per row in a fixed order)
   {
     constexpr int V = Vec16<T>::N;
-    constexpr int PER_ROW = D / V;  // consecutive threads of one row
-    static_assert(PER_ROW == 8 || PER_ROW == 16, "row of 8 or 16 vectors");
-    constexpr int TOTAL = D * PER_ROW;
+    constexpr int PPR = D / V;  // pieces per row
+    float* sPart = reinterpret_cast<float*>(smem + L::off_dT);
+    static_assert(D * PPR * 4 <= L::CT, "row partials fit the dT region");
+    TiledTile<kFW, D, T> rdH;
+    rdH.load(dhsrc);
 #pragma unroll
-    for (int i = 0; i < (TOTAL + kFW - 1) / kFW; ++i) {
-      const int idx = tid + i * kFW;
-      const int r = idx / PER_ROW, c = (idx - r * PER_ROW) * V;
+    for (int i = 0; i < TiledTile<kFW, D, T>::ITER; ++i) {
+      int r, c;
+      rdH.pos(i, r, c);
+      float x[V], hv[V];
+      Vec16<T>::unpack(rdH.r[i], x);
+      lds_vec<V>(sH + r * L::LD + c, hv);
       float part = 0.f;
-      if (idx < TOTAL) {
-        float x[V], hv[V];
-        Vec16<T>::load(dhsrc + r * D + c, x);
-        lds_vec<V>(sH + r * L::LD + c, hv);
 #pragma unroll
-        for (int j = 0; j < V; ++j) part += hv[j] * x[j];
-        store_vec<V>(sH + r * L::LD + c, x);
-      }
-#pragma unroll
-      for (int off = 1; off < PER_ROW; off <<= 1) part += __shfl_xor(part, off);
-      if (idx < TOTAL && (lane & (PER_ROW - 1)) == 0) sHD[r] = part;
+      for (int j = 0; j < V; ++j) part += hv[j] * x[j];
+      *reinterpret_cast<uint4*>(sH + r * L::LD + c) = rdH.r[i];  // this thread's own slots
+      sPart[r * PPR + c / V] = part;
+    }
+    __syncthreads();
+    if (tid < D) {
+      float sum = 0.f;
+      for (int k = 0; k < PPR; ++k) sum += sPart[tid * PPR + k];
+      sHD[tid] = sum;
     }
   }
   __syncthreads();

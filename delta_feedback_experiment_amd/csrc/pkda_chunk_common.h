@@ -22,6 +22,7 @@ constexpr int state_threads(int D, int BV) { return ((D / 16) * (BV / 16)) % 16 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // ----------------------------------------------------------------------------
 // Chunk geometry
@@ -226,7 +227,10 @@ template <> __device__ __forceinline__ float from_e<bf16_t>(bf16_t x) { return b
 
 // Row padding of LDS tiles: keeps 16-byte alignment and spreads rows over banks.
 template <typename E> struct Pad;
-template <> struct Pad<bf16_t> { static constexpr int v = 8; };
+#ifndef PKDA_BF16_PAD
+#define PKDA_BF16_PAD 8
+#endif
+template <> struct Pad<bf16_t> { static constexpr int v = PKDA_BF16_PAD; };
 template <> struct Pad<float> { static constexpr int v = 4; };
 
 // ----------------------------------------------------------------------------
@@ -391,10 +395,12 @@ struct RegTile {
   static constexpr int TOTAL = ROWS * PER_ROW;
   static constexpr int ITER = (TOTAL + NT - 1) / NT;
   uint4 r[ITER];
-  __device__ __forceinline__ void load(const T* g, int64_t gstride, int nvalid) {
+  __device__ __forceinline__ void load(const T* g, int64_t gstride, int nvalid) { load_as(threadIdx.x, g, gstride, nvalid); }
+  // as thread t of the NT that share the tile
+  __device__ __forceinline__ void load_as(int t, const T* g, int64_t gstride, int nvalid) {
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
-      const int idx = threadIdx.x + i * NT;
+      const int idx = t + i * NT;
       const int row = idx / PER_ROW;
       const int c = (idx - row * PER_ROW) * V;
       r[i] = (idx < TOTAL && row < nvalid) ? *reinterpret_cast<const uint4*>(g + row * gstride + c)
@@ -411,10 +417,11 @@ struct RegTile {
       if (idx < TOTAL) r[i] = *reinterpret_cast<const uint4*>(g + row * gstride + c);
     }
   }
-  __device__ __forceinline__ void store(T* lds, int ld) const {
+  __device__ __forceinline__ void store(T* lds, int ld) const { store_as(threadIdx.x, lds, ld); }
+  __device__ __forceinline__ void store_as(int t, T* lds, int ld) const {
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
-      const int idx = threadIdx.x + i * NT;
+      const int idx = t + i * NT;
       if (TOTAL % NT != 0 && idx >= TOTAL) break;
       const int row = idx / PER_ROW;
       const int c = (idx - row * PER_ROW) * V;
@@ -439,6 +446,38 @@ struct RegTile {
   }
 };
 
+// A tile-major [D x D] state checkpoint (see tile_offset) held in registers:
+// NT threads read it as consecutive 16-byte pieces (fully coalesced); pos()
+// gives the (row, first column) of piece i of this thread in the [D x D]
+// matrix, and store() writes the pieces to a row-major LDS tile.
+template <int NT, int D, typename T>
+struct TiledTile {
+  static constexpr int V = Vec16<T>::N;
+  static constexpr int TOTAL = D * D / V;
+  static constexpr int ITER = (TOTAL + NT - 1) / NT;
+  static constexpr int PER_TILE = 256 / V;
+  static_assert(TOTAL % NT == 0, "pieces split evenly over the threads");
+  uint4 r[ITER];
+  __device__ __forceinline__ void load(const T* g) {
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) r[i] = reinterpret_cast<const uint4*>(g)[threadIdx.x + i * NT];
+  }
+  __device__ __forceinline__ static void pos(int i, int& row, int& col) {
+    const int k = threadIdx.x + i * NT;
+    const int tile = k / PER_TILE, e = (k % PER_TILE) * V;
+    row = (tile / (D / 16)) * 16 + e / 16;
+    col = (tile % (D / 16)) * 16 + e % 16;
+  }
+  __device__ __forceinline__ void store(T* lds, int ld) const {
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      int row, col;
+      pos(i, row, col);
+      *reinterpret_cast<uint4*>(lds + row * ld + col) = r[i];
+    }
+  }
+};
+
 // Row-scaled variant helper: f(r, c, x) = s[r] * x.
 struct RowScale {
   const float* s;
@@ -458,15 +497,109 @@ __device__ __forceinline__ void store_rows(T* g, int64_t gstride, const E* lds, 
   }
 }
 
-// Store an accumulator tile (origin m0, n0) to global with row mask.
+// Store an accumulator tile (origin m0, n0) to global with row mask.  The
+// four lanes of a quad (16q + 4c + t, t = 0..3) hold columns 4c..4c+3 of rows
+// 4q..4q+3; two DPP exchanges inside the quad transpose that 4 x 4 block so
+// lane t holds row 4q + t, columns 4c..4c+3, written with one 8-byte (bf16)
+// or 16-byte (FP32) store instead of four scattered element stores.
+// Requires g + n0 and gstride to keep 4-element alignment.
+// Round-to-nearest-even of two floats into one packed pair (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2_t v;
+  v[0] = static_cast<__bf16>(a);
+  v[1] = static_cast<__bf16>(b);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint32_t quad_swap(uint32_t x, int ctrl_is_pair) {
+  return ctrl_is_pair ? __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true)   // lane ^ 1
+                      : __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);  // lane ^ 2
+}
+
+// 4 x 4 transpose of 16-bit elements in a quad: in, lane t holds column t as
+// (v0 = rows 0,1; v1 = rows 2,3); out, row t as (v0 = cols 0,1; v1 = cols 2,3).
+__device__ __forceinline__ void quad_transpose_b16(uint32_t& v0, uint32_t& v1, int lane) {
+  const bool odd = lane & 1, hi = lane & 2;
+  const uint32_t p0 = quad_swap(v0, 1), p1 = quad_swap(v1, 1);
+  v0 = odd ? ((p0 >> 16) | (v0 & 0xffff0000u)) : ((v0 & 0xffffu) | (p0 << 16));
+  v1 = odd ? ((p1 >> 16) | (v1 & 0xffff0000u)) : ((v1 & 0xffffu) | (p1 << 16));
+  const uint32_t s = quad_swap(hi ? v0 : v1, 0);
+  if (hi) v0 = s; else v1 = s;
+}
+
+// 4 x 4 transpose of 32-bit elements in a quad (a[j] = row j of column t in,
+// column j of row t out).
+__device__ __forceinline__ void quad_transpose_b32(float* a, int lane) {
+  const bool odd = lane & 1, hi = lane & 2;
+  const uint32_t r0 = quad_swap(__float_as_uint(odd ? a[0] : a[1]), 1);
+  const uint32_t r1 = quad_swap(__float_as_uint(odd ? a[2] : a[3]), 1);
+  if (odd) { a[0] = __uint_as_float(r0); a[2] = __uint_as_float(r1); }
+  else { a[1] = __uint_as_float(r0); a[3] = __uint_as_float(r1); }
+  const uint32_t s0 = quad_swap(__float_as_uint(hi ? a[0] : a[2]), 0);
+  const uint32_t s1 = quad_swap(__float_as_uint(hi ? a[1] : a[3]), 0);
+  if (hi) { a[0] = __uint_as_float(s0); a[1] = __uint_as_float(s1); }
+  else { a[2] = __uint_as_float(s0); a[3] = __uint_as_float(s1); }
+}
+
+// Row and first column of the lane's piece after the transpose.
+__device__ __forceinline__ int quad_row(int lane) { return 4 * (lane >> 4) + (lane & 3); }
+__device__ __forceinline__ int quad_col(int lane) { return 4 * ((lane >> 2) & 3); }
+
+// Store packed bf16 pairs of an accumulator-layout tile (v0 = rows 4q, 4q+1;
+// v1 = rows 4q+2, 4q+3 of column lane & 15) by rows.
+__device__ __forceinline__ void store_packed_rows(bf16_t* g, int64_t gstride, uint32_t v0, uint32_t v1, int m0, int n0,
+                                                  int nvalid, int lane) {
+  quad_transpose_b16(v0, v1, lane);
+  const int r = m0 + quad_row(lane);
+  if (r < nvalid) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2* dst = reinterpret_cast<u32x2*>(g + r * gstride + n0 + quad_col(lane));
+#ifdef PKDA_NT_STORES
+    __builtin_nontemporal_store(u32x2{v0, v1}, dst);
+#else
+    *dst = u32x2{v0, v1};
+#endif
+  }
+}
+
+// Tile-major [D x D] state checkpoints: 16 x 16 tiles, each row-major and
+// contiguous (256 elements), tile (rt, ct) at element (rt * (D / 16) + ct) * 256.
+// One accumulator tile is one contiguous 512-byte write.
+__device__ __forceinline__ void store_packed_tile(bf16_t* tile, uint32_t v0, uint32_t v1, int lane) {
+  quad_transpose_b16(v0, v1, lane);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2*>(tile + quad_row(lane) * 16 + quad_col(lane)) = u32x2{v0, v1};
+}
+__device__ __forceinline__ void store_acc_tile(bf16_t* tile, const f32x4& acc, int lane) {
+  store_packed_tile(tile, pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), lane);
+}
+__device__ __forceinline__ void store_acc_tile(float* tile, const f32x4& acc, int lane) {
+  float a[4] = {acc[0], acc[1], acc[2], acc[3]};
+  quad_transpose_b32(a, lane);
+  *reinterpret_cast<float4*>(tile + quad_row(lane) * 16 + quad_col(lane)) = make_float4(a[0], a[1], a[2], a[3]);
+}
+__device__ __forceinline__ int64_t tile_offset(int D, int rt, int ct) { return ((int64_t)rt * (D / 16) + ct) * 256; }
+
 template <typename T>
 __device__ __forceinline__ void store_acc_global(T* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
-                                                 int lane) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = m0 + acc_row(lane, j);
-    if (r < nvalid) io<T>::store(g + r * gstride + n0 + acc_col(lane), acc[j]);
-  }
+                                                 int lane);
+template <>
+__device__ __forceinline__ void store_acc_global<bf16_t>(bf16_t* g, int64_t gstride, const f32x4& acc, int m0, int n0,
+                                                         int nvalid, int lane) {
+  bf16x2_t a, b;
+  a[0] = static_cast<__bf16>(acc[0]);
+  a[1] = static_cast<__bf16>(acc[1]);
+  b[0] = static_cast<__bf16>(acc[2]);
+  b[1] = static_cast<__bf16>(acc[3]);
+  store_packed_rows(g, gstride, __builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), m0, n0, nvalid, lane);
+}
+template <>
+__device__ __forceinline__ void store_acc_global<float>(float* g, int64_t gstride, const f32x4& acc, int m0, int n0,
+                                                        int nvalid, int lane) {
+  float a[4] = {acc[0], acc[1], acc[2], acc[3]};
+  quad_transpose_b32(a, lane);
+  const int r = m0 + quad_row(lane);
+  if (r < nvalid) *reinterpret_cast<float4*>(g + r * gstride + n0 + quad_col(lane)) = make_float4(a[0], a[1], a[2], a[3]);
 }
 
 template <typename E>
@@ -491,6 +624,68 @@ __device__ __forceinline__ void row_sums_64(const float* lds, int ld, int ncols,
     for (int c = 0; c < ncols; ++c) s += lds[tid * ld + c];
     out[tid] = s;
   }
+}
+
+// ----------------------------------------------------------------------------
+// Register-resident bf16 MFMA operands.  An accumulator tile X (lane 16q + i
+// holds X[4q + j][i]) serves as the B operand of a 16x16x32 step over X's rows
+// without leaving registers when the step takes its 32 k indices in the order
+//   lane group q: rows 4q..4q+3 of tile 2kk, then rows 4q..4q+3 of tile 2kk+1,
+// i.e. k = 32kk + {4q..4q+3} and 32kk + 16 + {4q..4q+3}.  The A operand of
+// the same step is read from LDS in that order.  The k order inside one MFMA
+// does not change the product.
+// ----------------------------------------------------------------------------
+
+// B operand of step kk from accumulator tiles a (rows 32kk..) and b (rows 32kk + 16..).
+__device__ __forceinline__ s16x8_t pack_acc_pair(const f32x4& a, const f32x4& b) {
+  const uint4 w = make_uint4(pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                             pack_bf16x2(b[2], b[3]));
+  return __builtin_bit_cast(s16x8_t, w);
+}
+
+// The same with every element scaled: sa[j] for tile a, sb[j] for tile b.
+__device__ __forceinline__ s16x8_t pack_acc_pair_scaled(const f32x4& a, const float* sa, const f32x4& b,
+                                                        const float* sb) {
+  const uint4 w = make_uint4(pack_bf16x2(a[0] * sa[0], a[1] * sa[1]), pack_bf16x2(a[2] * sa[2], a[3] * sa[3]),
+                             pack_bf16x2(b[0] * sb[0], b[1] * sb[1]), pack_bf16x2(b[2] * sb[2], b[3] * sb[3]));
+  return __builtin_bit_cast(s16x8_t, w);
+}
+
+// A operand in that k order from a row-major LDS tile (element (m, k) at
+// A[m * lda + k], A offset to row m0): two 8-byte reads per lane.
+__device__ __forceinline__ s16x8_t lds_a_perm(const bf16_t* A, int lda, int k0, int lane) {
+  const bf16_t* p = A + (lane & 15) * lda + k0 + 4 * (lane >> 4);
+  const uint2 lo = *reinterpret_cast<const uint2*>(p);
+  const uint2 hi = *reinterpret_cast<const uint2*>(p + 16);
+  return __builtin_bit_cast(s16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
+// A operand in that k order from a k-major LDS tile (element (m, k) at
+// A[k * lda + m], A offset to column m0), and equally the B operand of a
+// k-major tile (element (k, n) at B[k * ldb + n]): two transposing reads.
+__device__ __forceinline__ s16x8_t lds_kmajor_perm(const bf16_t* A, int lda, int k0, int lane) {
+  const int i = lane & 15, q = lane >> 4;
+  const bf16_t* src = A + (k0 + 4 * q + (i >> 2)) * lda + 4 * (i & 3);
+  const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(src));
+  const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(src + 16 * lda));
+  const s16x4_t l = __builtin_bit_cast(s16x4_t, lo), h = __builtin_bit_cast(s16x4_t, hi);
+  return s16x8_t{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
+}
+
+// Every element of an operand in that k order scaled by the factor of its k
+// index (sf: 8 factors, lane's order), rounded back to bf16.
+__device__ __forceinline__ s16x8_t scale_frag(const s16x8_t& x, const float* sf) {
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    w[e] = pack_bf16x2(bf16_to_f32(static_cast<bf16_t>(x[2 * e])) * sf[2 * e],
+                       bf16_to_f32(static_cast<bf16_t>(x[2 * e + 1])) * sf[2 * e + 1]);
+  return __builtin_bit_cast(s16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+__device__ __forceinline__ void mfma_bf16(f32x4& acc, const s16x8_t& a, const s16x8_t& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), acc,
+                                                0, 0, 0);
 }
 
 }  // namespace pkda

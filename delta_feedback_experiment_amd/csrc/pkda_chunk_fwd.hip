@@ -23,6 +23,8 @@
 //   FP32 state slice lives in MFMA accumulators for the whole document; each
 //   chunk it is published to LDS (as the B operand), U, O and the update are
 //   MFMA products.
+#include <type_traits>
+
 #include "pkda_chunk_common.h"
 
 namespace pkda {
@@ -590,8 +592,8 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
       const int rt = ti / NCT, ct = ti % NCT;
       store_acc_lds(sS, L::LDV, S[i], 16 * rt, 16 * ct, lane);
       if (p.h) {
-        T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D + v0;
-        store_acc_global<T>(hb, D, S[i], 16 * rt, 16 * ct, D, lane);
+        T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D;
+        store_acc_tile(hb + tile_offset(D, rt, v0 / 16 + ct), S[i], lane);
       }
     }
     __syncthreads();
@@ -656,6 +658,225 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
   }
 }
 
+// ---------------------------------------------------------------------------
+// per-document state pass, BF16 with a per-head gate: register-resident form
+//
+// One workgroup per (document, head, BV value columns): BV/16 compute waves,
+// each owning 16 value columns, and kRrLoaders loader waves.  A compute wave
+// keeps its S [D x 16] slice in MFMA accumulators and the chunk's U [64 x 16]
+// in registers; both feed the next products directly as B operands (the k
+// order of pack_acc_pair), so a chunk has no LDS round trip of S or U and no
+// barrier between its products:
+//   U = u - W S,   O = diag(s e^G)(Q S) + Aqk U,
+//   S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U.
+// The loader waves move each chunk's read-only tiles (W, Q, KW, Aqk, the u
+// slice and G) from global memory into a double-buffered LDS stage one chunk
+// ahead.  They form two groups that take alternate chunks, each holding one
+// chunk in registers, so two chunks' loads are in flight while one chunk
+// computes and each wave only ever waits for its own loads (never for a
+// compute wave's stores).  One barrier per chunk.
+// ---------------------------------------------------------------------------
+constexpr int kRrLoaders = 4;  // two groups of two waves
+
+template <int D, int BV>
+struct RrFwdLayout {
+  static constexpr int LD = D + Pad<bf16_t>::v;
+  static constexpr int LDV = BV + Pad<bf16_t>::v;
+  static constexpr int LDC = C + Pad<bf16_t>::v;
+  static constexpr int off_W = 0;
+  static constexpr int off_Q = off_W + C * LD * 2;
+  static constexpr int off_KW = off_Q + C * LD * 2;
+  static constexpr int off_A = off_KW + C * LD * 2;
+  static constexpr int off_U = off_A + C * LDC * 2;
+  static constexpr int off_G = off_U + C * LDV * 2;
+  static constexpr int BUF = off_G + C * 4;
+  static constexpr int bytes = 2 * BUF;
+  static_assert(BUF % 16 == 0, "16-byte aligned stages");
+};
+
+template <int D, int BV>
+__global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_rr_kernel(FwdParams p) {
+  using L = RrFwdLayout<D, BV>;
+  using T = bf16_t;
+  constexpr int NC = BV / 16;           // compute waves
+  constexpr int NKT = D / 16;           // 16-row tiles of the state slice
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
+  const int H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t gs = (int64_t)H * D;
+  int first, count, dstart, dlen;
+  doc_chunks(p.geom, n, first, count, dstart, dlen);
+  const bool loader = wave >= NC;
+  constexpr int NGT = 64 * kRrLoaders / 2;         // threads of one loader group
+  const int lgroup = (tid - 64 * NC) / NGT;        // loader group: chunks jc with jc % 2 == lgroup
+  const int lt = (tid - 64 * NC) % NGT;
+
+  if (loader) {
+    // The two roles run separate loops with the same barriers, so neither
+    // keeps the other's registers live.
+    RegTile<NGT, C, D, T> rW, rQ, rKW;
+    RegTile<NGT, C, C, T> rA;
+    RegTile<NGT, C, BV, T> rU;
+    float rg = 0.f;
+    auto load = [&](int jc) {
+      const int cstart = dstart + jc * C;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)cstart * H + h;
+      rW.load_as(lt, static_cast<const T*>(p.w) + row0 * D, gs, clen);
+      rQ.load_as(lt, static_cast<const T*>(p.q) + row0 * D, gs, clen);
+      rKW.load_as(lt, static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+      rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+      rU.load_as(lt, static_cast<const T*>(p.u) + row0 * D + v0, gs, clen);
+      if (lt < C) rg = p.gcum[(int64_t)(cstart + min(lt, clen - 1)) * H + h];  // padded rows repeat the last gate
+    };
+    auto stash = [&](int b) {
+      char* buf = smem + b * L::BUF;
+      rW.store_as(lt, reinterpret_cast<T*>(buf + L::off_W), L::LD);
+      rQ.store_as(lt, reinterpret_cast<T*>(buf + L::off_Q), L::LD);
+      rKW.store_as(lt, reinterpret_cast<T*>(buf + L::off_KW), L::LD);
+      rA.store_as(lt, reinterpret_cast<T*>(buf + L::off_A), L::LDC);
+      rU.store_as(lt, reinterpret_cast<T*>(buf + L::off_U), L::LDV);
+      if (lt < C) reinterpret_cast<float*>(buf + L::off_G)[lt] = rg;
+    };
+    // group g holds chunks g, g + 2, ...; chunk 0 is staged before the loop
+    if (lgroup < count) load(lgroup);
+    if (lgroup == 0 && count > 0) {
+      stash(0);
+      if (count > 2) load(2);
+    }
+    for (int jc = 0; jc < count; ++jc) {
+      __syncthreads();
+      if (((jc + 1) & 1) == lgroup && jc + 1 < count) {
+        stash((jc + 1) & 1);
+        if (jc + 3 < count) load(jc + 3);
+      }
+    }
+    return;
+  }
+
+  const int q4 = 4 * (lane >> 4), il = lane & 15;
+  const int cl = 16 * wave + il;  // this lane's column within the slice (compute waves)
+  const int col0 = v0 + 16 * wave;  // first column of this wave's block
+  const int col = col0 + il;
+  f32x4 S[NKT];
+#pragma unroll
+  for (int rt = 0; rt < NKT; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      S[rt][j] = p.s0 ? p.s0[(((int64_t)n * H + h) * D + 16 * rt + q4 + j) * D + col] : 0.f;
+  const float scale = p.scale;
+
+  for (int jc = 0; jc < count; ++jc) {
+    __syncthreads();
+    const char* buf = smem + (jc & 1) * L::BUF;
+    const T* sW = reinterpret_cast<const T*>(buf + L::off_W);
+    const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
+    const T* sKW = reinterpret_cast<const T*>(buf + L::off_KW);
+    const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
+    const T* sU = reinterpret_cast<const T*>(buf + L::off_U);
+    const float* sG = reinterpret_cast<const float*>(buf + L::off_G);
+    const int cid = first + jc;
+    const int clen = min(C, dlen - jc * C);
+    const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+
+    // S as bf16 B operands; checkpoint the entering state
+    s16x8_t SB[NKT / 2];
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) SB[kk] = pack_acc_pair(S[2 * kk], S[2 * kk + 1]);
+    if (p.h) {
+      T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D;
+#pragma unroll
+      for (int kk = 0; kk < NKT / 2; ++kk) {
+        const uint4 w = __builtin_bit_cast(uint4, SB[kk]);
+        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+      }
+    }
+    // W S and Q S: for each k step the eight tiles are independent accumulators
+    f32x4 WS[4], QS[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) WS[rb] = QS[rb] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) {
+      s16x8_t aw[4], aq[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        aw[rb] = lds_a_perm(sW + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+        aq[rb] = lds_a_perm(sQ + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        mfma_bf16(WS[rb], aw[rb], SB[kk]);
+        mfma_bf16(QS[rb], aq[rb], SB[kk]);
+      }
+    }
+    // U = u - W S
+    f32x4 U[4];
+    T* u_io = static_cast<T*>(p.u) + row0 * D + col0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) U[rb][j] = bf16_to_f32(sU[(16 * rb + q4 + j) * L::LDV + cl]) - WS[rb][j];
+      store_acc_global<T>(u_io, gs, U[rb], 16 * rb, 0, clen, lane);
+    }
+    const s16x8_t UB[2] = {pack_acc_pair(U[0], U[1]), pack_acc_pair(U[2], U[3])};
+    // O = diag(s e^G) Q S + Aqk U   (Aqk is lower triangular: row block rb needs k steps kt <= rb / 2)
+    f32x4 AU[4];
+    {
+      s16x8_t aa[6];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) aa[rb] = lds_a_perm(sA + 16 * rb * L::LDC, L::LDC, 0, lane);
+      aa[4] = lds_a_perm(sA + 32 * L::LDC, L::LDC, 32, lane);
+      aa[5] = lds_a_perm(sA + 48 * L::LDC, L::LDC, 32, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        AU[rb] = zero4();
+        mfma_bf16(AU[rb], aa[rb], UB[0]);
+      }
+      mfma_bf16(AU[2], aa[4], UB[1]);
+      mfma_bf16(AU[3], aa[5], UB[1]);
+    }
+    T* o_out = static_cast<T*>(p.o) + row0 * D + col0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      f32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = scale * expf(sG[16 * rb + q4 + j]) * QS[rb][j] + AU[rb][j];
+      store_acc_global<T>(o_out, gs, o, 16 * rb, 0, clen, lane);
+    }
+    // S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U
+    const float gC = sG[C - 1];
+    s16x8_t UgB[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      float fa[4], fb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        fa[j] = expf(gC - sG[32 * kt + q4 + j]);
+        fb[j] = expf(gC - sG[32 * kt + 16 + q4 + j]);
+      }
+      UgB[kt] = pack_acc_pair_scaled(U[2 * kt], fa, U[2 * kt + 1], fb);
+    }
+    const float decay = expf(gC);
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt) S[rt] = S[rt] * decay;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s16x8_t ak[NKT];
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) ak[rt] = lds_kmajor_perm(sKW + 16 * rt, L::LD, 32 * kt, lane);
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) mfma_bf16(S[rt], ak[rt], UgB[kt]);
+    }
+  }
+  if (p.sT) {
+    float* sb = p.sT + ((int64_t)n * H + h) * D * D + col0;
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt) store_acc_global<float>(sb, D, S[rt], 16 * rt, 0, D, lane);
+  }
+}
+
 template <typename K>
 int set_smem(K kernel, int bytes) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -665,6 +886,26 @@ int set_smem(K kernel, int bytes) {
     return static_cast<int>(e);
   }
   return 0;
+}
+
+// Register-resident state pass: 64 value columns per workgroup, or 32 when
+// that leaves fewer workgroups than compute units.
+template <int D>
+int launch_state_fwd_rr(const FwdParams& p, hipStream_t s) {
+  const int N = p.geom.num_seqs;
+  if (N <= 0) return 0;
+#ifdef PKDA_RR_WIDE
+  constexpr int BW = D;
+#else
+  constexpr int BW = 64;
+#endif
+  const bool narrow = (int64_t)N * p.H * (D / BW) < 256;
+  auto kern = narrow ? chunk_state_fwd_rr_kernel<D, 32> : chunk_state_fwd_rr_kernel<D, BW>;
+  const int bytes = narrow ? RrFwdLayout<D, 32>::bytes : RrFwdLayout<D, BW>::bytes;
+  const int bv = narrow ? 32 : BW;
+  if (int st = set_smem(kern, bytes)) return st;
+  hipLaunchKernelGGL(kern, dim3(N, p.H, D / bv), dim3(64 * (bv / 16 + kRrLoaders)), bytes, s, p);
+  return launch_status("pkda_chunk_fwd(state)");
 }
 
 template <typename T, int D, int BV>
@@ -681,6 +922,9 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
   }
   if (all || (stages & PKDA_STAGE_FWD_STATE)) {
+    if constexpr (std::is_same<T, bf16_t>::value) {
+      if (!p.qg) return launch_state_fwd_rr<D>(p, s);
+    }
     auto kern = p.qg ? chunk_state_fwd_kernel<T, D, BV, true> : chunk_state_fwd_kernel<T, D, BV, false>;
     const int bytes = StateLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
