@@ -74,8 +74,8 @@ def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
 # as rocprofv3 names it (template arguments with bf16 for unsigned short).
 STAGE_KERNEL = {
     "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true>",
-    "fwd_state": "chunk_state_fwd_kernel<bf16, 128, 64, false>",
-    "bwd_state": "chunk_state_bwd_kernel<bf16, 128, 64, false>",
+    "fwd_state": "chunk_state_fwd_rr_kernel<128, 64>",
+    "bwd_state": "chunk_state_bwd_rr_kernel<128, 64>",
     "bwd_chunk": "chunk_fused_bwd_kernel<bf16, 128, bf16>",
     "decode": "decode_kernel<bf16, 128, 512>",
 }

@@ -25,6 +25,8 @@
 //                intermediate in LDS or registers; writes dq, dk, dkw, dv,
 //                dbeta and the cumulative-gate gradient once.
 // Every reduction has a fixed order: results are bitwise reproducible.
+#include <type_traits>
+
 #include "pkda_chunk_common.h"
 
 namespace pkda {
@@ -961,16 +963,243 @@ int set_smem(K kernel, int bytes) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// reverse state pass, BF16 with a per-head gate: register-resident form
+//
+// The structure of the forward's register-resident pass, chunks in reverse:
+// BV/16 compute waves each keep dS [D x 16] in MFMA accumulators and the
+// chunk's dU [64 x 16] in registers, and kRrLoaders loader waves stage the
+// read-only tiles (KW, Q, W, Aqk, the dO slice, G) through a double-buffered
+// LDS stage, two groups taking alternate chunks.  Per chunk:
+//   dU  = Aqk^T dO + diag(e^{G_C - G}) (KW dS)            -> du
+//   dS <- e^{G_C} dS + Q^T diag(s e^G) dO - W^T dU
+// ---------------------------------------------------------------------------
+template <int D, int BV>
+struct RrBwdLayout {
+  static constexpr int LD = D + Pad<bf16_t>::v;
+  static constexpr int LDV = BV + Pad<bf16_t>::v;
+  static constexpr int LDC = C + Pad<bf16_t>::v;
+  static constexpr int off_W = 0;
+  static constexpr int off_Q = off_W + C * LD * 2;
+  static constexpr int off_KW = off_Q + C * LD * 2;
+  static constexpr int off_A = off_KW + C * LD * 2;
+  static constexpr int off_dO = off_A + C * LDC * 2;
+  static constexpr int off_G = off_dO + C * LDV * 2;
+  static constexpr int BUF = off_G + C * 4;
+  static constexpr int bytes = 2 * BUF;
+  static_assert(BUF % 16 == 0, "16-byte aligned stages");
+};
+
+constexpr int kRrLoadersBwd = 4;  // two groups of two waves
+
+template <int D, int BV>
+__global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bwd_rr_kernel(BwdParams p) {
+  using L = RrBwdLayout<D, BV>;
+  using T = bf16_t;
+  constexpr int NC = BV / 16;
+  constexpr int NKT = D / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
+  const int H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t gs = (int64_t)H * D;
+  int first, count, dstart, dlen;
+  doc_chunks(p.geom, n, first, count, dstart, dlen);
+  const bool loader = wave >= NC;
+
+  // chunks are visited in the order s = 0, 1, ... as jc = count - 1 - s
+  if (loader) {
+    constexpr int NGT = 64 * kRrLoadersBwd / 2;
+    const int lgroup = (tid - 64 * NC) / NGT;  // takes visits s with s % 2 == lgroup
+    const int lt = (tid - 64 * NC) % NGT;
+    RegTile<NGT, C, D, T> rW, rQ, rKW;
+    RegTile<NGT, C, C, T> rA;
+    RegTile<NGT, C, BV, T> rdO;
+    float rg = 0.f;
+    auto load = [&](int s) {
+      const int jc = count - 1 - s;
+      const int cstart = dstart + jc * C;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)cstart * H + h;
+      rW.load_as(lt, static_cast<const T*>(p.w) + row0 * D, gs, clen);
+      rQ.load_as(lt, static_cast<const T*>(p.q) + row0 * D, gs, clen);
+      rKW.load_as(lt, static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+      rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+      rdO.load_as(lt, static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen);
+      if (lt < C) rg = p.gcum[(int64_t)(cstart + min(lt, clen - 1)) * H + h];
+    };
+    auto stash = [&](int b) {
+      char* buf = smem + b * L::BUF;
+      rW.store_as(lt, reinterpret_cast<T*>(buf + L::off_W), L::LD);
+      rQ.store_as(lt, reinterpret_cast<T*>(buf + L::off_Q), L::LD);
+      rKW.store_as(lt, reinterpret_cast<T*>(buf + L::off_KW), L::LD);
+      rA.store_as(lt, reinterpret_cast<T*>(buf + L::off_A), L::LDC);
+      rdO.store_as(lt, reinterpret_cast<T*>(buf + L::off_dO), L::LDV);
+      if (lt < C) reinterpret_cast<float*>(buf + L::off_G)[lt] = rg;
+    };
+    if (lgroup < count) load(lgroup);
+    if (lgroup == 0 && count > 0) {
+      stash(0);
+      if (count > 2) load(2);
+    }
+    for (int s = 0; s < count; ++s) {
+      __syncthreads();
+      if (((s + 1) & 1) == lgroup && s + 1 < count) {
+        stash((s + 1) & 1);
+        if (s + 3 < count) load(s + 3);
+      }
+    }
+    return;
+  }
+
+  const int q4 = 4 * (lane >> 4), il = lane & 15;
+  const int col0 = v0 + 16 * wave;
+  f32x4 dS[NKT];
+#pragma unroll
+  for (int rt = 0; rt < NKT; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dS[rt][j] = p.dht ? p.dht[(((int64_t)n * H + h) * D + 16 * rt + q4 + j) * D + col0 + il] : 0.f;
+  const float scale = p.scale;
+
+  for (int s = 0; s < count; ++s) {
+    __syncthreads();
+    const int jc = count - 1 - s;
+    const char* buf = smem + (s & 1) * L::BUF;
+    const T* sW = reinterpret_cast<const T*>(buf + L::off_W);
+    const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
+    const T* sKW = reinterpret_cast<const T*>(buf + L::off_KW);
+    const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
+    const T* sdO = reinterpret_cast<const T*>(buf + L::off_dO);
+    const float* sG = reinterpret_cast<const float*>(buf + L::off_G);
+    const int cid = first + jc;
+    const int clen = min(C, dlen - jc * C);
+    const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+
+    // dS_C as bf16 B operands; checkpoint it (tile-major)
+    s16x8_t dSB[NKT / 2];
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) dSB[kk] = pack_acc_pair(dS[2 * kk], dS[2 * kk + 1]);
+    {
+      T* hb = static_cast<T*>(p.dh) + ((int64_t)cid * H + h) * D * D;
+#pragma unroll
+      for (int kk = 0; kk < NKT / 2; ++kk) {
+        const uint4 w = __builtin_bit_cast(uint4, dSB[kk]);
+        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+      }
+    }
+    // KW dS (eight independent accumulators per k step)
+    f32x4 KS[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) KS[rb] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) {
+      s16x8_t ak[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) ak[rb] = lds_a_perm(sKW + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) mfma_bf16(KS[rb], ak[rb], dSB[kk]);
+    }
+    // dO of this wave's columns as B operands over the tokens
+    const s16x8_t dOB[2] = {lds_kmajor_perm(sdO + 16 * wave, L::LDV, 0, lane),
+                            lds_kmajor_perm(sdO + 16 * wave, L::LDV, 32, lane)};
+    // dU = Aqk^T dO + diag(e^{G_C - G}) KW dS   (Aqk^T row block rb needs k steps kt >= rb / 2)
+    const float gC = sG[C - 1];
+    f32x4 dU[4];
+    {
+      s16x8_t aa[6];
+      aa[0] = lds_kmajor_perm(sA + 0, L::LDC, 0, lane);
+      aa[1] = lds_kmajor_perm(sA + 0, L::LDC, 32, lane);
+      aa[2] = lds_kmajor_perm(sA + 16, L::LDC, 0, lane);
+      aa[3] = lds_kmajor_perm(sA + 16, L::LDC, 32, lane);
+      aa[4] = lds_kmajor_perm(sA + 32, L::LDC, 32, lane);
+      aa[5] = lds_kmajor_perm(sA + 48, L::LDC, 32, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) dU[rb] = zero4();
+      mfma_bf16(dU[0], aa[0], dOB[0]);
+      mfma_bf16(dU[1], aa[2], dOB[0]);
+      mfma_bf16(dU[0], aa[1], dOB[1]);
+      mfma_bf16(dU[1], aa[3], dOB[1]);
+      mfma_bf16(dU[2], aa[4], dOB[1]);
+      mfma_bf16(dU[3], aa[5], dOB[1]);
+    }
+    T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dU[rb][j] += expf(gC - sG[16 * rb + q4 + j]) * KS[rb][j];
+      store_acc_global<T>(du_out, gs, dU[rb], 16 * rb, 0, clen, lane);
+    }
+    // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU
+    s16x8_t dOgB[2], dUnB[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = scale * expf(sG[32 * kt + (e < 4 ? 0 : 16) + q4 + (e & 3)]);
+      dOgB[kt] = scale_frag(dOB[kt], f);
+      dUnB[kt] = pack_acc_pair(-dU[2 * kt], -dU[2 * kt + 1]);
+    }
+    const float decay = expf(gC);
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt) dS[rt] = dS[rt] * decay;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s16x8_t aq[NKT], aw[NKT];
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) {
+        aq[rt] = lds_kmajor_perm(sQ + 16 * rt, L::LD, 32 * kt, lane);
+        aw[rt] = lds_kmajor_perm(sW + 16 * rt, L::LD, 32 * kt, lane);
+      }
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) {
+        mfma_bf16(dS[rt], aq[rt], dOgB[kt]);
+        mfma_bf16(dS[rt], aw[rt], dUnB[kt]);
+      }
+    }
+  }
+  if (p.dh0) {
+    float* db = p.dh0 + ((int64_t)n * H + h) * D * D + col0;
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt) store_acc_global<float>(db, D, dS[rt], 16 * rt, 0, D, lane);
+  }
+}
+
+// Register-resident reverse pass: 64 value columns per workgroup, or 32 when
+// that leaves fewer workgroups than compute units.
+template <int D>
+int launch_state_bwd_rr(const BwdParams& p, hipStream_t s) {
+  const int N = p.geom.num_seqs;
+  if (N <= 0) return 0;
+  const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
+  auto kern = narrow ? chunk_state_bwd_rr_kernel<D, 32> : chunk_state_bwd_rr_kernel<D, 64>;
+  const int bytes = narrow ? RrBwdLayout<D, 32>::bytes : RrBwdLayout<D, 64>::bytes;
+  const int bv = narrow ? 32 : 64;
+  if (int st = set_smem(kern, bytes)) return st;
+  hipLaunchKernelGGL(kern, dim3(N, p.H, D / bv), dim3(64 * (bv / 16 + kRrLoadersBwd)), bytes, s, p);
+  return launch_status("pkda_chunk_bwd(state)");
+}
+
 template <typename T, int D, int BV, typename OT>
 int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const int N = p.geom.num_seqs;
   const bool all = stages == 0;
   if (all || (stages & PKDA_STAGE_BWD_STATE)) {
-    auto kern = p.qg ? chunk_state_bwd_kernel<T, D, BV, true> : chunk_state_bwd_kernel<T, D, BV, false>;
-    const int bytes = StateBwdLayout<T, D, BV>::bytes;
-    if (int st = set_smem(kern, bytes)) return st;
-    if (N > 0) hipLaunchKernelGGL(kern, dim3(N, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
-    if (int st = launch_status("pkda_chunk_bwd(state)")) return st;
+    bool done = false;
+    if constexpr (std::is_same<T, bf16_t>::value) {
+      if (!p.qg) {  // BF16, per-head gate: the register-resident pass
+        if (int st = launch_state_bwd_rr<D>(p, s)) return st;
+        done = true;
+      }
+    }
+    if (!done) {
+      auto kern = p.qg ? chunk_state_bwd_kernel<T, D, BV, true> : chunk_state_bwd_kernel<T, D, BV, false>;
+      const int bytes = StateBwdLayout<T, D, BV>::bytes;
+      if (int st = set_smem(kern, bytes)) return st;
+      if (N > 0) hipLaunchKernelGGL(kern, dim3(N, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
+      if (int st = launch_status("pkda_chunk_bwd(state)")) return st;
+    }
   }
   if (num_chunks == 0) return 0;
   if (all || (stages & PKDA_STAGE_BWD_CHUNK)) {

@@ -923,7 +923,7 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
   }
   if (all || (stages & PKDA_STAGE_FWD_STATE)) {
     if constexpr (std::is_same<T, bf16_t>::value) {
-      if (!p.qg) return launch_state_fwd_rr<D>(p, s);
+      if (!p.qg) return launch_state_fwd_rr<D>(p, s);  // BF16, per-head gate: the register-resident pass
     }
     auto kern = p.qg ? chunk_state_fwd_kernel<T, D, BV, true> : chunk_state_fwd_kernel<T, D, BV, false>;
     const int bytes = StateLayout<T, D, BV>::bytes;
