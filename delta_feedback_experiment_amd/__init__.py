@@ -4,12 +4,15 @@ A drop-in for the PKDA recurrence path of a9lim/delta-feedback-experiment
 (``delta_feedback_experiment/pkda.py:412-475`` and
 ``delta_feedback_experiment/fla_ops.py:252-569``).  The compute lives in
 ``libpkda_gfx950.so`` (``csrc/*.hip``, C ABI in ``include/pkda_gfx950.h``);
-this package is the PyTorch-facing host side.  Nothing here falls back to the
+this package is the PyTorch-facing host side.  It also carries the
+recurrence's producer, the fused Q/K/V short convolution + SiLU + L2 norm
+(``delta_feedback_experiment/fla_ops.py:134-249``).  Nothing here falls back to the
 CPU: without a HIP device and the built library every operator raises.
 """
 
 from .chunk import chunk_pkda
+from .conv import pkda_qkv_conv
 from .ops import pkda_recurrence
 from .pkda import fused_recurrent_pkda, pkda_decode_step_
 
-__all__ = ["chunk_pkda", "fused_recurrent_pkda", "pkda_decode_step_", "pkda_recurrence"]
+__all__ = ["chunk_pkda", "fused_recurrent_pkda", "pkda_decode_step_", "pkda_qkv_conv", "pkda_recurrence"]

@@ -97,7 +97,18 @@ class ChunkBwdArgs(ctypes.Structure):
     ]
 
 
-_ARG_KINDS = {0: RecurrentArgs, 1: GateArgs, 2: PrecondArgs, 3: ChunkFwdArgs, 4: ChunkBwdArgs}
+class QkvConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", c_int32), ("dtype", c_int32), ("w_dtype", c_int32),
+        ("batch", c_int32), ("seqlen", c_int32), ("width", c_int32), ("head_dim", c_int32),
+        ("norm_channels", c_int32), ("conv_size", c_int32), ("eps", c_float),
+        ("x", c_void_p), ("weight", c_void_p), ("q", c_void_p), ("k", c_void_p), ("v", c_void_p),
+        ("dq", c_void_p), ("dk", c_void_p), ("dv", c_void_p), ("dx", c_void_p), ("dw", c_void_p),
+        ("dw_part", c_void_p),
+    ]
+
+
+_ARG_KINDS = {0: RecurrentArgs, 1: GateArgs, 2: PrecondArgs, 3: ChunkFwdArgs, 4: ChunkBwdArgs, 5: QkvConvArgs}
 _LIB: ctypes.CDLL | None = None
 
 
@@ -147,11 +158,14 @@ def lib() -> ctypes.CDLL:
         ("pkda_gate_fwd", GateArgs), ("pkda_gate_bwd", GateArgs),
         ("pkda_precond_fwd", PrecondArgs), ("pkda_precond_bwd", PrecondArgs),
         ("pkda_chunk_fwd", ChunkFwdArgs), ("pkda_chunk_bwd", ChunkBwdArgs),
+        ("pkda_qkv_conv_fwd", QkvConvArgs), ("pkda_qkv_conv_bwd", QkvConvArgs),
     ):
         fn = getattr(handle, name, None)
         if fn is not None:
             fn.restype = c_int32
             fn.argtypes = [POINTER(struct), c_void_p]
+    handle.pkda_qkv_conv_workspace.restype = c_int64
+    handle.pkda_qkv_conv_workspace.argtypes = [c_int32, c_int32, c_int32, c_int32]
     handle.pkda_chunk_table.restype = c_int32
     handle.pkda_chunk_table.argtypes = [c_void_p, c_int32, c_int32, c_void_p, c_void_p]
     if handle.pkda_abi_version() != ABI_VERSION:

@@ -28,6 +28,7 @@ extern "C" int64_t pkda_args_size(int which) {
     case PKDA_ARGS_PRECOND: return sizeof(pkda_precond_args);
     case PKDA_ARGS_CHUNK_FWD: return sizeof(pkda_chunk_fwd_args);
     case PKDA_ARGS_CHUNK_BWD: return sizeof(pkda_chunk_bwd_args);
+    case PKDA_ARGS_QKV_CONV: return sizeof(pkda_qkv_conv_args);
     default: return -1;
   }
 }

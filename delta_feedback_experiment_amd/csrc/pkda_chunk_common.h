@@ -562,6 +562,17 @@ __device__ __forceinline__ void store_packed_rows(bf16_t* g, int64_t gstride, ui
   }
 }
 
+// Element-wise store of an accumulator tile (four scattered stores per lane).
+template <typename T>
+__device__ __forceinline__ void store_acc_elems(T* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
+                                                int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = m0 + acc_row(lane, j);
+    if (r < nvalid) io<T>::store(g + r * gstride + n0 + acc_col(lane), acc[j]);
+  }
+}
+
 // Tile-major [D x D] state checkpoints: 16 x 16 tiles, each row-major and
 // contiguous (256 elements), tile (rt, ct) at element (rt * (D / 16) + ct) * 256.
 // One accumulator tile is one contiguous 512-byte write.

@@ -69,7 +69,8 @@ enum pkda_args_kind {
   PKDA_ARGS_GATE = 1,
   PKDA_ARGS_PRECOND = 2,
   PKDA_ARGS_CHUNK_FWD = 3,
-  PKDA_ARGS_CHUNK_BWD = 4
+  PKDA_ARGS_CHUNK_BWD = 4,
+  PKDA_ARGS_QKV_CONV = 5
 };
 
 /* ---------------------------------------------------------------------------
@@ -324,6 +325,44 @@ typedef struct pkda_chunk_bwd_args {
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused Q/K/V short convolution + SiLU + per-head L2 normalisation.
+ *
+ * Replaces delta_feedback::pkda_qkv_conv and its backward op
+ * (delta_feedback_experiment/fla_ops.py:134-249), the producer of the
+ * recurrence's q, k, v (portable form: delta_feedback_experiment/pkda.py:
+ * 37-44,197-220,290-316).  x [batch, seqlen, 3 * width] holds the Q, K and V
+ * projections side by side; weight [3 * width, conv_size] is the depthwise
+ * causal filter (zero history before the first token).  Per channel c:
+ *   y = silu(sum_w weight[c, w] x[t - (conv_size - 1) + w, c]),
+ * then for c < norm_channels (Q and K) y / sqrt(sum over the head_dim channels
+ * of c's head of y^2 + eps); FP32 throughout, cast once to dtype.
+ *   forward:  q, k, v [batch, seqlen, width] (dtype).
+ *   backward: from dq, dk, dv (dtype): dx (dtype, shape of x) and dw (w_dtype,
+ *             shape of weight) through the caller's FP32 workspace dw_part of
+ *             pkda_qkv_conv_workspace(batch, seqlen, width, conv_size)
+ *             elements, summed in a fixed order (deterministic).
+ * head_dim 32, 64 or 128; conv_size 1..4; width a multiple of head_dim.
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_qkv_conv_args {
+  int32_t struct_size;
+  int32_t dtype;            /* of x, q, k, v, dq, dk, dv, dx */
+  int32_t w_dtype;          /* of weight and dw */
+  int32_t batch, seqlen, width, head_dim, norm_channels, conv_size;
+  float eps;
+  const void* x;
+  const void* weight;
+  void *q, *k, *v;          /* forward outputs */
+  const void *dq, *dk, *dv; /* backward inputs */
+  void* dx;                 /* backward outputs */
+  void* dw;
+  float* dw_part;           /* backward workspace */
+} pkda_qkv_conv_args;
+
+int64_t pkda_qkv_conv_workspace(int32_t batch, int32_t seqlen, int32_t width, int32_t conv_size);
+int pkda_qkv_conv_fwd(const pkda_qkv_conv_args* args, void* stream);
+int pkda_qkv_conv_bwd(const pkda_qkv_conv_args* args, void* stream);
 
 #ifdef __cplusplus
 }
