@@ -20,7 +20,10 @@ Printed as ONE JSON line:
                   recurrence) timed on this host over a bounded sample;
   decode          the batched slot-pool decode step (B=256 live sequences in
                   a 512-slot [512, 32, 128, 128] FP32 pool, 1000 steps),
-                  achieved HBM GB/s against 8 TB/s.
+                  achieved HBM GB/s against 8 TB/s;
+  qkv_conv        the recurrence's producer (fused Q/K/V short convolution +
+                  SiLU + L2 norm), forward and backward at the screen
+                  geometry, achieved HBM GB/s against 8 TB/s.
 
 Algorithmic work per token-head (C = 64, dk = dv = d; the triangular solve,
 gate scans and elementwise work are not counted):
@@ -346,6 +349,50 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
     }
 
 
+def bench_qkv_conv(dev: torch.device, reps: int = 20) -> dict:
+    """The recurrence's producer, the fused Q/K/V short convolution + SiLU +
+    per-head L2 norm (delta_feedback_experiment/fla_ops.py:134-249), forward
+    and backward at the reference's screen geometry: 8 rows x 4,096 tokens,
+    projection width 1,024 (8 heads of 128), conv_size 4, BF16 activations,
+    FP32 weights.  Algorithmic bytes: forward reads x and writes q, k, v;
+    backward reads x, dq, dk, dv and writes dx (dw and its per-tile partials
+    are not counted)."""
+    from delta_feedback_experiment_amd import pkda_qkv_conv
+    from delta_feedback_experiment_amd.conv import pkda_qkv_conv_backward
+
+    B, T, H, D, W = 8, 4096, 8, 128, 4
+    P = H * D
+    gen = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(B, T, 3 * P, generator=gen, device=dev).to(torch.bfloat16)
+    w = 0.5 * torch.randn(3 * P, W, generator=gen, device=dev)
+    do = [torch.randn(B, T, P, generator=gen, device=dev).to(torch.bfloat16) for _ in range(3)]
+
+    def timed(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    fwd_ms = timed(lambda: pkda_qkv_conv(x, w, D, 2 * P, 1e-6))
+    bwd_ms = timed(lambda: pkda_qkv_conv_backward(x, w, *do, D, 2 * P, 1e-6))
+    elem = B * T * 3 * P * 2
+    fwd_bytes, bwd_bytes = 2 * elem, 3 * elem
+    return {
+        "workload": "screen geometry: B8 T4096, 3 x 1024 channels (8 heads of 128), conv_size 4, bf16",
+        "fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
+        "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes,
+        "fwd_GBps": fwd_bytes / (fwd_ms / 1e3) / 1e9, "bwd_GBps": bwd_bytes / (bwd_ms / 1e3) / 1e9,
+        "fwd_frac_hbm": fwd_bytes / (fwd_ms / 1e3) / HBM_PEAK, "bwd_frac_hbm": bwd_bytes / (bwd_ms / 1e3) / HBM_PEAK,
+        "reference_h100_pcie_ms": {"fwd": 0.215, "bwd": 0.504,
+                                   "source": "delta_feedback_experiment/fla_ops.py:39-43, rows not stated"},
+    }
+
+
 def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
     """A plain device copy of ``nbytes`` (read + write), the practical HBM
     ceiling beside the kernels' rates and the scale for the byte counters."""
@@ -410,6 +457,7 @@ def main() -> None:
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-conv", action="store_true", help="skip the Q/K/V convolution lines")
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -491,6 +539,11 @@ def main() -> None:
     }
     result["copy"] = copy_bandwidth(dev)
     print(f"[bench] copy {result['copy']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
+    if not args.no_conv:
+        result["qkv_conv"] = bench_qkv_conv(dev)
+        c = result["qkv_conv"]
+        print(f"[bench] qkv conv fwd {c['fwd_ms']:.3f} ms ({c['fwd_GBps']:.0f} GB/s), "
+              f"bwd {c['bwd_ms']:.3f} ms ({c['bwd_GBps']:.0f} GB/s)", file=sys.stderr, flush=True)
     if not args.no_decode:
         del inp
         torch.cuda.empty_cache()

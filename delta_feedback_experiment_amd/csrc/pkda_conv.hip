@@ -30,7 +30,20 @@ namespace pkda {
 namespace {
 
 constexpr int kConvThreads = 128;  // 128 x 8 = 1024 channels per workgroup
-constexpr int kConvTile = 64;      // tokens per workgroup
+#ifndef PKDA_CONV_TILE_BWD
+#define PKDA_CONV_TILE_BWD 64
+#endif
+#ifndef PKDA_CONV_GROUP
+#define PKDA_CONV_GROUP 4
+#endif
+#ifndef PKDA_CONV_GROUP_BWD
+#define PKDA_CONV_GROUP_BWD 4
+#endif
+constexpr int kConvTileFwd = 32;                 // tokens per workgroup, forward
+constexpr int kConvTile = PKDA_CONV_TILE_BWD;    // tokens per workgroup, backward (and dw partials)
+constexpr int kGroup = PKDA_CONV_GROUP;          // token rows loaded together, forward
+constexpr int kGroupBwd = PKDA_CONV_GROUP_BWD;   // and backward
+constexpr int kDwSlices = 32;                    // first pass of the dw reduction
 
 struct ConvParams {
   const void* x;
@@ -82,6 +95,34 @@ template <> struct Vec8<float> {
   }
 };
 
+// Eight elements kept as raw 16-byte pieces (unpacked when used), so a
+// prefetched row costs 4 registers in BF16.
+template <typename T>
+struct Raw8 {
+  static constexpr int N = 8 * sizeof(T) / 16;
+  uint4 r[N];
+  __device__ __forceinline__ void load(const T* p) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = reinterpret_cast<const uint4*>(p)[i];
+  }
+  __device__ __forceinline__ void unpack(float* x) const {
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t w[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        x[4 * i] = __uint_as_float(r[i].x); x[4 * i + 1] = __uint_as_float(r[i].y);
+        x[4 * i + 2] = __uint_as_float(r[i].z); x[4 * i + 3] = __uint_as_float(r[i].w);
+      }
+    }
+  }
+};
+
 // Sum over the G lanes of one head (G a power of two, lanes aligned to G).
 template <int G>
 __device__ __forceinline__ float head_sum(float x) {
@@ -122,9 +163,10 @@ __device__ __forceinline__ void load_weights(const ConvParams& p, int c0, float 
 // ---------------------------------------------------------------------------
 template <typename T, int W, int G>
 __global__ __launch_bounds__(kConvThreads) void qkv_conv_fwd_kernel(ConvParams p) {
-  const int b = blockIdx.x / p.tiles_per_row;
-  const int t0 = (blockIdx.x - b * p.tiles_per_row) * kConvTile;
-  const int t1 = min(t0 + kConvTile, p.T);
+  const int tpr = (p.T + kConvTileFwd - 1) / kConvTileFwd;
+  const int b = blockIdx.x / tpr;
+  const int t0 = (blockIdx.x - b * tpr) * kConvTileFwd;
+  const int t1 = min(t0 + kConvTileFwd, p.T);
   const int c0 = (blockIdx.y * kConvThreads + threadIdx.x) * 8;
   if (c0 >= p.C) return;  // whole heads: the lanes of one head leave together
   const bool norm = c0 < p.norm_channels;
@@ -144,32 +186,48 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_fwd_kernel(ConvParams p
   }
   int off;
   T* out = slab_ptr<T>(p.q, p.k, p.v, p.P, c0, (int64_t)b * p.T, off) + off;
-  for (int t = t0; t < t1; ++t) {
-    float xt[8];
-    Vec8<T>::load(xs + (int64_t)t * p.C, xt);
-    float y[8];
-    float ss = 0.f;
+  // tokens in groups of kGroup rows, the next group's loads in flight while
+  // the current one computes
+  Raw8<T> xa[kGroup], xb[kGroup];
+  auto load_group = [&](int tg, Raw8<T> (&dst)[kGroup]) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float a = wt[j][W - 1] * xt[j];
+    for (int i = 0; i < kGroup; ++i)
+      if (tg + i < t1) dst[i].load(xs + (int64_t)(tg + i) * p.C);
+  };
+  load_group(t0, xa);
+  for (int tg = t0; tg < t1; tg += kGroup) {
+    if (tg + kGroup < t1) load_group(tg + kGroup, xb);
 #pragma unroll
-      for (int w = 0; w < W - 1; ++w) a += wt[j][w] * hist[w][j];
-      y[j] = a * sigmoid_fast(a);
-      ss += y[j] * y[j];
+    for (int i = 0; i < kGroup; ++i) {
+      if (tg + i >= t1) break;
+      float xt[8];
+      xa[i].unpack(xt);
+      float y[8];
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float a = wt[j][W - 1] * xt[j];
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w) a += wt[j][w] * hist[w][j];
+        y[j] = a * sigmoid_fast(a);
+        ss += y[j] * y[j];
+      }
+      if (norm) {
+        const float r = rsqrtf(head_sum<G>(ss) + p.eps);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] *= r;
+      }
+      Vec8<T>::store(out + (int64_t)(tg + i) * p.P, y);
+#pragma unroll
+      for (int w = 0; w + 1 < W - 1; ++w)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hist[w][j] = hist[w + 1][j];
+      if (W > 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hist[W > 1 ? W - 2 : 0][j] = xt[j];
     }
-    if (norm) {
-      const float r = rsqrtf(head_sum<G>(ss) + p.eps);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] *= r;
-    }
-    Vec8<T>::store(out + (int64_t)t * p.P, y);
-#pragma unroll
-    for (int w = 0; w + 1 < W - 1; ++w)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) hist[w][j] = hist[w + 1][j];
-    if (W > 1)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) hist[W > 1 ? W - 2 : 0][j] = xt[j];
+    for (int i = 0; i < kGroup; ++i) xa[i] = xb[i];
   }
 }
 
@@ -216,71 +274,93 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_bwd_kernel(ConvParams p
     }
   }
   const int tend = t1 + W - 1;  // da of the W - 1 rows after the tile reaches its dx
-  for (int t = t0; t < tend; ++t) {
-    float da[8];
-    if (t < p.T) {
-      Vec8<T>::load(xs + (int64_t)t * p.C, hist[W - 1]);
-      float dn[8];
-      Vec8<T>::load(dn_base + (int64_t)t * p.P, dn);
-      float a[8], y[8];
-      float ss = 0.f;
+  Raw8<T> xa[kGroupBwd], xb[kGroupBwd], na[kGroupBwd], nb[kGroupBwd];
+  const int tlast = min(tend, p.T);
+  auto load_group = [&](int tg, Raw8<T> (&dx_)[kGroupBwd], Raw8<T> (&dn_)[kGroupBwd]) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        a[j] = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) a[j] += wt[j][w] * hist[w][j];
-        y[j] = a[j] * sigmoid_fast(a[j]);
-        ss += y[j] * y[j];
+    for (int i = 0; i < kGroupBwd; ++i)
+      if (tg + i < tlast) {
+        dx_[i].load(xs + (int64_t)(tg + i) * p.C);
+        dn_[i].load(dn_base + (int64_t)(tg + i) * p.P);
       }
-      float dy[8];
-      if (norm) {
-        const float r = rsqrtf(head_sum<G>(ss) + p.eps);
-        float nd = 0.f;
+  };
+  load_group(t0, xa, na);
+  for (int tg = t0; tg < tend; tg += kGroupBwd) {
+    if (tg + kGroupBwd < tlast) load_group(tg + kGroupBwd, xb, nb);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) nd += y[j] * r * dn[j];
-        nd = head_sum<G>(nd);
+    for (int i = 0; i < kGroupBwd; ++i) {
+      const int t = tg + i;
+      if (t >= tend) break;
+      float da[8];
+      if (t < p.T) {
+        xa[i].unpack(hist[W - 1]);
+        float dn[8];
+        na[i].unpack(dn);
+        float a[8], y[8];
+        float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dy[j] = r * (dn[j] - y[j] * r * nd);
+        for (int j = 0; j < 8; ++j) {
+          a[j] = 0.f;
+#pragma unroll
+          for (int w = 0; w < W; ++w) a[j] += wt[j][w] * hist[w][j];
+          y[j] = a[j] * sigmoid_fast(a[j]);
+          ss += y[j] * y[j];
+        }
+        float dy[8];
+        if (norm) {
+          const float r = rsqrtf(head_sum<G>(ss) + p.eps);
+          float nd = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) nd += y[j] * r * dn[j];
+          nd = head_sum<G>(nd);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) dy[j] = r * (dn[j] - y[j] * r * nd);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) dy[j] = dn[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float s = sigmoid_fast(a[j]);
+          da[j] = dy[j] * s * (1.f + a[j] * (1.f - s));
+        }
+        if (t < t1) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int w = 0; w < W; ++w) dw[j][w] += da[j] * hist[w][j];
+        }
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dy[j] = dn[j];
+        for (int j = 0; j < 8; ++j) da[j] = 0.f;
       }
+      // slide the windows: dwin holds da[t - (W - 1) .. t]
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float s = sigmoid_fast(a[j]);
-        da[j] = dy[j] * s * (1.f + a[j] * (1.f - s));
+      for (int w = 0; w + 1 < W; ++w)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          dwin[w][j] = dwin[w + 1][j];
+          hist[w][j] = hist[w + 1][j];
+        }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dwin[W - 1][j] = da[j];
+      const int s = t - (W - 1);  // every da that reaches x[s] is known now
+      if (s >= t0) {
+        float dx[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int w = 0; w < W; ++w) acc += wt[j][w] * dwin[W - 1 - w][j];
+          dx[j] = acc;
+        }
+        Vec8<T>::store(dxs + (int64_t)s * p.C, dx);
       }
-      if (t < t1) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int w = 0; w < W; ++w) dw[j][w] += da[j] * hist[w][j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) da[j] = 0.f;
     }
-    // slide the windows: dwin holds da[t - (W - 1) .. t]
 #pragma unroll
-    for (int w = 0; w + 1 < W; ++w)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        dwin[w][j] = dwin[w + 1][j];
-        hist[w][j] = hist[w + 1][j];
-      }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dwin[W - 1][j] = da[j];
-    const int s = t - (W - 1);  // every da that reaches x[s] is known now
-    if (s >= t0) {
-      float dx[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float acc = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) acc += wt[j][w] * dwin[W - 1 - w][j];
-        dx[j] = acc;
-      }
-      Vec8<T>::store(dxs + (int64_t)s * p.C, dx);
+    for (int i = 0; i < kGroupBwd; ++i) {
+      xa[i] = xb[i];
+      na[i] = nb[i];
     }
   }
   float* part = p.dw_part + ((int64_t)tile * p.C + c0) * W;
@@ -290,30 +370,49 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_bwd_kernel(ConvParams p
     for (int w = 0; w < W; ++w) part[j * W + w] = dw[j][w];
 }
 
-// dw[c, w] = sum over tiles in order of dw_part[tile, c, w].
-__global__ __launch_bounds__(256) void qkv_conv_dw_kernel(ConvParams p, int W, int tiles) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.C * W) return;
+// dw[c, w] = sum over tiles of dw_part[tile, c, w] in a fixed order, in two
+// passes: slice y sums tiles y, y + S, y + 2S, ... and leaves the sum in place
+// of tile y (only this thread ever reads that entry), then the S slice sums
+// are added in order.
+__global__ __launch_bounds__(256) void qkv_conv_dw_slices_kernel(ConvParams p, int W, int tiles, int S) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int y = blockIdx.y;
+  const int64_t CW = (int64_t)p.C * W;
+  if (e >= CW) return;
   float s = 0.f;
-  for (int t = 0; t < tiles; ++t) s += p.dw_part[(int64_t)t * p.C * W + i];
+  for (int t = y; t < tiles; t += S) s += p.dw_part[t * CW + e];
+  p.dw_part[y * CW + e] = s;
+}
+
+__global__ __launch_bounds__(256) void qkv_conv_dw_kernel(ConvParams p, int W, int S) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int64_t CW = (int64_t)p.C * W;
+  if (e >= CW) return;
+  float s = 0.f;
+  for (int y = 0; y < S; ++y) s += p.dw_part[y * CW + e];
   if (p.w_dtype == PKDA_BF16) {
-    static_cast<bf16_t*>(p.dw)[i] = f32_to_bf16(s);
+    static_cast<bf16_t*>(p.dw)[e] = f32_to_bf16(s);
   } else {
-    static_cast<float*>(p.dw)[i] = s;
+    static_cast<float*>(p.dw)[e] = s;
   }
 }
 
 template <typename T, int W, int G>
 int launch_conv(const ConvParams& p, bool backward, hipStream_t s) {
-  const int tiles = p.B * p.tiles_per_row;
-  const dim3 grid(tiles, (p.C + 8 * kConvThreads - 1) / (8 * kConvThreads));
+  const int cblocks = (p.C + 8 * kConvThreads - 1) / (8 * kConvThreads);
   if (!backward) {
-    hipLaunchKernelGGL((qkv_conv_fwd_kernel<T, W, G>), grid, dim3(kConvThreads), 0, s, p);
+    const int tiles = p.B * ((p.T + kConvTileFwd - 1) / kConvTileFwd);
+    hipLaunchKernelGGL((qkv_conv_fwd_kernel<T, W, G>), dim3(tiles, cblocks), dim3(kConvThreads), 0, s, p);
     return launch_status("pkda_qkv_conv_fwd");
   }
-  hipLaunchKernelGGL((qkv_conv_bwd_kernel<T, W, G>), grid, dim3(kConvThreads), 0, s, p);
+  const int tiles = p.B * p.tiles_per_row;
+  hipLaunchKernelGGL((qkv_conv_bwd_kernel<T, W, G>), dim3(tiles, cblocks), dim3(kConvThreads), 0, s, p);
   if (int st = launch_status("pkda_qkv_conv_bwd")) return st;
-  hipLaunchKernelGGL(qkv_conv_dw_kernel, dim3((p.C * W + 255) / 256), dim3(256), 0, s, p, W, tiles);
+  const int S = min(kDwSlices, tiles);
+  const int eblocks = (p.C * W + 255) / 256;
+  hipLaunchKernelGGL(qkv_conv_dw_slices_kernel, dim3(eblocks, S), dim3(256), 0, s, p, W, tiles, S);
+  if (int st = launch_status("pkda_qkv_conv_bwd(dw slices)")) return st;
+  hipLaunchKernelGGL(qkv_conv_dw_kernel, dim3(eblocks), dim3(256), 0, s, p, W, S);
   return launch_status("pkda_qkv_conv_bwd(dw)");
 }
 
