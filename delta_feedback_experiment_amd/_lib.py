@@ -108,7 +108,17 @@ class QkvConvArgs(ctypes.Structure):
     ]
 
 
-_ARG_KINDS = {0: RecurrentArgs, 1: GateArgs, 2: PrecondArgs, 3: ChunkFwdArgs, 4: ChunkBwdArgs, 5: QkvConvArgs}
+class NormGateArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", c_int32), ("dtype", c_int32), ("w_dtype", c_int32), ("dim", c_int32),
+        ("rows", c_int64), ("eps", c_float),
+        ("x", c_void_p), ("gate", c_void_p), ("weight", c_void_p), ("y", c_void_p), ("rstd", c_void_p),
+        ("dy", c_void_p), ("dx", c_void_p), ("dgate", c_void_p), ("dw", c_void_p), ("dw_part", c_void_p),
+    ]
+
+
+_ARG_KINDS = {0: RecurrentArgs, 1: GateArgs, 2: PrecondArgs, 3: ChunkFwdArgs, 4: ChunkBwdArgs, 5: QkvConvArgs,
+              6: NormGateArgs}
 _LIB: ctypes.CDLL | None = None
 
 
@@ -159,6 +169,7 @@ def lib() -> ctypes.CDLL:
         ("pkda_precond_fwd", PrecondArgs), ("pkda_precond_bwd", PrecondArgs),
         ("pkda_chunk_fwd", ChunkFwdArgs), ("pkda_chunk_bwd", ChunkBwdArgs),
         ("pkda_qkv_conv_fwd", QkvConvArgs), ("pkda_qkv_conv_bwd", QkvConvArgs),
+        ("pkda_norm_gate_fwd", NormGateArgs), ("pkda_norm_gate_bwd", NormGateArgs),
     ):
         fn = getattr(handle, name, None)
         if fn is not None:
@@ -166,6 +177,8 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = [POINTER(struct), c_void_p]
     handle.pkda_qkv_conv_workspace.restype = c_int64
     handle.pkda_qkv_conv_workspace.argtypes = [c_int32, c_int32, c_int32, c_int32]
+    handle.pkda_norm_gate_workspace.restype = c_int64
+    handle.pkda_norm_gate_workspace.argtypes = [c_int64, c_int32]
     handle.pkda_chunk_table.restype = c_int32
     handle.pkda_chunk_table.argtypes = [c_void_p, c_int32, c_int32, c_void_p, c_void_p]
     if handle.pkda_abi_version() != ABI_VERSION:

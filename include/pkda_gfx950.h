@@ -70,7 +70,8 @@ enum pkda_args_kind {
   PKDA_ARGS_PRECOND = 2,
   PKDA_ARGS_CHUNK_FWD = 3,
   PKDA_ARGS_CHUNK_BWD = 4,
-  PKDA_ARGS_QKV_CONV = 5
+  PKDA_ARGS_QKV_CONV = 5,
+  PKDA_ARGS_NORM_GATE = 6
 };
 
 /* ---------------------------------------------------------------------------
@@ -363,6 +364,46 @@ typedef struct pkda_qkv_conv_args {
 int64_t pkda_qkv_conv_workspace(int32_t batch, int32_t seqlen, int32_t width, int32_t conv_size);
 int pkda_qkv_conv_fwd(const pkda_qkv_conv_args* args, void* stream);
 int pkda_qkv_conv_bwd(const pkda_qkv_conv_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * RMSNorm with a sigmoid output gate, the consumer of the recurrence output.
+ *
+ * Replaces delta_feedback::pkda_norm_gate and its backward op
+ * (delta_feedback_experiment/fla_ops.py:572-657), as
+ * PreconditionedKDA.forward applies it to o [B, T, H, d] with the gate logits
+ * and output_norm (delta_feedback_experiment/pkda.py:536-547).  Per row r of
+ * width dim (one head of one token), in FP32 with one rounding:
+ *   rstd[r] = 1 / sqrt(mean(x[r]^2) + eps),
+ *   y[r]    = x[r] rstd[r] weight sigmoid(gate[r]).
+ *   forward:  y (dtype), rstd [rows] FP32.
+ *   backward: from dy (dtype) and the forward's rstd: dx, dgate (dtype) and
+ *             dweight (w_dtype) through the caller's FP32 workspace dw_part
+ *             of pkda_norm_gate_workspace(rows, dim) elements, summed in a
+ *             fixed order (deterministic).
+ * x, gate, y, dy, dx, dgate share dtype; dim 64 or 128.
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_norm_gate_args {
+  int32_t struct_size;
+  int32_t dtype;       /* of x, gate, y, dy, dx, dgate */
+  int32_t w_dtype;     /* of weight and dweight */
+  int32_t dim;
+  int64_t rows;
+  float eps;
+  const void* x;
+  const void* gate;
+  const void* weight;  /* [dim] */
+  void* y;             /* forward outputs */
+  float* rstd;         /* forward output, backward input: [rows] */
+  const void* dy;      /* backward input */
+  void* dx;            /* backward outputs */
+  void* dgate;
+  void* dw;
+  float* dw_part;      /* backward workspace */
+} pkda_norm_gate_args;
+
+int64_t pkda_norm_gate_workspace(int64_t rows, int32_t dim);
+int pkda_norm_gate_fwd(const pkda_norm_gate_args* args, void* stream);
+int pkda_norm_gate_bwd(const pkda_norm_gate_args* args, void* stream);
 
 #ifdef __cplusplus
 }
