@@ -23,7 +23,9 @@ Printed as ONE JSON line:
                   achieved HBM GB/s against 8 TB/s;
   qkv_conv        the recurrence's producer (fused Q/K/V short convolution +
                   SiLU + L2 norm), forward and backward at the screen
-                  geometry, achieved HBM GB/s against 8 TB/s.
+                  geometry, achieved HBM GB/s against 8 TB/s;
+  norm_gate       its consumer (RMSNorm sigmoid output gate) on the c2
+                  output shape, achieved HBM GB/s against 8 TB/s.
 
 Algorithmic work per token-head (C = 64, dk = dv = d; the triangular solve,
 gate scans and elementwise work are not counted):
@@ -393,6 +395,45 @@ def bench_qkv_conv(dev: torch.device, reps: int = 20) -> dict:
     }
 
 
+def bench_norm_gate(dev: torch.device, reps: int = 20) -> dict:
+    """The recurrence's consumer, the RMSNorm sigmoid output gate
+    (delta_feedback_experiment/fla_ops.py:572-657), on the c2 recurrence
+    output [8, 4096, 16, 128] BF16 with an FP32 weight.  Algorithmic bytes:
+    forward reads x, gate and writes y, rstd; backward reads x, gate, dy, rstd
+    and writes dx, dgate (dweight and its partials are not counted)."""
+    from delta_feedback_experiment_amd import pkda_norm_gate
+    from delta_feedback_experiment_amd.norm_gate import pkda_norm_gate_backward
+
+    shape = (8, 4096, 16, 128)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    x, g, dy = (torch.randn(*shape, generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
+    w = torch.ones(shape[-1], device=dev)
+    _, rstd = pkda_norm_gate(x, g, w, 1e-6)
+
+    def timed(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    fwd_ms = timed(lambda: pkda_norm_gate(x, g, w, 1e-6))
+    bwd_ms = timed(lambda: pkda_norm_gate_backward(x, g, w, rstd, dy, 1e-6))
+    rows = x.numel() // shape[-1]
+    elem = x.numel() * 2
+    fwd_bytes, bwd_bytes = 3 * elem + 4 * rows, 5 * elem + 4 * rows
+    return {
+        "workload": "c2 recurrence output [8, 4096, 16, 128] bf16, fp32 weight",
+        "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes,
+        "fwd_GBps": fwd_bytes / (fwd_ms / 1e3) / 1e9, "bwd_GBps": bwd_bytes / (bwd_ms / 1e3) / 1e9,
+        "fwd_frac_hbm": fwd_bytes / (fwd_ms / 1e3) / HBM_PEAK, "bwd_frac_hbm": bwd_bytes / (bwd_ms / 1e3) / HBM_PEAK,
+    }
+
+
 def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
     """A plain device copy of ``nbytes`` (read + write), the practical HBM
     ceiling beside the kernels' rates and the scale for the byte counters."""
@@ -457,7 +498,7 @@ def main() -> None:
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-conv", action="store_true", help="skip the Q/K/V convolution lines")
+    ap.add_argument("--no-conv", action="store_true", help="skip the Q/K/V convolution and norm-gate lines")
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -543,6 +584,10 @@ def main() -> None:
         result["qkv_conv"] = bench_qkv_conv(dev)
         c = result["qkv_conv"]
         print(f"[bench] qkv conv fwd {c['fwd_ms']:.3f} ms ({c['fwd_GBps']:.0f} GB/s), "
+              f"bwd {c['bwd_ms']:.3f} ms ({c['bwd_GBps']:.0f} GB/s)", file=sys.stderr, flush=True)
+        result["norm_gate"] = bench_norm_gate(dev)
+        c = result["norm_gate"]
+        print(f"[bench] norm gate fwd {c['fwd_ms']:.3f} ms ({c['fwd_GBps']:.0f} GB/s), "
               f"bwd {c['bwd_ms']:.3f} ms ({c['bwd_GBps']:.0f} GB/s)", file=sys.stderr, flush=True)
     if not args.no_decode:
         del inp

@@ -172,11 +172,24 @@ __global__ __launch_bounds__(kNgThreads) void norm_gate_bwd_kernel(NgParams p) {
   }
 }
 
+// dweight[c] = sum over workgroups of dw_part[b, c] in a fixed order, in two
+// passes: slice y sums workgroups y, y + S, ... into dw_part[y] (only this
+// thread reads that entry), then the S slice sums are added in order.
+constexpr int kNgSlices = 32;
+
 template <int D>
-__global__ __launch_bounds__(D) void norm_gate_dw_kernel(NgParams p) {
+__global__ __launch_bounds__(D) void norm_gate_dw_slices_kernel(NgParams p, int S) {
+  const int c = threadIdx.x, y = blockIdx.x;
+  float s = 0.f;
+  for (int b = y; b < p.blocks; b += S) s += p.dw_part[(int64_t)b * D + c];
+  p.dw_part[(int64_t)y * D + c] = s;
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void norm_gate_dw_kernel(NgParams p, int S) {
   const int c = threadIdx.x;
   float s = 0.f;
-  for (int b = 0; b < p.blocks; ++b) s += p.dw_part[(int64_t)b * D + c];
+  for (int y = 0; y < S; ++y) s += p.dw_part[(int64_t)y * D + c];
   if (p.w_dtype == PKDA_BF16) {
     static_cast<bf16_t*>(p.dw)[c] = f32_to_bf16(s);
   } else {
@@ -192,7 +205,10 @@ int launch_ng(const NgParams& p, bool backward, hipStream_t s) {
   }
   hipLaunchKernelGGL((norm_gate_bwd_kernel<T, D>), dim3(p.blocks), dim3(kNgThreads), 0, s, p);
   if (int st = launch_status("pkda_norm_gate_bwd")) return st;
-  hipLaunchKernelGGL((norm_gate_dw_kernel<D>), dim3(1), dim3(D), 0, s, p);
+  const int S = p.blocks < kNgSlices ? p.blocks : kNgSlices;
+  hipLaunchKernelGGL((norm_gate_dw_slices_kernel<D>), dim3(S), dim3(D), 0, s, p, S);
+  if (int st = launch_status("pkda_norm_gate_bwd(dweight slices)")) return st;
+  hipLaunchKernelGGL((norm_gate_dw_kernel<D>), dim3(1), dim3(D), 0, s, p, S);
   return launch_status("pkda_norm_gate_bwd(dweight)");
 }
 
