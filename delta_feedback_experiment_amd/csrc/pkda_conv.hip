@@ -39,7 +39,7 @@ constexpr int kConvThreads = 128;  // 128 x 8 = 1024 channels per workgroup
 #ifndef PKDA_CONV_GROUP_BWD
 #define PKDA_CONV_GROUP_BWD 4
 #endif
-constexpr int kConvTileFwd = 32;                 // tokens per workgroup, forward
+constexpr int kConvTileFwd = 32;                 // tokens per workgroup, forward (swept: 16..64)
 constexpr int kConvTile = PKDA_CONV_TILE_BWD;    // tokens per workgroup, backward (and dw partials)
 constexpr int kGroup = PKDA_CONV_GROUP;          // token rows loaded together, forward
 constexpr int kGroupBwd = PKDA_CONV_GROUP_BWD;   // and backward
