@@ -218,7 +218,7 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
     if (!PC) {
       for (int i = tid; i < C * BV; i += kSW) {
         const int r = i / BV, c = i - r * BV;
-        sdOg[r * L::LDV + c] = to_e<E>(scale * expf(sGam[r]) * from_e<E>(sdO[r * L::LDV + c]));
+        sdOg[r * L::LDV + c] = to_e<E>(scale * exp_fast(sGam[r]) * from_e<E>(sdO[r * L::LDV + c]));
       }
     }
     // dU = Aqk^T dO + diag(e^{G_C - G}) KW dS     (tile ti: row block ti % 4, column tile ti / 4)
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
       const int r0 = 16 * (ti & 3), ct = ti >> 2;
       float egc[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) egc[e] = PC ? 1.f : expf(gC - sGam[r0 + acc_row(lane, e)]);
+      for (int e = 0; e < 4; ++e) egc[e] = PC ? 1.f : exp_fast(gC - sGam[r0 + acc_row(lane, e)]);
       f32x4 a1 = zero4(), a2 = zero4();
       mma_tile_range<E, COL, ROW>(a1, sAqk, L::LDC, r0, sdO, L::LDV, 16 * ct, kfloor<E>(r0), C, lane);
       mma_tile<E, ROW, ROW>(a2, sKW, L::LD, r0, sdS, L::LDV, 16 * ct, D, lane);
@@ -242,14 +242,14 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
     }
     __syncthreads();
     // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU   (per-channel: diag(e^{G_C}) dS + qg^T dO - W^T dU)
-    const float decay = expf(gC);
+    const float decay = exp_fast(gC);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
       if (PC) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dS[i][j] *= expf(sGC[16 * rt + acc_row(lane, j)]);
+        for (int j = 0; j < 4; ++j) dS[i][j] *= exp_fast(sGC[16 * rt + acc_row(lane, j)]);
       } else {
         dS[i] = dS[i] * decay;
       }
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dq[j][e] = scale * expf(sGam[r0 + acc_row(lane, e)]) * acc[e];
+    for (int e = 0; e < 4; ++e) dq[j][e] = scale * exp_fast(sGam[r0 + acc_row(lane, e)]) * acc[e];
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
-      const float val = (s <= t && t < len) ? scale * expf(sGam[t] - sGam[s]) * acc[e] : 0.f;
+      const float val = (s <= t && t < len) ? scale * exp_fast(sGam[t] - sGam[s]) * acc[e] : 0.f;
       sP2[t * L::LDC + s] = to_e<E>(val);
     }
   }
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sdBv, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dkb[j][e] = -expf(sGam[r0 + acc_row(lane, e)]) * acc[e];  // e^G dBw
+    for (int e = 0; e < 4; ++e) dkb[j][e] = -exp_fast(sGam[r0 + acc_row(lane, e)]) * acc[e];  // e^G dBw
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
-      const float raw = (s < t && t < len) ? -acc[e] * expf(sGam[t] - sGam[s]) : 0.f;
+      const float raw = (s < t && t < len) ? -acc[e] * exp_fast(sGam[t] - sGam[s]) : 0.f;
       sP1r[t * L::LDC + s] = to_e<E>(raw);
       sP1[t * L::LDC + s] = to_e<E>(sBeta[t] * raw);
     }
@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dkws[j][e] = expf(gC - sGam[r0 + acc_row(lane, e)]) * acc[e];
+    for (int e = 0; e < 4; ++e) dkws[j][e] = exp_fast(gC - sGam[r0 + acc_row(lane, e)]) * acc[e];
   }
   __syncthreads();
   rK.store(sK, L::LD);
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
         hd_sum += sWave[w];
         kg_sum += sWave[kFW / 64 + w];
       }
-      g += expf(gC) * hd_sum + kg_sum;
+      g += exp_fast(gC) * hd_sum + kg_sum;
     }
     p.dgcum[idx] = g;
     p.dbeta[idx] = sRowB[tid] + sRowB[C + tid];
@@ -670,7 +670,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dq[j][e] = scale * expf(G(r0 + acc_row(lane, e), c)) * acc[e];
+    for (int e = 0; e < 4; ++e) dq[j][e] = scale * exp_fast(G(r0 + acc_row(lane, e), c)) * acc[e];
     f32x4 acw = zero4();
     mma_tile<E, ROW, COL>(acw, sdU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
     store_acc_lds(sdW, L::LD, -acw, r0, 16 * ct, lane);
@@ -728,7 +728,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int s = r0 + acc_row(lane, e);
-      dkws[j][e] = expf(gC[c] - G(s, c)) * acc[e];
+      dkws[j][e] = exp_fast(gC[c] - G(s, c)) * acc[e];
       if (s < len) col += io<T>::load(kwg + s * gs + c) * dkws[j][e];
     }
     col += __shfl_xor(col, 16);
@@ -745,7 +745,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
     rV.store(sV, L::LD);
-    rK.store(sK, L::LD, [&](int r, int c, float x) { return sBeta[r] * expf(G(r, c)) * x; });  // Bw
+    rK.store(sK, L::LD, [&](int r, int c, float x) { return sBeta[r] * exp_fast(G(r, c)) * x; });  // Bw
     rT.store(sT, L::LDC);
     rQ.store(sQ, L::LD);
   }
@@ -764,7 +764,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int s = r0 + acc_row(lane, e);
-      const float eg = expf(G(s, c));
+      const float eg = exp_fast(G(s, c));
       const float kv = s < len ? io<T>::load(kg_ + s * gs + c) : 0.f;
       const float vv = from_e<E>(sV[s * L::LD + c]);
       dk[j][e] = sBeta[s] * eg * acc[e];
@@ -839,7 +839,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
           const int x = kk + jj;
           a1[jj] = from_e<E>(sP1r[(r0 + (lane & 15)) * L::LDC + x]);
           a2[jj] = from_e<E>(sP2[(r0 + (lane & 15)) * L::LDC + x]);
-          bx[jj] = x <= rlo ? from_e<E>(sKWr[x * L::LD + nn]) * expf(grlo - sG[x * L::LDG + nn]) : 0.f;
+          bx[jj] = x <= rlo ? from_e<E>(sKWr[x * L::LD + nn]) * exp_fast(grlo - sG[x * L::LDG + nn]) : 0.f;
         }
         F::mfma(akA, a1, bx);
         F::mfma(aqP, a2, bx);
@@ -857,7 +857,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
           const int t = kk + jj;
           a1[jj] = from_e<E>(sP1r[t * L::LDC + r0 + (lane & 15)]);
           a2[jj] = from_e<E>(sP2[t * L::LDC + r0 + (lane & 15)]);
-          const float f = t > rhi ? expf(sG[t * L::LDG + nn] - grhi) : 0.f;
+          const float f = t > rhi ? exp_fast(sG[t * L::LDG + nn] - grhi) : 0.f;
           b1[jj] = sBeta[t] * from_e<E>(sK[t * L::LD + nn]) * f;  // beta_t on the key, dAkk unscaled
           b2[jj] = from_e<E>(sQ[t * L::LD + nn]) * f;
         }
@@ -872,10 +872,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       gr[e] = sG[(r0 + acc_row(lane, e)) * L::LDG + c];
-      akA[e] *= expf(gr[e] - grlo_c);
-      aqP[e] *= expf(gr[e] - grlo_c);
-      awA[e] *= expf(grhi_c - gr[e]);
-      awP[e] *= expf(grhi_c - gr[e]);
+      akA[e] *= exp_fast(gr[e] - grlo_c);
+      aqP[e] *= exp_fast(gr[e] - grlo_c);
+      awA[e] *= exp_fast(grhi_c - gr[e]);
+      awP[e] *= exp_fast(grhi_c - gr[e]);
     }
     for (int xo = 0; xo < 16; ++xo) {
       const int x = r0 + xo;
@@ -887,12 +887,12 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const int r = r0 + acc_row(lane, e);
         if (x <= r) {  // x as the column of row r
-          const float ex = expf(gr[e] - gx);
+          const float ex = exp_fast(gr[e] - gx);
           if (x < r) akA[e] += from_e<E>(sP1r[r * L::LDC + x]) * kwx * ex;
           aqP[e] += from_e<E>(sP2[r * L::LDC + x]) * kwx * ex;
         }
         if (x >= r) {  // x as the row, r as the column
-          const float ex = expf(gx - gr[e]);
+          const float ex = exp_fast(gx - gr[e]);
           if (x > r) awA[e] += sBeta[x] * from_e<E>(sP1r[x * L::LDC + r]) * kx * ex;
           awP[e] += from_e<E>(sP2[x * L::LDC + r]) * qx * ex;
         }
@@ -930,7 +930,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       const float qv = from_e<E>(sQ[r * L::LD + c]);
       const float wv = from_e<E>(sKWr[r * L::LD + c]);
       dg[e] = qv * dq[j][e] + kv * dk[j][e] - wv * dkw[j][e];
-      if (r == len - 1) dg[e] += expf(gC[c]) * sHD[c] + kgc;
+      if (r == len - 1) dg[e] += exp_fast(gC[c]) * sHD[c] + kgc;
     }
     store_acc_global<float>(dgo, gs, dg, r0, 16 * ct, len, lane);
     store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
@@ -1128,7 +1128,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dU[rb][j] += expf(gC - sG[16 * rb + q4 + j]) * KS[rb][j];
+      for (int j = 0; j < 4; ++j) dU[rb][j] += exp_fast(gC - sG[16 * rb + q4 + j]) * KS[rb][j];
       store_acc_global<T>(du_out, gs, dU[rb], 16 * rb, 0, clen, lane);
     }
     // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU
@@ -1137,11 +1137,11 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
     for (int kt = 0; kt < 2; ++kt) {
       float f[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = scale * expf(sG[32 * kt + (e < 4 ? 0 : 16) + q4 + (e & 3)]);
+      for (int e = 0; e < 8; ++e) f[e] = scale * exp_fast(sG[32 * kt + (e < 4 ? 0 : 16) + q4 + (e & 3)]);
       dOgB[kt] = scale_frag(dOB[kt], f);
       dUnB[kt] = pack_acc_pair(-dU[2 * kt], -dU[2 * kt + 1]);
     }
-    const float decay = expf(gC);
+    const float decay = exp_fast(gC);
 #pragma unroll
     for (int rt = 0; rt < NKT; ++rt) dS[rt] = dS[rt] * decay;
 #pragma unroll

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     for (int j = 0; j < 4; ++j) {
       const int t = 16 * tb + acc_row(lane, j);
       const int s = 16 * sb + acc_col(lane);
-      const float dec = (s <= t && t < len) ? expf(sGam[t] - sGam[s]) : 0.f;
+      const float dec = (s <= t && t < len) ? exp_fast(sGam[t] - sGam[s]) : 0.f;
       sA[t * L::LDF + s] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
       sAqk[t * L::LDC + s] = to_e<E>(p.scale * dec * aqk[j]);
     }
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   // Bw = diag(beta e^G) K in place over K; Bv = diag(beta) V over Q
   for (int i = tid; i < C * D; i += kIW) {
     const int r = i / D, c = i - r * D;
-    sK[r * L::LD + c] = to_e<E>(sBeta[r] * expf(sGam[r]) * from_e<E>(sK[r * L::LD + c]));
+    sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sGam[r]) * from_e<E>(sK[r * L::LD + c]));
   }
   rV.store(sQ, L::LD, RowScale{sBeta});
   __syncthreads();
@@ -373,7 +373,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
         lds_vec<V>(sKW + s * L::LD + c, wx);
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-          const float e = expf(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
+          const float e = exp_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
           akk += kx[j] * wx[j] * e;
           aqk += qx[j] * wx[j] * e;
         }
@@ -395,8 +395,8 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
 #pragma unroll
         for (int j = 0; j < F::N; ++j) {
           const float gr = sG[r * L::LDG + kk + j];
-          const float fa = expf(sG[t * L::LDG + kk + j] - gr);
-          const float fb = expf(gr - sG[s * L::LDG + kk + j]);
+          const float fa = exp_fast(sG[t * L::LDG + kk + j] - gr);
+          const float fb = exp_fast(gr - sG[s * L::LDG + kk + j]);
           ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
           aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
           bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
@@ -424,8 +424,8 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         const float gv = sG[r * L::LDG + c + j];
-        qx[j] *= p.scale * expf(gv);
-        wx[j] *= expf(sG[(C - 1) * L::LDG + c + j] - gv);
+        qx[j] *= p.scale * exp_fast(gv);
+        wx[j] *= exp_fast(sG[(C - 1) * L::LDG + c + j] - gv);
       }
       store_vec<V>(qg_out + r * gs + c, qx);
       store_vec<V>(kg_out + r * gs + c, wx);
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   // Bw = diag(beta) (e^G * K) in place over K; Bv = diag(beta) V over Q
   for (int i = tid; i < C * D; i += kIW) {
     const int r = i / D, c = i - r * D;
-    sK[r * L::LD + c] = to_e<E>(sBeta[r] * expf(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+    sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
   }
   rV.store(sQ, L::LD, RowScale{sBeta});
   __syncthreads();
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
         const int r = r0 + acc_row(lane, e), c = 16 * ct + acc_col(lane);
         U[e] = from_e<E>(sUin[r * L::LDV + c]) - acc[e];
         sU[r * L::LDV + c] = to_e<E>(U[e]);
-        if (!PC) sUg[r * L::LDV + c] = to_e<E>(expf(gC - sGam[r]) * U[e]);
+        if (!PC) sUg[r * L::LDV + c] = to_e<E>(exp_fast(gC - sGam[r]) * U[e]);
       }
       store_acc_global<T>(u_io, gs, U, r0, 16 * ct, clen, lane);
     }
@@ -628,18 +628,18 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
       mma_tile_range<E, ROW, ROW>(a2, sAqk, L::LDC, r0, sU, L::LDV, 16 * ct, 0, kend, lane);
       f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (PC ? 1.f : scale * expf(sGam[r0 + acc_row(lane, e)])) * a1[e] + a2[e];
+      for (int e = 0; e < 4; ++e) o[e] = (PC ? 1.f : scale * exp_fast(sGam[r0 + acc_row(lane, e)])) * a1[e] + a2[e];
       store_acc_global<T>(o_out, gs, o, r0, 16 * ct, clen, lane);
     }
     // S <- e^{G_C} S + KW^T Ug   (per-channel: diag(e^{G_C}) S + kg^T U)
-    const float decay = expf(gC);
+    const float decay = exp_fast(gC);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
       if (PC) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[i][j] *= expf(sGC[16 * rt + acc_row(lane, j)]);
+        for (int j = 0; j < 4; ++j) S[i][j] *= exp_fast(sGC[16 * rt + acc_row(lane, j)]);
       } else {
         S[i] = S[i] * decay;
       }
@@ -842,7 +842,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
     for (int rb = 0; rb < 4; ++rb) {
       f32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = scale * expf(sG[16 * rb + q4 + j]) * QS[rb][j] + AU[rb][j];
+      for (int j = 0; j < 4; ++j) o[j] = scale * exp_fast(sG[16 * rb + q4 + j]) * QS[rb][j] + AU[rb][j];
       store_acc_global<T>(o_out, gs, o, 16 * rb, 0, clen, lane);
     }
     // S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U
@@ -853,12 +853,12 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
       float fa[4], fb[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        fa[j] = expf(gC - sG[32 * kt + q4 + j]);
-        fb[j] = expf(gC - sG[32 * kt + 16 + q4 + j]);
+        fa[j] = exp_fast(gC - sG[32 * kt + q4 + j]);
+        fb[j] = exp_fast(gC - sG[32 * kt + 16 + q4 + j]);
       }
       UgB[kt] = pack_acc_pair_scaled(U[2 * kt], fa, U[2 * kt + 1], fb);
     }
-    const float decay = expf(gC);
+    const float decay = exp_fast(gC);
 #pragma unroll
     for (int rt = 0; rt < NKT; ++rt) S[rt] = S[rt] * decay;
 #pragma unroll

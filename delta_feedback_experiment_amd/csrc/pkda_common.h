@@ -40,12 +40,15 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// gfx950 converts natively (v_cvt_pk_bf16_f32: round to nearest even).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<bf16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<bf16_t>(u >> 16);
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
+
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32).  The rounding of the
+// scaled argument costs a relative error of about |x| 6e-8; the chunk
+// kernels take it on decay factors e^(G_t - G_s) <= 1.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 template <typename T> struct io;
 template <> struct io<float> {
