@@ -1,7 +1,7 @@
 """PKDA recurrence benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c5]
-                    [--decode-steps 1000] [--no-decode] [--no-cpu]
+                    [--decode-steps 1000] [--no-decode] [--no-cpu] [--no-serve]
 
 Mirrors the structure of the reference's ``scripts/pkda_bench.py`` (seeded
 synthetic inputs, warm-up, event-timed repeats): one *step* is one forward +
@@ -25,7 +25,11 @@ Printed as ONE JSON line:
                   SiLU + L2 norm), forward and backward at the screen
                   geometry, achieved HBM GB/s against 8 TB/s;
   norm_gate       its consumer (RMSNorm sigmoid output gate) on the c2
-                  output shape, achieved HBM GB/s against 8 TB/s.
+                  output shape, achieved HBM GB/s against 8 TB/s;
+  serve           the slot-pool serving path: a cached prefill of the c2
+                  shape into pool slots (tokens/s, MFMA fraction) and one
+                  decode token of the convolution with slot histories
+                  (achieved GB/s).
 
 Algorithmic work per token-head (C = 64, dk = dv = d; the triangular solve,
 gate scans and elementwise work are not counted):
@@ -434,6 +438,62 @@ def bench_norm_gate(dev: torch.device, reps: int = 20) -> dict:
     }
 
 
+def bench_serve(dev: torch.device, reps: int = 10) -> dict:
+    """The slot-pool serving path (``delta_feedback_experiment_amd.serve``).
+
+    prefill: a cached prefill of the c2 shape (8 prompts x 4,096 tokens, H16
+    d128, BF16, per-head log-decay) whose final states land in 8 slots of a
+    64-slot FP32 pool -- the chunked forward only; algorithmic flops
+    6 d^2 + 8 C d + 2 C d per token-head (intra + state).
+    conv_token: one decode token of the fused Q/K/V convolution for the c4
+    batch (256 live sequences of a 512-slot history pool, 3 x 32 x 128
+    channels, conv_size 4, BF16): reads x and the 3-row histories, writes
+    q, k, v and the new histories (algorithmic bytes)."""
+    from delta_feedback_experiment_amd import pkda_prefill_, pkda_qkv_conv_cached_
+
+    def timed(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    w = WORKLOADS["c2"]
+    inp = make_chunk_inputs(w, dev, seed=11)
+    B, T, H, D = w["B"], w["T"], w["H"], w["D"]
+    pool = torch.zeros(64, H, D, D, device=dev)
+    slots = torch.randperm(64, generator=torch.Generator().manual_seed(1))[:B].to(torch.int32).to(dev)
+    prefill_ms = timed(lambda: pkda_prefill_(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], pool, slots))
+    per_th = stage_flops(D)
+    flops = B * T * H * (per_th["fwd_intra"] + per_th["fwd_state"])
+    del inp, pool
+    N, P, Hd, Wc = 256, 512, 32, 4
+    C = 3 * Hd * D
+    gen = torch.Generator(device=dev).manual_seed(12)
+    x = torch.randn(N, 1, C, generator=gen, device=dev).to(torch.bfloat16)
+    wt = 0.5 * torch.randn(C, Wc, generator=gen, device=dev)
+    hist = torch.randn(P, Wc - 1, C, generator=gen, device=dev).to(torch.bfloat16)
+    cslots = torch.randperm(P, generator=torch.Generator().manual_seed(2))[:N].to(torch.int32).to(dev)
+    conv_ms = timed(lambda: pkda_qkv_conv_cached_(x, wt, D, 2 * Hd * D, 1e-6, hist, cslots))
+    conv_bytes = N * C * 2 * (1 + 2 * (Wc - 1) + 1)
+    return {
+        "prefill": {
+            "workload": "c2 shape prefill into 8 of 64 FP32 slots: B8 T4096 H16 d128 bf16, forward only",
+            "ms": prefill_ms, "tokens_per_s": B * T / (prefill_ms / 1e3),
+            "mfma_frac": flops / (prefill_ms / 1e3) / MFMA_BF16_PEAK,
+        },
+        "conv_token": {
+            "workload": "c4 decode token: 256 of 512 history slots, 3 x 32 x 128 channels, conv_size 4, bf16",
+            "us": conv_ms * 1e3, "bytes": conv_bytes, "GBps": conv_bytes / (conv_ms / 1e3) / 1e9,
+            "frac_hbm": conv_bytes / (conv_ms / 1e3) / HBM_PEAK,
+        },
+    }
+
+
 def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
     """A plain device copy of ``nbytes`` (read + write), the practical HBM
     ceiling beside the kernels' rates and the scale for the byte counters."""
@@ -500,6 +560,7 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-conv", action="store_true", help="skip the Q/K/V convolution and norm-gate lines")
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only")
+    ap.add_argument("--no-serve", action="store_true", help="skip the slot-pool prefill and conv-token lines")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -589,6 +650,15 @@ def main() -> None:
         c = result["norm_gate"]
         print(f"[bench] norm gate fwd {c['fwd_ms']:.3f} ms ({c['fwd_GBps']:.0f} GB/s), "
               f"bwd {c['bwd_ms']:.3f} ms ({c['bwd_GBps']:.0f} GB/s)", file=sys.stderr, flush=True)
+    if not args.no_serve:
+        del inp
+        torch.cuda.empty_cache()
+        result["serve"] = bench_serve(dev)
+        c = result["serve"]
+        print(f"[bench] serve prefill {c['prefill']['ms']:.3f} ms ({c['prefill']['tokens_per_s'] / 1e6:.1f} M tok/s), "
+              f"conv token {c['conv_token']['us']:.1f} us ({c['conv_token']['GBps']:.0f} GB/s)", file=sys.stderr,
+              flush=True)
+        inp = None
     if not args.no_decode:
         del inp
         torch.cuda.empty_cache()

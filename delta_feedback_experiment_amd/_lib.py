@@ -22,7 +22,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class RecurrentArgs(ctypes.Structure):
@@ -65,7 +65,7 @@ class PrecondArgs(ctypes.Structure):
         ("kw", c_void_p), ("a_chunk", c_void_p), ("num_chunks", c_int32),
         ("dkw", c_void_p), ("dk", c_void_p), ("dg_atk", c_void_p), ("dbeta_atk", c_void_p),
         ("dcenter_part", c_void_p), ("dcenter", c_void_p), ("dA0", c_void_p), ("dA_T", c_void_p),
-        ("table", c_void_p),
+        ("table", c_void_p), ("slot_idx", c_void_p), ("pool_size", c_int64),
     ]
 
 
@@ -84,6 +84,7 @@ class ChunkFwdArgs(ctypes.Structure):
         ("final_state", c_void_p), ("o", c_void_p),
         ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
         ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p),
+        ("slot_idx", c_void_p), ("pool_size", c_int64),
     ]
 
 
@@ -104,7 +105,8 @@ class QkvConvArgs(ctypes.Structure):
         ("norm_channels", c_int32), ("conv_size", c_int32), ("eps", c_float),
         ("x", c_void_p), ("weight", c_void_p), ("q", c_void_p), ("k", c_void_p), ("v", c_void_p),
         ("dq", c_void_p), ("dk", c_void_p), ("dv", c_void_p), ("dx", c_void_p), ("dw", c_void_p),
-        ("dw_part", c_void_p),
+        ("dw_part", c_void_p), ("slot_idx", c_void_p), ("history_in", c_void_p), ("history_out", c_void_p),
+        ("pool_size", c_int64),
     ]
 
 

@@ -94,17 +94,25 @@ class FwdSaved:
 def chunk_forward(
     plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor,
     scale: float, initial_state: Tensor | None, output_final_state: bool, save_states: bool,
+    *, slot_idx: Tensor | None = None, final_state: Tensor | None = None, out: Tensor | None = None,
 ) -> tuple[Tensor, Tensor | None, FwdSaved]:
-    """Run the chunk forward on flat ``[N_tok, H, D]`` operands."""
+    """Run the chunk forward on flat ``[N_tok, H, D]`` operands.
+
+    With ``slot_idx`` (int32 ``[N]``) the states are rows of a pool:
+    ``initial_state`` (or zero when ``None``) and ``final_state`` are
+    ``[P, H, D, D]`` and document ``n`` uses row ``slot_idx[n]`` of each."""
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
-    o = torch.empty_like(v)
+    o = torch.empty_like(v) if out is None else out
     w = torch.empty_like(k)
     u = torch.empty_like(v)
     aqk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
     akk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
     h = torch.empty(plan.num_chunks, H, D, D, device=dev, dtype=q.dtype) if save_states else None
-    S_T = torch.empty(N, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
+    if slot_idx is not None:
+        S_T = final_state
+    else:
+        S_T = torch.empty(N, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
     per_channel = gcum.dim() == 3
     qg = torch.empty_like(q) if per_channel else None
     kg = torch.empty_like(k) if per_channel else None
@@ -114,6 +122,7 @@ def chunk_forward(
         gate_per_channel=int(per_channel), beta=_ptr(beta32), scale=float(scale),
         initial_state=_ptr(initial_state), final_state=_ptr(S_T), o=_ptr(o),
         w=_ptr(w), u=_ptr(u), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), qg=_ptr(qg), kg=_ptr(kg),
+        slot_idx=_ptr(slot_idx), pool_size=0 if S_T is None else S_T.shape[0],
     )
     _lib.call("pkda_chunk_fwd", args, _stream(dev))
     return o, S_T, FwdSaved(w, u, aqk, akk, h, qg, kg)

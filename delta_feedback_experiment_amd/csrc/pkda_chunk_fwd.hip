@@ -50,7 +50,11 @@ struct FwdParams {
   void* h;
   void* qg;   // per-channel gates: s e^G q
   void* kg;   // per-channel gates: e^{G_last - G} kw
+  const int32_t* slot;  // document -> state row (slot-indexed pools), or null
 };
+
+// Row of the initial/final state of document n.
+__device__ __forceinline__ int64_t state_row(const FwdParams& p, int n) { return p.slot ? p.slot[n] : n; }
 
 // ---------------------------------------------------------------------------
 // Blocked inverse of (I + A) in place, A strictly lower 64x64 FP32 in LDS
@@ -544,7 +548,7 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = 16 * rt + acc_row(lane, j), c = v0 + 16 * ct + acc_col(lane);
-      S[i][j] = p.s0 ? p.s0[((int64_t)n * H + h) * D * D + r * D + c] : 0.f;
+      S[i][j] = p.s0 ? p.s0[(state_row(p, n) * H + h) * D * D + r * D + c] : 0.f;
     }
   }
 
@@ -652,7 +656,7 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
     for (int i = 0; i < NS; ++i) {
       const int ti = wave * NS + i;
       const int rt = ti / NCT, ct = ti % NCT;
-      float* sb = p.sT + ((int64_t)n * H + h) * D * D + v0;
+      float* sb = p.sT + (state_row(p, n) * H + h) * D * D + v0;
       store_acc_global<float>(sb, D, S[i], 16 * rt, 16 * ct, D, lane);
     }
   }
@@ -764,7 +768,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
   for (int rt = 0; rt < NKT; ++rt)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      S[rt][j] = p.s0 ? p.s0[(((int64_t)n * H + h) * D + 16 * rt + q4 + j) * D + col] : 0.f;
+      S[rt][j] = p.s0 ? p.s0[((state_row(p, n) * H + h) * D + 16 * rt + q4 + j) * D + col] : 0.f;
   const float scale = p.scale;
 
   for (int jc = 0; jc < count; ++jc) {
@@ -871,7 +875,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
     }
   }
   if (p.sT) {
-    float* sb = p.sT + ((int64_t)n * H + h) * D * D + col0;
+    float* sb = p.sT + (state_row(p, n) * H + h) * D * D + col0;
 #pragma unroll
     for (int rt = 0; rt < NKT; ++rt) store_acc_global<float>(sb, D, S[rt], 16 * rt, 0, D, lane);
   }
@@ -976,6 +980,8 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   p.w = a->w; p.u = a->u; p.aqk = a->aqk; p.akk = a->akk; p.h = a->h;
   p.qg = a->gate_per_channel ? a->qg : nullptr;
   p.kg = a->gate_per_channel ? a->kg : nullptr;
+  p.slot = a->slot_idx;
+  PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed states need pool_size > 0");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   const int st = a->stages;

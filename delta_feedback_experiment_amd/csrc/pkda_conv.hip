@@ -58,6 +58,9 @@ struct ConvParams {
   void* dx;        // backward outputs
   float* dw_part;  // [tiles, C, W] FP32
   void* dw;        // [C, W] in w_dtype
+  const int32_t* slot;   // cached rows: row -> history slot, or null
+  const void* hist_in;   // [pool, W - 1, C] or null (zero history)
+  void* hist_out;        // [pool, W - 1, C] or null
   int B, T, C, P, head_dim, norm_channels, x_dtype;
   float eps;
   int tiles_per_row;
@@ -179,6 +182,9 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_fwd_kernel(ConvParams p
     const int t = t0 - (W - 1) + w;
     if (t >= 0) {
       Vec8<T>::load(xs + (int64_t)t * p.C, hist[w]);
+    } else if (p.hist_in) {  // the row's cached projections before its first token
+      const int64_t sb = p.slot ? p.slot[b] : b;
+      Vec8<T>::load(static_cast<const T*>(p.hist_in) + (sb * (W - 1) + (W - 1) + t) * p.C + c0, hist[w]);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) hist[w][j] = 0.f;
@@ -228,6 +234,16 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_fwd_kernel(ConvParams p
     }
 #pragma unroll
     for (int i = 0; i < kGroup; ++i) xa[i] = xb[i];
+  }
+  // a row that is one tile (a decode token, a short prompt) leaves its
+  // history here: hist holds its last W - 1 rows of history ++ x, and this
+  // thread read its slot's old history at the start (in place is safe)
+  if constexpr (W > 1) {
+    if (p.hist_out && tpr == 1) {
+      const int64_t sb = p.slot ? p.slot[b] : b;
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w) Vec8<T>::store(static_cast<T*>(p.hist_out) + (sb * (W - 1) + w) * p.C + c0, hist[w]);
+    }
   }
 }
 
@@ -397,13 +413,131 @@ __global__ __launch_bounds__(256) void qkv_conv_dw_kernel(ConvParams p, int W, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// decode tokens: rows of one token, each continuing its slot's history.  A
+// thread owns 8 channels of kTokRows rows: it loads its weights once, and
+// every row's W - 1 history rows and new projection row before computing;
+// out = the normalised silu(conv), and the slot's history shifts by one row
+// in place (each thread reads its channels' rows before writing them).
+// ---------------------------------------------------------------------------
+constexpr int kTokRows = 8;
+
+template <typename T, int W, int G>
+__global__ __launch_bounds__(kConvThreads) void qkv_conv_token_kernel(ConvParams p) {
+  const int c0 = (blockIdx.y * kConvThreads + threadIdx.x) * 8;
+  if (c0 >= p.C) return;
+  const bool norm = c0 < p.norm_channels;
+  float wt[8][W];
+  load_weights<W>(p, c0, wt);
+  const int b0 = blockIdx.x * kTokRows;
+  const int nb = min(kTokRows, p.B - b0);
+  Raw8<T> hr[kTokRows][W - 1], xr[kTokRows];
+#pragma unroll
+  for (int r = 0; r < kTokRows; ++r) {
+    if (r >= nb) break;
+    const int b = b0 + r;
+    const int64_t sb = p.slot ? p.slot[b] : b;
+    xr[r].load(static_cast<const T*>(p.x) + (int64_t)b * p.C + c0);
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) {
+      if (p.hist_in) {
+        hr[r][w].load(static_cast<const T*>(p.hist_in) + (sb * (W - 1) + w) * p.C + c0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < Raw8<T>::N; ++i) hr[r][w].r[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kTokRows; ++r) {
+    if (r >= nb) break;
+    const int b = b0 + r;
+    const int64_t sb = p.slot ? p.slot[b] : b;
+    float xt[8], hist[W - 1][8];
+    xr[r].unpack(xt);
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) hr[r][w].unpack(hist[w]);
+    float y[8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float a = wt[j][W - 1] * xt[j];
+#pragma unroll
+      for (int w = 0; w < W - 1; ++w) a += wt[j][w] * hist[w][j];
+      y[j] = a * sigmoid_fast(a);
+      ss += y[j] * y[j];
+    }
+    if (norm) {
+      const float rn = rsqrtf(head_sum<G>(ss) + p.eps);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] *= rn;
+    }
+    int off;
+    T* out = slab_ptr<T>(p.q, p.k, p.v, p.P, c0, (int64_t)b, off) + off;
+    Vec8<T>::store(out, y);
+    if (p.hist_out) {
+      T* ho = static_cast<T*>(p.hist_out) + sb * (W - 1) * p.C + c0;
+#pragma unroll
+      for (int w = 0; w + 1 < W - 1; ++w) Vec8<T>::store(ho + (int64_t)w * p.C, hist[w + 1]);
+      Vec8<T>::store(ho + (int64_t)(W - 2) * p.C, xt);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// cached rows longer than one forward tile: the history left for the next
+// call, the last W - 1 rows of history ++ x.  One thread per 8 channels of
+// one row reads every row it needs before writing any, so history_out may
+// alias history_in; it runs after the forward kernel (whose first tile of a
+// row reads history_in) on the same stream.
+// ---------------------------------------------------------------------------
+template <typename T, int W>
+__global__ __launch_bounds__(kConvThreads) void qkv_conv_history_kernel(ConvParams p) {
+  const int b = blockIdx.x;
+  const int c0 = (blockIdx.y * kConvThreads + threadIdx.x) * 8;
+  if (c0 >= p.C) return;
+  const int64_t sb = p.slot ? p.slot[b] : b;
+  const T* xs = static_cast<const T*>(p.x) + (int64_t)b * p.T * p.C + c0;
+  float rows[W - 1][8];
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) {
+    const int t = p.T - (W - 1) + j;  // position relative to the row's first token
+    if (t >= 0) {
+      Vec8<T>::load(xs + (int64_t)t * p.C, rows[j]);
+    } else if (p.hist_in) {
+      Vec8<T>::load(static_cast<const T*>(p.hist_in) + (sb * (W - 1) + (W - 1) + t) * p.C + c0, rows[j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rows[j][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < W - 1; ++j) Vec8<T>::store(static_cast<T*>(p.hist_out) + (sb * (W - 1) + j) * p.C + c0, rows[j]);
+}
+
 template <typename T, int W, int G>
 int launch_conv(const ConvParams& p, bool backward, hipStream_t s) {
   const int cblocks = (p.C + 8 * kConvThreads - 1) / (8 * kConvThreads);
   if (!backward) {
-    const int tiles = p.B * ((p.T + kConvTileFwd - 1) / kConvTileFwd);
-    hipLaunchKernelGGL((qkv_conv_fwd_kernel<T, W, G>), dim3(tiles, cblocks), dim3(kConvThreads), 0, s, p);
-    return launch_status("pkda_qkv_conv_fwd");
+    if constexpr (W > 1) {
+      if (p.T == 1 && (p.hist_in || p.hist_out)) {  // decode tokens
+        hipLaunchKernelGGL((qkv_conv_token_kernel<T, W, G>), dim3((p.B + kTokRows - 1) / kTokRows, cblocks),
+                           dim3(kConvThreads), 0, s, p);
+        return launch_status("pkda_qkv_conv_fwd(token)");
+      }
+    }
+    if (p.T > 0) {
+      const int tiles = p.B * ((p.T + kConvTileFwd - 1) / kConvTileFwd);
+      hipLaunchKernelGGL((qkv_conv_fwd_kernel<T, W, G>), dim3(tiles, cblocks), dim3(kConvThreads), 0, s, p);
+      if (int st = launch_status("pkda_qkv_conv_fwd")) return st;
+    }
+    if constexpr (W > 1) {
+      if (p.hist_out && (p.T == 0 || p.T > kConvTileFwd)) {  // else the forward kernel wrote it
+        hipLaunchKernelGGL((qkv_conv_history_kernel<T, W>), dim3(p.B, cblocks), dim3(kConvThreads), 0, s, p);
+        return launch_status("pkda_qkv_conv_fwd(history)");
+      }
+    }
+    return 0;
   }
   const int tiles = p.B * p.tiles_per_row;
   hipLaunchKernelGGL((qkv_conv_bwd_kernel<T, W, G>), dim3(tiles, cblocks), dim3(kConvThreads), 0, s, p);
@@ -466,7 +600,14 @@ int conv_call(const pkda_qkv_conv_args* a, void* stream, bool backward) {
   p.q = a->q; p.k = a->k; p.v = a->v;
   p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
   p.dx = a->dx; p.dw = a->dw; p.dw_part = a->dw_part;
-  if (p.B == 0 || p.T == 0) {
+  p.slot = a->slot_idx;
+  p.hist_in = a->history_in;
+  p.hist_out = a->history_out;
+  const bool cached = a->history_in || a->history_out;
+  PKDA_REQUIRE(!backward || !cached, PKDA_EUNSUPPORTED, "conv histories are a forward (cached rows) feature");
+  PKDA_REQUIRE(!cached || a->conv_size > 1, PKDA_EINVAL, "conv_size 1 keeps no history");
+  PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed histories need pool_size > 0");
+  if (p.B == 0 || (p.T == 0 && !(a->history_out && !backward))) {
     PKDA_REQUIRE(!backward || a->dw, PKDA_EINVAL, "null dw");
     return 0;  // an empty batch: nothing to launch (dw is the caller's zeros)
   }
@@ -474,7 +615,7 @@ int conv_call(const pkda_qkv_conv_args* a, void* stream, bool backward) {
     PKDA_REQUIRE(a->x && a->weight && a->dq && a->dk && a->dv && a->dx && a->dw && a->dw_part, PKDA_EINVAL,
                  "null tensor");
   } else {
-    PKDA_REQUIRE(a->x && a->weight && a->q && a->k && a->v, PKDA_EINVAL, "null tensor");
+    PKDA_REQUIRE(p.T == 0 || (a->x && a->weight && a->q && a->k && a->v), PKDA_EINVAL, "null tensor");
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   return a->dtype == PKDA_BF16 ? dispatch<bf16_t>(p, a->conv_size, backward, s)

@@ -46,6 +46,7 @@ struct PrecondParams {
   float* dcenter_part;
   float* dA0;
   const float* dA_T;
+  const int32_t* slot;  // forward: document -> A-state row, or null
 };
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(PrecondThreads<D>::v) void precond_fwd_kernel(Preco
   const int H = p.H;
   int first, count, dstart, dlen;
   doc_chunks(p.geom, n, first, count, dstart, dlen);
-  const int64_t sh = (int64_t)n * H + h;
+  const int64_t sh = (int64_t)(p.slot ? p.slot[n] : n) * H + h;  // state row
   float a = p.a0 ? p.a0[sh * D + c] : 0.f;
   const float center = p.center[h];
   const T* k = static_cast<const T*>(p.k);
@@ -191,6 +192,8 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
   p.dcenter_part = a->dcenter_part;
   p.dA0 = a->dA0;
   p.dA_T = a->dA_T;
+  p.slot = a->slot_idx;
+  PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed A states need pool_size > 0");
   return 0;
 }
 
@@ -241,6 +244,7 @@ extern "C" int pkda_precond_fwd(const pkda_precond_args* a, void* stream) {
 extern "C" int pkda_precond_bwd(const pkda_precond_args* a, void* stream) {
   PrecondParams p;
   if (int st = precond_common(a, p)) return st;
+  PKDA_REQUIRE(!a->slot_idx, PKDA_EUNSUPPORTED, "slot-indexed A states are a forward (prefill) feature");
   PKDA_REQUIRE(a->dcenter && a->dcenter_part, PKDA_EINVAL, "preconditioner backward needs dcenter buffers");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->num_seqs > 0) {

@@ -32,24 +32,34 @@ def _flat2(t: Tensor, plan) -> Tensor:
 
 
 def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
-                    initial_A_state: Tensor | None) -> PrecondState:
-    """Write keys for flat ``kf [N_tok, H, K]``; returns the scan's state."""
+                    initial_A_state: Tensor | None, *, slot_idx: Tensor | None = None,
+                    final_A: Tensor | None = None) -> PrecondState:
+    """Write keys for flat ``kf [N_tok, H, K]``; returns the scan's state.
+
+    With ``slot_idx`` the A states are rows of a pool: ``initial_A_state``
+    (zero when ``None``) and ``final_A`` are contiguous FP32 ``[P, H, K]``,
+    used in place (no conversion copy), document ``n`` at row ``slot_idx[n]``."""
     dev = kf.device
     H, K, N = plan.heads, plan.head_dim, plan.num_seqs
     ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
     if cen.shape != (H,):
         raise ValueError(f"log_atk_scale must be [{H}]")
-    a0 = _f32(initial_A_state)
-    if a0 is not None and tuple(a0.shape) != (N, H, K):
-        raise ValueError(f"initial_A_state must be {(N, H, K)}")
+    if slot_idx is not None:
+        a0 = initial_A_state
+    else:
+        a0 = _f32(initial_A_state)
+        if a0 is not None and tuple(a0.shape) != (N, H, K):
+            raise ValueError(f"initial_A_state must be {(N, H, K)}")
     kw = torch.empty_like(kf)
     a_chunk = torch.empty(plan.num_chunks, H, K, device=dev, dtype=torch.float32)
-    final_A = torch.empty(N, H, K, device=dev, dtype=torch.float32)
+    if final_A is None:
+        final_A = torch.empty(N, H, K, device=dev, dtype=torch.float32)
     args = _lib.PrecondArgs(
         dtype=_dtype_code(kf), num_seqs=N, seqlen=plan.seqlen, heads=H, head_dim=K,
         cu_seqlens=_ptr(plan.cu_seqlens), k=_ptr(kf), g_atk=_ptr(ga), beta_atk=_ptr(ba), center=_ptr(cen),
         squash_x=float(x), squash_eps=float(eps), initial_A_state=_ptr(a0), final_A_state=_ptr(final_A),
         kw=_ptr(kw), a_chunk=_ptr(a_chunk), num_chunks=plan.num_chunks, table=_ptr(plan.table),
+        slot_idx=_ptr(slot_idx), pool_size=final_A.shape[0] if slot_idx is not None else 0,
     )
     _lib.call("pkda_precond_fwd", args, _stream(dev))
     return PrecondState(kw, a_chunk, final_A, a0)

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 2
+#define PKDA_ABI_VERSION 3
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -224,6 +224,10 @@ typedef struct pkda_precond_args {
   float* dA0;                    /* [N,H,K] or NULL */
   const float* dA_T;             /* [N,H,K] or NULL */
   const int32_t* table;          /* pkda_chunk_table output or NULL */
+  /* forward only: slot-indexed A states, as pkda_chunk_fwd_args.slot_idx
+   * (initial_A_state / final_A_state are then [pool_size, H, K]) */
+  const int32_t* slot_idx;
+  int64_t pool_size;
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
@@ -283,6 +287,14 @@ typedef struct pkda_chunk_fwd_args {
   void *w, *u, *aqk, *akk, *h;
   int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
   void *qg, *kg;               /* per-channel gates only, else NULL */
+  /* Slot-indexed states (cached prefill into a decode pool): when slot_idx
+   * (int32 [num_seqs], device) is given, document n starts from
+   * initial_state[slot_idx[n]] (zero when initial_state is NULL) and leaves its
+   * final state in final_state[slot_idx[n]]; both are then
+   * [pool_size, H, K, V] and may be the same pool (in place: slots must be
+   * unique).  NULL: document n uses row n. */
+  const int32_t* slot_idx;
+  int64_t pool_size;
 } pkda_chunk_fwd_args;
 
 int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
@@ -345,6 +357,14 @@ int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);
  *             pkda_qkv_conv_workspace(batch, seqlen, width, conv_size)
  *             elements, summed in a fixed order (deterministic).
  * head_dim 32, 64 or 128; conv_size 1..4; width a multiple of head_dim.
+ *
+ * Cached rows (forward only; the decode-time counterpart of the reference's
+ * conv_state, delta_feedback_experiment/pkda.py:240-260): history_in
+ * [pool_size, conv_size - 1, 3 * width] (dtype) holds, per slot, the raw
+ * projections of the conv_size - 1 positions before the row's first token
+ * (oldest first; zero history when NULL); history_out (same shape, may be
+ * history_in itself) receives the last conv_size - 1 rows of history ++ x.
+ * Row b uses slot slot_idx[b] (int32 [batch], device; row b when NULL).
  * ------------------------------------------------------------------------- */
 typedef struct pkda_qkv_conv_args {
   int32_t struct_size;
@@ -359,6 +379,10 @@ typedef struct pkda_qkv_conv_args {
   void* dx;                 /* backward outputs */
   void* dw;
   float* dw_part;           /* backward workspace */
+  const int32_t* slot_idx;  /* cached rows, forward only (see above) */
+  const void* history_in;
+  void* history_out;
+  int64_t pool_size;
 } pkda_qkv_conv_args;
 
 int64_t pkda_qkv_conv_workspace(int32_t batch, int32_t seqlen, int32_t width, int32_t conv_size);

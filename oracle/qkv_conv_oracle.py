@@ -27,28 +27,43 @@ import torch.nn.functional as F
 from torch import Tensor
 
 
-def causal_conv_silu(x: Tensor, weight: Tensor, dtype: torch.dtype = torch.float32) -> Tensor:
-    """``silu(sum_w weight[c, w] x[b, t - (W - 1) + w, c])`` with zero history.
+def causal_conv_silu(x: Tensor, weight: Tensor, dtype: torch.dtype = torch.float32,
+                     history: Tensor | None = None) -> Tensor:
+    """``silu(sum_w weight[c, w] x[b, t - (W - 1) + w, c])``.
 
-    ``x`` is ``[B, T, C]``, ``weight`` ``[C, W]``; computed in ``dtype``.
+    ``x`` is ``[B, T, C]``, ``weight`` ``[C, W]``; computed in ``dtype``.  The
+    rows before ``t = 0`` are ``history [B, W - 1, C]`` (oldest first) or zero:
+    a cached row's stored conv state prepended to its new projections
+    (``delta_feedback_experiment/pkda.py:205-219,240-260``).
     """
     xf, wf = x.to(dtype), weight.to(dtype)
     B, T, C = xf.shape
     W = wf.shape[1]
-    padded = torch.cat((xf.new_zeros(B, W - 1, C), xf), dim=1)
+    before = xf.new_zeros(B, W - 1, C) if history is None else history.to(dtype)
+    padded = torch.cat((before, xf), dim=1)
     a = sum(wf[:, w] * padded[:, w:w + T] for w in range(W))
     return F.silu(a)
 
 
+def history_after(x: Tensor, history: Tensor | None, conv_size: int) -> Tensor:
+    """The conv state a cached row keeps: the last ``conv_size - 1`` rows of
+    ``history ++ x`` (``combined[..., -history:]``, pkda.py:219 and 248-258),
+    ``[B, conv_size - 1, C]`` in ``x.dtype``."""
+    B, T, C = x.shape
+    before = x.new_zeros(B, conv_size - 1, C) if history is None else history.to(x.dtype)
+    return torch.cat((before, x), dim=1)[:, T:]
+
+
 def qkv_conv_reference(x: Tensor, weight: Tensor, head_dim: int, norm_channels: int, eps: float = 1e-6,
                        dtype: torch.dtype = torch.float32, out_dtype: torch.dtype | None = None,
-                       ) -> tuple[Tensor, Tensor, Tensor]:
+                       history: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """``(q, k, v)`` slabs ``[B, T, C / 3]`` of the fused op (fla_ops.py:134-170).
 
     Differentiable (FP32 or FP64 autograd is the gradient oracle).  The outputs
-    come in ``out_dtype`` (default: ``x.dtype``).
+    come in ``out_dtype`` (default: ``x.dtype``).  ``history`` as in
+    :func:`causal_conv_silu`.
     """
-    y = causal_conv_silu(x, weight, dtype)
+    y = causal_conv_silu(x, weight, dtype, history)
     B, T, C = y.shape
     if norm_channels:
         yn = y[..., :norm_channels].reshape(B, T, norm_channels // head_dim, head_dim)

@@ -9,6 +9,10 @@
 * The normalised slabs have unit L2 norm per head (up to eps), the value slab
   is left unnormalised.
 * Planted mistakes (taps reversed, a non-causal offset) fail the first check.
+* Cached rows (a stored history in front of the projections): the reference's
+  formulation with its conv state concatenated (pkda.py:205-219), and
+  splitting a row anywhere -- the second piece continuing from the history the
+  first one leaves -- reproduces the unsplit row exactly.
 """
 
 from __future__ import annotations
@@ -75,3 +79,48 @@ def test_planted_mistakes_fail(mistake):
         padded = torch.cat((x, x.new_zeros(1, 3, 8)), dim=1)  # future instead of history
         got = F.silu(sum(w[:, i] * padded[:, i:i + 16] for i in range(4)))
     assert not torch.allclose(got, _reference_formulation(x, w), atol=1e-6)
+
+
+def _reference_with_state(x, weight, state):
+    """pkda.py:203-219 with a conv state [B, C, W - 1]: cat(state, x_t), then conv1d."""
+    C, W = weight.shape
+    combined = torch.cat((state, x.transpose(1, 2)), dim=-1)
+    out = F.conv1d(combined, weight.unsqueeze(1), bias=None, groups=C).transpose(1, 2)
+    return F.silu(out), combined[..., -(W - 1):]
+
+
+@pytest.mark.parametrize("W", [2, 3, 4])
+@pytest.mark.parametrize("T", [1, 2, 9])
+def test_history_matches_the_reference_conv_state(W, T):
+    gen = torch.Generator().manual_seed(10 * W + T)
+    x = torch.randn(2, T, 12, generator=gen, dtype=torch.float64)
+    w = torch.randn(12, W, generator=gen, dtype=torch.float64)
+    hist = torch.randn(2, W - 1, 12, generator=gen, dtype=torch.float64)
+    want, state = _reference_with_state(x, w, hist.transpose(1, 2))
+    assert torch.allclose(co.causal_conv_silu(x, w, torch.float64, hist), want, atol=1e-12, rtol=0)
+    assert torch.equal(co.history_after(x, hist, W), state.transpose(1, 2))
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 17, 39])
+def test_split_rows_continue_from_the_history(split):
+    gen = torch.Generator().manual_seed(split)
+    B, T, H, d, W = 2, 40, 2, 8, 4
+    x = torch.randn(B, T, 3 * H * d, generator=gen, dtype=torch.float64)
+    w = torch.randn(3 * H * d, W, generator=gen, dtype=torch.float64)
+    whole = co.qkv_conv_reference(x, w, d, 2 * H * d, dtype=torch.float64)
+    first = co.qkv_conv_reference(x[:, :split], w, d, 2 * H * d, dtype=torch.float64)
+    hist = co.history_after(x[:, :split], None, W)
+    second = co.qkv_conv_reference(x[:, split:], w, d, 2 * H * d, dtype=torch.float64, history=hist)
+    for a, b, c in zip(whole, first, second):
+        assert torch.equal(a, torch.cat((b, c), dim=1))
+    assert torch.equal(co.history_after(x[:, split:], hist, W), x[:, -(W - 1):])
+
+
+def test_planted_history_mistake_fails():
+    """Oldest-last history order would still convolve, but not the same rows."""
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(1, 5, 6, generator=gen, dtype=torch.float64)
+    w = torch.randn(6, 4, generator=gen, dtype=torch.float64)
+    hist = torch.randn(1, 3, 6, generator=gen, dtype=torch.float64)
+    want, _ = _reference_with_state(x, w, hist.transpose(1, 2))
+    assert not torch.allclose(co.causal_conv_silu(x, w, torch.float64, hist.flip(1)), want, atol=1e-6)
