@@ -26,6 +26,9 @@ Printed as ONE JSON line:
                   geometry, achieved HBM GB/s against 8 TB/s;
   norm_gate       its consumer (RMSNorm sigmoid output gate) on the c2
                   output shape, achieved HBM GB/s against 8 TB/s;
+  controls        the control path at the c2 geometry: control activations
+                  and their packed gradient, and the gate with the decay
+                  expansion fused against the materialised form;
   serve           the slot-pool serving path: a cached prefill of the c2
                   shape into pool slots (tokens/s, MFMA fraction) and one
                   decode token of the convolution with slot histories
@@ -494,6 +497,69 @@ def bench_serve(dev: torch.device, reps: int = 10) -> dict:
     }
 
 
+def bench_controls(dev: torch.device, reps: int = 20) -> dict:
+    """The control path at the c2 geometry (8 x 4,096 tokens, H16 d128, BF16):
+    the control activations with their packed gradient, and the gate with the
+    decay expansion fused (hidden rows in, chunk-local cumsum out) against the
+    materialised form (F.linear's raw decay, then the raw-gate kernel).
+    Algorithmic bytes: controls forward reads the 3H logits and writes beta,
+    precond_decay (FP32), precond_beta; backward reads the logits and five
+    gradients and writes the packed gradient; the gate reads the hidden rows
+    and writes the FP32 cumsum [N, H, d]."""
+    from delta_feedback_experiment_amd import _lib, pkda_controls
+    from delta_feedback_experiment_amd.chunk import ChunkPlan, gate_forward, low_rank_rows
+    from delta_feedback_experiment_amd.controls import pkda_controls_act, pkda_controls_backward
+
+    def timed(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    B, T, H, D = 8, 4096, 16, 128
+    N = B * T
+    width = 2 * D + 3 * H
+    gen = torch.Generator(device=dev).manual_seed(21)
+    packed = (torch.randn(B, T, width, generator=gen, device=dev) / 3 ** 0.5).to(torch.bfloat16)
+    A_p = torch.rand(H, generator=gen, device=dev) + 1
+    dt_p = 0.1 * torch.randn(H, generator=gen, device=dev)
+    grads = (torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16),
+             torch.randn(B, T, H, generator=gen, device=dev).to(torch.bfloat16),
+             torch.randn(B, T, H, generator=gen, device=dev),
+             torch.randn(B, T, H, generator=gen, device=dev).to(torch.bfloat16),
+             torch.randn(B, T, D, generator=gen, device=dev).to(torch.bfloat16))
+    fwd_ms = timed(lambda: pkda_controls_act(packed, A_p, dt_p, D, H))
+    bwd_ms = timed(lambda: pkda_controls_backward(packed, A_p, dt_p, *grads, D, H))
+    fwd_bytes = N * 3 * H * 2 + N * H * (2 + 4 + 2)
+    bwd_bytes = N * 3 * H * 2 + N * (2 * D * 2 + H * (2 + 4 + 2)) + N * width * 2
+    hidden = pkda_controls(packed, A_p, dt_p, D, H)[0]
+    up = ((torch.rand(H * D, D, generator=gen, device=dev) * 2 - 1) / D ** 0.5).to(torch.bfloat16)
+    A_log = torch.rand(H, generator=gen, device=dev) + 1
+    dt = 0.1 * torch.randn(H * D, generator=gen, device=dev)
+    plan = ChunkPlan.make(torch.empty(B, T, H, D, device=dev, dtype=torch.bfloat16), None)
+    rows = low_rank_rows(hidden, N)
+    fused_ms = timed(lambda: gate_forward(plan, rows, _lib.GATE_LOW_RANK, A_log, dt, up))
+
+    def materialised():
+        raw = torch.nn.functional.linear(hidden, up).reshape(N, H, D)
+        return gate_forward(plan, raw, _lib.GATE_RAW_CHANNEL, A_log, dt)
+
+    mat_ms = timed(materialised)
+    gate_bytes = N * D * 2 + N * H * D * 4
+    return {
+        "workload": "c2 geometry: 8 x 4096 tokens, H16 d128, bf16 packed controls [.., 2d + 3H]",
+        "controls_fwd_us": fwd_ms * 1e3, "controls_bwd_us": bwd_ms * 1e3,
+        "controls_fwd_GBps": fwd_bytes / (fwd_ms / 1e3) / 1e9, "controls_bwd_GBps": bwd_bytes / (bwd_ms / 1e3) / 1e9,
+        "gate_fused_ms": fused_ms, "gate_materialised_ms": mat_ms,
+        "gate_fused_GBps": gate_bytes / (fused_ms / 1e3) / 1e9,
+    }
+
+
 def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
     """A plain device copy of ``nbytes`` (read + write), the practical HBM
     ceiling beside the kernels' rates and the scale for the byte counters."""
@@ -650,6 +716,12 @@ def main() -> None:
         c = result["norm_gate"]
         print(f"[bench] norm gate fwd {c['fwd_ms']:.3f} ms ({c['fwd_GBps']:.0f} GB/s), "
               f"bwd {c['bwd_ms']:.3f} ms ({c['bwd_GBps']:.0f} GB/s)", file=sys.stderr, flush=True)
+    if not args.no_conv:
+        result["controls"] = bench_controls(dev)
+        c = result["controls"]
+        print(f"[bench] controls fwd {c['controls_fwd_us']:.1f} us, bwd {c['controls_bwd_us']:.1f} us; "
+              f"gate with decay expansion {c['gate_fused_ms']:.3f} ms (materialised {c['gate_materialised_ms']:.3f} ms)",
+              file=sys.stderr, flush=True)
     if not args.no_serve:
         del inp
         torch.cuda.empty_cache()

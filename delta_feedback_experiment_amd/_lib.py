@@ -18,6 +18,7 @@ PKDA_BF16 = 1
 GATE_LOG_HEAD = 0
 GATE_LOG_CHANNEL = 1
 GATE_RAW_CHANNEL = 2
+GATE_LOW_RANK = 3
 STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
@@ -52,6 +53,7 @@ class GateArgs(ctypes.Structure):
         ("gcum", c_void_p), ("dgcum", c_void_p), ("dg", c_void_p), ("dA_log_part", c_void_p),
         ("ddt_bias_part", c_void_p), ("dA_log", c_void_p), ("ddt_bias", c_void_p),
         ("num_chunks", c_int32), ("table", c_void_p),
+        ("up_weight", c_void_p), ("rank", c_int32), ("g_stride", c_int32),
     ]
 
 
@@ -119,8 +121,20 @@ class NormGateArgs(ctypes.Structure):
     ]
 
 
+class ControlsArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", c_int32), ("dtype", c_int32), ("rows", c_int64),
+        ("heads", c_int32), ("rank", c_int32), ("gate_width", c_int32), ("row_stride", c_int32),
+        ("packed", c_void_p), ("A_log_p", c_void_p), ("dt_bias_p", c_void_p),
+        ("beta", c_void_p), ("precond_decay", c_void_p), ("precond_beta", c_void_p),
+        ("d_decay_hidden", c_void_p), ("dbeta", c_void_p), ("dprecond_decay", c_void_p),
+        ("dprecond_beta", c_void_p), ("d_gate_hidden", c_void_p),
+        ("dpacked", c_void_p), ("part", c_void_p), ("dA_log_p", c_void_p), ("ddt_bias_p", c_void_p),
+    ]
+
+
 _ARG_KINDS = {0: RecurrentArgs, 1: GateArgs, 2: PrecondArgs, 3: ChunkFwdArgs, 4: ChunkBwdArgs, 5: QkvConvArgs,
-              6: NormGateArgs}
+              6: NormGateArgs, 7: ControlsArgs}
 _LIB: ctypes.CDLL | None = None
 
 
@@ -172,6 +186,7 @@ def lib() -> ctypes.CDLL:
         ("pkda_chunk_fwd", ChunkFwdArgs), ("pkda_chunk_bwd", ChunkBwdArgs),
         ("pkda_qkv_conv_fwd", QkvConvArgs), ("pkda_qkv_conv_bwd", QkvConvArgs),
         ("pkda_norm_gate_fwd", NormGateArgs), ("pkda_norm_gate_bwd", NormGateArgs),
+        ("pkda_controls_fwd", ControlsArgs), ("pkda_controls_bwd", ControlsArgs),
     ):
         fn = getattr(handle, name, None)
         if fn is not None:
@@ -181,6 +196,8 @@ def lib() -> ctypes.CDLL:
     handle.pkda_qkv_conv_workspace.argtypes = [c_int32, c_int32, c_int32, c_int32]
     handle.pkda_norm_gate_workspace.restype = c_int64
     handle.pkda_norm_gate_workspace.argtypes = [c_int64, c_int32]
+    handle.pkda_controls_workspace.restype = c_int64
+    handle.pkda_controls_workspace.argtypes = [c_int64, c_int32]
     handle.pkda_chunk_table.restype = c_int32
     handle.pkda_chunk_table.argtypes = [c_void_p, c_int32, c_int32, c_void_p, c_void_p]
     if handle.pkda_abi_version() != ABI_VERSION:

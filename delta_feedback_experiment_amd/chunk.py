@@ -66,8 +66,12 @@ class ChunkPlan:
         )
 
 
-def gate_forward(plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt_bias: Tensor | None) -> Tensor:
-    """Chunk-local cumulative natural-log decay, FP32, ``[N_tok, H]`` or ``[N_tok, H, K]``."""
+def gate_forward(plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt_bias: Tensor | None,
+                 up_weight: Tensor | None = None) -> Tensor:
+    """Chunk-local cumulative natural-log decay, FP32, ``[N_tok, H]`` or ``[N_tok, H, K]``.
+
+    The low-rank form takes ``g`` as the decay hidden rows ``[N_tok, R]``
+    (unit column stride, any row stride) and ``up_weight [H*K, R]``."""
     shape = (plan.num_tokens, plan.heads) if kind == _lib.GATE_LOG_HEAD else (plan.num_tokens, plan.heads, plan.head_dim)
     gcum = torch.empty(shape, device=g.device, dtype=torch.float32)
     args = _lib.GateArgs(
@@ -76,8 +80,23 @@ def gate_forward(plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt
         A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), gcum=_ptr(gcum),
         num_chunks=plan.num_chunks, table=_ptr(plan.table),
     )
+    if kind == _lib.GATE_LOW_RANK:
+        args.up_weight, args.rank, args.g_stride = _ptr(up_weight), g.shape[-1], g.stride(0)
     _lib.call("pkda_gate_fwd", args, _stream(g.device))
     return gcum
+
+
+def low_rank_rows(hidden: Tensor, num_tokens: int) -> Tensor:
+    """The decay hidden ``[..., R]`` as ``[N_tok, R]`` rows the gate kernels
+    read with 16-byte loads: a view when its rows are evenly strided and
+    aligned (the reference's slice of the packed control projection), else a
+    contiguous copy."""
+    R = hidden.shape[-1]
+    rows = hidden.reshape(num_tokens, R)
+    vec = 16 // hidden.element_size()
+    if rows.stride(1) != 1 or rows.stride(0) % vec or rows.data_ptr() % 16:
+        rows = rows.contiguous()
+    return rows
 
 
 @dataclass
@@ -181,11 +200,16 @@ def chunk_backward(
 
 def gate_backward(
     plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt_bias: Tensor | None, dgcum: Tensor,
+    up_weight: Tensor | None = None,
 ) -> tuple[Tensor, Tensor | None, Tensor | None]:
-    """``dg`` (FP32, shape of ``g``) and, for the raw gate, ``dA_log``, ``ddt_bias``."""
+    """``dg`` (FP32, shape of ``g``) and, for the raw gate, ``dA_log``, ``ddt_bias``.
+
+    The low-rank form returns the raw gate's gradient ``[N_tok, H, K]`` as
+    ``dg``; the hidden rows' and the weight's gradients are two GEMMs of it
+    (:func:`low_rank_grads`)."""
     dev = dgcum.device
     dg = torch.empty(dgcum.shape, device=dev, dtype=torch.float32)
-    raw = kind == _lib.GATE_RAW_CHANNEL
+    raw = kind in (_lib.GATE_RAW_CHANNEL, _lib.GATE_LOW_RANK)
     dA_part = ddt_part = dA_log = ddt_bias = None
     if raw:
         H, D = plan.heads, plan.head_dim
@@ -200,8 +224,19 @@ def gate_backward(
         dA_log_part=_ptr(dA_part), ddt_bias_part=_ptr(ddt_part), dA_log=_ptr(dA_log), ddt_bias=_ptr(ddt_bias),
         num_chunks=plan.num_chunks, table=_ptr(plan.table),
     )
+    if kind == _lib.GATE_LOW_RANK:
+        args.up_weight, args.rank, args.g_stride = _ptr(up_weight), g.shape[-1], g.stride(0)
     _lib.call("pkda_gate_bwd", args, _stream(dev))
     return dg, dA_log, ddt_bias
+
+
+def low_rank_grads(draw: Tensor, hidden_rows: Tensor, up_weight: Tensor) -> tuple[Tensor, Tensor]:
+    """Gradients of ``raw = hidden up_weight^T`` from the raw gate's gradient
+    ``draw [N_tok, H, K]`` (FP32): ``(d hidden [N_tok, R], d up_weight [H*K, R])``,
+    FP32 library GEMMs (the backward of the reference's ``F.linear``,
+    delta_feedback_experiment/pkda.py:334-339)."""
+    d2 = draw.reshape(draw.shape[0], -1)
+    return d2 @ up_weight.float(), d2.t() @ hidden_rows.float()
 
 
 def _flat(t: Tensor, plan: ChunkPlan) -> Tensor:
@@ -219,21 +254,25 @@ class _ChunkPKDA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, g_atk, beta_atk, A_log, dt_bias, log_atk_scale,
-                initial_state, initial_A_state, cu_seqlens, opts):
+                initial_state, initial_A_state, cu_seqlens, decay_up, opts):
         from .pkda import gate_form
         from . import precond as pre
 
         use_gate, scale, output_final_state, x, eps, lean = opts
         plan = ChunkPlan.make(q, cu_seqlens)
-        kind, g_used = gate_form(g, q.shape[:-1], q.shape[-1], use_gate, A_log, dt_bias)
-        g_used = g_used.contiguous()
-        if g_used.dtype not in (torch.float32, torch.bfloat16):
-            g_used = g_used.float()
+        if decay_up is not None:  # g is the decay hidden; the expansion runs in the gate kernel
+            kind, g_used = _lib.GATE_LOW_RANK, low_rank_rows(g, plan.num_tokens)
+            decay_up = decay_up.to(g_used.dtype).contiguous()
+        else:
+            kind, g_used = gate_form(g, q.shape[:-1], q.shape[-1], use_gate, A_log, dt_bias)
+            g_used = g_used.contiguous()
+            if g_used.dtype not in (torch.float32, torch.bfloat16):
+                g_used = g_used.float()
         A_log32, dt32 = _f32(A_log), _f32(dt_bias)
         qf, kf, vf = (_flat(t.contiguous(), plan) for t in (q, k, v))
         beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
         s0 = _f32(initial_state)
-        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32)
+        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32, decay_up)
         precond = g_atk is not None
         if precond:
             pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, x, eps, initial_A_state)
@@ -245,7 +284,10 @@ class _ChunkPKDA(torch.autograd.Function):
                                       output_final_state, save_states=needs_grad and not lean)
         if needs_grad:
             ctx.plan, ctx.kind, ctx.scale, ctx.lean, ctx.x, ctx.eps = plan, kind, scale, lean, x, eps
-            ctx.per_head_raw = use_gate and g.dim() == q.dim() - 1
+            ctx.per_head_raw = use_gate and decay_up is None and g.dim() == q.dim() - 1
+            ctx.g_shape = tuple(g.shape)
+            ctx.decay_up = decay_up
+            ctx.up_dtype = None if decay_up is None else decay_up.dtype
             ctx.dtypes = tuple(None if t is None else t.dtype for t in (q, k, v, g, beta, g_atk, beta_atk,
                                                                           A_log, dt_bias, log_atk_scale,
                                                                           initial_state, initial_A_state))
@@ -283,7 +325,8 @@ class _ChunkPKDA(torch.autograd.Function):
                                       gr.dkw, dk, None if dA_T is None else dA_T.float().contiguous(),
                                       want_dA0=ctx.needs_input_grad[11])
             dg_atk, dbeta_atk, dcenter, dA0 = pg
-        dg, dA_log, ddt_bias = gate_backward(plan, _flat(g_used, plan), ctx.kind, A_log32, dt32, gr.dgcum)
+        dg, dA_log, ddt_bias = gate_backward(plan, _flat(g_used, plan), ctx.kind, A_log32, dt32, gr.dgcum,
+                                             ctx.decay_up)
         shape = tuple(do.shape)
         dt = ctx.dtypes
 
@@ -293,15 +336,21 @@ class _ChunkPKDA(torch.autograd.Function):
             x = x if shp is None else x.reshape(shp)
             return x.to(dt[i])
 
-        dg = dg.reshape(*shape[:-1], *dg.shape[2:])
-        if ctx.per_head_raw:
-            dg = dg.sum(-1)
+        d_up = None
+        if ctx.kind == _lib.GATE_LOW_RANK:
+            dg, d_up = low_rank_grads(dg, g_used, ctx.decay_up)
+            dg = dg.reshape(ctx.g_shape)
+            d_up = d_up.to(ctx.up_dtype) if ctx.needs_input_grad[13] else None
+        else:
+            dg = dg.reshape(*shape[:-1], *dg.shape[2:])
+            if ctx.per_head_raw:
+                dg = dg.sum(-1)
         return (
             cast(gr.dq, 0, shape), cast(dk, 1, shape), cast(gr.dv, 2, shape), cast(dg, 3),
             cast(gr.dbeta, 4, shape[:-1]),
             cast(dg_atk, 5, shape[:-1]), cast(dbeta_atk, 6, shape[:-1]),
             cast(dA_log, 7), cast(ddt_bias, 8), cast(dcenter, 9),
-            cast(gr.dh0, 10), cast(dA0, 11), None, None,
+            cast(gr.dh0, 10), cast(dA0, 11), None, d_up, None,
         )
 
 
@@ -327,6 +376,7 @@ def chunk_pkda(
     log_atk_scale: Tensor | None = None,
     lean: bool = False,
     use_qk_l2norm_in_kernel: bool = False,
+    decay_up: Tensor | None = None,
     **_ignored,
 ) -> tuple[Tensor, Tensor | None, Tensor | None]:
     """Stateful, differentiable chunked PKDA: ``(o, S_T, A_T)``.
@@ -339,6 +389,13 @@ def chunk_pkda(
     ``eps``) runs when ``g_atk`` is given.  ``scale`` defaults to ``K**-0.5``.
     Gradients flow to every tensor input including ``initial_state`` and
     ``initial_A_state``.
+
+    With ``decay_up`` (the module's ``decay_up.weight [H*K, K]``,
+    pkda.py:168) ``g`` is the decay hidden ``[B, T, K]`` -- e.g. the first
+    slice of the packed control projection -- and the raw gate
+    ``g @ decay_up^T`` (pkda.py:334-339) is formed inside the gate kernel on
+    MFMA instead of being materialised; ``use_gate_in_kernel`` must be set.
+    ``decay_up`` receives its gradient too.
     """
     from .pkda import _check_common, _require_cuda
 
@@ -352,13 +409,21 @@ def chunk_pkda(
     D = q.shape[-1]
     if scale is None:
         scale = D ** -0.5
+    if decay_up is not None:
+        _require_cuda(decay_up)
+        H = q.shape[2]
+        if not use_gate_in_kernel or A_log is None or dt_bias is None:
+            raise ValueError("decay_up forms the raw gate: it needs use_gate_in_kernel with A_log and dt_bias")
+        if tuple(decay_up.shape) != (H * D, D) or tuple(g.shape) != (*q.shape[:2], D):
+            raise ValueError(f"decay_up [{H * D}, {D}] with g the decay hidden {(*q.shape[:2], D)} expected, got "
+                             f"{tuple(decay_up.shape)} and {tuple(g.shape)}")
     N = q.shape[0] if cu_seqlens is None else cu_seqlens.numel() - 1
     if initial_state is not None and tuple(initial_state.shape) != (N, q.shape[2], D, D):
         raise ValueError(f"initial_state must be {(N, q.shape[2], D, D)}")
     opts = (use_gate_in_kernel, float(scale), output_final_state, float(x), float(eps), lean)
     with torch.cuda.device(q.device):
         o, S_T, A_T = _ChunkPKDA.apply(q, k, v, g, beta, g_atk, beta_atk, A_log, dt_bias, log_atk_scale,
-                                      initial_state, initial_A_state, cu_seqlens, opts)
+                                      initial_state, initial_A_state, cu_seqlens, decay_up, opts)
     if not output_final_state:
         return o, None, None
     return o, S_T, A_T

@@ -30,6 +30,7 @@ extern "C" int64_t pkda_args_size(int which) {
     case PKDA_ARGS_CHUNK_BWD: return sizeof(pkda_chunk_bwd_args);
     case PKDA_ARGS_QKV_CONV: return sizeof(pkda_qkv_conv_args);
     case PKDA_ARGS_NORM_GATE: return sizeof(pkda_norm_gate_args);
+    case PKDA_ARGS_CONTROLS: return sizeof(pkda_controls_args);
     default: return -1;
   }
 }

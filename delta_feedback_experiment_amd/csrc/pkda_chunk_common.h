@@ -626,6 +626,27 @@ __device__ __forceinline__ void store_acc_lds_t(E* lds, int ld, const f32x4& acc
   for (int j = 0; j < 4; ++j) lds[(n0 + acc_col(lane)) * ld + m0 + acc_row(lane, j)] = to_e<E>(acc[j]);
 }
 
+// out[i] = sum over p of part[p * n + i], p in [0, count): one 256-thread
+// workgroup per output element (grid = n); thread t adds the partials
+// t, t + 256, ... in order, then a fixed halving tree combines the threads.
+// Deterministic, and every load of a thread is independent of its sum, so the
+// partials stream in rather than paying one memory latency each.
+namespace {  // one copy per translation unit
+__global__ __launch_bounds__(256) void sum_partials_tree_kernel(const float* part, int count, int n, float* out) {
+  __shared__ float s[256];
+  const int i = blockIdx.x;
+  float acc = 0.f;
+  for (int q = threadIdx.x; q < count; q += 256) acc += part[(int64_t)q * n + i];
+  s[threadIdx.x] = acc;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (threadIdx.x < off) s[threadIdx.x] += s[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[i] = s[0];
+}
+}  // namespace
+
 // Deterministic row sums of an fp32 [64 x ncols] LDS tile into out[64]
 // (fixed summation order; one wave per 16 rows).
 __device__ __forceinline__ void row_sums_64(const float* lds, int ld, int ncols, float* out) {

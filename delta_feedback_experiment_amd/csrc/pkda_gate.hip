@@ -67,6 +67,8 @@ struct GateParams {
   float* dg;
   float* dA_log_part;
   float* ddt_bias_part;
+  const void* up_weight;  // low-rank gate: [H*K, R]
+  int rank, g_stride;
 };
 
 __device__ __forceinline__ float gate_value(const GateParams& p, int64_t idx, int h, int c, float a_scale) {
@@ -159,23 +161,227 @@ __global__ __launch_bounds__(kWG) void gate_bwd_kernel(GateParams p) {
   if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = s_red[0];
 }
 
-// out[i] = sum_c part[c * n + i] for c in [0, num_chunks), fixed order.
-__global__ __launch_bounds__(kWG) void sum_partials_kernel(const float* part, int num_chunks, int n, float* out) {
-  const int i = blockIdx.x * kWG + threadIdx.x;
-  if (i >= n) return;
-  float s = 0.f;
-  for (int c = 0; c < num_chunks; ++c) s += part[(int64_t)c * n + i];
-  out[i] = s;
+// ---- low-rank gate: the decay expansion on MFMA, fused with the activation ----
+// Per (chunk, head), one 4-wave workgroup, wave w owning rows 16w..16w+15:
+//   raw[t, c] = sum_r hidden[t, r] up_weight[h K + c, r]
+// as 16x16 MFMA tiles whose operands come straight from global memory (a lane
+// reads 16 contiguous bytes of a hidden row or a weight row; the hidden rows
+// are shared by every head of the chunk and the weights by every chunk, so
+// both stay in L2), rounded to the activation dtype as the reference's
+// materialised raw decay (F.linear output, delta_feedback_experiment/pkda.py:
+// 334-339), then glog = -exp(A_log[h]) softplus(raw + dt_bias[h K + c]).  The
+// chunk-local cumsum runs on the accumulators: over a lane's four rows, then
+// across its wave's four lane groups (shuffles), then across the four waves
+// (their totals through LDS); the result leaves with 16-byte row stores.  The
+// backward recomputes raw the same way, reverse-scans dgcum and writes the raw
+// gate's gradient; the two GEMMs back to the hidden rows and the weight are
+// plain library products on the host side.  Rows past the chunk's end read
+// the last valid row (every load stays inside the document) and are never
+// stored or summed.
+template <typename T> struct LrFrag;
+template <> struct LrFrag<bf16_t> {  // 16x16x32: lane (i, q) holds k = 8q .. 8q + 7 of row i
+  static constexpr int KS = 32;
+  using F = s16x8_t;
+  __device__ __forceinline__ static F load(const bf16_t* row, int k0, int lane) {
+    return *reinterpret_cast<const s16x8_t*>(row + k0 + 8 * (lane >> 4));
+  }
+  __device__ __forceinline__ static void mfma(f32x4& acc, const F& a, const F& b) { Mma<bf16_t>::mfma(acc, a, b); }
+};
+template <> struct LrFrag<float> {  // 16x16x4: lane (i, q) holds k = q of row i
+  static constexpr int KS = 4;
+  using F = float;
+  __device__ __forceinline__ static F load(const float* row, int k0, int lane) { return row[k0 + (lane >> 4)]; }
+  __device__ __forceinline__ static void mfma(f32x4& acc, const F& a, const F& b) { Mma<float>::mfma(acc, a, b); }
+};
+
+// z = raw + dt_bias for this lane's accumulator elements: acc[ct][j] is row
+// 16 wave + 4 q + j, column 16 ct + i.
+template <typename T, int K, int R>
+__device__ __forceinline__ void low_rank_z(const GateParams& p, const ChunkInfo& ci, int h, int wave, int lane,
+                                           f32x4 (&acc)[K / 16]) {
+  using Fr = LrFrag<T>;
+  const int row = min(16 * wave + (lane & 15), ci.len - 1);
+  const T* xrow = static_cast<const T*>(p.g) + (int64_t)(ci.start + row) * p.g_stride;
+  const T* wh = static_cast<const T*>(p.up_weight) + (int64_t)h * K * R;
+  typename Fr::F a[R / Fr::KS];
+#pragma unroll
+  for (int ks = 0; ks < R / Fr::KS; ++ks) a[ks] = Fr::load(xrow, ks * Fr::KS, lane);
+#pragma unroll
+  for (int ct = 0; ct < K / 16; ++ct) {
+    const T* wrow = wh + (int64_t)(16 * ct + (lane & 15)) * R;
+    acc[ct] = zero4();
+#pragma unroll
+    for (int ks = 0; ks < R / Fr::KS; ++ks) Fr::mfma(acc[ct], a[ks], Fr::load(wrow, ks * Fr::KS, lane));
+    const float bias = p.dt_bias[(int64_t)h * K + 16 * ct + (lane & 15)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[ct][j] = from_e<T>(to_e<T>(acc[ct][j])) + bias;
+  }
+}
+
+// Sum over the 64 lanes of a wave, fixed order; every lane gets the result.
+__device__ __forceinline__ float lr_wave_sum(float x) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Inclusive prefix over this lane group's four rows and the lower lane groups
+// of the wave (rows 4q + j ascending); returns the wave's column total.
+__device__ __forceinline__ float wave_prefix_rows(f32x4& v, int lane) {
+  v[1] += v[0];
+  v[2] += v[1];
+  v[3] += v[2];
+  const int q = lane >> 4;
+  float t = v[3];  // this group's total, then the inclusive prefix of the group totals
+  float u = __shfl_up(t, 16);
+  if (q >= 1) t += u;
+  u = __shfl_up(t, 32);
+  if (q >= 2) t += u;
+  const float carry = t - v[3];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += carry;
+  return __shfl(t, 48 + (lane & 15));  // group 3's inclusive value: the wave total
+}
+
+// Reverse (suffix) form: rows descending.
+__device__ __forceinline__ float wave_suffix_rows(f32x4& v, int lane) {
+  v[2] += v[3];
+  v[1] += v[2];
+  v[0] += v[1];
+  const int q = lane >> 4;
+  float t = v[0];
+  float u = __shfl_down(t, 16);
+  if (q <= 2) t += u;
+  u = __shfl_down(t, 32);
+  if (q <= 1) t += u;
+  const float carry = t - v[0];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += carry;
+  return __shfl(t, lane & 15);  // group 0's inclusive value: the wave total
+}
+
+template <typename T, int K, int R>
+__global__ __launch_bounds__(kWG) void gate_low_rank_fwd_kernel(GateParams p) {
+  __shared__ float s_tot[4][K];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len <= 0) return;
+  const int h = blockIdx.y, H = p.heads;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  f32x4 acc[K / 16];
+  low_rank_z<T, K, R>(p, ci, h, wave, lane, acc);
+  const float a_scale = -expf(p.A_log[h]);
+#pragma unroll
+  for (int ct = 0; ct < K / 16; ++ct) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[ct][j] = a_scale * softplus_f(acc[ct][j]);
+    const float tot = wave_prefix_rows(acc[ct], lane);
+    if (lane < 16) s_tot[wave][16 * ct + lane] = tot;
+  }
+  __syncthreads();
+  float* out = p.gcum + ((int64_t)ci.start * H + h) * K;
+#pragma unroll
+  for (int ct = 0; ct < K / 16; ++ct) {
+    float carry = 0.f;
+    for (int w = 0; w < wave; ++w) carry += s_tot[w][16 * ct + (lane & 15)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[ct][j] += carry;
+    store_acc_global<float>(out, (int64_t)H * K, acc[ct], 16 * wave, 16 * ct, ci.len, lane);
+  }
+}
+
+template <typename T, int K, int R>
+__global__ __launch_bounds__(kWG) void gate_low_rank_bwd_kernel(GateParams p) {
+  __shared__ float s_tot[4][K];
+  __shared__ float s_col[4][K];
+  __shared__ float s_dA[4];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const int h = blockIdx.y, H = p.heads;
+  float* dtb = p.ddt_bias_part + ((int64_t)blockIdx.x * H + h) * K;
+  if (ci.len <= 0) {  // an empty slot of the packed launch bound: zero partials
+    for (int c = threadIdx.x; c < K; c += kWG) dtb[c] = 0.f;
+    if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = 0.f;
+    return;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  f32x4 z[K / 16];
+  low_rank_z<T, K, R>(p, ci, h, wave, lane, z);
+  const float A = expf(p.A_log[h]);
+  const int64_t base = ((int64_t)ci.start * H + h) * K;
+  f32x4 suf[K / 16];
+#pragma unroll
+  for (int ct = 0; ct < K / 16; ++ct) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 16 * wave + acc_row(lane, j);
+      suf[ct][j] = r < ci.len ? p.dgcum[base + (int64_t)r * H * K + 16 * ct + acc_col(lane)] : 0.f;
+    }
+    const float tot = wave_suffix_rows(suf[ct], lane);
+    if (lane < 16) s_tot[wave][16 * ct + lane] = tot;
+  }
+  __syncthreads();
+  float dA = 0.f;
+#pragma unroll
+  for (int ct = 0; ct < K / 16; ++ct) {
+    float carry = 0.f;
+    for (int w = wave + 1; w < 4; ++w) carry += s_tot[w][16 * ct + (lane & 15)];
+    f32x4 dg;
+    float col = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool valid = 16 * wave + acc_row(lane, j) < ci.len;
+      const float s = suf[ct][j] + carry;
+      dg[j] = valid ? s * (-A) * sigmoid_f(z[ct][j]) : 0.f;
+      dA += valid ? s * (-A * softplus_f(z[ct][j])) : 0.f;
+      col += dg[j];
+    }
+    store_acc_global<float>(p.dg + base, (int64_t)H * K, dg, 16 * wave, 16 * ct, ci.len, lane);
+    col += __shfl_xor(col, 16);
+    col += __shfl_xor(col, 32);
+    if (lane < 16) s_col[wave][16 * ct + lane] = col;
+  }
+  dA = lr_wave_sum(dA);
+  if (lane == 0) s_dA[wave] = dA;
+  __syncthreads();
+  for (int c = threadIdx.x; c < K; c += kWG) dtb[c] = ((s_col[0][c] + s_col[1][c]) + s_col[2][c]) + s_col[3][c];
+  if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = ((s_dA[0] + s_dA[1]) + s_dA[2]) + s_dA[3];
+}
+
+int dispatch_low_rank(const GateParams& p, int num_chunks, bool backward, hipStream_t s) {
+  const dim3 grid(num_chunks, p.heads);
+#define PKDA_LOW_RANK(TT, KK)                                                                       \
+  do {                                                                                              \
+    if (backward) {                                                                                 \
+      hipLaunchKernelGGL((gate_low_rank_bwd_kernel<TT, KK, KK>), grid, dim3(kWG), 0, s, p);         \
+    } else {                                                                                        \
+      hipLaunchKernelGGL((gate_low_rank_fwd_kernel<TT, KK, KK>), grid, dim3(kWG), 0, s, p);         \
+    }                                                                                               \
+  } while (0)
+  if (p.g_dtype == PKDA_BF16) {
+    if (p.D == 128) PKDA_LOW_RANK(bf16_t, 128); else PKDA_LOW_RANK(bf16_t, 64);
+  } else {
+    PKDA_LOW_RANK(float, 64);
+  }
+#undef PKDA_LOW_RANK
+  return launch_status(backward ? "pkda_gate_bwd(low rank)" : "pkda_gate_fwd(low rank)");
 }
 
 int gate_common(const pkda_gate_args* a, GateParams& p) {
   PKDA_REQUIRE(a != nullptr, PKDA_EINVAL, "null args");
   PKDA_REQUIRE(a->struct_size == (int32_t)sizeof(pkda_gate_args), PKDA_EINVAL, "pkda_gate_args size mismatch");
-  PKDA_REQUIRE(a->gate_kind >= 0 && a->gate_kind <= 2, PKDA_EINVAL, "gate_kind %d", a->gate_kind);
+  PKDA_REQUIRE(a->gate_kind >= 0 && a->gate_kind <= 3, PKDA_EINVAL, "gate_kind %d", a->gate_kind);
   PKDA_REQUIRE(a->g_dtype == PKDA_F32 || a->g_dtype == PKDA_BF16, PKDA_EUNSUPPORTED, "g dtype");
   PKDA_REQUIRE(a->heads > 0 && a->head_dim > 0 && a->num_seqs >= 0 && a->num_chunks >= 0, PKDA_EINVAL, "sizes");
   PKDA_REQUIRE(!a->cu_seqlens || a->table, PKDA_EINVAL, "packed documents need the chunk table");
-  PKDA_REQUIRE(a->gate_kind != PKDA_GATE_RAW_CHANNEL || (a->A_log && a->dt_bias), PKDA_EINVAL, "raw gate needs A_log, dt_bias");
+  PKDA_REQUIRE(a->gate_kind < PKDA_GATE_RAW_CHANNEL || (a->A_log && a->dt_bias), PKDA_EINVAL,
+               "raw and low-rank gates need A_log, dt_bias");
+  if (a->gate_kind == PKDA_GATE_LOW_RANK) {
+    PKDA_REQUIRE(a->up_weight, PKDA_EINVAL, "the low-rank gate needs up_weight");
+    PKDA_REQUIRE(a->rank == a->head_dim && (a->head_dim == 64 || (a->head_dim == 128 && a->g_dtype == PKDA_BF16)),
+                 PKDA_EUNSUPPORTED, "low-rank gate built for rank == head_dim in {64, 128} (128: bf16)");
+    const int vec = a->g_dtype == PKDA_BF16 ? 8 : 4;
+    PKDA_REQUIRE(a->g_stride >= a->rank && a->g_stride % vec == 0, PKDA_EINVAL,
+                 "g_stride %d (>= rank, a multiple of %d elements)", a->g_stride, vec);
+  }
   p.geom.num_seqs = a->num_seqs;
   p.geom.seqlen = a->seqlen;
   p.geom.nt = a->cu_seqlens ? 0 : (a->seqlen + C - 1) / C;
@@ -197,6 +403,9 @@ int gate_common(const pkda_gate_args* a, GateParams& p) {
   p.dg = a->dg;
   p.dA_log_part = a->dA_log_part;
   p.ddt_bias_part = a->ddt_bias_part;
+  p.up_weight = a->up_weight;
+  p.rank = a->rank;
+  p.g_stride = a->g_stride;
   return 0;
 }
 
@@ -223,6 +432,8 @@ extern "C" int pkda_gate_fwd(const pkda_gate_args* a, void* stream) {
   if (st) return st;
   PKDA_REQUIRE(a->g && a->gcum, PKDA_EINVAL, "gate forward needs g and gcum");
   if (a->num_chunks == 0) return 0;
+  if (a->gate_kind == PKDA_GATE_LOW_RANK)
+    return dispatch_low_rank(p, a->num_chunks, false, static_cast<hipStream_t>(stream));
   hipLaunchKernelGGL(gate_fwd_kernel, dim3(a->num_chunks, a->heads), dim3(kWG), 0, static_cast<hipStream_t>(stream), p);
   return launch_status("pkda_gate_fwd");
 }
@@ -232,18 +443,23 @@ extern "C" int pkda_gate_bwd(const pkda_gate_args* a, void* stream) {
   int st = gate_common(a, p);
   if (st) return st;
   PKDA_REQUIRE(a->dgcum && a->dg, PKDA_EINVAL, "gate backward needs dgcum and dg");
-  const bool raw = a->gate_kind == PKDA_GATE_RAW_CHANNEL;
+  const bool raw = a->gate_kind >= PKDA_GATE_RAW_CHANNEL;
   PKDA_REQUIRE(!raw || (a->g && a->dA_log_part && a->ddt_bias_part && a->dA_log && a->ddt_bias), PKDA_EINVAL,
                "raw gate backward needs g and the dA_log / ddt_bias buffers");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (a->num_chunks > 0)
-    hipLaunchKernelGGL(gate_bwd_kernel, dim3(a->num_chunks, a->heads), dim3(kWG), 0, s, p);
+  if (a->num_chunks > 0) {
+    if (a->gate_kind == PKDA_GATE_LOW_RANK) {
+      if (int e = dispatch_low_rank(p, a->num_chunks, true, s)) return e;
+    } else {
+      hipLaunchKernelGGL(gate_bwd_kernel, dim3(a->num_chunks, a->heads), dim3(kWG), 0, s, p);
+    }
+  }
   if (raw) {
     const int nH = a->heads, nHK = a->heads * a->head_dim;
-    hipLaunchKernelGGL(sum_partials_kernel, dim3((nH + kWG - 1) / kWG), dim3(kWG), 0, s, a->dA_log_part,
-                       a->num_chunks, nH, a->dA_log);
-    hipLaunchKernelGGL(sum_partials_kernel, dim3((nHK + kWG - 1) / kWG), dim3(kWG), 0, s, a->ddt_bias_part,
-                       a->num_chunks, nHK, a->ddt_bias);
+    hipLaunchKernelGGL(sum_partials_tree_kernel, dim3(nH), dim3(256), 0, s, a->dA_log_part, a->num_chunks, nH,
+                       a->dA_log);
+    hipLaunchKernelGGL(sum_partials_tree_kernel, dim3(nHK), dim3(256), 0, s, a->ddt_bias_part, a->num_chunks, nHK,
+                       a->ddt_bias);
   }
   return launch_status("pkda_gate_bwd");
 }

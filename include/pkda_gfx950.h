@@ -54,7 +54,10 @@ enum pkda_status {
 enum pkda_gate_kind {
   PKDA_GATE_LOG_HEAD = 0,    /* g [N_tok, H]    log-decay per token and head          */
   PKDA_GATE_LOG_CHANNEL = 1, /* g [N_tok, H, K] log-decay per key channel             */
-  PKDA_GATE_RAW_CHANNEL = 2  /* g [N_tok, H, K] raw; -exp(A_log[h]) softplus(g + dt_bias[h,c]) */
+  PKDA_GATE_RAW_CHANNEL = 2, /* g [N_tok, H, K] raw; -exp(A_log[h]) softplus(g + dt_bias[h,c]) */
+  PKDA_GATE_LOW_RANK = 3     /* g = decay hidden [N_tok, rank] (row stride g_stride); the raw
+                                gate is g up_weight^T [N_tok, H*K], rounded to g's dtype,
+                                then activated as PKDA_GATE_RAW_CHANNEL */
 };
 
 /* ---------------------------------------------------------------------------
@@ -71,7 +74,8 @@ enum pkda_args_kind {
   PKDA_ARGS_CHUNK_FWD = 3,
   PKDA_ARGS_CHUNK_BWD = 4,
   PKDA_ARGS_QKV_CONV = 5,
-  PKDA_ARGS_NORM_GATE = 6
+  PKDA_ARGS_NORM_GATE = 6,
+  PKDA_ARGS_CONTROLS = 7
 };
 
 /* ---------------------------------------------------------------------------
@@ -171,13 +175,21 @@ typedef struct pkda_gate_args {
   const float* dt_bias;
   float* gcum;              /* forward output */
   const float* dgcum;       /* backward input */
-  float* dg;                /* backward output, FP32, shape of g */
-  float* dA_log_part;       /* [num_chunks, H]   workspace (raw gate) */
-  float* ddt_bias_part;     /* [num_chunks, H*K] workspace (raw gate) */
-  float* dA_log;            /* [H]   (raw gate) */
-  float* ddt_bias;          /* [H*K] (raw gate) */
+  float* dg;                /* backward output, FP32, shape of g; PKDA_GATE_LOW_RANK: the
+                               gradient of the raw gate [N_tok, H, K] (the host turns it into
+                               the decay hidden's and up_weight's gradients with two GEMMs) */
+  float* dA_log_part;       /* [num_chunks, H]   workspace (raw and low-rank gates) */
+  float* ddt_bias_part;     /* [num_chunks, H*K] workspace (raw and low-rank gates) */
+  float* dA_log;            /* [H]   (raw and low-rank gates) */
+  float* ddt_bias;          /* [H*K] (raw and low-rank gates) */
   int32_t num_chunks;       /* chunks (equal rows) or num_chunks_max (packed) */
   const int32_t* table;     /* pkda_chunk_table output or NULL */
+  /* PKDA_GATE_LOW_RANK: the decay expansion (decay_up, delta_feedback_experiment/
+   * pkda.py:168,334-339) fused into the gate: up_weight [H*K, rank] in g_dtype,
+   * rank 64 or 128 (== head_dim as in the reference), g_stride >= rank. */
+  const void* up_weight;
+  int32_t rank;
+  int32_t g_stride;
 } pkda_gate_args;
 
 int pkda_gate_fwd(const pkda_gate_args* args, void* stream);
@@ -428,6 +440,58 @@ typedef struct pkda_norm_gate_args {
 int64_t pkda_norm_gate_workspace(int64_t rows, int32_t dim);
 int pkda_norm_gate_fwd(const pkda_norm_gate_args* args, void* stream);
 int pkda_norm_gate_bwd(const pkda_norm_gate_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * PKDA control activations and their packed gradient.
+ *
+ * Replaces the activation half of PreconditionedKDA._controls
+ * (delta_feedback_experiment/pkda.py:318-353) and, backward, the
+ * _PackedControlSplit backward with pack_control_gradients
+ * (delta_feedback_experiment/pkda.py:56-74, cuda_kernels.py:1081-1172).
+ * packed [rows, row_stride] (dtype) holds per token the five control
+ * projections side by side (width = rank + 3 H + gate_width columns):
+ *   decay hidden [rank] | beta logits [H] | preconditioner decay logits [H] |
+ *   preconditioner beta logits [H] | output-gate hidden [gate_width].
+ *   forward:  beta = sigmoid(beta logit), precond_beta = sigmoid(its logit)
+ *             (dtype, [rows, H]); precond_decay = -exp(A_log_p[h])
+ *             softplus(logit + dt_bias_p[h]) (FP32, [rows, H]).  The two
+ *             hidden slices stay where they are (the caller's views).
+ *   backward: from d_decay_hidden [rows, rank], dbeta, dprecond_beta
+ *             [rows, H] (dtype), dprecond_decay [rows, H] (FP32) and
+ *             d_gate_hidden [rows, gate_width] (dtype; any may be NULL for a
+ *             zero gradient), dpacked [rows, width] (dtype, contiguous) in one
+ *             pass, with the sigmoid and softplus derivatives applied; and
+ *             dA_log_p [H], ddt_bias_p [H] (FP32) through the caller's FP32
+ *             workspace part of pkda_controls_workspace(rows, H) elements,
+ *             summed in a fixed order (deterministic).
+ * The sigmoid outputs are taken as rounded to dtype, as the reference's
+ * tensors are, in both directions.
+ * ------------------------------------------------------------------------- */
+typedef struct pkda_controls_args {
+  int32_t struct_size;
+  int32_t dtype;              /* of packed, beta, precond_beta and the dtype gradients */
+  int64_t rows;
+  int32_t heads, rank, gate_width, row_stride;
+  const void* packed;
+  const float* A_log_p;       /* [H] */
+  const float* dt_bias_p;     /* [H] */
+  void* beta;                 /* forward outputs */
+  float* precond_decay;
+  void* precond_beta;
+  const void* d_decay_hidden; /* backward inputs */
+  const void* dbeta;
+  const float* dprecond_decay;
+  const void* dprecond_beta;
+  const void* d_gate_hidden;
+  void* dpacked;              /* backward outputs */
+  float* part;
+  float* dA_log_p;
+  float* ddt_bias_p;
+} pkda_controls_args;
+
+int64_t pkda_controls_workspace(int64_t rows, int32_t heads);
+int pkda_controls_fwd(const pkda_controls_args* args, void* stream);
+int pkda_controls_bwd(const pkda_controls_args* args, void* stream);
 
 #ifdef __cplusplus
 }
