@@ -67,6 +67,11 @@ __device__ __forceinline__ int64_t state_row(const FwdParams& p, int n) { return
 // ---------------------------------------------------------------------------
 constexpr int SLD = 17;
 
+// Orders this wave's LDS accesses (its stores before its later loads): the
+// diagonal-block phase of the solve touches only wave-private scratch, so a
+// wavefront fence stands in for a workgroup barrier there.
+__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
 __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* scratch) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -76,7 +81,7 @@ __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* sc
   float* P = M + 16 * SLD;
   float* X = P + 16 * SLD;
   float* N = s + (16 * b) * ldf + 16 * b;
-  if (active) {
+  if (active) {  // wave-private: M, P and this wave's diagonal block
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = acc_row(lane, j), c = acc_col(lane);
@@ -84,24 +89,20 @@ __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* sc
       M[r * SLD + c] = n;
       P[r * SLD + c] = (r == c ? 1.f : 0.f) - n;
     }
-  }
-  __syncthreads();
-  for (int step = 0; step < 3; ++step) {
-    f32x4 acc = zero4(), pacc = zero4();
-    if (active) {
+    for (int step = 0; step < 3; ++step) {
+      wave_lds_fence();
+      f32x4 acc = zero4(), pacc;
       mma_tile<float, ROW, ROW>(acc, M, SLD, 0, M, SLD, 0, 16, lane);  // M <- M^2
 #pragma unroll
       for (int j = 0; j < 4; ++j) pacc[j] = P[acc_row(lane, j) * SLD + acc_col(lane)];
+      wave_lds_fence();
+      store_acc_lds(M, SLD, acc, 0, 0, lane);
+      wave_lds_fence();
+      mma_tile<float, ROW, ROW>(pacc, P, SLD, 0, M, SLD, 0, 16, lane);  // P <- P (I + M)
+      wave_lds_fence();
+      store_acc_lds(P, SLD, pacc, 0, 0, lane);
     }
-    __syncthreads();
-    if (active) store_acc_lds(M, SLD, acc, 0, 0, lane);
-    __syncthreads();
-    if (active) mma_tile<float, ROW, ROW>(pacc, P, SLD, 0, M, SLD, 0, 16, lane);  // P <- P (I + M)
-    __syncthreads();
-    if (active) store_acc_lds(P, SLD, pacc, 0, 0, lane);
-    __syncthreads();
-  }
-  if (active) {
+    wave_lds_fence();
 #pragma unroll
     for (int j = 0; j < 4; ++j) N[acc_row(lane, j) * ldf + acc_col(lane)] = P[acc_row(lane, j) * SLD + acc_col(lane)];
   }
@@ -109,33 +110,40 @@ __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* sc
   for (int i = 1; i < 4; ++i) {
     const int j = b;
     const bool on = active && j < i;
-    if (on) {
+    f32x4 y = zero4();
+    if (on) {  // X is this wave's own
       f32x4 x = zero4();
       for (int k = j; k < i; ++k)
         mma_tile<float, ROW, ROW>(x, s + (16 * i) * ldf + 16 * k, ldf, 0, s + (16 * k) * ldf + 16 * j, ldf, 0, 16,
                                   lane);
       store_acc_lds(X, SLD, x, 0, 0, lane);
-    }
-    __syncthreads();
-    if (on) {
-      f32x4 y = zero4();
+      wave_lds_fence();
       mma_tile<float, ROW, ROW>(y, s + (16 * i) * ldf + 16 * i, ldf, 0, X, SLD, 0, 16, lane);
+    }
+    __syncthreads();  // every wave has read row i's A blocks before T_ij replaces them
+    if (on) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) s[(16 * i + acc_row(lane, jj)) * ldf + 16 * j + acc_col(lane)] = -y[jj];
     }
-    __syncthreads();
+    __syncthreads();  // row i of T is complete before row i + 1 reads it
   }
 }
 
 
 // ---------------------------------------------------------------------------
 // intra-chunk forward: one 8-wave workgroup per (chunk, head).
-//   Akk, Aqk   the ten 16x16 blocks on or below the diagonal, one or two per
-//              wave (raw k.kw and q.kw products, then the pairwise decay);
+//   Akk, Aqk   the ten 16x16 blocks on or below the diagonal (raw k.kw and
+//              q.kw products, then the pairwise decay): Akk into LDS (FP32)
+//              for the solve, Aqk straight from the accumulators to global
+//              memory; the six blocks above the diagonal are written as zeros;
 //   T          in place over Akk (waves 0..3);
 //   W, u       T (diag(beta e^G) K), T (diag(beta) V): wave w owns row block
-//              w % 4 and column half w / 4.
-// All outputs leave through LDS with 16-byte stores.
+//              w % 4 and column half w / 4; they leave from the accumulators.
+// LDS is three [64 x D] regions, reused as the work moves on (52 KB at
+// D = 128 BF16, three workgroups per compute unit):
+//   region K:  K, then Bw = diag(beta e^G) K
+//   region Q:  Q, then the solve's scratch, then T in the operand type
+//   region A:  Akk / T in FP32, then Bv = diag(beta) V (V waits in registers)
 // ---------------------------------------------------------------------------
 constexpr int kIW = 512;
 
@@ -145,15 +153,16 @@ struct IntraLayout {
   static constexpr int LDC = C + Pad<T>::v;
   static constexpr int LDF = C + 4;
   static constexpr int RT = C * LD * (int)sizeof(T);
-  static constexpr int SCR = 4 * 3 * 16 * SLD * 4;      // solve scratch
-  static constexpr int QR = RT > SCR ? RT : SCR;
-  static constexpr int off_K = 0;                       // K, then Bw, then W
-  static constexpr int off_Q = off_K + RT;              // Q, then solve scratch, then Bv, then u
-  static constexpr int off_KW = off_Q + QR;             // KW (when not aliased to K)
-  static constexpr int off_A = off_KW + (ALIAS ? 0 : RT);  // fp32 [64][LDF]: Akk, then T
-  static constexpr int off_Te = off_A + C * LDF * 4;    // [64][LDC] T in the operand type
-  static constexpr int off_Aqk = off_Te + C * LDC * (int)sizeof(T);
-  static constexpr int off_beta = off_Aqk + C * LDC * (int)sizeof(T);
+  static constexpr int SCR = 4 * 3 * 16 * SLD * 4;       // solve scratch
+  static constexpr int TE = C * LDC * (int)sizeof(T);    // T in the operand type
+  static constexpr int max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
+  static constexpr int QR = max3(RT, SCR, TE);
+  static constexpr int AR = C * LDF * 4 > RT ? C * LDF * 4 : RT;
+  static constexpr int off_K = 0;                         // K, then Bw
+  static constexpr int off_Q = off_K + RT;                // Q, then solve scratch, then Te
+  static constexpr int off_KW = off_Q + QR;               // KW (when not aliased to K)
+  static constexpr int off_A = off_KW + (ALIAS ? 0 : RT); // fp32 [64][LDF]: Akk, then T; then Bv
+  static constexpr int off_beta = off_A + AR;
   static constexpr int off_gam = off_beta + C * 4;
   static constexpr int bytes = off_gam + C * 4;
 };
@@ -175,10 +184,10 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
 
   E* sK = reinterpret_cast<E*>(smem + L::off_K);
   E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
+  E* sTe = sQ;
   E* sKW = ALIAS ? sK : reinterpret_cast<E*>(smem + L::off_KW);
   float* sA = reinterpret_cast<float*>(smem + L::off_A);
-  E* sTe = reinterpret_cast<E*>(smem + L::off_Te);
-  E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
+  E* sBv = reinterpret_cast<E*>(smem + L::off_A);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
 
@@ -192,7 +201,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     sGam[tid] = p.gcum[idx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
     sBeta[tid] = tid < len ? p.beta[idx] : 0.f;
   }
-  // all tiles in one memory round trip; V waits in registers until Q's slot frees
+  // all tiles in one memory round trip; V waits in registers until region A frees
   RegTile<kIW, C, D, T> rV;
   {
     RegTile<kIW, C, D, T> rK, rQ, rKW;
@@ -211,67 +220,64 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   }
   __syncthreads();
 
-  // ---- Akk, Aqk on the ten blocks (tb >= sb) --------------------------------
-  for (int blk = wave; blk < 10; blk += 8) {
-    const int tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
-    const int sb = blk - tb * (tb + 1) / 2;
-    f32x4 akk = zero4(), aqk = zero4();
-    mma_tile<E, ROW, COL>(akk, sK, L::LD, 16 * tb, sKW, L::LD, 16 * sb, D, lane);
-    mma_tile<E, ROW, COL>(aqk, sQ, L::LD, 16 * tb, sKW, L::LD, 16 * sb, D, lane);
+  // ---- Akk, Aqk: lower blocks 0..9 on MFMA, upper blocks 10..15 zero ----------
+  T* aqk_out = static_cast<T*>(p.aqk) + row0 * C;
+  for (int blk = wave; blk < 16; blk += 8) {
+    if (blk < 10) {
+      const int tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
+      const int sb = blk - tb * (tb + 1) / 2;
+      f32x4 akk = zero4(), aqk = zero4();
+      mma_tile<E, ROW, COL>(akk, sK, L::LD, 16 * tb, sKW, L::LD, 16 * sb, D, lane);
+      mma_tile<E, ROW, COL>(aqk, sQ, L::LD, 16 * tb, sKW, L::LD, 16 * sb, D, lane);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 16 * tb + acc_row(lane, j);
-      const int s = 16 * sb + acc_col(lane);
-      const float dec = (s <= t && t < len) ? exp_fast(sGam[t] - sGam[s]) : 0.f;
-      sA[t * L::LDF + s] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
-      sAqk[t * L::LDC + s] = to_e<E>(p.scale * dec * aqk[j]);
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tb + acc_row(lane, j);
+        const int s = 16 * sb + acc_col(lane);
+        const float dec = (s <= t && t < len) ? exp_fast(sGam[t] - sGam[s]) : 0.f;
+        sA[t * L::LDF + s] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
+        aqk[j] = p.scale * dec * aqk[j];
+      }
+      store_acc_global<T>(aqk_out, (int64_t)H * C, aqk, 16 * tb, 16 * sb, len, lane);
+    } else {  // (tb, sb) above the diagonal
+      const int u = blk - 10;  // 0..5: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+      const int tb = u < 3 ? 0 : u < 5 ? 1 : 2;
+      const int sb = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
+      store_acc_global<T>(aqk_out, (int64_t)H * C, zero4(), 16 * tb, 16 * sb, len, lane);
     }
-  }
-  for (int i = tid; i < C * C; i += kIW) {  // Aqk blocks above the diagonal
-    const int r = i / C, c = i - r * C;
-    if ((c >> 4) > (r >> 4)) sAqk[r * L::LDC + c] = to_e<E>(0.f);
   }
   __syncthreads();
 
-  // ---- T = (I + Akk)^-1 in place; Aqk leaves meanwhile ------------------------
-  store_tile<kIW, C, C>(static_cast<T*>(p.aqk) + row0 * C, (int64_t)H * C, sAqk, L::LDC, len);
+  // ---- T = (I + Akk)^-1 in place (scratch over Q, dead since Aqk) -------------
   solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
+  // T in the operand type over the scratch; Bw = diag(beta e^G) K in place
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
     sTe[r * L::LDC + c] = to_e<E>(sA[r * L::LDF + c]);
   }
-  // Bw = diag(beta e^G) K in place over K; Bv = diag(beta) V over Q
   for (int i = tid; i < C * D; i += kIW) {
     const int r = i / D, c = i - r * D;
     sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sGam[r]) * from_e<E>(sK[r * L::LD + c]));
   }
-  rV.store(sQ, L::LD, RowScale{sBeta});
+  __syncthreads();
+  rV.store(sBv, L::LD, RowScale{sBeta});  // Bv over T's FP32 copy, read above
   __syncthreads();
   store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
 
-  // ---- W = T Bw, u = T Bv ------------------------------------------------------
+  // ---- W = T Bw, u = T Bv, from the accumulators -------------------------------
   const int rb = wave & 3, ch = wave >> 2;
   const int kend = kceil<E>(16 * rb + 16);  // T is lower triangular
-  f32x4 aw[HCT], au[HCT];
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
-    aw[j] = zero4();
-    au[j] = zero4();
-    mma_tile_range<E, ROW, ROW>(aw[j], sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
-    mma_tile_range<E, ROW, ROW>(au[j], sTe, L::LDC, 16 * rb, sQ, L::LD, 16 * ct, 0, kend, lane);
+    f32x4 aw = zero4(), au = zero4();
+    mma_tile_range<E, ROW, ROW>(aw, sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
+    mma_tile_range<E, ROW, ROW>(au, sTe, L::LDC, 16 * rb, sBv, L::LD, 16 * ct, 0, kend, lane);
+    store_acc_global<T>(static_cast<T*>(p.w) + row0 * D, gs, aw, 16 * rb, 16 * ct, len, lane);
+    store_acc_global<T>(static_cast<T*>(p.u) + row0 * D, gs, au, 16 * rb, 16 * ct, len, lane);
   }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < HCT; ++j) {
-    const int ct = ch * HCT + j;
-    store_acc_lds(sK, L::LD, aw[j], 16 * rb, 16 * ct, lane);
-    store_acc_lds(sQ, L::LD, au[j], 16 * rb, 16 * ct, lane);
-  }
-  __syncthreads();
-  store_tile<kIW, C, D>(static_cast<T*>(p.w) + row0 * D, gs, sK, L::LD, len);
-  store_tile<kIW, C, D>(static_cast<T*>(p.u) + row0 * D, gs, sQ, L::LD, len);
 }
+
+
 // ---------------------------------------------------------------------------
 // intra-chunk forward, per-channel gate (G [64][D] per chunk).
 //   Akk[t,s] = beta_t sum_c k[t,c] kw[s,c] e^{G[t,c]-G[s,c]},  Aqk likewise
