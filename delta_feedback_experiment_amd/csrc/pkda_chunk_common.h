@@ -307,6 +307,11 @@ template <> struct Vec16<bf16_t> {
   }
 };
 
+// Round-to-nearest-even of two floats into one packed BF16 pair.
+__device__ __forceinline__ uint32_t pack_bf16x2_(float a, float b) {
+  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
 // Store n (4 or 8) consecutive floats to LDS as E with one 8- or 16-byte write.
 template <int N> __device__ __forceinline__ void store_vec(float* dst, const float* x) {
   if constexpr (N == 4) {
@@ -371,6 +376,34 @@ __device__ __forceinline__ void store_tile(T* g, int64_t gstride, const T* lds, 
     const int r = idx / PER_ROW;
     const int c = (idx - r * PER_ROW) * V;
     if (r < nvalid) *reinterpret_cast<uint4*>(g + r * gstride + c) = *reinterpret_cast<const uint4*>(lds + r * ld + c);
+  }
+}
+
+// Rows [0, nvalid) of an FP32 LDS tile [ROWS][NC] (ld a multiple of 4) to
+// global memory in T, 16-byte stores (8 BF16 or 4 FP32 per piece).
+template <int NT, int ROWS, int NC, typename T>
+__device__ __forceinline__ void store_tile_from_f32(T* g, int64_t gstride, const float* lds, int ld, int nvalid) {
+  constexpr int V = Vec16<T>::N;
+  constexpr int PER_ROW = NC / V;
+  constexpr int TOTAL = ROWS * PER_ROW;
+  for (int idx = threadIdx.x; idx < TOTAL; idx += NT) {
+    const int r = idx / PER_ROW;
+    const int c = (idx - r * PER_ROW) * V;
+    if (r >= nvalid) continue;
+    float x[V];
+#pragma unroll
+    for (int j = 0; j < V; j += 4) {
+      const float4 f = *reinterpret_cast<const float4*>(lds + r * ld + c + j);
+      x[j] = f.x; x[j + 1] = f.y; x[j + 2] = f.z; x[j + 3] = f.w;
+    }
+    uint4 out;
+    if constexpr (sizeof(T) == 2) {
+      out = make_uint4(pack_bf16x2_(x[0], x[1]), pack_bf16x2_(x[2], x[3]), pack_bf16x2_(x[4], x[5]),
+                       pack_bf16x2_(x[6], x[7]));
+    } else {
+      out = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+    }
+    *reinterpret_cast<uint4*>(g + r * gstride + c) = out;
   }
 }
 

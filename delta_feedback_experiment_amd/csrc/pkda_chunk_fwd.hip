@@ -137,13 +137,15 @@ __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* sc
 //              for the solve, Aqk straight from the accumulators to global
 //              memory; the six blocks above the diagonal are written as zeros;
 //   T          in place over Akk (waves 0..3);
-//   W, u       T (diag(beta e^G) K), T (diag(beta) V): wave w owns row block
+//   W, u       (T diag(beta e^G)) K, (T diag(beta)) V: wave w owns row block
 //              w % 4 and column half w / 4; they leave from the accumulators.
 // LDS is three [64 x D] regions, reused as the work moves on (52 KB at
 // D = 128 BF16, three workgroups per compute unit):
-//   region K:  K, then Bw = diag(beta e^G) K
-//   region Q:  Q, then the solve's scratch, then T in the operand type
-//   region A:  Akk / T in FP32, then Bv = diag(beta) V (V waits in registers)
+//   region K:  K
+//   region Q:  Q, then the solve's scratch, then T diag(beta e^G) and
+//              T diag(beta) in the operand type (the row scalings of K and V
+//              folded into T's columns)
+//   region A:  Akk / T in FP32, then V (which waits in registers)
 // ---------------------------------------------------------------------------
 constexpr int kIW = 512;
 
@@ -156,12 +158,12 @@ struct IntraLayout {
   static constexpr int SCR = 4 * 3 * 16 * SLD * 4;       // solve scratch
   static constexpr int TE = C * LDC * (int)sizeof(T);    // T in the operand type
   static constexpr int max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
-  static constexpr int QR = max3(RT, SCR, TE);
+  static constexpr int QR = max3(RT, SCR, 2 * TE);
   static constexpr int AR = C * LDF * 4 > RT ? C * LDF * 4 : RT;
   static constexpr int off_K = 0;                         // K, then Bw
-  static constexpr int off_Q = off_K + RT;                // Q, then solve scratch, then Te
+  static constexpr int off_Q = off_K + RT;                // Q, then solve scratch, then Tw | Tu
   static constexpr int off_KW = off_Q + QR;               // KW (when not aliased to K)
-  static constexpr int off_A = off_KW + (ALIAS ? 0 : RT); // fp32 [64][LDF]: Akk, then T; then Bv
+  static constexpr int off_A = off_KW + (ALIAS ? 0 : RT); // fp32 [64][LDF]: Akk, then T; then V
   static constexpr int off_beta = off_A + AR;
   static constexpr int off_gam = off_beta + C * 4;
   static constexpr int bytes = off_gam + C * 4;
@@ -184,10 +186,11 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
 
   E* sK = reinterpret_cast<E*>(smem + L::off_K);
   E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
-  E* sTe = sQ;
+  E* sTw = sQ;                 // T diag(beta e^G)
+  E* sTu = sQ + C * L::LDC;    // T diag(beta)
   E* sKW = ALIAS ? sK : reinterpret_cast<E*>(smem + L::off_KW);
   float* sA = reinterpret_cast<float*>(smem + L::off_A);
-  E* sBv = reinterpret_cast<E*>(smem + L::off_A);
+  E* sV = reinterpret_cast<E*>(smem + L::off_A);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
 
@@ -212,11 +215,6 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     rK.store(sK, L::LD);
     rQ.store(sQ, L::LD);
     if (!ALIAS) rKW.store(sKW, L::LD);
-  }
-  // blocks above the diagonal of Akk / T are zero
-  for (int i = tid; i < C * C; i += kIW) {
-    const int r = i / C, c = i - r * C;
-    if ((c >> 4) > (r >> 4)) sA[r * L::LDF + c] = 0.f;
   }
   __syncthreads();
 
@@ -243,25 +241,25 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
       const int tb = u < 3 ? 0 : u < 5 ? 1 : 2;
       const int sb = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
       store_acc_global<T>(aqk_out, (int64_t)H * C, zero4(), 16 * tb, 16 * sb, len, lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sA[(16 * tb + acc_row(lane, j)) * L::LDF + 16 * sb + acc_col(lane)] = 0.f;
     }
   }
   __syncthreads();
 
   // ---- T = (I + Akk)^-1 in place (scratch over Q, dead since Aqk) -------------
   solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
-  // T in the operand type over the scratch; Bw = diag(beta e^G) K in place
+  // T's two column-scaled copies over the scratch, and T itself to global
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
-    sTe[r * L::LDC + c] = to_e<E>(sA[r * L::LDF + c]);
+    const float t = sA[r * L::LDF + c];
+    sTw[r * L::LDC + c] = to_e<E>(t * (sBeta[c] * exp_fast(sGam[c])));
+    sTu[r * L::LDC + c] = to_e<E>(t * sBeta[c]);
   }
-  for (int i = tid; i < C * D; i += kIW) {
-    const int r = i / D, c = i - r * D;
-    sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sGam[r]) * from_e<E>(sK[r * L::LD + c]));
-  }
+  store_tile_from_f32<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sA, L::LDF, len);
   __syncthreads();
-  rV.store(sBv, L::LD, RowScale{sBeta});  // Bv over T's FP32 copy, read above
+  rV.store(sV, L::LD);  // over T's FP32 copy, read above
   __syncthreads();
-  store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
 
   // ---- W = T Bw, u = T Bv, from the accumulators -------------------------------
   const int rb = wave & 3, ch = wave >> 2;
@@ -270,8 +268,8 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
     f32x4 aw = zero4(), au = zero4();
-    mma_tile_range<E, ROW, ROW>(aw, sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
-    mma_tile_range<E, ROW, ROW>(au, sTe, L::LDC, 16 * rb, sBv, L::LD, 16 * ct, 0, kend, lane);
+    mma_tile_range<E, ROW, ROW>(aw, sTw, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
+    mma_tile_range<E, ROW, ROW>(au, sTu, L::LDC, 16 * rb, sV, L::LD, 16 * ct, 0, kend, lane);
     store_acc_global<T>(static_cast<T*>(p.w) + row0 * D, gs, aw, 16 * rb, 16 * ct, len, lane);
     store_acc_global<T>(static_cast<T*>(p.u) + row0 * D, gs, au, 16 * rb, 16 * ct, len, lane);
   }
