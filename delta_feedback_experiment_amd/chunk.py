@@ -101,7 +101,7 @@ def low_rank_rows(hidden: Tensor, num_tokens: int) -> Tensor:
 
 @dataclass
 class FwdSaved:
-    w: Tensor
+    w: Tensor | None   # None for BF16 with a per-head gate (never stored)
     u: Tensor
     aqk: Tensor
     akk: Tensor
@@ -123,7 +123,9 @@ def chunk_forward(
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
     o = torch.empty_like(v) if out is None else out
-    w = torch.empty_like(k)
+    per_channel = gcum.dim() == 3
+    # BF16 with a per-head gate: the state passes form W S and W^T dU from T and k
+    w = None if (q.dtype == torch.bfloat16 and not per_channel) else torch.empty_like(k)
     u = torch.empty_like(v)
     aqk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
     akk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
@@ -132,7 +134,6 @@ def chunk_forward(
         S_T = final_state
     else:
         S_T = torch.empty(N, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
-    per_channel = gcum.dim() == 3
     qg = torch.empty_like(q) if per_channel else None
     kg = torch.empty_like(k) if per_channel else None
     args = _lib.ChunkFwdArgs(

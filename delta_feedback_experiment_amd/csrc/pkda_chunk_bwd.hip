@@ -969,32 +969,36 @@ int set_smem(K kernel, int bytes) {
 // The structure of the forward's register-resident pass, chunks in reverse:
 // BV/16 compute waves each keep dS [D x 16] in MFMA accumulators and the
 // chunk's dU [64 x 16] in registers, and kRrLoaders loader waves stage the
-// read-only tiles (KW, Q, W, Aqk, the dO slice, G) through a double-buffered
-// LDS stage, two groups taking alternate chunks.  Per chunk:
+// read-only tiles (Q, KW, K when it is not KW, Aqk, T, the dO slice, G and
+// beta) through a double-buffered LDS stage, two groups taking alternate
+// chunks.  Per chunk, with W = T diag(beta e^G) K never formed:
 //   dU  = Aqk^T dO + diag(e^{G_C - G}) (KW dS)            -> du
-//   dS <- e^{G_C} dS + Q^T diag(s e^G) dO - W^T dU
+//   dS <- e^{G_C} dS + Q^T diag(s e^G) dO - K^T diag(beta e^G) (T^T dU)
 // ---------------------------------------------------------------------------
-template <int D, int BV>
+template <int D, int BV, bool ALIAS>
 struct RrBwdLayout {
   static constexpr int LD = D + Pad<bf16_t>::v;
   static constexpr int LDV = BV + Pad<bf16_t>::v;
   static constexpr int LDC = C + Pad<bf16_t>::v;
-  static constexpr int off_W = 0;
-  static constexpr int off_Q = off_W + C * LD * 2;
+  static constexpr int off_Q = 0;
   static constexpr int off_KW = off_Q + C * LD * 2;
-  static constexpr int off_A = off_KW + C * LD * 2;
-  static constexpr int off_dO = off_A + C * LDC * 2;
+  static constexpr int off_K = off_KW + C * LD * 2;               // K when it is not KW
+  static constexpr int off_A = off_K + (ALIAS ? 0 : C * LD * 2);  // Aqk
+  static constexpr int off_T = off_A + C * LDC * 2;
+  static constexpr int off_dO = off_T + C * LDC * 2;
   static constexpr int off_G = off_dO + C * LDV * 2;
-  static constexpr int BUF = off_G + C * 4;
+  static constexpr int off_B = off_G + C * 4;                     // beta (0 past the chunk's end)
+  static constexpr int BUF = off_B + C * 4;
   static constexpr int bytes = 2 * BUF;
   static_assert(BUF % 16 == 0, "16-byte aligned stages");
+  static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
 };
 
 constexpr int kRrLoadersBwd = 4;  // two groups of two waves
 
-template <int D, int BV>
+template <int D, int BV, bool ALIAS>
 __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bwd_rr_kernel(BwdParams p) {
-  using L = RrBwdLayout<D, BV>;
+  using L = RrBwdLayout<D, BV, ALIAS>;
   using T = bf16_t;
   constexpr int NC = BV / 16;
   constexpr int NKT = D / 16;
@@ -1012,30 +1016,39 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
     constexpr int NGT = 64 * kRrLoadersBwd / 2;
     const int lgroup = (tid - 64 * NC) / NGT;  // takes visits s with s % 2 == lgroup
     const int lt = (tid - 64 * NC) % NGT;
-    RegTile<NGT, C, D, T> rW, rQ, rKW;
-    RegTile<NGT, C, C, T> rA;
+    RegTile<NGT, C, D, T> rQ, rKW, rK;
+    RegTile<NGT, C, C, T> rA, rT;
     RegTile<NGT, C, BV, T> rdO;
-    float rg = 0.f;
+    float rg = 0.f, rb = 0.f;
     auto load = [&](int s) {
       const int jc = count - 1 - s;
       const int cstart = dstart + jc * C;
       const int clen = min(C, dlen - jc * C);
       const int64_t row0 = (int64_t)cstart * H + h;
-      rW.load_as(lt, static_cast<const T*>(p.w) + row0 * D, gs, clen);
       rQ.load_as(lt, static_cast<const T*>(p.q) + row0 * D, gs, clen);
       rKW.load_as(lt, static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+      if (!ALIAS) rK.load_as(lt, static_cast<const T*>(p.k) + row0 * D, gs, clen);
       rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+      rT.load_as(lt, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, clen);
       rdO.load_as(lt, static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen);
-      if (lt < C) rg = p.gcum[(int64_t)(cstart + min(lt, clen - 1)) * H + h];
+      if (lt < C) {
+        const int64_t gi = (int64_t)(cstart + min(lt, clen - 1)) * H + h;
+        rg = p.gcum[gi];
+        rb = lt < clen ? p.beta[gi] : 0.f;
+      }
     };
     auto stash = [&](int b) {
       char* buf = smem + b * L::BUF;
-      rW.store_as(lt, reinterpret_cast<T*>(buf + L::off_W), L::LD);
       rQ.store_as(lt, reinterpret_cast<T*>(buf + L::off_Q), L::LD);
       rKW.store_as(lt, reinterpret_cast<T*>(buf + L::off_KW), L::LD);
+      if (!ALIAS) rK.store_as(lt, reinterpret_cast<T*>(buf + L::off_K), L::LD);
       rA.store_as(lt, reinterpret_cast<T*>(buf + L::off_A), L::LDC);
+      rT.store_as(lt, reinterpret_cast<T*>(buf + L::off_T), L::LDC);
       rdO.store_as(lt, reinterpret_cast<T*>(buf + L::off_dO), L::LDV);
-      if (lt < C) reinterpret_cast<float*>(buf + L::off_G)[lt] = rg;
+      if (lt < C) {
+        reinterpret_cast<float*>(buf + L::off_G)[lt] = rg;
+        reinterpret_cast<float*>(buf + L::off_B)[lt] = rb;
+      }
     };
     if (lgroup < count) load(lgroup);
     if (lgroup == 0 && count > 0) {
@@ -1066,12 +1079,14 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
     __syncthreads();
     const int jc = count - 1 - s;
     const char* buf = smem + (s & 1) * L::BUF;
-    const T* sW = reinterpret_cast<const T*>(buf + L::off_W);
     const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
     const T* sKW = reinterpret_cast<const T*>(buf + L::off_KW);
+    const T* sK = ALIAS ? sKW : reinterpret_cast<const T*>(buf + L::off_K);
     const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
+    const T* sT = reinterpret_cast<const T*>(buf + L::off_T);
     const T* sdO = reinterpret_cast<const T*>(buf + L::off_dO);
     const float* sG = reinterpret_cast<const float*>(buf + L::off_G);
+    const float* sB = reinterpret_cast<const float*>(buf + L::off_B);
     const int cid = first + jc;
     const int clen = min(C, dlen - jc * C);
     const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
@@ -1131,7 +1146,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       for (int j = 0; j < 4; ++j) dU[rb][j] += exp_fast(gC - sG[16 * rb + q4 + j]) * KS[rb][j];
       store_acc_global<T>(du_out, gs, dU[rb], 16 * rb, 0, clen, lane);
     }
-    // dS <- e^{G_C} dS + Q^T (s e^G dO) - W^T dU
+    // Z = T^T (-dU)   (T^T is upper triangular: row block rb needs k steps kt >= rb / 2)
     s16x8_t dOgB[2], dUnB[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
@@ -1141,21 +1156,52 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       dOgB[kt] = scale_frag(dOB[kt], f);
       dUnB[kt] = pack_acc_pair(-dU[2 * kt], -dU[2 * kt + 1]);
     }
+    f32x4 Z[4];
+    {
+      s16x8_t at[6];
+      at[0] = lds_kmajor_perm(sT + 0, L::LDC, 0, lane);
+      at[1] = lds_kmajor_perm(sT + 0, L::LDC, 32, lane);
+      at[2] = lds_kmajor_perm(sT + 16, L::LDC, 0, lane);
+      at[3] = lds_kmajor_perm(sT + 16, L::LDC, 32, lane);
+      at[4] = lds_kmajor_perm(sT + 32, L::LDC, 32, lane);
+      at[5] = lds_kmajor_perm(sT + 48, L::LDC, 32, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) Z[rb] = zero4();
+      mfma_bf16(Z[0], at[0], dUnB[0]);
+      mfma_bf16(Z[1], at[2], dUnB[0]);
+      mfma_bf16(Z[0], at[1], dUnB[1]);
+      mfma_bf16(Z[1], at[3], dUnB[1]);
+      mfma_bf16(Z[2], at[4], dUnB[1]);
+      mfma_bf16(Z[3], at[5], dUnB[1]);
+    }
+    // dS <- e^{G_C} dS + Q^T (s e^G dO) + K^T diag(beta e^G) Z
+    s16x8_t ZB[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      float fa[4], fb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ra = 32 * kt + q4 + j, rb = ra + 16;
+        fa[j] = sB[ra] * exp_fast(sG[ra]);
+        fb[j] = sB[rb] * exp_fast(sG[rb]);
+      }
+      ZB[kt] = pack_acc_pair_scaled(Z[2 * kt], fa, Z[2 * kt + 1], fb);
+    }
     const float decay = exp_fast(gC);
 #pragma unroll
     for (int rt = 0; rt < NKT; ++rt) dS[rt] = dS[rt] * decay;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      s16x8_t aq[NKT], aw[NKT];
+      s16x8_t aq[NKT], ak[NKT];
 #pragma unroll
       for (int rt = 0; rt < NKT; ++rt) {
         aq[rt] = lds_kmajor_perm(sQ + 16 * rt, L::LD, 32 * kt, lane);
-        aw[rt] = lds_kmajor_perm(sW + 16 * rt, L::LD, 32 * kt, lane);
+        ak[rt] = lds_kmajor_perm(sK + 16 * rt, L::LD, 32 * kt, lane);
       }
 #pragma unroll
       for (int rt = 0; rt < NKT; ++rt) {
         mfma_bf16(dS[rt], aq[rt], dOgB[kt]);
-        mfma_bf16(dS[rt], aw[rt], dUnB[kt]);
+        mfma_bf16(dS[rt], ak[rt], ZB[kt]);
       }
     }
   }
@@ -1166,6 +1212,15 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
   }
 }
 
+template <int D, int BV, bool ALIAS>
+int launch_state_bwd_rr_as(const BwdParams& p, hipStream_t s) {
+  auto kern = chunk_state_bwd_rr_kernel<D, BV, ALIAS>;
+  constexpr int bytes = RrBwdLayout<D, BV, ALIAS>::bytes;
+  if (int st = set_smem(kern, bytes)) return st;
+  hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoadersBwd)), bytes, s, p);
+  return launch_status("pkda_chunk_bwd(state)");
+}
+
 // Register-resident reverse pass: 64 value columns per workgroup, or 32 when
 // that leaves fewer workgroups than compute units.
 template <int D>
@@ -1173,12 +1228,8 @@ int launch_state_bwd_rr(const BwdParams& p, hipStream_t s) {
   const int N = p.geom.num_seqs;
   if (N <= 0) return 0;
   const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
-  auto kern = narrow ? chunk_state_bwd_rr_kernel<D, 32> : chunk_state_bwd_rr_kernel<D, 64>;
-  const int bytes = narrow ? RrBwdLayout<D, 32>::bytes : RrBwdLayout<D, 64>::bytes;
-  const int bv = narrow ? 32 : 64;
-  if (int st = set_smem(kern, bytes)) return st;
-  hipLaunchKernelGGL(kern, dim3(N, p.H, D / bv), dim3(64 * (bv / 16 + kRrLoadersBwd)), bytes, s, p);
-  return launch_status("pkda_chunk_bwd(state)");
+  if (narrow) return p.kw_is_k ? launch_state_bwd_rr_as<D, 32, true>(p, s) : launch_state_bwd_rr_as<D, 32, false>(p, s);
+  return p.kw_is_k ? launch_state_bwd_rr_as<D, 64, true>(p, s) : launch_state_bwd_rr_as<D, 64, false>(p, s);
 }
 
 template <typename T, int D, int BV, typename OT>
@@ -1231,9 +1282,11 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   BwdParams p;
   if (int st = chunk_geom_from(a->cu_seqlens, a->num_seqs, a->seqlen, a->num_chunks, a->table, p.geom)) return st;
   if (a->num_seqs == 0) return 0;
-  PKDA_REQUIRE(a->q && a->k && a->v && a->gcum && a->beta && a->w && a->u && a->aqk && a->akk && a->h && a->do_ &&
+  PKDA_REQUIRE(a->q && a->k && a->v && a->gcum && a->beta && a->u && a->aqk && a->akk && a->h && a->do_ &&
                    a->dh && a->du && a->dq && a->dk && a->dv && a->dbeta && a->dgcum,
                PKDA_EINVAL, "null tensor");
+  PKDA_REQUIRE(a->w || (a->dtype == PKDA_BF16 && !a->gate_per_channel), PKDA_EINVAL,
+               "this dtype / gate needs the forward's w");
   const bool kw_is_k = a->kw == nullptr || a->kw == a->k;
   PKDA_REQUIRE(kw_is_k || a->dkw, PKDA_EINVAL, "a separate write key needs dkw");
   const int st = a->stages;

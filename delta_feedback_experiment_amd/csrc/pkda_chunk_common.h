@@ -18,6 +18,9 @@ constexpr int kWG = 256;       // 4 waves
 // Sequential state passes: 16 waves when the [D x BV] state slice splits
 // into whole pairs of 16x16 tiles per wave, else 8.
 constexpr int state_threads(int D, int BV) { return ((D / 16) * (BV / 16)) % 16 == 0 ? 1024 : 512; }
+// BF16 with a per-head gate: the state passes form W S and W^T dU from T and K
+// (W = T diag(beta e^G) K, u = T diag(beta) V are never stored).
+template <typename T> constexpr bool implicit_w() { return __is_same(T, bf16_t); }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));

@@ -136,9 +136,11 @@ __device__ __forceinline__ void solve_unit_lower_64(float* s, int ldf, float* sc
 //              q.kw products, then the pairwise decay): Akk into LDS (FP32)
 //              for the solve, Aqk straight from the accumulators to global
 //              memory; the six blocks above the diagonal are written as zeros;
-//   T          in place over Akk (waves 0..3);
-//   W, u       (T diag(beta e^G)) K, (T diag(beta)) V: wave w owns row block
-//              w % 4 and column half w / 4; they leave from the accumulators.
+//   T          in place over Akk (waves 0..3), then to global memory;
+//   W, u       (WU only) (T diag(beta e^G)) K, (T diag(beta)) V: wave w owns
+//              row block w % 4 and column half w / 4; they leave from the
+//              accumulators.  Without WU the state passes form W S and W^T dU
+//              from T and K themselves, and V is not read here.
 // LDS is three [64 x D] regions, reused as the work moves on (52 KB at
 // D = 128 BF16, three workgroups per compute unit):
 //   region K:  K
@@ -169,7 +171,7 @@ struct IntraLayout {
   static constexpr int bytes = off_gam + C * 4;
 };
 
-template <typename T, int D, bool ALIAS>
+template <typename T, int D, bool ALIAS, bool WU>
 __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   using L = IntraLayout<T, D, ALIAS>;
   using E = T;
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     rK.load(k, gs, len);
     rQ.load(q, gs, len);
     if (!ALIAS) rKW.load(kw, gs, len);
-    rV.load(v, gs, len);
+    if (WU) rV.load(v, gs, len);
     rK.store(sK, L::LD);
     rQ.store(sQ, L::LD);
     if (!ALIAS) rKW.store(sKW, L::LD);
@@ -249,6 +251,10 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
 
   // ---- T = (I + Akk)^-1 in place (scratch over Q, dead since Aqk) -------------
   solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
+  if (!WU) {
+    store_tile_from_f32<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sA, L::LDF, len);
+    return;
+  }
   // T's two column-scaled copies over the scratch, and T itself to global
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
@@ -674,37 +680,44 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
 // keeps its S [D x 16] slice in MFMA accumulators and the chunk's U [64 x 16]
 // in registers; both feed the next products directly as B operands (the k
 // order of pack_acc_pair), so a chunk has no LDS round trip of S or U and no
-// barrier between its products:
-//   U = u - W S,   O = diag(s e^G)(Q S) + Aqk U,
+// barrier between its products.  W = T diag(beta e^G) K and u = T diag(beta) V
+// are never formed; with Y the prediction error of the chunk,
+//   Y = diag(beta) (V - diag(e^G) (K S)),   U = T Y   (= u - W S),
+//   O = diag(s e^G)(Q S) + Aqk U,
 //   S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U.
-// The loader waves move each chunk's read-only tiles (W, Q, KW, Aqk, the u
-// slice and G) from global memory into a double-buffered LDS stage one chunk
-// ahead.  They form two groups that take alternate chunks, each holding one
-// chunk in registers, so two chunks' loads are in flight while one chunk
-// computes and each wave only ever waits for its own loads (never for a
-// compute wave's stores).  One barrier per chunk.
+// Reading T (64 x 64) and the V slice costs fewer bytes than W (64 x D) and
+// the u slice, and the intra pass writes neither.
+// The loader waves move each chunk's read-only tiles (Q, KW, K when it is not
+// KW, Aqk, T, the V slice, G and beta) from global memory into a
+// double-buffered LDS stage one chunk ahead.  They form two groups that take
+// alternate chunks, each holding one chunk in registers, so two chunks' loads
+// are in flight while one chunk computes and each wave only ever waits for its
+// own loads (never for a compute wave's stores).  One barrier per chunk.
 // ---------------------------------------------------------------------------
 constexpr int kRrLoaders = 4;  // two groups of two waves
 
-template <int D, int BV>
+template <int D, int BV, bool ALIAS>
 struct RrFwdLayout {
   static constexpr int LD = D + Pad<bf16_t>::v;
   static constexpr int LDV = BV + Pad<bf16_t>::v;
   static constexpr int LDC = C + Pad<bf16_t>::v;
-  static constexpr int off_W = 0;
-  static constexpr int off_Q = off_W + C * LD * 2;
+  static constexpr int off_Q = 0;
   static constexpr int off_KW = off_Q + C * LD * 2;
-  static constexpr int off_A = off_KW + C * LD * 2;
-  static constexpr int off_U = off_A + C * LDC * 2;
-  static constexpr int off_G = off_U + C * LDV * 2;
-  static constexpr int BUF = off_G + C * 4;
+  static constexpr int off_K = off_KW + C * LD * 2;               // K when it is not KW
+  static constexpr int off_A = off_K + (ALIAS ? 0 : C * LD * 2);  // Aqk
+  static constexpr int off_T = off_A + C * LDC * 2;
+  static constexpr int off_V = off_T + C * LDC * 2;
+  static constexpr int off_G = off_V + C * LDV * 2;
+  static constexpr int off_B = off_G + C * 4;                     // beta (0 past the chunk's end)
+  static constexpr int BUF = off_B + C * 4;
   static constexpr int bytes = 2 * BUF;
   static_assert(BUF % 16 == 0, "16-byte aligned stages");
+  static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
 };
 
-template <int D, int BV>
+template <int D, int BV, bool ALIAS>
 __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_rr_kernel(FwdParams p) {
-  using L = RrFwdLayout<D, BV>;
+  using L = RrFwdLayout<D, BV, ALIAS>;
   using T = bf16_t;
   constexpr int NC = BV / 16;           // compute waves
   constexpr int NKT = D / 16;           // 16-row tiles of the state slice
@@ -723,29 +736,38 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
   if (loader) {
     // The two roles run separate loops with the same barriers, so neither
     // keeps the other's registers live.
-    RegTile<NGT, C, D, T> rW, rQ, rKW;
-    RegTile<NGT, C, C, T> rA;
-    RegTile<NGT, C, BV, T> rU;
-    float rg = 0.f;
+    RegTile<NGT, C, D, T> rQ, rKW, rK;
+    RegTile<NGT, C, C, T> rA, rT;
+    RegTile<NGT, C, BV, T> rV;
+    float rg = 0.f, rb = 0.f;
     auto load = [&](int jc) {
       const int cstart = dstart + jc * C;
       const int clen = min(C, dlen - jc * C);
       const int64_t row0 = (int64_t)cstart * H + h;
-      rW.load_as(lt, static_cast<const T*>(p.w) + row0 * D, gs, clen);
       rQ.load_as(lt, static_cast<const T*>(p.q) + row0 * D, gs, clen);
       rKW.load_as(lt, static_cast<const T*>(p.kw) + row0 * D, gs, clen);
+      if (!ALIAS) rK.load_as(lt, static_cast<const T*>(p.k) + row0 * D, gs, clen);
       rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
-      rU.load_as(lt, static_cast<const T*>(p.u) + row0 * D + v0, gs, clen);
-      if (lt < C) rg = p.gcum[(int64_t)(cstart + min(lt, clen - 1)) * H + h];  // padded rows repeat the last gate
+      rT.load_as(lt, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, clen);
+      rV.load_as(lt, static_cast<const T*>(p.v) + row0 * D + v0, gs, clen);
+      if (lt < C) {
+        const int64_t gi = (int64_t)(cstart + min(lt, clen - 1)) * H + h;
+        rg = p.gcum[gi];  // padded rows repeat the last gate
+        rb = lt < clen ? p.beta[gi] : 0.f;
+      }
     };
     auto stash = [&](int b) {
       char* buf = smem + b * L::BUF;
-      rW.store_as(lt, reinterpret_cast<T*>(buf + L::off_W), L::LD);
       rQ.store_as(lt, reinterpret_cast<T*>(buf + L::off_Q), L::LD);
       rKW.store_as(lt, reinterpret_cast<T*>(buf + L::off_KW), L::LD);
+      if (!ALIAS) rK.store_as(lt, reinterpret_cast<T*>(buf + L::off_K), L::LD);
       rA.store_as(lt, reinterpret_cast<T*>(buf + L::off_A), L::LDC);
-      rU.store_as(lt, reinterpret_cast<T*>(buf + L::off_U), L::LDV);
-      if (lt < C) reinterpret_cast<float*>(buf + L::off_G)[lt] = rg;
+      rT.store_as(lt, reinterpret_cast<T*>(buf + L::off_T), L::LDC);
+      rV.store_as(lt, reinterpret_cast<T*>(buf + L::off_V), L::LDV);
+      if (lt < C) {
+        reinterpret_cast<float*>(buf + L::off_G)[lt] = rg;
+        reinterpret_cast<float*>(buf + L::off_B)[lt] = rb;
+      }
     };
     // group g holds chunks g, g + 2, ...; chunk 0 is staged before the loop
     if (lgroup < count) load(lgroup);
@@ -778,12 +800,14 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
   for (int jc = 0; jc < count; ++jc) {
     __syncthreads();
     const char* buf = smem + (jc & 1) * L::BUF;
-    const T* sW = reinterpret_cast<const T*>(buf + L::off_W);
     const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
     const T* sKW = reinterpret_cast<const T*>(buf + L::off_KW);
+    const T* sK = ALIAS ? sKW : reinterpret_cast<const T*>(buf + L::off_K);
     const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
-    const T* sU = reinterpret_cast<const T*>(buf + L::off_U);
+    const T* sT = reinterpret_cast<const T*>(buf + L::off_T);
+    const T* sV = reinterpret_cast<const T*>(buf + L::off_V);
     const float* sG = reinterpret_cast<const float*>(buf + L::off_G);
+    const float* sB = reinterpret_cast<const float*>(buf + L::off_B);
     const int cid = first + jc;
     const int clen = min(C, dlen - jc * C);
     const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
@@ -801,33 +825,58 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
         store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
       }
     }
-    // W S and Q S: for each k step the eight tiles are independent accumulators
-    f32x4 WS[4], QS[4];
+    // K S and Q S: for each k step the eight tiles are independent accumulators
+    f32x4 KS[4], QS[4];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) WS[rb] = QS[rb] = zero4();
+    for (int rb = 0; rb < 4; ++rb) KS[rb] = QS[rb] = zero4();
 #pragma unroll
     for (int kk = 0; kk < NKT / 2; ++kk) {
-      s16x8_t aw[4], aq[4];
+      s16x8_t ak[4], aq[4];
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
-        aw[rb] = lds_a_perm(sW + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+        ak[rb] = lds_a_perm(sK + 16 * rb * L::LD, L::LD, 32 * kk, lane);
         aq[rb] = lds_a_perm(sQ + 16 * rb * L::LD, L::LD, 32 * kk, lane);
       }
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
-        mfma_bf16(WS[rb], aw[rb], SB[kk]);
+        mfma_bf16(KS[rb], ak[rb], SB[kk]);
         mfma_bf16(QS[rb], aq[rb], SB[kk]);
       }
     }
-    // U = u - W S
-    f32x4 U[4];
-    T* u_io = static_cast<T*>(p.u) + row0 * D + col0;
+    // Y = diag(beta) (V - diag(e^G) K S) as B operands over the tokens
+    s16x8_t YB[2];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int kt = 0; kt < 2; ++kt) {
+      f32x4 y[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) U[rb][j] = bf16_to_f32(sU[(16 * rb + q4 + j) * L::LDV + cl]) - WS[rb][j];
-      store_acc_global<T>(u_io, gs, U[rb], 16 * rb, 0, clen, lane);
+      for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 32 * kt + 16 * hf + q4 + j;
+          y[hf][j] = sB[r] * (bf16_to_f32(sV[r * L::LDV + cl]) - exp_fast(sG[r]) * KS[2 * kt + hf][j]);
+        }
+      }
+      YB[kt] = pack_acc_pair(y[0], y[1]);
     }
+    // U = T Y   (T is lower triangular: row block rb needs k steps kt <= rb / 2)
+    f32x4 U[4];
+    {
+      s16x8_t at[6];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) at[rb] = lds_a_perm(sT + 16 * rb * L::LDC, L::LDC, 0, lane);
+      at[4] = lds_a_perm(sT + 32 * L::LDC, L::LDC, 32, lane);
+      at[5] = lds_a_perm(sT + 48 * L::LDC, L::LDC, 32, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        U[rb] = zero4();
+        mfma_bf16(U[rb], at[rb], YB[0]);
+      }
+      mfma_bf16(U[2], at[4], YB[1]);
+      mfma_bf16(U[3], at[5], YB[1]);
+    }
+    T* u_out = static_cast<T*>(p.u) + row0 * D + col0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(u_out, gs, U[rb], 16 * rb, 0, clen, lane);
     const s16x8_t UB[2] = {pack_acc_pair(U[0], U[1]), pack_acc_pair(U[2], U[3])};
     // O = diag(s e^G) Q S + Aqk U   (Aqk is lower triangular: row block rb needs k steps kt <= rb / 2)
     f32x4 AU[4];
@@ -896,24 +945,25 @@ int set_smem(K kernel, int bytes) {
   return 0;
 }
 
+template <int D, int BV, bool ALIAS>
+int launch_state_fwd_rr_as(const FwdParams& p, hipStream_t s) {
+  auto kern = chunk_state_fwd_rr_kernel<D, BV, ALIAS>;
+  constexpr int bytes = RrFwdLayout<D, BV, ALIAS>::bytes;
+  if (int st = set_smem(kern, bytes)) return st;
+  hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoaders)), bytes, s, p);
+  return launch_status("pkda_chunk_fwd(state)");
+}
+
 // Register-resident state pass: 64 value columns per workgroup, or 32 when
 // that leaves fewer workgroups than compute units.
 template <int D>
 int launch_state_fwd_rr(const FwdParams& p, hipStream_t s) {
   const int N = p.geom.num_seqs;
   if (N <= 0) return 0;
-#ifdef PKDA_RR_WIDE
-  constexpr int BW = D;
-#else
-  constexpr int BW = 64;
-#endif
-  const bool narrow = (int64_t)N * p.H * (D / BW) < 256;
-  auto kern = narrow ? chunk_state_fwd_rr_kernel<D, 32> : chunk_state_fwd_rr_kernel<D, BW>;
-  const int bytes = narrow ? RrFwdLayout<D, 32>::bytes : RrFwdLayout<D, BW>::bytes;
-  const int bv = narrow ? 32 : BW;
-  if (int st = set_smem(kern, bytes)) return st;
-  hipLaunchKernelGGL(kern, dim3(N, p.H, D / bv), dim3(64 * (bv / 16 + kRrLoaders)), bytes, s, p);
-  return launch_status("pkda_chunk_fwd(state)");
+  const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
+  const bool alias = p.kw == p.k;
+  if (narrow) return alias ? launch_state_fwd_rr_as<D, 32, true>(p, s) : launch_state_fwd_rr_as<D, 32, false>(p, s);
+  return alias ? launch_state_fwd_rr_as<D, 64, true>(p, s) : launch_state_fwd_rr_as<D, 64, false>(p, s);
 }
 
 template <typename T, int D, int BV>
@@ -921,8 +971,9 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const bool all = stages == 0;
   if (all || (stages & PKDA_STAGE_FWD_INTRA)) {
     const bool alias = p.kw == p.k;
+    constexpr bool WU = !implicit_w<T>();
     auto kern = p.qg ? (alias ? chunk_intra_fwd_pc_kernel<T, D, true> : chunk_intra_fwd_pc_kernel<T, D, false>)
-                     : (alias ? chunk_intra_fwd_kernel<T, D, true> : chunk_intra_fwd_kernel<T, D, false>);
+                     : (alias ? chunk_intra_fwd_kernel<T, D, true, WU> : chunk_intra_fwd_kernel<T, D, false, WU>);
     const int bytes = p.qg ? (alias ? IntraPcLayout<T, D, true>::bytes : IntraPcLayout<T, D, false>::bytes)
                            : (alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes);
     if (int st = set_smem(kern, bytes)) return st;
@@ -975,8 +1026,10 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   FwdParams p;
   if (int st = chunk_geom_from(a->cu_seqlens, a->num_seqs, a->seqlen, a->num_chunks, a->table, p.geom)) return st;
   if (a->num_seqs == 0) return 0;
-  PKDA_REQUIRE(a->q && a->k && a->v && a->gcum && a->beta && a->o && a->w && a->u && a->aqk && a->akk, PKDA_EINVAL,
+  PKDA_REQUIRE(a->q && a->k && a->v && a->gcum && a->beta && a->o && a->u && a->aqk && a->akk, PKDA_EINVAL,
                "null tensor");
+  const bool needs_w = a->dtype != PKDA_BF16 || a->gate_per_channel;  // BF16, per-head gate: W is never stored
+  PKDA_REQUIRE(a->w || !needs_w, PKDA_EINVAL, "this dtype / gate needs the w buffer");
   p.H = a->heads;
   p.q = a->q; p.k = a->k; p.kw = a->kw ? a->kw : a->k; p.v = a->v;
   p.gcum = a->gcum; p.beta = a->beta; p.scale = a->scale;

@@ -253,7 +253,7 @@ int pkda_precond_bwd(const pkda_precond_args* args, void* stream);
  * ------------------------------------------------------------------------- */
 enum pkda_chunk_stage {
   PKDA_STAGE_ALL = 0,
-  PKDA_STAGE_FWD_INTRA = 1, /* per chunk: Akk, T = (I + Akk)^-1, w, u, Aqk     */
+  PKDA_STAGE_FWD_INTRA = 1, /* per chunk: Akk, T = (I + Akk)^-1, Aqk (w, u)   */
   PKDA_STAGE_FWD_STATE = 2, /* per document: U, o, the chunk states h, S_T     */
   PKDA_STAGE_BWD_STATE = 1, /* per document, reverse: dh, dU, dS0            */
   PKDA_STAGE_BWD_CHUNK = 2  /* per chunk: every gradient of the chunk          */
@@ -273,6 +273,10 @@ enum pkda_chunk_stage {
  * Saved for the backward (all [N_tok, H, *] in dtype unless stated):
  * w, u (overwritten with U), aqk [.., 64], akk (= T) [.., 64],
  * h [num_chunks, H, K, V] (state entering each chunk; NULL when not training).
+ * BF16 with a per-head gate never stores w (it may be NULL, here and in the
+ * backward) nor the intermediate u: its state passes form U = T diag(beta)
+ * (v - exp(gcum) * (k S)) and w^T dU = k^T diag(beta exp(gcum)) T^T dU from
+ * akk, k and v, and u receives U alone.
  * Per-channel gates (gate_per_channel != 0, gcum [N_tok, H, K]): the decay
  * sits inside every key contraction.  Pairs of tokens in different 16-token
  * sub-blocks are products of operands each scaled by a decay <= 1 relative
