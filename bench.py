@@ -36,12 +36,16 @@ Printed as ONE JSON line:
 
 Algorithmic work per token-head (C = 64, dk = dv = d; the triangular solve,
 gate scans and elementwise work are not counted):
-  fwd intra   8Cd           (Akk, Aqk, W, Uu)
-  fwd state   6d^2 + 2Cd    (W S, Q S, Kg^T U; Aqk U)
-  bwd state   6d^2 + 2Cd    (Kg dS, Qg^T dO, W^T dU; Aqk^T dO)
+  fwd intra   4Cd           (Akk, Aqk)
+  fwd state   6d^2 + 4Cd    (K S, Q S, Kg^T U; U = T Y, Aqk U)
+  bwd state   6d^2 + 4Cd    (Kg dS, Qg^T dO, K^T (beta e^G T^T dU); T^T dU,
+                             Aqk^T dO)
   bwd chunk   6d^2 + 18Cd   (dO S^T, dU S^T, U dS^T; dO U^T; T^T dW, T^T dU,
                              dW Bw^T, dU Bv^T; pairwise dq, dk, dkw products)
   total       18d^2 + 30Cd = 540,672 flop at d = 128
+(BF16 with a per-head gate never forms W = T diag(beta e^G) K or u: the state
+passes contract with T instead, which moves 4Cd out of the intra kernel and
+2Cd into each state pass.)
 """
 
 from __future__ import annotations
@@ -75,9 +79,9 @@ WORKLOADS = {
 def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
     """Algorithmic flops per token-head of each kernel of the step."""
     return {
-        "fwd_intra": 8 * C * D,
-        "fwd_state": 6 * D * D + 2 * C * D,
-        "bwd_state": 6 * D * D + 2 * C * D,
+        "fwd_intra": 4 * C * D,
+        "fwd_state": 6 * D * D + 4 * C * D,
+        "bwd_state": 6 * D * D + 4 * C * D,
         "bwd_chunk": 6 * D * D + 2 * C * D + 8 * C * D + 8 * C * D,
     }
 
@@ -85,9 +89,9 @@ def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
 # The kernel each timed stage launches for the default BF16, d = 128 workloads,
 # as rocprofv3 names it (template arguments with bf16 for unsigned short).
 STAGE_KERNEL = {
-    "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true>",
-    "fwd_state": "chunk_state_fwd_rr_kernel<128, 64>",
-    "bwd_state": "chunk_state_bwd_rr_kernel<128, 64>",
+    "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true, false>",
+    "fwd_state": "chunk_state_fwd_rr_kernel<128, 64, true>",
+    "bwd_state": "chunk_state_bwd_rr_kernel<128, 64, true>",
     "bwd_chunk": "chunk_fused_bwd_kernel<bf16, 128, bf16>",
     "decode": "decode_kernel<bf16, 128, 512>",
 }
