@@ -302,7 +302,7 @@ struct FusedBwdLayout {
   static constexpr int bytes = off_red + kFW * 4;
 };
 
-template <typename T, int D, typename OT>
+template <typename T, int D, typename OT, bool ALIAS>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   using L = FusedBwdLayout<T, D>;
   using E = T;
@@ -405,12 +405,13 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     }
   }
   __syncthreads();
-  // ---- phase 2: dBv over dU; Q, KW and dS_C start their way in -------------
-  RegTile<kFW, C, D, T> rQ, rKW;
+  // ---- phase 2: dBv over dU; Q, KW, dS_C and K start their way in ---------
+  RegTile<kFW, C, D, T> rQ, rKW, rK;
   TiledTile<kFW, D, T> rdH;
   rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
-  if (!p.kw_is_k) rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, len);
+  if (!ALIAS) rKW.load(static_cast<const T*>(p.kw) + row0 * D, gs, len);
   rdH.load(dhsrc);
+  rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);  // waits in registers until U's region frees
 #pragma unroll
   for (int j = 0; j < HCT; ++j) store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
   __syncthreads();
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   }
   // Q and KW regions (dO, V) have been free since phase 1
   rQ.store(sQ, L::LD);
-  if (!p.kw_is_k) rKW.store(sKW, L::LD);
+  if (!ALIAS) rKW.store(sKW, L::LD);
   __syncthreads();
   // ---- phase 4: dS_C replaces S0; sum(S0 * dS_C) ------------------------------
   float hd = 0.f;
@@ -458,8 +459,6 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   }
   __syncthreads();
   // ---- phase 5: dKg = U dS_C^T (write-key gradient of the state path) ---------
-  RegTile<kFW, C, D, T> rK;
-  rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -471,7 +470,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   __syncthreads();
   rK.store(sK, L::LD);
   __syncthreads();
-  const E* sKWr = p.kw_is_k ? sK : sKW;
+  const E* sKWr = ALIAS ? sK : sKW;
   // ---- phase 6: pairwise terms ------------------------------------------------
   float gsum[4] = {0.f, 0.f, 0.f, 0.f};
   float kgd = 0.f;
@@ -479,7 +478,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   OT* dko = static_cast<OT*>(p.dk) + row0 * D;
   // outputs in the activation dtype with the write-key gradient folded into
   // dk leave through LDS (16-byte stores)
-  const bool kStage = sizeof(OT) == sizeof(T) && p.kw_is_k;
+  constexpr bool kStage = sizeof(OT) == sizeof(T) && ALIAS;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -504,12 +503,12 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
       kgd += wv * dkws[j][e];
       gsum[e] += qv * dq[j][e] + kv * dk[e] - wv * dkw[e];
     }
-    if (kStage) {  // S0's and dBv's regions are free: stage for 16-byte stores
+    if constexpr (kStage) {  // S0's and dBv's regions are free: stage for 16-byte stores
       store_acc_lds(sH, L::LD, dq[j], r0, 16 * ct, lane);
       store_acc_lds(sdBv, L::LD, dk + dkw, r0, 16 * ct, lane);
     } else {
       store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
-      if (p.kw_is_k) {
+      if (ALIAS) {
         store_acc_global<OT>(dko, gs, dk + dkw, r0, 16 * ct, len, lane);
       } else {
         store_acc_global<OT>(dko, gs, dk, r0, 16 * ct, len, lane);
@@ -537,7 +536,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     sWave[kFW / 64 + wave] = kgd;
   }
   __syncthreads();
-  if (kStage) {
+  if constexpr (kStage) {
     store_tile<kFW, C, D>(dqo, gs, reinterpret_cast<const OT*>(sH), L::LD, len);
     store_tile<kFW, C, D>(dko, gs, reinterpret_cast<const OT*>(sdBv), L::LD, len);
   }
@@ -1254,7 +1253,8 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   }
   if (num_chunks == 0) return 0;
   if (all || (stages & PKDA_STAGE_BWD_CHUNK)) {
-    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D, OT> : chunk_fused_bwd_kernel<T, D, OT>;
+    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D, OT>
+                     : (p.kw_is_k ? chunk_fused_bwd_kernel<T, D, OT, true> : chunk_fused_bwd_kernel<T, D, OT, false>);
     const int bytes = p.qg ? FusedBwdPcLayout<T, D>::bytes : FusedBwdLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kFW), bytes, s, p);
