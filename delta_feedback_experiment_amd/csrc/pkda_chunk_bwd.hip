@@ -371,6 +371,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 
   f32x4 dq[HCT], dkb[HCT], dkws[HCT], dBv[HCT];
   float db[4] = {0.f, 0.f, 0.f, 0.f};
+  // dv in the activation dtype leaves through V's region, free after phase 1
+  // when the write key is the read key (16-byte stores)
+  constexpr bool vStage = sizeof(OT) == sizeof(T) && ALIAS;
+  OT* dvo = static_cast<OT*>(p.dv) + row0 * D;
   // ---- phase 1: dBv = T^T dU (-> dv), dQg = dO S0^T, dAqk = dO U^T ------------
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
@@ -379,14 +383,14 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     f32x4 acv = zero4();
     mma_tile<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, C, lane);
     dBv[j] = acv;
-    f32x4 dv;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int s = r0 + acc_row(lane, e);
-      dv[e] = sBeta[s] * acv[e];
-      db[e] += acv[e] * from_e<E>(sV[s * L::LD + c]);
+    for (int e = 0; e < 4; ++e) db[e] += acv[e] * from_e<E>(sV[(r0 + acc_row(lane, e)) * L::LD + c]);
+    if constexpr (!vStage) {
+      f32x4 dv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dv[e] = sBeta[r0 + acc_row(lane, e)] * acv[e];
+      store_acc_global<OT>(dvo, gs, dv, r0, 16 * ct, len, lane);  // final
     }
-    store_acc_global<OT>(static_cast<OT*>(p.dv) + row0 * D, gs, dv, r0, 16 * ct, len, lane);  // final
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
@@ -413,8 +417,17 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   rdH.load(dhsrc);
   rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);  // waits in registers until U's region frees
 #pragma unroll
-  for (int j = 0; j < HCT; ++j) store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
+  for (int j = 0; j < HCT; ++j) {
+    store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
+    if constexpr (vStage) {
+      f32x4 dv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dv[e] = sBeta[r0 + acc_row(lane, e)] * dBv[j][e];
+      store_acc_lds(sV, L::LD, dv, r0, 16 * (ch * HCT + j), lane);
+    }
+  }
   __syncthreads();
+  if constexpr (vStage) store_tile<kFW, C, D>(dvo, gs, sV, L::LD, len);  // final
   // ---- phase 3: dBw = -dBv S0^T, dAkk = -dBv U^T --------------------------------
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
