@@ -50,7 +50,7 @@ class ChunkPlan:
         if N < 0:
             raise ValueError("cu_seqlens needs at least one element")
         bound = -(-T // CHUNK_SIZE) + N
-        table = torch.empty(4 * bound + N + 1, device=q.device, dtype=torch.int32)
+        table = torch.empty(4 * bound + 2 * N + 1, device=q.device, dtype=torch.int32)
         with torch.cuda.device(q.device):
             status = _lib.lib().pkda_chunk_table(
                 _ptr(cu), N, bound, _ptr(table), _stream(q.device)

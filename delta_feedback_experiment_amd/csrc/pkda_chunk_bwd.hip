@@ -148,7 +148,8 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
   float* sGC = reinterpret_cast<float*>(smem + L::off_gc);
 
-  const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
+  const DocSlot ds = doc_slot(p.geom, p.H, D / BV);
+  const int n = ds.n, h = ds.h, v0 = ds.z * BV;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t gs = (int64_t)H * D;
@@ -1015,7 +1016,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
   constexpr int NC = BV / 16;
   constexpr int NKT = D / 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
+  const DocSlot ds = doc_slot(p.geom, p.H, D / BV);
+  const int n = ds.n, h = ds.h, v0 = ds.z * BV;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t gs = (int64_t)H * D;
@@ -1229,7 +1231,7 @@ int launch_state_bwd_rr_as(const BwdParams& p, hipStream_t s) {
   auto kern = chunk_state_bwd_rr_kernel<D, BV, ALIAS>;
   constexpr int bytes = RrBwdLayout<D, BV, ALIAS>::bytes;
   if (int st = set_smem(kern, bytes)) return st;
-  hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoadersBwd)), bytes, s, p);
+  hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoadersBwd)), bytes, s, p);
   return launch_status("pkda_chunk_bwd(state)");
 }
 
@@ -1260,7 +1262,7 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
       auto kern = p.qg ? chunk_state_bwd_kernel<T, D, BV, true> : chunk_state_bwd_kernel<T, D, BV, false>;
       const int bytes = StateBwdLayout<T, D, BV>::bytes;
       if (int st = set_smem(kern, bytes)) return st;
-      if (N > 0) hipLaunchKernelGGL(kern, dim3(N, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
+      if (N > 0) hipLaunchKernelGGL(kern, doc_grid(N, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
       if (int st = launch_status("pkda_chunk_bwd(state)")) return st;
     }
   }

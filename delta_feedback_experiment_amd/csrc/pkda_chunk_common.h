@@ -37,6 +37,7 @@ struct ChunkGeom {
   const int32_t* cu;   // [num_seqs+1] or nullptr
   const int4* table;   // [num_chunks] {n, start, len, -} (varlen)
   const int32_t* offsets;  // [num_seqs+1] first chunk id of each document (varlen)
+  const int32_t* order;    // [num_seqs] documents by length, longest first (varlen)
   int num_chunks;      // launch bound
 };
 
@@ -66,6 +67,27 @@ __device__ __forceinline__ ChunkInfo chunk_info(const ChunkGeom& g, int c) {
 }
 
 // First chunk id, chunk count and first token of document n.
+// Per-document launches run on a 1-D grid of num_seqs * H * S workgroups
+// (S value slices per head): the H * S workgroups of one document are
+// consecutive, slice-major (the slices of one (document, head) are H apart,
+// so on one XCD and its L2 when H % 8 == 0), and packed documents come
+// longest first, so the longest sequential passes start before the short
+// ones fill in behind them.
+struct DocSlot {
+  int n, h, z;
+};
+__device__ __forceinline__ DocSlot doc_slot(const ChunkGeom& g, int H, int S) {
+  const int hs = H * S;
+  const int rank = blockIdx.x / hs;
+  const int r = blockIdx.x - rank * hs;
+  DocSlot d;
+  d.n = g.order ? g.order[rank] : rank;
+  d.z = r / H;
+  d.h = r - d.z * H;
+  return d;
+}
+inline dim3 doc_grid(int num_seqs, int H, int S) { return dim3((unsigned)((int64_t)num_seqs * H * S)); }
+
 __device__ __forceinline__ void doc_chunks(const ChunkGeom& g, int n, int& first, int& count, int& start, int& len) {
   if (g.cu) {
     first = g.offsets[n];

@@ -543,7 +543,8 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
   float* sGC = reinterpret_cast<float*>(smem + L::off_gc);
 
-  const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
+  const DocSlot ds = doc_slot(p.geom, p.H, D / BV);
+  const int n = ds.n, h = ds.h, v0 = ds.z * BV;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t gs = (int64_t)H * D;
@@ -722,7 +723,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
   constexpr int NC = BV / 16;           // compute waves
   constexpr int NKT = D / 16;           // 16-row tiles of the state slice
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int n = blockIdx.x, h = blockIdx.y, v0 = blockIdx.z * BV;
+  const DocSlot ds = doc_slot(p.geom, p.H, D / BV);
+  const int n = ds.n, h = ds.h, v0 = ds.z * BV;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t gs = (int64_t)H * D;
@@ -950,7 +952,7 @@ int launch_state_fwd_rr_as(const FwdParams& p, hipStream_t s) {
   auto kern = chunk_state_fwd_rr_kernel<D, BV, ALIAS>;
   constexpr int bytes = RrFwdLayout<D, BV, ALIAS>::bytes;
   if (int st = set_smem(kern, bytes)) return st;
-  hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoaders)), bytes, s, p);
+  hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoaders)), bytes, s, p);
   return launch_status("pkda_chunk_fwd(state)");
 }
 
@@ -987,7 +989,8 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
     auto kern = p.qg ? chunk_state_fwd_kernel<T, D, BV, true> : chunk_state_fwd_kernel<T, D, BV, false>;
     const int bytes = StateLayout<T, D, BV>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
-    if (p.geom.num_seqs > 0) hipLaunchKernelGGL(kern, dim3(p.geom.num_seqs, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
+    if (p.geom.num_seqs > 0)
+      hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(state_threads(D, BV)), bytes, s, p);
     if (int st = launch_status("pkda_chunk_fwd(state)")) return st;
   }
   return 0;
@@ -1003,6 +1006,7 @@ int chunk_geom_from(const int32_t* cu, int num_seqs, int seqlen, int num_chunks,
   g.nt = cu ? 0 : (seqlen + C - 1) / C;
   g.table = reinterpret_cast<const int4*>(table);
   g.offsets = table ? table + 4 * num_chunks : nullptr;
+  g.order = table ? g.offsets + num_seqs + 1 : nullptr;
   g.num_chunks = num_chunks;
   PKDA_REQUIRE(!cu || table, PKDA_EINVAL, "packed documents need the chunk table (pkda_chunk_table)");
   PKDA_REQUIRE(cu || num_chunks == num_seqs * g.nt, PKDA_EINVAL, "num_chunks %d != num_seqs * ceil(seqlen / 64) = %d",

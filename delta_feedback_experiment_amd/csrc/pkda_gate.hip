@@ -55,6 +55,28 @@ __global__ __launch_bounds__(kWG) void chunk_fill_kernel(const int32_t* cu, int 
   table[c] = e;
 }
 
+// Documents by length, longest first, ties by index: order[rank] = document.
+// Each thread ranks its document against all others (a strict total order,
+// so the ranks are a permutation), reading the lengths in LDS tiles.
+__global__ __launch_bounds__(kWG) void chunk_order_kernel(const int32_t* cu, int N, int32_t* order) {
+  __shared__ int s_len[kWG];
+  const int n = blockIdx.x * kWG + threadIdx.x;
+  const int len = n < N ? cu[n + 1] - cu[n] : 0;
+  int rank = 0;
+  for (int base = 0; base < N; base += kWG) {
+    const int m = base + threadIdx.x;
+    s_len[threadIdx.x] = m < N ? cu[m + 1] - cu[m] : 0;
+    __syncthreads();
+    const int cnt = min(kWG, N - base);
+    for (int i = 0; i < cnt; ++i) {
+      const int lm = s_len[i];
+      rank += (lm > len) || (lm == len && base + i < n);
+    }
+    __syncthreads();
+  }
+  if (n < N) order[rank] = n;
+}
+
 // ---- gate forward --------------------------------------------------------------
 struct GateParams {
   ChunkGeom geom;
@@ -388,6 +410,7 @@ int gate_common(const pkda_gate_args* a, GateParams& p) {
   p.geom.cu = a->cu_seqlens;
   p.geom.table = reinterpret_cast<const int4*>(a->table);
   p.geom.offsets = a->table ? a->table + 4 * a->num_chunks : nullptr;
+  p.geom.order = a->table ? p.geom.offsets + a->num_seqs + 1 : nullptr;
   p.geom.num_chunks = a->num_chunks;
   PKDA_REQUIRE(a->cu_seqlens || a->num_chunks == a->num_seqs * p.geom.nt, PKDA_EINVAL,
                "num_chunks %d != num_seqs * ceil(seqlen / 64)", a->num_chunks);
@@ -423,6 +446,9 @@ extern "C" int pkda_chunk_table(const int32_t* cu_seqlens, int32_t num_seqs, int
   if (num_chunks_max > 0)
     hipLaunchKernelGGL(chunk_fill_kernel, dim3((num_chunks_max + kWG - 1) / kWG), dim3(kWG), 0, s, cu_seqlens,
                        num_seqs, offsets, num_chunks_max, reinterpret_cast<int4*>(table));
+  if (num_seqs > 0)
+    hipLaunchKernelGGL(chunk_order_kernel, dim3((num_seqs + kWG - 1) / kWG), dim3(kWG), 0, s, cu_seqlens, num_seqs,
+                       offsets + num_seqs + 1);
   return launch_status("pkda_chunk_table");
 }
 

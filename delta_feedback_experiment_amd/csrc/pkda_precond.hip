@@ -53,7 +53,8 @@ template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : 
 
 template <typename T, int D>
 __global__ __launch_bounds__(PrecondThreads<D>::v) void precond_fwd_kernel(PrecondParams p) {
-  const int n = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
+  const DocSlot ds = doc_slot(p.geom, p.H, 1);
+  const int n = ds.n, h = ds.h, c = threadIdx.x;
   if (c >= D) return;
   const int H = p.H;
   int first, count, dstart, dlen;
@@ -88,7 +89,8 @@ __global__ __launch_bounds__(PrecondThreads<D>::v) void precond_bwd_kernel(Preco
   float* sA = smem_f;              // [C][LDA]
   float* sCb = sA + C * LDA;       // [C][LDA]  lambda_t k_t^2
   float* sRed = sCb + C * LDA;     // [NT]
-  const int n = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
+  const DocSlot ds = doc_slot(p.geom, p.H, 1);
+  const int n = ds.n, h = ds.h, c = threadIdx.x;
   const bool active = c < D;
   const int H = p.H;
   int first, count, dstart, dlen;
@@ -200,7 +202,7 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
 template <typename T, int D>
 int launch_precond(const PrecondParams& p, bool backward, hipStream_t s) {
   constexpr int NT = PrecondThreads<D>::v;
-  const dim3 grid(p.geom.num_seqs, p.H);
+  const dim3 grid = doc_grid(p.geom.num_seqs, p.H, 1);
   if (backward) {
     const int bytes = (2 * C * (D + 1) + NT) * (int)sizeof(float);
     auto kern = precond_bwd_kernel<T, D>;

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 3
+#define PKDA_ABI_VERSION 4
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -143,7 +143,10 @@ int pkda_decode_step(const pkda_recurrent_args* args, void* stream);
  * Chunks of PKDA_CHUNK tokens start at every document's first token.  With
  * cu_seqlens the chunk list depends on the data, so it is built on the device
  * into a caller-provided int32 workspace `table` of
- *   4 * num_chunks_max + num_seqs + 1 elements,
+ *   4 * num_chunks_max + 2 * num_seqs + 1 elements
+ * (per chunk {document, first token, length, -}, each document's first chunk
+ * id plus the total, and the documents ordered by length, longest first: the
+ * per-document passes start the longest documents first),
  * num_chunks_max = ceil(N_tok / 64) + num_seqs (an upper bound the host knows
  * without reading cu_seqlens).  Every chunked entry point below takes the same
  * table; launches sized by num_chunks_max skip the unused tail.  Equal-length

@@ -29,6 +29,39 @@ def dev():
     return torch.device("cuda:0")
 
 
+def test_chunk_table_documents_longest_first(dev):
+    """The packed-document table: per chunk {document, first token, length},
+    each document's first chunk id, and the documents by length, longest first
+    with ties by index (the order the per-document passes start them in).
+    700 documents (three 256-thread tiles), repeated lengths and empty ones."""
+    from delta_feedback_experiment_amd.chunk import ChunkPlan
+
+    print("[gpu] chunk table order", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    lens = torch.randint(0, 300, (700,), generator=gen)
+    lens[::7] = 64
+    lens[3::11] = 0
+    lens[10] = 2000
+    lens = lens.tolist()
+    N, T = len(lens), sum(lens)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    q = torch.empty(1, T, 1, 64, device=dev, dtype=torch.bfloat16)
+    plan = ChunkPlan.make(q, cu.to(dev))
+    table = plan.table.cpu()
+    bound = plan.num_chunks
+    assert table.numel() == 4 * bound + 2 * N + 1
+    counts = [-(-n // 64) for n in lens]
+    offsets = table[4 * bound:4 * bound + N + 1].tolist()
+    assert offsets == [sum(counts[:n]) for n in range(N + 1)]
+    entries = table[:4 * bound].reshape(bound, 4)
+    for n in (0, 10, N - 1):
+        for j in range(counts[n]):
+            doc, start, ln = entries[offsets[n] + j, :3].tolist()
+            assert (doc, start, ln) == (n, int(cu[n]) + 64 * j, min(64, lens[n] - 64 * j))
+    order = table[4 * bound + N + 1:].tolist()
+    assert order == sorted(range(N), key=lambda n: (-lens[n], n))
+
+
 def make_inputs(B, T, H, D, dtype, seed=0, strong=False, per_channel=False):
     gen = torch.Generator().manual_seed(seed)
 
