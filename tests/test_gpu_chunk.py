@@ -62,6 +62,55 @@ def test_chunk_table_documents_longest_first(dev):
     assert order == sorted(range(N), key=lambda n: (-lens[n], n))
 
 
+def test_state_pass_forms_agree_bitwise(dev):
+    """Every kernel works per head and the state passes per value column, so
+    32 heads in one call (64 value columns per state-pass workgroup at this
+    size) and the same heads four at a time (32 columns) give identical bits: output,
+    final S and A and every gradient, with the write-key preconditioner
+    (k != kw), packed documents and nonzero initial states."""
+    from delta_feedback_experiment_amd.chunk import chunk_pkda
+
+    print("[gpu] state-pass forms, 32 heads vs groups of 4", flush=True)
+    T, H, D = 600, 32, 128
+    cu = torch.tensor([0, 150, 151, 400, 600], dtype=torch.int32)
+    N = cu.numel() - 1
+    q, k, v, g, beta = make_inputs(1, T, H, D, torch.bfloat16, seed=31, strong=True)
+    gen = torch.Generator().manual_seed(32)
+    g_atk, beta_atk, center = _precond_inputs(1, T, H, gen)
+    S0 = 0.02 * torch.randn(N, H, D, D, generator=gen)
+    A0 = 0.1 * torch.randn(N, H, D, generator=gen).abs()
+    do = torch.randn(1, T, H, D, generator=gen).to(torch.bfloat16)
+    dS = torch.randn(N, H, D, D, generator=gen)
+    dA = torch.randn(N, H, D, generator=gen)
+    base = [t.to(dev) for t in (q, k, v, g, beta, g_atk, beta_atk, center, S0, A0)]
+    cu_d = cu.to(dev)
+
+    def run(hs):
+        leaves = [t[:, :, hs].clone() if t.dim() >= 3 and t.shape[1] == T else
+                  (t[hs].clone() if t.dim() == 1 else t[:, hs].clone()) for t in base]
+        leaves = [t.requires_grad_() for t in leaves]
+        o, S, A = chunk_pkda(*leaves[:5], g_atk=leaves[5], beta_atk=leaves[6], log_atk_scale=leaves[7],
+                             initial_state=leaves[8], initial_A_state=leaves[9], output_final_state=True,
+                             x=1.5, eps=1e-6, cu_seqlens=cu_d)
+        loss = (o.float() * do.to(dev)[:, :, hs].float()).sum() + (S * dS.to(dev)[:, hs]).sum() \
+            + (A * dA.to(dev)[:, hs]).sum()
+        return [o, S, A, *torch.autograd.grad(loss, leaves)]
+
+    whole = run(slice(0, H))
+    parts = [run(slice(h, h + 4)) for h in range(0, H, 4)]
+    torch.cuda.synchronize()
+    names = ("o", "S", "A", "dq", "dk", "dv", "dg", "dbeta", "dg_atk", "dbeta_atk", "dcenter", "dS0", "dA0")
+    for i, name in enumerate(names):
+        w = whole[i]
+        if w.dim() == 1:
+            joined = torch.cat([pt[i] for pt in parts])
+        elif name in ("S", "A", "dS0", "dA0"):
+            joined = torch.cat([pt[i] for pt in parts], dim=1)
+        else:
+            joined = torch.cat([pt[i] for pt in parts], dim=2)
+        assert torch.equal(w, joined), name
+
+
 def make_inputs(B, T, H, D, dtype, seed=0, strong=False, per_channel=False):
     gen = torch.Generator().manual_seed(seed)
 
