@@ -84,8 +84,23 @@ __device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
 }
 
 // torch.nn.functional.softplus with beta = 1, threshold = 20.
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+// softplus(z) and sigmoid(z) from one e = e^{-|z|} in (0, 1] on the hardware
+// exp2 / log2 / reciprocal units:
+//   softplus = max(z, 0) + log1p(e),   sigmoid = (z >= 0 ? 1 : e) / (1 + e),
+// with log1p(e) = log(u) e / (u - 1), u = 1 + e, which cancels the rounding
+// of 1 + e (D. Goldberg, "What every computer scientist should know about
+// floating-point arithmetic", 1991, Theorem 4); u == 1 leaves log1p(e) = e.
+// A few ulps from the correctly rounded values; for z > 20 softplus is z
+// (log1p(e) < ulp(z)), as torch's softplus with its threshold of 20 gives.
+struct SoftplusSigmoid {
+  float softplus, sigmoid;
+};
+__device__ __forceinline__ SoftplusSigmoid softplus_sigmoid_fast(float z) {
+  const float e = __builtin_amdgcn_exp2f(-fabsf(z) * 1.44269504088896341f);
+  const float u = 1.f + e;
+  const float l = u == 1.f ? e : __builtin_amdgcn_logf(u) * 0.693147180559945309f * (e * __builtin_amdgcn_rcpf(u - 1.f));
+  return {fmaxf(z, 0.f) + l, (z >= 0.f ? 1.f : e) * __builtin_amdgcn_rcpf(u)};
+}
 
 // Sequence bounds for flat token tensors: packed documents or equal rows.
 struct SeqBounds {

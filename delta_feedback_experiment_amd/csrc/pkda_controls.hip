@@ -61,9 +61,9 @@ __global__ __launch_bounds__(kCtlThreads) void controls_fwd_kernel(CtlParams p) 
     const int64_t row = r0 + r;
     const float x = io<T>::load(packed + row * p.stride + p.rank + j);
     if (which == 1) {
-      p.pdecay[row * H + h] = -expf(p.A_log_p[h]) * softplus_f(x + p.dt_bias_p[h]);
+      p.pdecay[row * H + h] = -expf(p.A_log_p[h]) * softplus_sigmoid_fast(x + p.dt_bias_p[h]).softplus;
     } else {
-      io<T>::store(static_cast<T*>(which == 0 ? p.beta : p.pbeta) + row * H + h, sigmoid_f(x));
+      io<T>::store(static_cast<T*>(which == 0 ? p.beta : p.pbeta) + row * H + h, softplus_sigmoid_fast(x).sigmoid);
     }
   }
 }
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kCtlThreads) void controls_bwd_kernel(CtlParams p) 
     } else if (c < rank + H || (c >= rank + 2 * H && c < rank + 3 * H)) {
       const bool is_beta = c < rank + H;
       const int h = c - rank - (is_beta ? 0 : 2 * H);
-      const float y = rounded<T>(sigmoid_f(io<T>::load(packed + row * p.stride + c)));
+      const float y = rounded<T>(softplus_sigmoid_fast(io<T>::load(packed + row * p.stride + c)).sigmoid);
       d = load_or_zero<T>(is_beta ? p.dbeta : p.dpbeta, row * H + h) * (y * (1.f - y));
     } else if (c < rank + 2 * H) {
       continue;  // preconditioner decay: below
@@ -108,9 +108,10 @@ __global__ __launch_bounds__(kCtlThreads) void controls_bwd_kernel(CtlParams p) 
     const float A = expf(p.A_log_p[h]);
     const float z = io<T>::load(packed + row * p.stride + rank + H + h) + p.dt_bias_p[h];
     const float gd = p.dpdecay ? p.dpdecay[row * H + h] : 0.f;
-    const float dz = gd * (-A) * sigmoid_f(z);
+    const SoftplusSigmoid f = softplus_sigmoid_fast(z);
+    const float dz = gd * (-A) * f.sigmoid;
     io<T>::store(dpacked + row * W + rank + H + h, dz);
-    s_terms[r * H + h] = gd * (-A * softplus_f(z));
+    s_terms[r * H + h] = gd * (-A * f.softplus);
     s_terms[(kCtlRows + r) * H + h] = dz;
   }
   __syncthreads();

@@ -95,7 +95,7 @@ struct GateParams {
 
 __device__ __forceinline__ float gate_value(const GateParams& p, int64_t idx, int h, int c, float a_scale) {
   const float x = load_any(p.g, idx, p.g_dtype);
-  if (p.kind == PKDA_GATE_RAW_CHANNEL) return a_scale * softplus_f(x + p.dt_bias[h * p.D + c]);
+  if (p.kind == PKDA_GATE_RAW_CHANNEL) return a_scale * softplus_sigmoid_fast(x + p.dt_bias[h * p.D + c]).softplus;
   return x;
 }
 
@@ -162,8 +162,9 @@ __global__ __launch_bounds__(kWG) void gate_bwd_kernel(GateParams p) {
       suffix += p.dgcum[idx];
       if (raw) {
         const float z = load_any(p.g, idx, p.g_dtype) + p.dt_bias[h * p.D + c];
-        const float glog = -A * softplus_f(z);
-        const float dgr = suffix * (-A) * sigmoid_f(z);
+        const SoftplusSigmoid f = softplus_sigmoid_fast(z);
+        const float glog = -A * f.softplus;
+        const float dgr = suffix * (-A) * f.sigmoid;
         p.dg[idx] = dgr;
         dA_acc += suffix * glog;
         ddt += dgr;
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(kWG) void gate_low_rank_fwd_kernel(GateParams p) {
 #pragma unroll
   for (int ct = 0; ct < K / 16; ++ct) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[ct][j] = a_scale * softplus_f(acc[ct][j]);
+    for (int j = 0; j < 4; ++j) acc[ct][j] = a_scale * softplus_sigmoid_fast(acc[ct][j]).softplus;
     const float tot = wave_prefix_rows(acc[ct], lane);
     if (lane < 16) s_tot[wave][16 * ct + lane] = tot;
   }
@@ -352,8 +353,9 @@ __global__ __launch_bounds__(kWG) void gate_low_rank_bwd_kernel(GateParams p) {
     for (int j = 0; j < 4; ++j) {
       const bool valid = 16 * wave + acc_row(lane, j) < ci.len;
       const float s = suf[ct][j] + carry;
-      dg[j] = valid ? s * (-A) * sigmoid_f(z[ct][j]) : 0.f;
-      dA += valid ? s * (-A * softplus_f(z[ct][j])) : 0.f;
+      const SoftplusSigmoid f = softplus_sigmoid_fast(z[ct][j]);
+      dg[j] = valid ? s * (-A) * f.sigmoid : 0.f;
+      dA += valid ? s * (-A * f.softplus) : 0.f;
       col += dg[j];
     }
     store_acc_global<float>(p.dg + base, (int64_t)H * K, dg, 16 * wave, 16 * ct, ci.len, lane);

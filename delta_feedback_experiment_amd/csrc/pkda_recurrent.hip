@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(RecParams p) {
       } else if (p.gate_kind == PKDA_GATE_LOG_CHANNEL) {
         gl = load_any(p.g, th * D + c, p.g_dtype);
       } else {
-        gl = A_scale * softplus_f(load_any(p.g, th * D + c, p.g_dtype) + p.dt_bias[h * D + c]);
+        gl = A_scale * softplus_sigmoid_fast(load_any(p.g, th * D + c, p.g_dtype) + p.dt_bias[h * D + c]).softplus;
       }
       const float al = expf(gl);
       float kw = kc;
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(NTH) void decode_kernel(RecParams p) {
       const float kc = cur.k;
       const float vc = cur.v;
       float gl = cur.g;
-      if (p.gate_kind == PKDA_GATE_RAW_CHANNEL) gl = -expf(p.A_log[h]) * softplus_f(gl + p.dt_bias[h * D + c]);
+      if (p.gate_kind == PKDA_GATE_RAW_CHANNEL) gl = -expf(p.A_log[h]) * softplus_sigmoid_fast(gl + p.dt_bias[h * D + c]).softplus;
       const float al = expf(gl);
       float kw = kc;
       if (precond) {
