@@ -217,21 +217,35 @@ template <> struct LrFrag<float> {  // 16x16x4: lane (i, q) holds k = q of row i
   __device__ __forceinline__ static void mfma(f32x4& acc, const F& a, const F& b) { Mma<float>::mfma(acc, a, b); }
 };
 
+// A workgroup takes kLrChunks chunks of one head: the head's weight rows
+// [K x R] are staged in LDS once (row stride LDW) and read from there.
+constexpr int kLrChunks = 4;
+template <typename T, int R> struct LrW { static constexpr int LDW = R + Pad<T>::v; };
+
+template <typename T, int K, int R>
+__device__ __forceinline__ void stage_up_weight(const GateParams& p, int h, T* sW) {
+  constexpr int V = 16 / (int)sizeof(T), LDW = LrW<T, R>::LDW;
+  const T* wh = static_cast<const T*>(p.up_weight) + (int64_t)h * K * R;
+  for (int i = threadIdx.x; i < K * R / V; i += kWG) {
+    const int r = i / (R / V), c = (i - r * (R / V)) * V;
+    *reinterpret_cast<uint4*>(sW + r * LDW + c) = *reinterpret_cast<const uint4*>(wh + (int64_t)r * R + c);
+  }
+}
+
 // z = raw + dt_bias for this lane's accumulator elements: acc[ct][j] is row
-// 16 wave + 4 q + j, column 16 ct + i.
+// 16 wave + 4 q + j, column 16 ct + i.  sW: the head's weight in LDS.
 template <typename T, int K, int R>
 __device__ __forceinline__ void low_rank_z(const GateParams& p, const ChunkInfo& ci, int h, int wave, int lane,
-                                           f32x4 (&acc)[K / 16]) {
+                                           const T* sW, f32x4 (&acc)[K / 16]) {
   using Fr = LrFrag<T>;
   const int row = min(16 * wave + (lane & 15), ci.len - 1);
   const T* xrow = static_cast<const T*>(p.g) + (int64_t)(ci.start + row) * p.g_stride;
-  const T* wh = static_cast<const T*>(p.up_weight) + (int64_t)h * K * R;
   typename Fr::F a[R / Fr::KS];
 #pragma unroll
   for (int ks = 0; ks < R / Fr::KS; ++ks) a[ks] = Fr::load(xrow, ks * Fr::KS, lane);
 #pragma unroll
   for (int ct = 0; ct < K / 16; ++ct) {
-    const T* wrow = wh + (int64_t)(16 * ct + (lane & 15)) * R;
+    const T* wrow = sW + (16 * ct + (lane & 15)) * LrW<T, R>::LDW;
     acc[ct] = zero4();
 #pragma unroll
     for (int ks = 0; ks < R / Fr::KS; ++ks) Fr::mfma(acc[ct], a[ks], Fr::load(wrow, ks * Fr::KS, lane));
@@ -286,49 +300,48 @@ __device__ __forceinline__ float wave_suffix_rows(f32x4& v, int lane) {
 template <typename T, int K, int R>
 __global__ __launch_bounds__(kWG) void gate_low_rank_fwd_kernel(GateParams p) {
   __shared__ float s_tot[4][K];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
+  __shared__ __attribute__((aligned(16))) T sW[K * LrW<T, R>::LDW];
   const int h = blockIdx.y, H = p.heads;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  f32x4 acc[K / 16];
-  low_rank_z<T, K, R>(p, ci, h, wave, lane, acc);
-  const float a_scale = -expf(p.A_log[h]);
-#pragma unroll
-  for (int ct = 0; ct < K / 16; ++ct) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[ct][j] = a_scale * softplus_sigmoid_fast(acc[ct][j]).softplus;
-    const float tot = wave_prefix_rows(acc[ct], lane);
-    if (lane < 16) s_tot[wave][16 * ct + lane] = tot;
-  }
+  stage_up_weight<T, K, R>(p, h, sW);
   __syncthreads();
-  float* out = p.gcum + ((int64_t)ci.start * H + h) * K;
+  const float a_scale = -expf(p.A_log[h]);
+#pragma unroll 1
+  for (int i = 0; i < kLrChunks; ++i) {
+    const int c = blockIdx.x * kLrChunks + i;
+    if (c >= p.geom.num_chunks) break;
+    const ChunkInfo ci = chunk_info(p.geom, c);  // the same for every thread
+    if (ci.len <= 0) continue;
+    f32x4 acc[K / 16];
+    low_rank_z<T, K, R>(p, ci, h, wave, lane, sW, acc);
 #pragma unroll
-  for (int ct = 0; ct < K / 16; ++ct) {
-    float carry = 0.f;
-    for (int w = 0; w < wave; ++w) carry += s_tot[w][16 * ct + (lane & 15)];
+    for (int ct = 0; ct < K / 16; ++ct) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[ct][j] += carry;
-    store_acc_global<float>(out, (int64_t)H * K, acc[ct], 16 * wave, 16 * ct, ci.len, lane);
+      for (int j = 0; j < 4; ++j) acc[ct][j] = a_scale * softplus_sigmoid_fast(acc[ct][j]).softplus;
+      const float tot = wave_prefix_rows(acc[ct], lane);
+      if (lane < 16) s_tot[wave][16 * ct + lane] = tot;
+    }
+    __syncthreads();
+    float* out = p.gcum + ((int64_t)ci.start * H + h) * K;
+#pragma unroll
+    for (int ct = 0; ct < K / 16; ++ct) {
+      float carry = 0.f;
+      for (int w = 0; w < wave; ++w) carry += s_tot[w][16 * ct + (lane & 15)];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[ct][j] += carry;
+      store_acc_global<float>(out, (int64_t)H * K, acc[ct], 16 * wave, 16 * ct, ci.len, lane);
+    }
+    __syncthreads();  // s_tot is read before the next chunk writes it
   }
 }
 
 template <typename T, int K, int R>
-__global__ __launch_bounds__(kWG) void gate_low_rank_bwd_kernel(GateParams p) {
-  __shared__ float s_tot[4][K];
-  __shared__ float s_col[4][K];
-  __shared__ float s_dA[4];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  const int h = blockIdx.y, H = p.heads;
-  float* dtb = p.ddt_bias_part + ((int64_t)blockIdx.x * H + h) * K;
-  if (ci.len <= 0) {  // an empty slot of the packed launch bound: zero partials
-    for (int c = threadIdx.x; c < K; c += kWG) dtb[c] = 0.f;
-    if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = 0.f;
-    return;
-  }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ void gate_low_rank_bwd_chunk(const GateParams& p, const ChunkInfo& ci, int h, int H,
+                                                        int wave, int lane, const T* sW, float A, float* dtb,
+                                                        int cidx, float (&s_tot)[4][K], float (&s_col)[4][K],
+                                                        float (&s_dA)[4]) {
   f32x4 z[K / 16];
-  low_rank_z<T, K, R>(p, ci, h, wave, lane, z);
-  const float A = expf(p.A_log[h]);
+  low_rank_z<T, K, R>(p, ci, h, wave, lane, sW, z);
   const int64_t base = ((int64_t)ci.start * H + h) * K;
   f32x4 suf[K / 16];
 #pragma unroll
@@ -367,11 +380,41 @@ __global__ __launch_bounds__(kWG) void gate_low_rank_bwd_kernel(GateParams p) {
   if (lane == 0) s_dA[wave] = dA;
   __syncthreads();
   for (int c = threadIdx.x; c < K; c += kWG) dtb[c] = ((s_col[0][c] + s_col[1][c]) + s_col[2][c]) + s_col[3][c];
-  if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = ((s_dA[0] + s_dA[1]) + s_dA[2]) + s_dA[3];
+  if (threadIdx.x == 0) p.dA_log_part[(int64_t)cidx * H + h] = ((s_dA[0] + s_dA[1]) + s_dA[2]) + s_dA[3];
+}
+
+template <typename T, int K, int R>
+__global__ __launch_bounds__(kWG) void gate_low_rank_bwd_kernel(GateParams p) {
+  __shared__ float s_tot[4][K];
+  __shared__ float s_col[4][K];
+  __shared__ float s_dA[4];
+  __shared__ __attribute__((aligned(16))) T sW[K * LrW<T, R>::LDW];
+  const int h = blockIdx.y, H = p.heads;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  stage_up_weight<T, K, R>(p, h, sW);
+  __syncthreads();
+  const float A = expf(p.A_log[h]);
+  // ci is the same for every thread, so every thread reaches every barrier;
+  // a chunk reads s_tot before its second barrier and s_col, s_dA after it,
+  // and the next chunk writes them only after reaching its own first barrier
+#pragma unroll 1
+  for (int i = 0; i < kLrChunks; ++i) {
+    const int cidx = blockIdx.x * kLrChunks + i;
+    if (cidx >= p.geom.num_chunks) break;
+    const ChunkInfo ci = chunk_info(p.geom, cidx);
+    float* dtb = p.ddt_bias_part + ((int64_t)cidx * H + h) * K;
+    if (ci.len <= 0) {  // an empty slot of the packed launch bound: zero partials
+      for (int c = threadIdx.x; c < K; c += kWG) dtb[c] = 0.f;
+      if (threadIdx.x == 0) p.dA_log_part[(int64_t)cidx * H + h] = 0.f;
+      continue;
+    }
+    gate_low_rank_bwd_chunk<T, K, R>(p, ci, h, H, wave, lane, sW, A, dtb, cidx, s_tot, s_col, s_dA);
+  }
 }
 
 int dispatch_low_rank(const GateParams& p, int num_chunks, bool backward, hipStream_t s) {
-  const dim3 grid(num_chunks, p.heads);
+  if (num_chunks <= 0) return 0;
+  const dim3 grid((num_chunks + kLrChunks - 1) / kLrChunks, p.heads);
 #define PKDA_LOW_RANK(TT, KK)                                                                       \
   do {                                                                                              \
     if (backward) {                                                                                 \
