@@ -258,45 +258,7 @@ template <typename E> struct Pad;
 template <> struct Pad<bf16_t> { static constexpr int v = PKDA_BF16_PAD; };
 template <> struct Pad<float> { static constexpr int v = 4; };
 
-// ----------------------------------------------------------------------------
-// Cooperative tile loads (256 threads).  Rows r >= nvalid load as zero, so a
-// partial chunk never touches the next document's tokens.
-// f(r, c, x) maps the loaded value (as float) before it is stored.
-// ----------------------------------------------------------------------------
-template <typename T, typename E, int NC, typename F>
-__device__ __forceinline__ void load_rows(E* lds, int ld, const T* g, int64_t gstride, int nrows, int nvalid, F f) {
-  constexpr int V = 4;  // elements per thread per step
-  constexpr int PER_ROW = NC / V;
-  for (int idx = threadIdx.x; idx < nrows * PER_ROW; idx += kWG) {
-    const int r = idx / PER_ROW;
-    const int c = (idx - r * PER_ROW) * V;
-    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (r < nvalid) x = load4(g + r * gstride + c);
-    E* dst = lds + r * ld + c;
-    dst[0] = to_e<E>(f(r, c + 0, x.x));
-    dst[1] = to_e<E>(f(r, c + 1, x.y));
-    dst[2] = to_e<E>(f(r, c + 2, x.z));
-    dst[3] = to_e<E>(f(r, c + 3, x.w));
-  }
-}
-
-// Same, stored transposed: lds[c*ld + r].
-template <typename T, typename E, int NC, typename F>
-__device__ __forceinline__ void load_rows_t(E* lds, int ld, const T* g, int64_t gstride, int nrows, int nvalid, F f) {
-  constexpr int V = 4;
-  constexpr int PER_ROW = NC / V;
-  for (int idx = threadIdx.x; idx < nrows * PER_ROW; idx += kWG) {
-    const int r = idx % nrows;  // consecutive threads walk rows: contiguous LDS writes
-    const int c = (idx / nrows) * V;
-    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (r < nvalid) x = load4(g + r * gstride + c);
-    lds[(c + 0) * ld + r] = to_e<E>(f(r, c + 0, x.x));
-    lds[(c + 1) * ld + r] = to_e<E>(f(r, c + 1, x.y));
-    lds[(c + 2) * ld + r] = to_e<E>(f(r, c + 2, x.z));
-    lds[(c + 3) * ld + r] = to_e<E>(f(r, c + 3, x.w));
-  }
-}
-
+// Identity value map for the tile loads below.
 struct Ident {
   __device__ __forceinline__ float operator()(int, int, float x) const { return x; }
 };
@@ -542,18 +504,6 @@ struct RowScale {
   __device__ __forceinline__ float operator()(int r, int, float x) const { return s[r] * x; }
 };
 
-// Store a [nrows x NC] row-major LDS/register-free tile back to global rows < nvalid.
-template <typename T, typename E, int NC>
-__device__ __forceinline__ void store_rows(T* g, int64_t gstride, const E* lds, int ld, int nvalid) {
-  constexpr int V = 4;
-  constexpr int PER_ROW = NC / V;
-  for (int idx = threadIdx.x; idx < nvalid * PER_ROW; idx += kWG) {
-    const int r = idx / PER_ROW;
-    const int c = (idx - r * PER_ROW) * V;
-    const E* src = lds + r * ld + c;
-    store4(g + r * gstride + c, make_float4(from_e<E>(src[0]), from_e<E>(src[1]), from_e<E>(src[2]), from_e<E>(src[3])));
-  }
-}
 
 // Store an accumulator tile (origin m0, n0) to global with row mask.  The
 // four lanes of a quad (16q + 4c + t, t = 0..3) hold columns 4c..4c+3 of rows
@@ -611,25 +561,10 @@ __device__ __forceinline__ void store_packed_rows(bf16_t* g, int64_t gstride, ui
   const int r = m0 + quad_row(lane);
   if (r < nvalid) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    u32x2* dst = reinterpret_cast<u32x2*>(g + r * gstride + n0 + quad_col(lane));
-#ifdef PKDA_NT_STORES
-    __builtin_nontemporal_store(u32x2{v0, v1}, dst);
-#else
-    *dst = u32x2{v0, v1};
-#endif
+    *reinterpret_cast<u32x2*>(g + r * gstride + n0 + quad_col(lane)) = u32x2{v0, v1};
   }
 }
 
-// Element-wise store of an accumulator tile (four scattered stores per lane).
-template <typename T>
-__device__ __forceinline__ void store_acc_elems(T* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
-                                                int lane) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = m0 + acc_row(lane, j);
-    if (r < nvalid) io<T>::store(g + r * gstride + n0 + acc_col(lane), acc[j]);
-  }
-}
 
 // Tile-major [D x D] state checkpoints: 16 x 16 tiles, each row-major and
 // contiguous (256 elements), tile (rt, ct) at element (rt * (D / 16) + ct) * 256.
@@ -677,12 +612,6 @@ __device__ __forceinline__ void store_acc_lds(E* lds, int ld, const f32x4& acc, 
   for (int j = 0; j < 4; ++j) lds[(m0 + acc_row(lane, j)) * ld + n0 + acc_col(lane)] = to_e<E>(acc[j]);
 }
 
-// Transposed: lds[(n0+col)*ld + m0+row]; the four rows of a lane are contiguous.
-template <typename E>
-__device__ __forceinline__ void store_acc_lds_t(E* lds, int ld, const f32x4& acc, int m0, int n0, int lane) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) lds[(n0 + acc_col(lane)) * ld + m0 + acc_row(lane, j)] = to_e<E>(acc[j]);
-}
 
 // out[i] = sum over p of part[p * n + i], p in [0, count): one 256-thread
 // workgroup per output element (grid = n); thread t adds the partials
@@ -705,16 +634,6 @@ __global__ __launch_bounds__(256) void sum_partials_tree_kernel(const float* par
 }
 }  // namespace
 
-// Deterministic row sums of an fp32 [64 x ncols] LDS tile into out[64]
-// (fixed summation order; one wave per 16 rows).
-__device__ __forceinline__ void row_sums_64(const float* lds, int ld, int ncols, float* out) {
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    float s = 0.f;
-    for (int c = 0; c < ncols; ++c) s += lds[tid * ld + c];
-    out[tid] = s;
-  }
-}
 
 // ----------------------------------------------------------------------------
 // Register-resident bf16 MFMA operands.  An accumulator tile X (lane 16q + i
