@@ -276,7 +276,9 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_bwd_kernel(B
 //   dBw  = T^T dW = -dBv S0^T
 //   dT   = dW Bw^T + dU Bv^T = dU (T^-1 U)^T   so   dAkk = -T^T dT T^T = -dBv U^T.
 // Phases (8 waves, wave (rb, ch): row block rb, column half ch):
-//   1  dBv = T^T dU -> dv;  dQg = dO S0^T;  dAqk = dO U^T -> P2
+//   1  dBv = T^T dU -> dv (BF16 with a per-head gate: the reverse pass has
+//      formed dBv and hands it over instead of dU);  dQg = dO S0^T;
+//      dAqk = dO U^T -> P2
 //   2  dBv to LDS over dU
 //   3  dBw = -dBv S0^T;  dAkk = -dBv U^T -> P1r = dAkk E, P1 = beta_t P1r
 //   4  dS_C replaces S0; sum(S0 * dS_C)
@@ -307,6 +309,8 @@ template <typename T, int D, typename OT, bool ALIAS>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   using L = FusedBwdLayout<T, D>;
   using E = T;
+  // BF16 with a per-head gate: the reverse pass hands over dBv = T^T dU in du
+  constexpr bool kDbv = implicit_w<T>();
   constexpr int HCT = D / 32;  // column tiles per wave of a [64 x D] output
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
@@ -355,13 +359,13 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
     rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
     rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
-    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
+    if (!kDbv) rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rH.load(hsrc);
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
     rV.store(sV, L::LD);
-    rT.store(sT, L::LDC);
+    if (!kDbv) rT.store(sT, L::LDC);
     rH.store(sH, L::LD);
   }
   __syncthreads();
@@ -382,7 +386,12 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     f32x4 acv = zero4();
-    mma_tile<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, C, lane);
+    if constexpr (kDbv) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acv[e] = from_e<E>(sdU[(r0 + acc_row(lane, e)) * L::LD + c]);
+    } else {
+      mma_tile<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, C, lane);
+    }
     dBv[j] = acv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) db[e] += acv[e] * from_e<E>(sV[(r0 + acc_row(lane, e)) * L::LD + c]);
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   rK.load(static_cast<const T*>(p.k) + row0 * D, gs, len);  // waits in registers until U's region frees
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
-    store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
+    if constexpr (!kDbv) store_acc_lds(sdBv, L::LD, dBv[j], r0, 16 * (ch * HCT + j), lane);
     if constexpr (vStage) {
       f32x4 dv;
 #pragma unroll
@@ -985,8 +994,9 @@ int set_smem(K kernel, int bytes) {
 // read-only tiles (Q, KW, K when it is not KW, Aqk, T, the dO slice, G and
 // beta) through a double-buffered LDS stage, two groups taking alternate
 // chunks.  Per chunk, with W = T diag(beta e^G) K never formed:
-//   dU  = Aqk^T dO + diag(e^{G_C - G}) (KW dS)            -> du
-//   dS <- e^{G_C} dS + Q^T diag(s e^G) dO - K^T diag(beta e^G) (T^T dU)
+//   dU  = Aqk^T dO + diag(e^{G_C - G}) (KW dS)
+//   dBv = T^T dU                                          -> du
+//   dS <- e^{G_C} dS + Q^T diag(s e^G) dO - K^T diag(beta e^G) dBv
 // ---------------------------------------------------------------------------
 template <int D, int BV, bool ALIAS>
 struct RrBwdLayout {
@@ -1153,13 +1163,10 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       mfma_bf16(dU[2], aa[4], dOB[1]);
       mfma_bf16(dU[3], aa[5], dOB[1]);
     }
-    T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) dU[rb][j] += exp_fast(gC - sG[16 * rb + q4 + j]) * KS[rb][j];
-      store_acc_global<T>(du_out, gs, dU[rb], 16 * rb, 0, clen, lane);
-    }
     // Z = T^T (-dU)   (T^T is upper triangular: row block rb needs k steps kt >= rb / 2)
     s16x8_t dOgB[2], dUnB[2];
 #pragma unroll
@@ -1188,6 +1195,10 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       mfma_bf16(Z[2], at[4], dUnB[1]);
       mfma_bf16(Z[3], at[5], dUnB[1]);
     }
+    // the per-chunk kernel needs dU only through dBv = T^T dU = -Z: hand it that
+    T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(du_out, gs, -Z[rb], 16 * rb, 0, clen, lane);
     // dS <- e^{G_C} dS + Q^T (s e^G dO) + K^T diag(beta e^G) Z
     s16x8_t ZB[2];
 #pragma unroll
