@@ -35,17 +35,19 @@ Printed as ONE JSON line:
                   (achieved GB/s).
 
 Algorithmic work per token-head (C = 64, dk = dv = d; the triangular solve,
-gate scans and elementwise work are not counted):
+gate scans and elementwise work are not counted).  The step's MFMA fraction
+uses the fixed convention 18d^2 + 30Cd = 540,672 flop at d = 128 (the
+forward as Akk, Aqk, w, u, Aqk U plus the three d^2 products, the backward
+twice that); each kernel's figure below is the work it performs:
   fwd intra   4Cd           (Akk, Aqk)
   fwd state   6d^2 + 4Cd    (K S, Q S, Kg^T U; U = T Y, Aqk U)
-  bwd state   6d^2 + 4Cd    (Kg dS, Qg^T dO, K^T (beta e^G T^T dU); T^T dU,
+  bwd state   6d^2 + 4Cd    (Kg dS, Qg^T dO, K^T (beta e^G dBv); dBv = T^T dU,
                              Aqk^T dO)
-  bwd chunk   6d^2 + 18Cd   (dO S^T, dU S^T, U dS^T; dO U^T; T^T dW, T^T dU,
-                             dW Bw^T, dU Bv^T; pairwise dq, dk, dkw products)
-  total       18d^2 + 30Cd = 540,672 flop at d = 128
-(BF16 with a per-head gate never forms W = T diag(beta e^G) K or u: the state
-passes contract with T instead, which moves 4Cd out of the intra kernel and
-2Cd into each state pass.)
+  bwd chunk   6d^2 + 16Cd   (dO S^T, dBv S^T, U dS^T; dO U^T, dBv U^T, dW-side
+                             T^T terms; pairwise dq, dk, dkw products)
+BF16 with a per-head gate never forms W = T diag(beta e^G) K or u: the state
+passes contract with T instead (18d^2 + 28Cd performed in all), and the
+reverse pass hands dBv = T^T dU to the per-chunk kernel.
 """
 
 from __future__ import annotations
@@ -77,13 +79,19 @@ WORKLOADS = {
 
 
 def stage_flops(D: int, C: int = CHUNK) -> dict[str, int]:
-    """Algorithmic flops per token-head of each kernel of the step."""
+    """Algorithmic flops per token-head that each kernel of the step performs."""
     return {
         "fwd_intra": 4 * C * D,
         "fwd_state": 6 * D * D + 4 * C * D,
         "bwd_state": 6 * D * D + 4 * C * D,
-        "bwd_chunk": 6 * D * D + 2 * C * D + 8 * C * D + 8 * C * D,
+        "bwd_chunk": 6 * D * D + 16 * C * D,
     }
+
+
+def step_flops_convention(D: int, C: int = CHUNK) -> int:
+    """The fixed algorithmic work of one fwd+bwd per token-head the MFMA
+    fraction is quoted on: F_fwd = 6 dk dv + 2C (3 dk + 2 dv), total 3 F_fwd."""
+    return 3 * (6 * D * D + 2 * C * (3 * D + 2 * D))
 
 
 # The kernel each timed stage launches for the default BF16, d = 128 workloads,
@@ -475,8 +483,7 @@ def bench_serve(dev: torch.device, reps: int = 10) -> dict:
     pool = torch.zeros(64, H, D, D, device=dev)
     slots = torch.randperm(64, generator=torch.Generator().manual_seed(1))[:B].to(torch.int32).to(dev)
     prefill_ms = timed(lambda: pkda_prefill_(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], pool, slots))
-    per_th = stage_flops(D)
-    flops = B * T * H * (per_th["fwd_intra"] + per_th["fwd_state"])
+    flops = B * T * H * step_flops_convention(D) // 3  # the forward of the convention
     del inp, pool
     N, P, Hd, Wc = 256, 512, 32, 4
     C = 3 * Hd * D
@@ -665,7 +672,7 @@ def main() -> None:
             print(f"[bench] graph capture failed ({exc}); reporting eager timing", file=sys.stderr, flush=True)
     per_th = stage_flops(w["D"])
     token_heads = ntok * w["H"]
-    step_flops = token_heads * sum(per_th.values())
+    step_flops = token_heads * step_flops_convention(w["D"])
     stage_ms = time_stages(inp, w, args.steps)
     print(f"[bench] stages (ms): {json.dumps({k: round(v, 4) for k, v in stage_ms.items()})}",
           file=sys.stderr, flush=True)
