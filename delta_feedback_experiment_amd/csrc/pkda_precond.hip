@@ -18,10 +18,22 @@
 //   dcenter     = -sum_{t,c} dkw_t k_t f'(r_t)
 //   dA_0        = e^{g_atk_first} lambda_first
 //
-// One workgroup per (document, head), one thread per key channel.  The
-// forward checkpoints A at every chunk start; the backward walks the chunks in
-// reverse, recomputes the chunk's A_t into LDS, runs the reverse recurrence
-// and reduces the per-token channel sums from LDS in a fixed order.
+// Both recurrences are linear with inputs known up front (lambda's input
+// only needs the forward's A), so each runs chunk-parallel in three launches
+// instead of one sequential walk per (document, head):
+//   1. per (chunk, head): the chunk's end value from a zero start
+//      (A forward, lambda in reverse);
+//   2. per (document, head): the scan over the document's chunks,
+//      x_out = exp(sum of the chunk's g_atk) x_in + local end, which leaves
+//      the value entering each chunk in place of its local end
+//      (a_chunk: A entering the chunk; lam_chunk: lambda entering it from
+//      the right);
+//   3. per (chunk, head): the chunk again from its entering value, writing
+//      kw (forward) or the gradients (backward).
+// The forward's third launch and both backward chunk launches recompute A
+// inside the chunk from a_chunk with the same arithmetic, so the backward
+// sees exactly the A the forward squashed.  Channel sums (dg_atk, dbeta_atk,
+// dcenter) reduce in a fixed order: lanes of a 16-lane row, then rows.
 #include "pkda_chunk_common.h"
 
 namespace pkda {
@@ -47,122 +59,329 @@ struct PrecondParams {
   float* dA0;
   const float* dA_T;
   const int32_t* slot;  // forward: document -> A-state row, or null
+  float* lam_chunk;
 };
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
 
-template <typename T, int D>
-__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_fwd_kernel(PrecondParams p) {
-  const DocSlot ds = doc_slot(p.geom, p.H, 1);
-  const int n = ds.n, h = ds.h, c = threadIdx.x;
-  if (c >= D) return;
-  const int H = p.H;
-  int first, count, dstart, dlen;
-  doc_chunks(p.geom, n, first, count, dstart, dlen);
-  const int64_t sh = (int64_t)(p.slot ? p.slot[n] : n) * H + h;  // state row
-  float a = p.a0 ? p.a0[sh * D + c] : 0.f;
-  const float center = p.center[h];
-  const T* k = static_cast<const T*>(p.k);
-  T* kw = static_cast<T*>(p.kw);
-  for (int jc = 0; jc < count; ++jc) {
-    if (p.a_chunk) p.a_chunk[((int64_t)(first + jc) * H + h) * D + c] = a;
-    const int t0 = dstart + jc * C;
-    const int len = min(C, dlen - jc * C);
-    for (int t = 0; t < len; ++t) {
-      const int64_t th = (int64_t)(t0 + t) * H + h;
-      const float kc = io<T>::load(k + th * D + c);
-      a = expf(p.g_atk[th]) * a + p.beta_atk[th] * (kc * kc);
-      const float r = logf(a + p.eps) - center;
-      io<T>::store(kw + th * D + c, kc * expf(-p.log_x * (r / (1.f + fabsf(r)))));
-    }
-  }
-  if (p.aT) p.aT[sh * D + c] = a;
+// Per-(chunk, head) launches: workgroup b takes chunk b / H of head b % H, so
+// neighbouring workgroups read neighbouring head slices of the same tokens.
+struct ChunkHead {
+  int j, h;
+};
+__device__ __forceinline__ ChunkHead chunk_head(int H) {
+  ChunkHead ch;
+  ch.j = blockIdx.x / H;
+  ch.h = blockIdx.x - ch.j * H;
+  return ch;
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_bwd_kernel(PrecondParams p) {
+// exp(sum of g_atk over the chunk) for chunks j0 .. j0 + nb - 1 of a document
+// (first token dstart, dlen tokens), chunk j0 + i at s[i]; thread i sums its
+// chunk's tokens in order.
+__device__ __forceinline__ void chunk_decays(const PrecondParams& p, int h, int dstart, int dlen, int j0, int nb,
+                                             float* s) {
+  const int i = threadIdx.x;
+  if (i < nb) {
+    const int t0 = dstart + (j0 + i) * C;
+    const int len = min(C, dlen - (j0 + i) * C);
+    float g = 0.f;
+    for (int t = 0; t < len; ++t) g += p.g_atk[(int64_t)(t0 + t) * p.H + h];
+    s[i] = expf(g);
+  }
+}
+
+// Chunk-level scan of one (document, head): buf holds, per chunk of the
+// document (row (chunk * H + h) * D + channel), the chunk's local end value;
+// it is replaced by the value entering the chunk, walking the chunks forward
+// (REVERSE = false) or backward.  Returns the value after the last chunk
+// walked.
+template <int D, bool REVERSE>
+__device__ __forceinline__ float chunk_scan(const PrecondParams& p, float* buf, int h, int first, int count,
+                                            int dstart, int dlen, float x, float* sDecay) {
   constexpr int NT = PrecondThreads<D>::v;
-  constexpr int LDA = D + 1;
-  // sA holds A_t of the current chunk; the reverse pass overwrites row t with
-  // lambda_t e^{g_atk_t} A_{t-1} once rows t and t-1 have been read.
-  extern __shared__ __attribute__((aligned(16))) float smem_f[];
-  float* sA = smem_f;              // [C][LDA]
-  float* sCb = sA + C * LDA;       // [C][LDA]  lambda_t k_t^2
-  float* sRed = sCb + C * LDA;     // [NT]
+  const int c = threadIdx.x;
+  const int64_t step = (int64_t)p.H * D;
+  for (int b = 0; b < count; b += NT) {
+    const int nb = min(NT, count - b);
+    const int j0 = REVERSE ? count - b - nb : b;  // first chunk of this block
+    __syncthreads();
+    chunk_decays(p, h, dstart, dlen, j0, nb, sDecay);
+    __syncthreads();
+    if (c < D) {
+      float* base = buf + ((int64_t)(first + j0) * p.H + h) * D + c;
+      for (int i0 = 0; i0 < nb; i0 += 8) {
+        float l[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = REVERSE ? nb - 1 - (i0 + u) : i0 + u;
+          l[u] = i0 + u < nb ? base[i * step] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (i0 + u < nb) {
+            const int i = REVERSE ? nb - 1 - (i0 + u) : i0 + u;
+            base[i * step] = x;
+            x = sDecay[i] * x + l[u];
+          }
+        }
+      }
+    }
+  }
+  return x;
+}
+
+// Forward launches 1 (APPLY = false: local end A from zero into a_chunk) and
+// 3 (APPLY: A from a_chunk, kw out).  The chunk runs in sub-blocks of 16
+// tokens whose k rows load before their chain runs; a short chunk
+// (FULL = false) clamps its loads to its last token and leaves the state
+// unchanged past it, so no load sits behind a branch.
+template <typename T, int D, bool APPLY, bool FULL>
+__device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j, int h, int start, int len) {
+  constexpr int G = 16;
+  const int H = p.H, c = threadIdx.x;
+  const T* __restrict__ k = static_cast<const T*>(p.k);
+  T* __restrict__ kw = static_cast<T*>(p.kw);
+  const float* __restrict__ g_atk = p.g_atk;
+  const float* __restrict__ beta_atk = p.beta_atk;
+  float* slot = p.a_chunk + ((int64_t)j * H + h) * D + c;
+  float a = APPLY ? *slot : 0.f;
+  const float center = APPLY ? p.center[h] : 0.f;
+  auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
+#pragma unroll 1
+  for (int g0 = 0; g0 < C; g0 += G) {
+    float kc[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) kc[u] = io<T>::load(k + tok(g0 + u) * D + c);
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int t = g0 + u;
+      const int64_t th = tok(t);
+      const float an = expf(g_atk[th]) * a + beta_atk[th] * (kc[u] * kc[u]);
+      a = (FULL || t < len) ? an : a;
+      if (APPLY) {
+        const float r = logf(a + p.eps) - center;
+        const float w = kc[u] * expf(-p.log_x * (r / (1.f + fabsf(r))));
+        if (FULL || t < len) io<T>::store(kw + th * D + c, w);
+      }
+    }
+  }
+  if (!APPLY) *slot = a;
+}
+
+template <typename T, int D, bool APPLY>
+__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_fwd_chunk_kernel(PrecondParams p) {
+  const ChunkHead ch = chunk_head(p.H);
+  if (threadIdx.x >= D) return;
+  const ChunkInfo ci = chunk_info(p.geom, ch.j);
+  if (ci.len == C)
+    precond_fwd_chunk<T, D, APPLY, true>(p, ch.j, ch.h, ci.start, C);
+  else if (ci.len > 0)
+    precond_fwd_chunk<T, D, APPLY, false>(p, ch.j, ch.h, ci.start, ci.len);
+}
+
+// Forward launch 2: per (document, head), A entering every chunk and the
+// final A.
+template <int D>
+__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_fwd_scan_kernel(PrecondParams p) {
+  __shared__ float sDecay[PrecondThreads<D>::v];
   const DocSlot ds = doc_slot(p.geom, p.H, 1);
   const int n = ds.n, h = ds.h, c = threadIdx.x;
-  const bool active = c < D;
-  const int H = p.H;
   int first, count, dstart, dlen;
   doc_chunks(p.geom, n, first, count, dstart, dlen);
-  const int64_t sh = (int64_t)n * H + h;
-  const float center = p.center[h];
-  const T* k = static_cast<const T*>(p.k);
-  float lam = (active && p.dA_T) ? p.dA_T[sh * D + c] : 0.f;  // dL/dA after the last token
-  float dcen = 0.f;
-  for (int jc = count - 1; jc >= 0; --jc) {
-    const int t0 = dstart + jc * C;
-    const int len = min(C, dlen - jc * C);
-    const float a_in = active ? p.a_chunk[((int64_t)(first + jc) * H + h) * D + c] : 0.f;
-    if (active) {
-      float a = a_in;
-      for (int t = 0; t < len; ++t) {
-        const int64_t th = (int64_t)(t0 + t) * H + h;
-        const float kc = io<T>::load(k + th * D + c);
-        a = expf(p.g_atk[th]) * a + p.beta_atk[th] * (kc * kc);
-        sA[t * LDA + c] = a;
-      }
-      for (int t = len - 1; t >= 0; --t) {
-        const int64_t th = (int64_t)(t0 + t) * H + h;
-        const float kc = io<T>::load(k + th * D + c);
-        const float a = sA[t * LDA + c];
-        const float a_prev = t > 0 ? sA[(t - 1) * LDA + c] : a_in;
-        const float r = logf(a + p.eps) - center;
-        const float den = 1.f + fabsf(r);
-        const float f = expf(-p.log_x * (r / den));
-        const float dkw = p.dkw[th * D + c];
-        const float dr = dkw * kc * f * (-p.log_x) / (den * den);
-        dcen -= dr;
-        lam += dr / (a + p.eps);
-        const float ba = p.beta_atk[th];
-        p.dk[th * D + c] += dkw * f + 2.f * ba * kc * lam;
-        const float eg = expf(p.g_atk[th]);
-        sA[t * LDA + c] = lam * eg * a_prev;
-        sCb[t * LDA + c] = lam * kc * kc;
-        lam *= eg;  // carry to A_{t-1}
-      }
+  const int64_t sh = (int64_t)(p.slot ? p.slot[n] : n) * p.H + h;  // state row
+  float a = (c < D && p.a0) ? p.a0[sh * D + c] : 0.f;
+  a = chunk_scan<D, false>(p, p.a_chunk, h, first, count, dstart, dlen, a, sDecay);
+  if (c < D && p.aT) p.aT[sh * D + c] = a;
+}
+
+// Sum of v over each 16-lane row, in every lane of the row (fixed order).
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)); // half-row mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)); // row mirror
+  return v;
+}
+
+// Backward launches 1 (APPLY = false: lambda's local value before the chunk
+// from a zero start after it, into lam_chunk) and 3 (APPLY: from the lambda
+// entering the chunk, the gradients).  The chunk is walked in reverse in
+// sub-blocks of 16 tokens: a first forward pass keeps A at each sub-block's
+// start, and each sub-block recomputes its 16 A_t from there (the same
+// arithmetic, so the same values) with its k, dkw and dk rows in registers.
+// Loads clamp as in the forward.  The per-token channel sums leave each
+// 16-lane row in lane (t mod 16) of that row (register t / 16), then cross
+// the rows through LDS.
+template <typename T, int D, bool APPLY, bool FULL>
+__device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j, int h, int start, int len,
+                                                  float (*sRow)[C][PrecondThreads<D>::v / 16 + 1], float* sCen) {
+  constexpr int NR = PrecondThreads<D>::v / 16;  // 16-lane rows
+  constexpr int G = 16;                          // tokens per sub-block
+  constexpr int NB = C / G;
+  const int H = p.H, c = threadIdx.x, lane16 = c & 15;
+  const bool active = c < D;
+  const int cc = active ? c : 0;  // channel the lane reads (idle lanes mirror channel 0, contribute 0)
+  const T* __restrict__ k = static_cast<const T*>(p.k);
+  const float* __restrict__ dkw_p = p.dkw;
+  float* __restrict__ dk_p = p.dk;
+  const float* __restrict__ g_atk = p.g_atk;
+  const float* __restrict__ beta_atk = p.beta_atk;
+  const int64_t row = ((int64_t)j * H + h) * D + cc;
+  const float a_in = active ? p.a_chunk[row] : 0.f;
+  float lam = (APPLY && active) ? p.lam_chunk[row] : 0.f;
+  const float center = p.center[h], lx = p.log_x, eps = p.eps;
+  auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
+  auto step = [&](int t, float a, float kc) -> float {
+    const int64_t th = tok(t);
+    const float an = expf(g_atk[th]) * a + beta_atk[th] * (kc * kc);
+    return (FULL || t < len) ? an : a;
+  };
+  // Register arrays indexed by the (rolled) sub-block number go through
+  // compile-time selects so they stay in registers.
+  float a_blk[NB];  // A entering each sub-block
+  {
+    float a = a_in;
+#pragma unroll 1
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int q = 0; q < NB; ++q) a_blk[q] = q == b ? a : a_blk[q];
+      float kb[G];
+#pragma unroll
+      for (int u = 0; u < G; ++u) kb[u] = io<T>::load(k + tok(b * G + u) * D + cc);
+#pragma unroll
+      for (int u = 0; u < G; ++u) a = step(b * G + u, a, active ? kb[u] : 0.f);
     }
-    __syncthreads();
-    // per-token channel sums, fixed order
-    for (int t = threadIdx.x; t < len; t += NT) {
-      float sg = 0.f, sb = 0.f;
-      for (int j = 0; j < D; ++j) {
-        sg += sA[t * LDA + j];
-        sb += sCb[t * LDA + j];
-      }
-      const int64_t th = (int64_t)(t0 + t) * H + h;
-      p.dg_atk[th] = sg;
-      p.dbeta_atk[th] = sb;
-    }
-    __syncthreads();
   }
-  if (active && p.dA0) p.dA0[sh * D + c] = lam;
-  sRed[threadIdx.x] = active ? dcen : 0.f;
+  float dcen = 0.f;
+  float sg[NB], sb[NB];
+#pragma unroll
+  for (int q = 0; q < NB; ++q) sg[q] = sb[q] = 0.f;
+#pragma unroll 1
+  for (int b = NB - 1; b >= 0; --b) {
+    const int g0 = b * G;
+    float a_b = a_blk[0];
+#pragma unroll
+    for (int q = 1; q < NB; ++q) a_b = q == b ? a_blk[q] : a_b;
+    float rk[G], ra[G], rdkw[G], rdk[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      rk[u] = io<T>::load(k + tok(g0 + u) * D + cc);
+      rdkw[u] = dkw_p[tok(g0 + u) * D + cc];
+      if (APPLY) rdk[u] = dk_p[tok(g0 + u) * D + cc];
+    }
+    {
+      float a = a_b;
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        rk[u] = active ? rk[u] : 0.f;
+        a = step(g0 + u, a, rk[u]);
+        ra[u] = a;
+      }
+    }
+#pragma unroll
+    for (int u = G - 1; u >= 0; --u) {
+      const int t = g0 + u;
+      const bool in = FULL || t < len;
+      const int64_t th = tok(t);
+      const float kc = rk[u], at = ra[u];
+      const float eg = expf(g_atk[th]);
+      const float r = logf(at + eps) - center;
+      const float den = 1.f + fabsf(r);
+      const float f = expf(-lx * (r / den));
+      const float dkw = active && in ? rdkw[u] : 0.f;
+      const float dr = dkw * kc * f * (-lx) / (den * den);
+      const float lam_t = lam + dr / (at + eps);
+      if (APPLY) {
+        dcen -= dr;
+        if (active && in) dk_p[th * D + cc] = rdk[u] + (dkw * f + 2.f * beta_atk[th] * kc * lam_t);
+        const float a_prev = u > 0 ? ra[u - 1] : a_b;
+        const float vg = row_sum16(lam_t * eg * a_prev);
+        const float vb = row_sum16(lam_t * kc * kc);
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+          const bool mine = q == b && lane16 == u;
+          sg[q] = mine ? vg : sg[q];
+          sb[q] = mine ? vb : sb[q];
+        }
+      }
+      lam = in ? lam_t * eg : lam;  // carry to A_{t-1}
+    }
+  }
+  if (!APPLY) {
+    if (active) p.lam_chunk[row] = lam;
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    sRow[0][16 * q + lane16][c >> 4] = sg[q];
+    sRow[1][16 * q + lane16][c >> 4] = sb[q];
+  }
+  dcen = row_sum16(dcen);
+  if (lane16 == 0) sCen[c >> 4] = dcen;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-    for (int j = 0; j < NT; ++j) s += sRed[j];
-    p.dcenter_part[sh] = s;
+  if (c < len) {
+    float tg = 0.f, tb = 0.f;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      tg += sRow[0][c][r];
+      tb += sRow[1][c][r];
+    }
+    const int64_t th = (int64_t)(start + c) * H + h;
+    p.dg_atk[th] = tg;
+    p.dbeta_atk[th] = tb;
+  }
+  if (c == 0) {
+    float tot = 0.f;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) tot += sCen[r];
+    p.dcenter_part[(int64_t)j * H + h] = tot;
   }
 }
 
-// dcenter[h] = sum_n part[n, h], fixed order.
-__global__ void precond_dcenter_kernel(const float* part, int N, int H, float* out) {
-  const int h = blockIdx.x * blockDim.x + threadIdx.x;
-  if (h >= H) return;
-  float s = 0.f;
-  for (int n = 0; n < N; ++n) s += part[(int64_t)n * H + h];
-  out[h] = s;
+template <typename T, int D, bool APPLY>
+__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_bwd_chunk_kernel(PrecondParams p) {
+  __shared__ float sRow[2][C][PrecondThreads<D>::v / 16 + 1];
+  __shared__ float sCen[PrecondThreads<D>::v / 16];
+  const ChunkHead ch = chunk_head(p.H);
+  const ChunkInfo ci = chunk_info(p.geom, ch.j);
+  if (ci.len == C)
+    precond_bwd_chunk<T, D, APPLY, true>(p, ch.j, ch.h, ci.start, C, sRow, sCen);
+  else if (ci.len > 0)
+    precond_bwd_chunk<T, D, APPLY, false>(p, ch.j, ch.h, ci.start, ci.len, sRow, sCen);
+  else if (APPLY && threadIdx.x == 0)
+    p.dcenter_part[(int64_t)ch.j * p.H + ch.h] = 0.f;
+}
+
+// Backward launch 2: per (document, head), lambda entering every chunk from
+// the right, walking the chunks last to first, and dA_0.
+template <int D>
+__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_bwd_scan_kernel(PrecondParams p) {
+  __shared__ float sDecay[PrecondThreads<D>::v];
+  const DocSlot ds = doc_slot(p.geom, p.H, 1);
+  const int n = ds.n, h = ds.h, c = threadIdx.x;
+  int first, count, dstart, dlen;
+  doc_chunks(p.geom, n, first, count, dstart, dlen);
+  const int64_t sh = (int64_t)n * p.H + h;
+  float lam = (c < D && p.dA_T) ? p.dA_T[sh * D + c] : 0.f;  // dL/dA after the last token
+  lam = chunk_scan<D, true>(p, p.lam_chunk, h, first, count, dstart, dlen, lam, sDecay);
+  if (c < D && p.dA0) p.dA0[sh * D + c] = lam;
+}
+
+// dcenter[h] = sum over the chunk partials part[j, h], fixed order: 256
+// strided partial sums, then a tree.
+__global__ __launch_bounds__(256) void precond_dcenter_kernel(const float* part, int M, int H, float* out) {
+  __shared__ float s[256];
+  const int h = blockIdx.x, i = threadIdx.x;
+  float acc = 0.f;
+  for (int j = i; j < M; j += 256) acc += part[(int64_t)j * H + h];
+  s[i] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (i < w) s[i] += s[i + w];
+    __syncthreads();
+  }
+  if (i == 0) out[h] = s[0];
 }
 
 int precond_common(const pkda_precond_args* a, PrecondParams& p) {
@@ -195,6 +414,7 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
   p.dA0 = a->dA0;
   p.dA_T = a->dA_T;
   p.slot = a->slot_idx;
+  p.lam_chunk = a->lam_chunk;
   PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed A states need pool_size > 0");
   return 0;
 }
@@ -202,19 +422,17 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
 template <typename T, int D>
 int launch_precond(const PrecondParams& p, bool backward, hipStream_t s) {
   constexpr int NT = PrecondThreads<D>::v;
-  const dim3 grid = doc_grid(p.geom.num_seqs, p.H, 1);
+  const dim3 chunks((unsigned)((int64_t)p.geom.num_chunks * p.H));
+  const dim3 docs = doc_grid(p.geom.num_seqs, p.H, 1);
+  const bool any = p.geom.num_chunks > 0;
   if (backward) {
-    const int bytes = (2 * C * (D + 1) + NT) * (int)sizeof(float);
-    auto kern = precond_bwd_kernel<T, D>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) {
-      set_error("hipFuncSetAttribute(%d bytes): %s", bytes, hipGetErrorString(e));
-      return static_cast<int>(e);
-    }
-    hipLaunchKernelGGL(kern, grid, dim3(NT), bytes, s, p);
+    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, false>), chunks, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((precond_bwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, true>), chunks, dim3(NT), 0, s, p);
   } else {
-    hipLaunchKernelGGL((precond_fwd_kernel<T, D>), grid, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, false>), chunks, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((precond_fwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, true>), chunks, dim3(NT), 0, s, p);
   }
   return launch_status(backward ? "pkda_precond_bwd" : "pkda_precond_fwd");
 }
@@ -237,7 +455,7 @@ extern "C" int pkda_precond_fwd(const pkda_precond_args* a, void* stream) {
   PrecondParams p;
   if (int st = precond_common(a, p)) return st;
   if (a->num_seqs == 0) return 0;
-  PKDA_REQUIRE(a->kw, PKDA_EINVAL, "preconditioner forward needs kw");
+  PKDA_REQUIRE(a->kw && a->a_chunk, PKDA_EINVAL, "preconditioner forward needs kw and a_chunk");
   hipStream_t s = static_cast<hipStream_t>(stream);
   return a->dtype == PKDA_F32 ? dispatch_precond<float>(p, a->head_dim, false, s)
                               : dispatch_precond<bf16_t>(p, a->head_dim, false, s);
@@ -250,13 +468,13 @@ extern "C" int pkda_precond_bwd(const pkda_precond_args* a, void* stream) {
   PKDA_REQUIRE(a->dcenter && a->dcenter_part, PKDA_EINVAL, "preconditioner backward needs dcenter buffers");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->num_seqs > 0) {
-    PKDA_REQUIRE(a->a_chunk && a->dkw && a->dk && a->dg_atk && a->dbeta_atk, PKDA_EINVAL,
-                 "preconditioner backward needs a_chunk, dkw, dk, dg_atk and dbeta_atk");
+    PKDA_REQUIRE(a->a_chunk && a->lam_chunk && a->dkw && a->dk && a->dg_atk && a->dbeta_atk, PKDA_EINVAL,
+                 "preconditioner backward needs a_chunk, lam_chunk, dkw, dk, dg_atk and dbeta_atk");
     const int st = a->dtype == PKDA_F32 ? dispatch_precond<float>(p, a->head_dim, true, s)
                                         : dispatch_precond<bf16_t>(p, a->head_dim, true, s);
     if (st) return st;
   }
-  hipLaunchKernelGGL(precond_dcenter_kernel, dim3((a->heads + 63) / 64), dim3(64), 0, s, a->dcenter_part,
-                     a->num_seqs, a->heads, a->dcenter);
+  hipLaunchKernelGGL(precond_dcenter_kernel, dim3(a->heads), dim3(256), 0, s, a->dcenter_part,
+                     a->num_seqs > 0 ? a->num_chunks : 0, a->heads, a->dcenter);
   return launch_status("pkda_precond_bwd(dcenter)");
 }

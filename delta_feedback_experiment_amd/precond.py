@@ -5,7 +5,9 @@ The forward turns the raw key into the write key
 ``A_t = exp(g_atk_t) A_{t-1} + beta_atk_t k_t^2``
 (``delta_feedback_experiment/pkda.py:392-398``), checkpointing ``A`` at every
 chunk start; the backward is its reverse scan.  Both run in
-``libpkda_gfx950.so`` (``pkda_precond_fwd`` / ``pkda_precond_bwd``).
+``libpkda_gfx950.so`` (``pkda_precond_fwd`` / ``pkda_precond_bwd``),
+chunk-parallel: local chunk ends, a scan over each document's chunks, then
+the chunks again from their entering values.
 """
 
 from __future__ import annotations
@@ -76,7 +78,8 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
     f32 = dict(device=dev, dtype=torch.float32)
     dg_atk = torch.empty(plan.num_tokens, H, **f32)
     dbeta_atk = torch.empty(plan.num_tokens, H, **f32)
-    dcenter_part = torch.empty(max(N, 1), H, **f32)
+    dcenter_part = torch.empty(max(plan.num_chunks, 1), H, **f32)
+    lam_chunk = torch.empty(plan.num_chunks, H, K, **f32)
     dcenter = torch.empty(H, **f32)
     dA0 = torch.empty(N, H, K, **f32) if want_dA0 else None
     dAT = None if dA_T is None else _f32(dA_T)
@@ -86,7 +89,7 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
         squash_x=float(x), squash_eps=float(eps), a_chunk=_ptr(state.a_chunk), num_chunks=plan.num_chunks,
         dkw=_ptr(dkw), dk=_ptr(dk), dg_atk=_ptr(dg_atk), dbeta_atk=_ptr(dbeta_atk),
         dcenter_part=_ptr(dcenter_part), dcenter=_ptr(dcenter), dA0=_ptr(dA0), dA_T=_ptr(dAT),
-        table=_ptr(plan.table),
+        table=_ptr(plan.table), lam_chunk=_ptr(lam_chunk),
     )
     _lib.call("pkda_precond_bwd", args, _stream(dev))
     return dg_atk, dbeta_atk, dcenter, dA0

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 4
+#define PKDA_ABI_VERSION 5
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -211,9 +211,13 @@ int pkda_gate_bwd(const pkda_gate_args* args, void* stream);
  *             per-document partials dcenter_part [num_seqs, H], summed in a
  *             fixed order), dA0 [N,H,K] when dA0 != NULL; dA_T optional
  *             gradient of the final A.
- * One workgroup per (document, head) scans its key channels in parallel; the
- * backward recomputes A inside each chunk from a_chunk.  Packed documents
- * take the pkda_chunk_table `table` (NULL for equal rows).
+ * Both scans run chunk-parallel: per (chunk, head) the chunk's local end
+ * value, per (document, head) a scan over the document's chunks, per
+ * (chunk, head) the chunk again from the value entering it.  a_chunk is that
+ * scan's buffer in the forward (A entering each chunk on return) and
+ * lam_chunk in the backward; the backward recomputes A inside each chunk
+ * from a_chunk.  Packed documents take the pkda_chunk_table `table` (NULL
+ * for equal rows).
  * ------------------------------------------------------------------------- */
 typedef struct pkda_precond_args {
   int32_t struct_size;
@@ -234,7 +238,7 @@ typedef struct pkda_precond_args {
   float* dk;                     /* backward: accumulated into */
   float* dg_atk;
   float* dbeta_atk;
-  float* dcenter_part;           /* [num_seqs, H] workspace */
+  float* dcenter_part;           /* [num_chunks, H] workspace */
   float* dcenter;                /* [H] */
   float* dA0;                    /* [N,H,K] or NULL */
   const float* dA_T;             /* [N,H,K] or NULL */
@@ -243,6 +247,7 @@ typedef struct pkda_precond_args {
    * (initial_A_state / final_A_state are then [pool_size, H, K]) */
   const int32_t* slot_idx;
   int64_t pool_size;
+  float* lam_chunk;              /* backward workspace [num_chunks, H, K] */
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
