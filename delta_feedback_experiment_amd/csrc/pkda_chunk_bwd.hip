@@ -616,6 +616,10 @@ struct FusedBwdPcLayout {
   static constexpr int off_kg = off_hd + D * 4;         // [4][D]
   static constexpr int off_red = off_kg + 4 * D * 4;    // [kFW]
   static constexpr int bytes = off_red + kFW * 4;
+  // phase 4, over dU: the diagonal 16 x 16 blocks of dAkk and dAqk transposed, [4][16 x][16 t] each
+  static constexpr int off_P1T = off_dU;
+  static constexpr int off_P2T = off_P1T + 4 * 256 * (int)sizeof(T);
+  static_assert(8 * 256 * (int)sizeof(T) <= RT, "transposed blocks fit the dU region");
   static constexpr int G_BYTES = C * LDG * 4;
   static constexpr int off_KW = D == 2 * C ? off_H + C * LD * (int)sizeof(T) : off_U + G_BYTES;
   static_assert(G_BYTES <= off_dO, "G fits the U..X region");
@@ -654,6 +658,8 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   E* sQ = sH;
   E* sKW = reinterpret_cast<E*>(smem + L::off_KW);
   E* sP2 = reinterpret_cast<E*>(smem + L::off_P2);
+  E* sP1T = reinterpret_cast<E*>(smem + L::off_P1T);
+  E* sP2T = reinterpret_cast<E*>(smem + L::off_P2T);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
   float* sHD = reinterpret_cast<float*>(smem + L::off_hd);
   float* sKG = reinterpret_cast<float*>(smem + L::off_kg);
@@ -839,6 +845,13 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         *reinterpret_cast<const float4*>(gg + (int64_t)min(r, len - 1) * gs + c);
   }
   if (!p.kw_is_k && D != 2 * C) load_tile<kFW, C, D>(sKW, L::LD, kwg, gs, len, Ident());
+  if (ch == 0) {  // this row block's diagonal blocks, transposed (dU is dead)
+    for (int i = lane; i < 256; i += 64) {
+      const int xo = i >> 4, to = i & 15;
+      sP1T[(16 * rb + xo) * 16 + to] = sP1r[(r0 + to) * L::LDC + r0 + xo];
+      sP2T[(16 * rb + xo) * 16 + to] = sP2[(r0 + to) * L::LDC + r0 + xo];
+    }
+  }
   __syncthreads();
   const E* sKWr = p.kw_is_k ? sK : sKW;
   const int rlo = r0 - 1;   // last row before this row block (G[-1] = 0)
@@ -899,24 +912,50 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       awA[e] *= exp_fast(grhi_c - gr[e]);
       awP[e] *= exp_fast(grhi_c - gr[e]);
     }
-    for (int xo = 0; xo < 16; ++xo) {
-      const int x = r0 + xo;
-      const float gx = sG[x * L::LDG + c];
-      const float kwx = from_e<E>(sKWr[x * L::LD + c]);
-      const float kx = from_e<E>(sK[x * L::LD + c]);
-      const float qx = from_e<E>(sQ[x * L::LD + c]);
+    // Pairs inside the row block, exactly: e^{G[a]-G[b]} (a >= b) is the
+    // running product of the per-token decays e^{G[y]-G[y-1]} (each <= 1)
+    // from b + 1 to a, started at 1 on the diagonal and 0 past it.  dAkk and
+    // dAqk are zero off their triangles, so no pair needs a mask.
+    {
+      const int rq = 4 * (lane >> 4);  // this lane's rows r0 + rq + e
+      float ex[4] = {0.f, 0.f, 0.f, 0.f};
+      float gnext = 0.f;
+#pragma unroll 1
+      for (int xo = 15; xo >= 0; --xo) {  // x as the column of rows r > x
+        const int x = r0 + xo;
+        const float gx = sG[x * L::LDG + c];
+        const float d = xo < 15 ? exp_fast(gnext - gx) : 0.f;  // decay of token x + 1
+        gnext = gx;
+        const float kwx = from_e<E>(sKWr[x * L::LD + c]);
+        float p1[4], p2[4];
+        lds4(sP1T + (16 * rb + xo) * 16 + rq, p1);
+        lds4(sP2T + (16 * rb + xo) * 16 + rq, p2);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = r0 + acc_row(lane, e);
-        if (x <= r) {  // x as the column of row r
-          const float ex = exp_fast(gr[e] - gx);
-          if (x < r) akA[e] += from_e<E>(sP1r[r * L::LDC + x]) * kwx * ex;
-          aqP[e] += from_e<E>(sP2[r * L::LDC + x]) * kwx * ex;
+        for (int e = 0; e < 4; ++e) {
+          ex[e] = xo == rq + e ? 1.f : ex[e] * d;
+          akA[e] += p1[e] * kwx * ex[e];
+          aqP[e] += p2[e] * kwx * ex[e];
         }
-        if (x >= r) {  // x as the row, r as the column
-          const float ex = exp_fast(gx - gr[e]);
-          if (x > r) awA[e] += sBeta[x] * from_e<E>(sP1r[x * L::LDC + r]) * kx * ex;
-          awP[e] += from_e<E>(sP2[x * L::LDC + r]) * qx * ex;
+      }
+      float gprev = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ex[e] = 0.f;
+#pragma unroll 1
+      for (int xo = 0; xo < 16; ++xo) {  // x as the row of columns r < x
+        const int x = r0 + xo;
+        const float gx = sG[x * L::LDG + c];
+        const float d = xo > 0 ? exp_fast(gx - gprev) : 0.f;  // decay of token x
+        gprev = gx;
+        const float kx = sBeta[x] * from_e<E>(sK[x * L::LD + c]);
+        const float qx = from_e<E>(sQ[x * L::LD + c]);
+        float p1[4], p2[4];
+        lds4(sP1r + x * L::LDC + r0 + rq, p1);
+        lds4(sP2 + x * L::LDC + r0 + rq, p2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ex[e] = xo == rq + e ? 1.f : ex[e] * d;
+          awA[e] += p1[e] * kx * ex[e];
+          awP[e] += p2[e] * qx * ex[e];
         }
       }
     }

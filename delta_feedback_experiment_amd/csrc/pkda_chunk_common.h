@@ -404,6 +404,23 @@ template <int V> __device__ __forceinline__ void lds_vec(const bf16_t* p, float*
   for (int j = 0; j < V; ++j) x[j] = bf16_to_f32(p[j]);
 }
 
+// Four consecutive LDS elements as floats in one read (8-byte aligned for
+// bf16, 16-byte for FP32).
+__device__ __forceinline__ void lds4(const float* p, float* x) {
+  const float4 w = *reinterpret_cast<const float4*>(p);
+  x[0] = w.x;
+  x[1] = w.y;
+  x[2] = w.z;
+  x[3] = w.w;
+}
+__device__ __forceinline__ void lds4(const bf16_t* p, float* x) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  x[0] = __uint_as_float(w.x << 16);
+  x[1] = __uint_as_float(w.x & 0xffff0000u);
+  x[2] = __uint_as_float(w.y << 16);
+  x[3] = __uint_as_float(w.y & 0xffff0000u);
+}
+
 // A [ROWS x NC] global tile held in registers as raw 16-byte pieces, so the
 // next chunk's operands can be in flight while the current chunk computes.
 // Rows r >= nvalid hold zeros.  store() copies the pieces to an LDS tile of
