@@ -571,6 +571,56 @@ def bench_controls(dev: torch.device, reps: int = 20) -> dict:
     }
 
 
+def bench_production(dev: torch.device, steps: int = 10, warmup: int = 3) -> dict:
+    """The reference model's own training operator (``pkda_recurrence``:
+    raw per-channel decay projection with the gate computed on the device,
+    write-key preconditioner with x = 1.5, ``fla_ops.py:252-569``) at the c2
+    geometry (B8 T4096 H16 d128, BF16), forward and backward of all ten
+    inputs, intermediates retained (``lean=False``).  Flops are reported on
+    the same fixed per-token-head convention as the headline step."""
+    import torch.nn.functional as F
+    from delta_feedback_experiment_amd import pkda_recurrence
+
+    B, T, H, D = 8, 4096, 16, 128
+    gen = torch.Generator(device=dev).manual_seed(31)
+
+    def rn(*s):
+        return torch.randn(*s, generator=gen, device=dev)
+
+    q, k = l2norm(rn(B, T, H, D)).to(torch.bfloat16), l2norm(rn(B, T, H, D)).to(torch.bfloat16)
+    v = rn(B, T, H, D).to(torch.bfloat16)
+    g_raw = (0.2 * rn(B, T, H, D)).to(torch.bfloat16)
+    beta = torch.sigmoid(0.2 * rn(B, T, H))
+    A_log = torch.empty(H, device=dev).uniform_(1, 16, generator=gen).log()
+    dt_bias = 0.1 * rn(H * D)
+    g_atk = -F.softplus(0.2 * rn(B, T, H) + 0.3)
+    beta_atk = torch.sigmoid(rn(B, T, H))
+    center = -0.2 + 0.1 * rn(H)
+    do = rn(B, T, H, D).to(torch.bfloat16)
+    leaves = [x.clone().requires_grad_() for x in (q, k, v, g_raw, g_atk, beta_atk, beta, A_log, dt_bias, center)]
+
+    def step():
+        o, _ = pkda_recurrence(*leaves, D ** -0.5, 1.5, 1e-6, False)
+        return torch.autograd.grad(o, leaves, do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    return {
+        "workload": "c2 geometry, production operator: B8 T4096 H16 d128 bf16, raw per-channel gate, "
+                    "preconditioner x=1.5, fwd+bwd of all ten inputs",
+        "ms_per_step": ms, "tokens_per_s": B * T / (ms / 1e3),
+        "mfma_frac_step": B * T * H * step_flops_convention(D) / (ms / 1e3) / MFMA_BF16_PEAK,
+    }
+
+
 def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
     """A plain device copy of ``nbytes`` (read + write), the practical HBM
     ceiling beside the kernels' rates and the scale for the byte counters."""
@@ -638,6 +688,8 @@ def main() -> None:
     ap.add_argument("--no-conv", action="store_true", help="skip the Q/K/V convolution and norm-gate lines")
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only")
     ap.add_argument("--no-serve", action="store_true", help="skip the slot-pool prefill and conv-token lines")
+    ap.add_argument("--no-production", action="store_true",
+                    help="skip the production-operator line (per-channel gate + preconditioner)")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -741,6 +793,14 @@ def main() -> None:
         print(f"[bench] serve prefill {c['prefill']['ms']:.3f} ms ({c['prefill']['tokens_per_s'] / 1e6:.1f} M tok/s), "
               f"conv token {c['conv_token']['us']:.1f} us ({c['conv_token']['GBps']:.0f} GB/s)", file=sys.stderr,
               flush=True)
+        inp = None
+    if not args.no_production:
+        del inp
+        torch.cuda.empty_cache()
+        result["production"] = bench_production(dev, args.steps, args.warmup)
+        c = result["production"]
+        print(f"[bench] production operator {c['ms_per_step']:.3f} ms/step "
+              f"({c['tokens_per_s'] / 1e6:.2f} M tok/s)", file=sys.stderr, flush=True)
         inp = None
     if not args.no_decode:
         del inp

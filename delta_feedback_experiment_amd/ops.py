@@ -187,9 +187,13 @@ def _setup_context(ctx, inputs, output) -> None:
     ctx.save_for_backward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, *saved)
     ctx.scalars = tuple(scalars)
     ctx.mark_non_differentiable(*saved)
+    # the saved intermediates never receive gradients: do not fill zeros for them
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, do, _dsaved):
+    if do is None:
+        return (None,) * 14
     tensors = ctx.saved_tensors
     inputs, saved = tensors[:10], list(tensors[10:])
     scale, squash_x, squash_eps, lean = ctx.scalars
