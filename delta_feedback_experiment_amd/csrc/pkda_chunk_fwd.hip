@@ -369,32 +369,37 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   }
   __syncthreads();
 
-  if (wave < 4) {
-    // ---- diagonal block tb = wave, exactly: one (t, s) pair, s <= t, per lane --
-    const int tb = wave;
-    for (int pr = lane; pr < 136; pr += 64) {
-      int tl = 0, rest = pr;
-      while (rest > tl) {
-        rest -= tl + 1;
-        ++tl;
-      }
-      const int t = 16 * tb + tl, s = 16 * tb + rest;
-      float akk = 0.f, aqk = 0.f;
-      for (int c = 0; c < D; c += V) {
-        float kx[V], qx[V], wx[V];
-        lds_vec<V>(sK + t * L::LD + c, kx);
-        lds_vec<V>(sQ + t * L::LD + c, qx);
-        lds_vec<V>(sKW + s * L::LD + c, wx);
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          const float e = exp_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
-          akk += kx[j] * wx[j] * e;
-          aqk += qx[j] * wx[j] * e;
-        }
-      }
-      sA[t * L::LDF + s] = (s < t && t < len) ? sBeta[t] * akk : 0.f;
-      sAqk[t * L::LDC + s] = to_e<E>(t < len ? p.scale * aqk : 0.f);
+  // ---- diagonal blocks, exactly: one (t, s) pair, s <= t, per lane -----------
+  // The 4 x 136 pairs are numbered block by block; waves 0-3 take pairs
+  // 0..511 (two per lane), and waves 6 and 7, which hold one off-diagonal
+  // block each (waves 4 and 5 hold two), take the last 32 after it.
+  auto diag_pair = [&](int pg) {
+    const int tb = pg / 136;
+    int tl = 0, rest = pg - tb * 136;
+    while (rest > tl) {
+      rest -= tl + 1;
+      ++tl;
     }
+    const int t = 16 * tb + tl, s = 16 * tb + rest;
+    float akk = 0.f, aqk = 0.f;
+    for (int c = 0; c < D; c += V) {
+      float kx[V], qx[V], wx[V];
+      lds_vec<V>(sK + t * L::LD + c, kx);
+      lds_vec<V>(sQ + t * L::LD + c, qx);
+      lds_vec<V>(sKW + s * L::LD + c, wx);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float e = exp_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
+        akk += kx[j] * wx[j] * e;
+        aqk += qx[j] * wx[j] * e;
+      }
+    }
+    sA[t * L::LDF + s] = (s < t && t < len) ? sBeta[t] * akk : 0.f;
+    sAqk[t * L::LDC + s] = to_e<E>(t < len ? p.scale * aqk : 0.f);
+  };
+  if (wave < 4) {
+    diag_pair(lane + 64 * wave);
+    diag_pair(lane + 64 * (wave + 4));
   } else {
     // ---- off-diagonal blocks (tb > sb) with the split decay --------------------
     for (int blk = wave - 4; blk < 6; blk += 4) {
@@ -425,6 +430,7 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
         sAqk[tt * L::LDC + ss] = to_e<E>(tt < len ? p.scale * aqk[e] : 0.f);
       }
     }
+    if (wave >= 6 && lane < 16) diag_pair(512 + 16 * (wave - 6) + lane);
   }
   // ---- qg = s e^G q and kg = e^{G_last - G} kw, straight to global -----------
   T* qg_out = static_cast<T*>(p.qg) + row0 * D;
