@@ -93,38 +93,51 @@ struct GateParams {
   int rank, g_stride;
 };
 
-__device__ __forceinline__ float gate_value(const GateParams& p, int64_t idx, int h, int c, float a_scale) {
-  const float x = load_any(p.g, idx, p.g_dtype);
-  if (p.kind == PKDA_GATE_RAW_CHANNEL) return a_scale * softplus_sigmoid_fast(x + p.dt_bias[h * p.D + c]).softplus;
-  return x;
-}
-
-__global__ __launch_bounds__(kWG) void gate_fwd_kernel(GateParams p) {
+// Per-head form: one wave, lane t scans the chunk.
+__global__ __launch_bounds__(64) void gate_fwd_kernel(GateParams p) {
   const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
   if (ci.len <= 0) return;
   const int h = blockIdx.y;
   const int H = p.heads;
-  if (p.kind == PKDA_GATE_LOG_HEAD) {
-    // one wave: lane t scans the chunk
-    if (threadIdx.x >= 64) return;
-    const int t = threadIdx.x;
-    const int64_t idx = (int64_t)(ci.start + t) * H + h;
-    float x = t < ci.len ? load_any(p.g, idx, p.g_dtype) : 0.f;
+  const int t = threadIdx.x;
+  const int64_t idx = (int64_t)(ci.start + t) * H + h;
+  float x = t < ci.len ? load_any(p.g, idx, p.g_dtype) : 0.f;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(x, off);
-      if (t >= off) x += y;
-    }
-    if (t < ci.len) p.gcum[idx] = x;
-    return;
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_up(x, off);
+    if (t >= off) x += y;
   }
-  const float a_scale = p.kind == PKDA_GATE_RAW_CHANNEL ? -expf(p.A_log[h]) : 0.f;
-  for (int c = threadIdx.x; c < p.D; c += kWG) {
+  if (t < ci.len) p.gcum[idx] = x;
+}
+
+// Per-channel forms (log or raw), one lane per channel and chunk: a lane
+// walks its chunk in groups of 16 tokens whose loads (indices clamped to the
+// chunk's last token) go out before the scan runs over them, so the walk is
+// not one memory latency per token.  Same arithmetic, in the same order, as
+// a plain sequential scan.
+template <typename G, bool RAW, int NT>
+__global__ __launch_bounds__(NT) void gate_channel_fwd_kernel(GateParams p) {
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const int len = ci.len;
+  if (len <= 0) return;
+  const int h = blockIdx.y, H = p.heads, D = p.D;
+  const G* __restrict__ g = static_cast<const G*>(p.g);
+  float* __restrict__ out = p.gcum;
+  const float a_scale = RAW ? -expf(p.A_log[h]) : 0.f;
+  const int64_t step = (int64_t)H * D;
+  for (int c = threadIdx.x; c < D; c += NT) {
+    const float bias = RAW ? p.dt_bias[h * D + c] : 0.f;
+    const int64_t base = ((int64_t)ci.start * H + h) * D + c;
     float acc = 0.f;
-    for (int t = 0; t < ci.len; ++t) {
-      const int64_t idx = ((int64_t)(ci.start + t) * H + h) * p.D + c;
-      acc += gate_value(p, idx, h, c, a_scale);
-      p.gcum[idx] = acc;
+    for (int t0 = 0; t0 < len; t0 += 16) {
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = io<G>::load(g + base + (int64_t)min(t0 + u, len - 1) * step);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        acc += RAW ? a_scale * softplus_sigmoid_fast(x[u] + bias).softplus : x[u];
+        if (t0 + u < len) out[base + (int64_t)(t0 + u) * step] = acc;
+      }
     }
   }
 }
@@ -133,55 +146,106 @@ __global__ __launch_bounds__(kWG) void gate_fwd_kernel(GateParams p) {
 // dglog[t] = sum_{s >= t in chunk} dgcum[s]; raw form also
 // dg = dglog * (-exp(A_log)) * sigmoid(g + dt_bias), dA_log += dglog * glog,
 // ddt_bias += dg.  Per-chunk partials, reduced by gate_reduce_kernel.
-__global__ __launch_bounds__(kWG) void gate_bwd_kernel(GateParams p) {
+__global__ __launch_bounds__(64) void gate_bwd_kernel(GateParams p) {
   const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len <= 0) return;
   const int h = blockIdx.y;
   const int H = p.heads;
-  const bool raw = p.kind == PKDA_GATE_RAW_CHANNEL;
-  if (p.kind == PKDA_GATE_LOG_HEAD) {
-    if (ci.len <= 0 || threadIdx.x >= 64) return;
-    const int t = threadIdx.x;
-    const int64_t idx = (int64_t)(ci.start + t) * H + h;
-    float x = t < ci.len ? p.dgcum[idx] : 0.f;
+  const int t = threadIdx.x;
+  const int64_t idx = (int64_t)(ci.start + t) * H + h;
+  float x = t < ci.len ? p.dgcum[idx] : 0.f;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {  // suffix sum
-      const float y = __shfl_down(x, off);
-      if (t + off < 64) x += y;
-    }
-    if (t < ci.len) p.dg[idx] = x;
-    return;
+  for (int off = 1; off < 64; off <<= 1) {  // suffix sum
+    const float y = __shfl_down(x, off);
+    if (t + off < 64) x += y;
   }
-  __shared__ float s_red[kWG];
-  const float A = raw ? expf(p.A_log[h]) : 0.f;
+  if (t < ci.len) p.dg[idx] = x;
+}
+
+// Per-channel backward, grouped loads as in the forward (tokens walked last
+// to first, indices clamped at 0).  The dA_log partial reduces over NT >= D
+// lanes (a power of two) with the same halving tree a wider workgroup with
+// zero-filled lanes would take.
+template <typename G, bool RAW, int NT>
+__global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
+  __shared__ float s_red[NT];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const int len = ci.len;
+  const int h = blockIdx.y, H = p.heads, D = p.D;
+  const G* __restrict__ g = static_cast<const G*>(p.g);
+  const float* __restrict__ dgcum = p.dgcum;
+  float* __restrict__ dg = p.dg;
+  const float A = RAW ? expf(p.A_log[h]) : 0.f;
+  const int64_t step = (int64_t)H * D;
   float dA_acc = 0.f;
-  for (int c = threadIdx.x; c < p.D; c += kWG) {
-    float suffix = 0.f;
-    float ddt = 0.f;
-    for (int t = ci.len - 1; t >= 0; --t) {
-      const int64_t idx = ((int64_t)(ci.start + t) * H + h) * p.D + c;
-      suffix += p.dgcum[idx];
-      if (raw) {
-        const float z = load_any(p.g, idx, p.g_dtype) + p.dt_bias[h * p.D + c];
-        const SoftplusSigmoid f = softplus_sigmoid_fast(z);
-        const float glog = -A * f.softplus;
-        const float dgr = suffix * (-A) * f.sigmoid;
-        p.dg[idx] = dgr;
-        dA_acc += suffix * glog;
-        ddt += dgr;
-      } else {
-        p.dg[idx] = suffix;
+  for (int c = threadIdx.x; c < D; c += NT) {
+    const float bias = RAW ? p.dt_bias[h * D + c] : 0.f;
+    const int64_t base = ((int64_t)ci.start * H + h) * D + c;
+    float suffix = 0.f, ddt = 0.f;
+    for (int tb = len - 1; tb >= 0; tb -= 16) {
+      float dgc[16], x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int64_t idx = base + (int64_t)max(tb - u, 0) * step;
+        dgc[u] = dgcum[idx];
+        if (RAW) x[u] = io<G>::load(g + idx);
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int t = tb - u;
+        if (t < 0) break;
+        const int64_t idx = base + (int64_t)t * step;
+        suffix += dgc[u];
+        if (RAW) {
+          const SoftplusSigmoid f = softplus_sigmoid_fast(x[u] + bias);
+          const float glog = -A * f.softplus;
+          const float dgr = suffix * (-A) * f.sigmoid;
+          dg[idx] = dgr;
+          dA_acc += suffix * glog;
+          ddt += dgr;
+        } else {
+          dg[idx] = suffix;
+        }
       }
     }
-    if (raw) p.ddt_bias_part[((int64_t)blockIdx.x * H + h) * p.D + c] = ci.len > 0 ? ddt : 0.f;
+    if (RAW) p.ddt_bias_part[((int64_t)blockIdx.x * H + h) * D + c] = len > 0 ? ddt : 0.f;
   }
-  if (!raw) return;
+  if (!RAW) return;
   s_red[threadIdx.x] = dA_acc;
   __syncthreads();
-  for (int off = kWG / 2; off > 0; off >>= 1) {
+  for (int off = NT / 2; off > 0; off >>= 1) {
     if (threadIdx.x < off) s_red[threadIdx.x] += s_red[threadIdx.x + off];
     __syncthreads();
   }
   if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = s_red[0];
+}
+
+template <bool BWD, typename G, bool RAW>
+void launch_gate_channel_nt(const GateParams& p, int num_chunks, hipStream_t s) {
+  const dim3 grid(num_chunks, p.heads);
+  if (p.D <= 64) {
+    if (BWD) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 64>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 64>), grid, dim3(64), 0, s, p);
+  } else if (p.D <= 128) {
+    if (BWD) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 128>), grid, dim3(128), 0, s, p);
+    else hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 128>), grid, dim3(128), 0, s, p);
+  } else {
+    if (BWD) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 256>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 256>), grid, dim3(256), 0, s, p);
+  }
+}
+
+// Per-channel gate forms (PKDA_GATE_LOG_CHANNEL, PKDA_GATE_RAW_CHANNEL).
+template <bool BWD>
+void launch_gate_channel(const GateParams& p, int num_chunks, hipStream_t s) {
+  const bool raw = p.kind == PKDA_GATE_RAW_CHANNEL;
+  if (p.g_dtype == PKDA_BF16) {
+    if (raw) launch_gate_channel_nt<BWD, bf16_t, true>(p, num_chunks, s);
+    else launch_gate_channel_nt<BWD, bf16_t, false>(p, num_chunks, s);
+  } else {
+    if (raw) launch_gate_channel_nt<BWD, float, true>(p, num_chunks, s);
+    else launch_gate_channel_nt<BWD, float, false>(p, num_chunks, s);
+  }
 }
 
 // ---- low-rank gate: the decay expansion on MFMA, fused with the activation ----
@@ -505,7 +569,10 @@ extern "C" int pkda_gate_fwd(const pkda_gate_args* a, void* stream) {
   if (a->num_chunks == 0) return 0;
   if (a->gate_kind == PKDA_GATE_LOW_RANK)
     return dispatch_low_rank(p, a->num_chunks, false, static_cast<hipStream_t>(stream));
-  hipLaunchKernelGGL(gate_fwd_kernel, dim3(a->num_chunks, a->heads), dim3(kWG), 0, static_cast<hipStream_t>(stream), p);
+  if (a->gate_kind == PKDA_GATE_LOG_HEAD)
+    hipLaunchKernelGGL(gate_fwd_kernel, dim3(a->num_chunks, a->heads), dim3(64), 0, static_cast<hipStream_t>(stream), p);
+  else
+    launch_gate_channel<false>(p, a->num_chunks, static_cast<hipStream_t>(stream));
   return launch_status("pkda_gate_fwd");
 }
 
@@ -521,8 +588,10 @@ extern "C" int pkda_gate_bwd(const pkda_gate_args* a, void* stream) {
   if (a->num_chunks > 0) {
     if (a->gate_kind == PKDA_GATE_LOW_RANK) {
       if (int e = dispatch_low_rank(p, a->num_chunks, true, s)) return e;
+    } else if (a->gate_kind == PKDA_GATE_LOG_HEAD) {
+      hipLaunchKernelGGL(gate_bwd_kernel, dim3(a->num_chunks, a->heads), dim3(64), 0, s, p);
     } else {
-      hipLaunchKernelGGL(gate_bwd_kernel, dim3(a->num_chunks, a->heads), dim3(kWG), 0, s, p);
+      launch_gate_channel<true>(p, a->num_chunks, s);
     }
   }
   if (raw) {
