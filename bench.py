@@ -100,7 +100,7 @@ STAGE_KERNEL = {
     "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true, false>",
     "fwd_state": "chunk_state_fwd_rr_kernel<128, 64, true>",
     "bwd_state": "chunk_state_bwd_rr_kernel<128, 64, true>",
-    "bwd_chunk": "chunk_fused_bwd_kernel<bf16, 128, bf16, true>",
+    "bwd_chunk": "chunk_fused_bwd_kernel<bf16, 128, bf16, bf16, true>",
     "decode": "decode_kernel<bf16, 128, 512>",
 }
 TRAFFIC_PROFILE = ROOT / "profiles" / "pkda_chunk_c2_decode_c4_hbm_traffic.md"
@@ -266,7 +266,7 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
         gate_per_channel=0, beta=_ptr(beta), scale=scale, initial_state=_ptr(s0),
         w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), do=_ptr(do), dht=None, dh=_ptr(dh),
         du=_ptr(du), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
-        dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None, grad_dtype=_lib.PKDA_BF16,
+        dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None, grad_dtype=_lib.PKDA_BF16, key_grad_dtype=_lib.PKDA_BF16,
     )
     stages = [
         ("fwd_intra", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_INTRA),

@@ -23,7 +23,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class RecurrentArgs(ctypes.Structure):
@@ -97,6 +97,7 @@ class ChunkBwdArgs(ctypes.Structure):
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
         ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p), ("grad_dtype", c_int32),
+        ("key_grad_dtype", c_int32),
     ]
 
 

@@ -162,22 +162,29 @@ class BwdGrads:
 def chunk_backward(
     plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor, scale: float,
     initial_state: Tensor | None, saved: FwdSaved, do: Tensor, dht: Tensor | None, want_dh0: bool,
-    grad_dtype: torch.dtype = torch.float32,
+    grad_dtype: torch.dtype = torch.float32, key_grad_dtype: torch.dtype | None = None,
 ) -> BwdGrads:
-    """Chunk backward on flat operands.  ``dq, dk, dkw, dv`` come in
-    ``grad_dtype`` (FP32, or ``q.dtype``: the FP32 value rounded once in the
-    kernel); the other gradients are FP32."""
+    """Chunk backward on flat operands.  ``dq, dv`` come in ``grad_dtype``
+    (FP32, or ``q.dtype``: the FP32 value rounded once in the kernel), ``dk,
+    dkw`` in ``key_grad_dtype`` (default ``grad_dtype``; FP32 with a
+    ``q.dtype`` ``grad_dtype`` for a caller that adds the preconditioner's
+    terms into them); the other gradients are FP32."""
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
     ntok = plan.num_tokens
     f32 = dict(device=dev, dtype=torch.float32)
     if grad_dtype not in (torch.float32, q.dtype):
         raise ValueError(f"grad_dtype must be float32 or {q.dtype}, got {grad_dtype}")
+    if key_grad_dtype is None:
+        key_grad_dtype = grad_dtype
+    if key_grad_dtype not in (grad_dtype, torch.float32):
+        raise ValueError(f"key_grad_dtype must be {grad_dtype} or float32, got {key_grad_dtype}")
     gd = dict(device=dev, dtype=grad_dtype)
+    kd = dict(device=dev, dtype=key_grad_dtype)
     kw_is_k = kw.data_ptr() == k.data_ptr()
     dq = torch.empty(ntok, H, D, **gd)
-    dk = torch.empty(ntok, H, D, **gd)
-    dkw = None if kw_is_k else torch.empty(ntok, H, D, **gd)
+    dk = torch.empty(ntok, H, D, **kd)
+    dkw = None if kw_is_k else torch.empty(ntok, H, D, **kd)
     dv = torch.empty(ntok, H, D, **gd)
     dbeta = torch.empty(ntok, H, **f32)
     dgcum = torch.empty_like(gcum)
@@ -194,6 +201,7 @@ def chunk_backward(
         dq=_ptr(dq), dk=_ptr(dk), dkw=_ptr(dkw), dv=_ptr(dv), dbeta=_ptr(dbeta), dgcum=_ptr(dgcum),
         dh0=_ptr(dh0), qg=_ptr(saved.qg), kg=_ptr(saved.kg),
         grad_dtype=_lib.PKDA_F32 if grad_dtype == torch.float32 else _dtype_code(q),
+        key_grad_dtype=_lib.PKDA_F32 if key_grad_dtype == torch.float32 else _dtype_code(q),
     )
     _lib.call("pkda_chunk_bwd", args, _stream(dev))
     return BwdGrads(dq, dk, dkw, dv, dbeta, dgcum, dh0)
@@ -314,11 +322,14 @@ class _ChunkPKDA(torch.autograd.Function):
         dof = _flat(do.to(qf.dtype).contiguous(), plan)
         dht = None if dS_T is None else dS_T.float().contiguous()
         want_dh0 = ctx.needs_input_grad[10]
-        # without the preconditioner nothing consumes dq, dk, dv after the
-        # kernel but the cast to the input dtype, which the kernel then does
-        direct = ctx.pstate is None and all(d == qf.dtype for d in ctx.dtypes[:3])
+        # nothing consumes dq, dv after the kernel but the cast to the input
+        # dtype, which the kernel then does; dk too unless the preconditioner
+        # adds its terms into it (then FP32, as is dkw)
+        direct = ctx.dtypes[0] == qf.dtype and ctx.dtypes[2] == qf.dtype
+        key_direct = direct and ctx.pstate is None and ctx.dtypes[1] == qf.dtype
         gr = chunk_backward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, saved, dof, dht, want_dh0,
-                            grad_dtype=qf.dtype if direct else torch.float32)
+                            grad_dtype=qf.dtype if direct else torch.float32,
+                            key_grad_dtype=qf.dtype if key_direct else torch.float32)
         dk = gr.dk
         dg_atk = dbeta_atk = dcenter = dA0 = None
         if ctx.pstate is not None:

@@ -305,7 +305,7 @@ struct FusedBwdLayout {
   static constexpr int bytes = off_red + kFW * 4;
 };
 
-template <typename T, int D, typename OT, bool ALIAS>
+template <typename T, int D, typename OT, typename OK, bool ALIAS>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   using L = FusedBwdLayout<T, D>;
   using E = T;
@@ -498,10 +498,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   float gsum[4] = {0.f, 0.f, 0.f, 0.f};
   float kgd = 0.f;
   OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
-  OT* dko = static_cast<OT*>(p.dk) + row0 * D;
+  OK* dko = static_cast<OK*>(p.dk) + row0 * D;
   // outputs in the activation dtype with the write-key gradient folded into
   // dk leave through LDS (16-byte stores)
-  constexpr bool kStage = sizeof(OT) == sizeof(T) && ALIAS;
+  constexpr bool kStage = sizeof(OT) == sizeof(T) && sizeof(OK) == sizeof(T) && ALIAS;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -532,10 +532,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
     } else {
       store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
       if (ALIAS) {
-        store_acc_global<OT>(dko, gs, dk + dkw, r0, 16 * ct, len, lane);
+        store_acc_global<OK>(dko, gs, dk + dkw, r0, 16 * ct, len, lane);
       } else {
-        store_acc_global<OT>(dko, gs, dk, r0, 16 * ct, len, lane);
-        store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw, r0, 16 * ct, len, lane);
+        store_acc_global<OK>(dko, gs, dk, r0, 16 * ct, len, lane);
+        store_acc_global<OK>(static_cast<OK*>(p.dkw) + row0 * D, gs, dkw, r0, 16 * ct, len, lane);
       }
     }
   }
@@ -626,7 +626,7 @@ struct FusedBwdPcLayout {
   static_assert(D == 2 * C || G_BYTES + RT <= off_dO, "KW fits after G");
 };
 
-template <typename T, int D, typename OT>
+template <typename T, int D, typename OT, typename OK>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   using L = FusedBwdPcLayout<T, D>;
   using E = T;
@@ -973,7 +973,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   // ---- outputs -------------------------------------------------------------
   OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
-  OT* dko = static_cast<OT*>(p.dk) + row0 * D;
+  OK* dko = static_cast<OK*>(p.dk) + row0 * D;
   OT* dvo = static_cast<OT*>(p.dv) + row0 * D;
   float* dgo = p.dgcum + row0 * D;
 #pragma unroll
@@ -997,10 +997,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
     store_acc_global<OT>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
     if (p.kw_is_k) {
-      store_acc_global<OT>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OK>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
     } else {
-      store_acc_global<OT>(dko, gs, dk[j], r0, 16 * ct, len, lane);
-      store_acc_global<OT>(static_cast<OT*>(p.dkw) + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OK>(dko, gs, dk[j], r0, 16 * ct, len, lane);
+      store_acc_global<OK>(static_cast<OK*>(p.dkw) + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
     }
   }
   float* sRowB = sRed;  // [2][64]
@@ -1296,7 +1296,7 @@ int launch_state_bwd_rr(const BwdParams& p, hipStream_t s) {
   return p.kw_is_k ? launch_state_bwd_rr_as<D, 64, true>(p, s) : launch_state_bwd_rr_as<D, 64, false>(p, s);
 }
 
-template <typename T, int D, int BV, typename OT>
+template <typename T, int D, int BV, typename OT, typename OK>
 int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const int N = p.geom.num_seqs;
   const bool all = stages == 0;
@@ -1318,8 +1318,9 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   }
   if (num_chunks == 0) return 0;
   if (all || (stages & PKDA_STAGE_BWD_CHUNK)) {
-    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D, OT>
-                     : (p.kw_is_k ? chunk_fused_bwd_kernel<T, D, OT, true> : chunk_fused_bwd_kernel<T, D, OT, false>);
+    auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D, OT, OK>
+                     : (p.kw_is_k ? chunk_fused_bwd_kernel<T, D, OT, OK, true>
+                                  : chunk_fused_bwd_kernel<T, D, OT, OK, false>);
     const int bytes = p.qg ? FusedBwdPcLayout<T, D>::bytes : FusedBwdLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
     hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kFW), bytes, s, p);
@@ -1344,6 +1345,9 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   PKDA_REQUIRE(!a->gate_per_channel || (a->qg && a->kg), PKDA_EINVAL, "per-channel gates need the forward's qg and kg");
   PKDA_REQUIRE(a->grad_dtype == PKDA_F32 || a->grad_dtype == a->dtype, PKDA_EUNSUPPORTED,
                "grad_dtype %d (FP32 or the activation dtype)", a->grad_dtype);
+  PKDA_REQUIRE(a->key_grad_dtype == a->grad_dtype || (a->key_grad_dtype == PKDA_F32 && a->grad_dtype == a->dtype),
+               PKDA_EUNSUPPORTED, "key_grad_dtype %d with grad_dtype %d (equal, or FP32 key gradients)",
+               a->key_grad_dtype, a->grad_dtype);
   BwdParams p;
   if (int st = chunk_geom_from(a->cu_seqlens, a->num_seqs, a->seqlen, a->num_chunks, a->table, p.geom)) return st;
   if (a->num_seqs == 0) return 0;
@@ -1368,12 +1372,16 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   if (a->dtype == PKDA_BF16) {
-    if (a->grad_dtype == PKDA_BF16) {
-      return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, bf16_t>(p, nc, st, s)
-                                : launch_bwd<bf16_t, 64, 64, bf16_t>(p, nc, st, s);
+    if (a->grad_dtype == PKDA_BF16 && a->key_grad_dtype == PKDA_BF16) {
+      return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, bf16_t, bf16_t>(p, nc, st, s)
+                                : launch_bwd<bf16_t, 64, 64, bf16_t, bf16_t>(p, nc, st, s);
     }
-    return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, float>(p, nc, st, s)
-                              : launch_bwd<bf16_t, 64, 64, float>(p, nc, st, s);
+    if (a->grad_dtype == PKDA_BF16) {
+      return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, bf16_t, float>(p, nc, st, s)
+                                : launch_bwd<bf16_t, 64, 64, bf16_t, float>(p, nc, st, s);
+    }
+    return a->head_dim == 128 ? launch_bwd<bf16_t, 128, 64, float, float>(p, nc, st, s)
+                              : launch_bwd<bf16_t, 64, 64, float, float>(p, nc, st, s);
   }
-  return launch_bwd<float, 64, 64, float>(p, nc, st, s);
+  return launch_bwd<float, 64, 64, float, float>(p, nc, st, s);
 }

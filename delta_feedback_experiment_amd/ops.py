@@ -159,7 +159,10 @@ def pkda_recurrence_backward(
         else:
             fs = FwdSaved(*saved[2:9])
         dof = flat(do.to(q.dtype))
-        gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False)
+        # dq, dv leave the kernel in the input dtype; dk, dkw stay FP32 for the
+        # preconditioner's terms
+        gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False,
+                            grad_dtype=qf.dtype, key_grad_dtype=torch.float32)
         pstate = pre.PrecondState(kw, a_chunk, None, None)
         dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(
             plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, pstate, gr.dkw, gr.dk, None, False)

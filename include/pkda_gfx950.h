@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 5
+#define PKDA_ABI_VERSION 6
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -331,10 +331,12 @@ int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
  * entry points above).  Consumes the forward's saved tensors and do
  * (and dht, the final-state gradient, or NULL).  Workspace (caller):
  * dh [num_chunks, H, K, V] and du [N_tok, H, V], both in dtype.  Outputs:
- * dq, dk (read key), dkw (write key; when kw == k it is added into dk and may
- * be NULL), dv in grad_dtype (FP32, or dtype when the caller wants the input
- * dtype directly); dbeta [N_tok,H], dgcum (shape of gcum), dh0 [N,H,K,V]
- * (NULL if not wanted) in FP32.
+ * dq, dv in grad_dtype and dk (read key), dkw (write key; when kw == k it is
+ * added into dk and may be NULL) in key_grad_dtype (FP32, or dtype when the
+ * caller wants the input dtype directly; FP32 key gradients with dtype dq, dv
+ * for a caller that accumulates the preconditioner's terms into dk and dkw);
+ * dbeta [N_tok,H], dgcum (shape of gcum), dh0 [N,H,K,V] (NULL if not wanted)
+ * in FP32.
  * ------------------------------------------------------------------------- */
 typedef struct pkda_chunk_bwd_args {
   int32_t struct_size;
@@ -354,11 +356,12 @@ typedef struct pkda_chunk_bwd_args {
   const float* dht;
   void* dh;
   void* du;
-  void *dq, *dk, *dkw, *dv;     /* in grad_dtype */
+  void *dq, *dk, *dkw, *dv;     /* dq, dv in grad_dtype; dk, dkw in key_grad_dtype */
   float *dbeta, *dgcum, *dh0;
   int32_t stages;              /* pkda_chunk_stage mask, 0 = all */
   const void *qg, *kg;         /* per-channel gates only: the forward's qg, kg */
-  int32_t grad_dtype;          /* dq, dk, dkw, dv: PKDA_F32 or dtype (one rounding of the FP32 value) */
+  int32_t grad_dtype;          /* dq, dv: PKDA_F32 or dtype (one rounding of the FP32 value) */
+  int32_t key_grad_dtype;      /* dk, dkw: grad_dtype, or PKDA_F32 when grad_dtype is dtype */
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);
