@@ -56,6 +56,11 @@ def test_rejected_arguments_raise_before_any_launch():
     args = _lib.RecurrentArgs(dtype=0, num_seqs=1, seqlen=2, heads=1, head_dim=64)
     with pytest.raises(ValueError, match="seqlen == 1"):
         _lib.call("pkda_decode_step", args, 0)
+    # key gradients narrower than dq, dv: not a supported combination
+    args = _lib.ChunkBwdArgs(dtype=_lib.PKDA_BF16, num_seqs=1, seqlen=64, heads=1, head_dim=64,
+                             grad_dtype=_lib.PKDA_F32, key_grad_dtype=_lib.PKDA_BF16)
+    with pytest.raises(ValueError, match="key_grad_dtype"):
+        _lib.call("pkda_chunk_bwd", args, 0)
 
 
 def test_operators_refuse_cpu_tensors():
