@@ -23,7 +23,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class RecurrentArgs(ctypes.Structure):
@@ -53,7 +53,7 @@ class GateArgs(ctypes.Structure):
         ("gcum", c_void_p), ("dgcum", c_void_p), ("dg", c_void_p), ("dA_log_part", c_void_p),
         ("ddt_bias_part", c_void_p), ("dA_log", c_void_p), ("ddt_bias", c_void_p),
         ("num_chunks", c_int32), ("table", c_void_p),
-        ("up_weight", c_void_p), ("rank", c_int32), ("g_stride", c_int32),
+        ("up_weight", c_void_p), ("rank", c_int32), ("g_stride", c_int32), ("dg_dtype", c_int32),
     ]
 
 
@@ -68,6 +68,7 @@ class PrecondArgs(ctypes.Structure):
         ("dkw", c_void_p), ("dk", c_void_p), ("dg_atk", c_void_p), ("dbeta_atk", c_void_p),
         ("dcenter_part", c_void_p), ("dcenter", c_void_p), ("dA0", c_void_p), ("dA_T", c_void_p),
         ("table", c_void_p), ("slot_idx", c_void_p), ("pool_size", c_int64), ("lam_chunk", c_void_p),
+        ("dk_final", c_void_p),
     ]
 
 

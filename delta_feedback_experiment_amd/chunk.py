@@ -209,15 +209,16 @@ def chunk_backward(
 
 def gate_backward(
     plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt_bias: Tensor | None, dgcum: Tensor,
-    up_weight: Tensor | None = None,
+    up_weight: Tensor | None = None, dg_dtype: torch.dtype = torch.float32,
 ) -> tuple[Tensor, Tensor | None, Tensor | None]:
-    """``dg`` (FP32, shape of ``g``) and, for the raw gate, ``dA_log``, ``ddt_bias``.
+    """``dg`` (``dg_dtype``: FP32, or ``g.dtype`` for the per-channel forms;
+    shape of ``g``) and, for the raw gate, ``dA_log``, ``ddt_bias``.
 
     The low-rank form returns the raw gate's gradient ``[N_tok, H, K]`` as
     ``dg``; the hidden rows' and the weight's gradients are two GEMMs of it
     (:func:`low_rank_grads`)."""
     dev = dgcum.device
-    dg = torch.empty(dgcum.shape, device=dev, dtype=torch.float32)
+    dg = torch.empty(dgcum.shape, device=dev, dtype=dg_dtype)
     raw = kind in (_lib.GATE_RAW_CHANNEL, _lib.GATE_LOW_RANK)
     dA_part = ddt_part = dA_log = ddt_bias = None
     if raw:
@@ -232,6 +233,7 @@ def gate_backward(
         A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), dgcum=_ptr(dgcum), dg=_ptr(dg),
         dA_log_part=_ptr(dA_part), ddt_bias_part=_ptr(ddt_part), dA_log=_ptr(dA_log), ddt_bias=_ptr(ddt_bias),
         num_chunks=plan.num_chunks, table=_ptr(plan.table),
+        dg_dtype=_lib.PKDA_F32 if dg_dtype == torch.float32 else _dtype_code(g),
     )
     if kind == _lib.GATE_LOW_RANK:
         args.up_weight, args.rank, args.g_stride = _ptr(up_weight), g.shape[-1], g.stride(0)

@@ -86,11 +86,12 @@ struct GateParams {
   const float* dt_bias;
   float* gcum;
   const float* dgcum;
-  float* dg;
+  void* dg;  // FP32 except the per-channel backward with dg_dtype = g's dtype
   float* dA_log_part;
   float* ddt_bias_part;
   const void* up_weight;  // low-rank gate: [H*K, R]
   int rank, g_stride;
+  int dg_dtype;  // per-channel backward: dg in FP32 or g's dtype
 };
 
 // Per-head form: one wave, lane t scans the chunk.
@@ -159,14 +160,14 @@ __global__ __launch_bounds__(64) void gate_bwd_kernel(GateParams p) {
     const float y = __shfl_down(x, off);
     if (t + off < 64) x += y;
   }
-  if (t < ci.len) p.dg[idx] = x;
+  if (t < ci.len) static_cast<float*>(p.dg)[idx] = x;
 }
 
 // Per-channel backward, grouped loads as in the forward (tokens walked last
 // to first, indices clamped at 0).  The dA_log partial reduces over NT >= D
 // lanes (a power of two) with the same halving tree a wider workgroup with
 // zero-filled lanes would take.
-template <typename G, bool RAW, int NT>
+template <typename G, bool RAW, int NT, typename DG>
 __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
   __shared__ float s_red[NT];
   const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
   const int h = blockIdx.y, H = p.heads, D = p.D;
   const G* __restrict__ g = static_cast<const G*>(p.g);
   const float* __restrict__ dgcum = p.dgcum;
-  float* __restrict__ dg = p.dg;
+  DG* __restrict__ dg = reinterpret_cast<DG*>(p.dg);
   const float A = RAW ? expf(p.A_log[h]) : 0.f;
   const int64_t step = (int64_t)H * D;
   float dA_acc = 0.f;
@@ -200,11 +201,11 @@ __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
           const SoftplusSigmoid f = softplus_sigmoid_fast(x[u] + bias);
           const float glog = -A * f.softplus;
           const float dgr = suffix * (-A) * f.sigmoid;
-          dg[idx] = dgr;
+          io<DG>::store(dg + idx, dgr);
           dA_acc += suffix * glog;
           ddt += dgr;
         } else {
-          dg[idx] = suffix;
+          io<DG>::store(dg + idx, suffix);
         }
       }
     }
@@ -223,15 +224,19 @@ __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
 template <bool BWD, typename G, bool RAW>
 void launch_gate_channel_nt(const GateParams& p, int num_chunks, hipStream_t s) {
   const dim3 grid(num_chunks, p.heads);
+  const bool narrow = p.dg_dtype != PKDA_F32;  // backward: dg in G
   if (p.D <= 64) {
-    if (BWD) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 64>), grid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 64>), grid, dim3(64), 0, s, p);
+    if (!BWD) hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 64>), grid, dim3(64), 0, s, p);
+    else if (narrow) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 64, G>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 64, float>), grid, dim3(64), 0, s, p);
   } else if (p.D <= 128) {
-    if (BWD) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 128>), grid, dim3(128), 0, s, p);
-    else hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 128>), grid, dim3(128), 0, s, p);
+    if (!BWD) hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 128>), grid, dim3(128), 0, s, p);
+    else if (narrow) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 128, G>), grid, dim3(128), 0, s, p);
+    else hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 128, float>), grid, dim3(128), 0, s, p);
   } else {
-    if (BWD) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 256>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 256>), grid, dim3(256), 0, s, p);
+    if (!BWD) hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 256>), grid, dim3(256), 0, s, p);
+    else if (narrow) hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 256, G>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gate_channel_bwd_kernel<G, RAW, 256, float>), grid, dim3(256), 0, s, p);
   }
 }
 
@@ -435,7 +440,7 @@ __device__ __forceinline__ void gate_low_rank_bwd_chunk(const GateParams& p, con
       dA += valid ? s * (-A * f.softplus) : 0.f;
       col += dg[j];
     }
-    store_acc_global<float>(p.dg + base, (int64_t)H * K, dg, 16 * wave, 16 * ct, ci.len, lane);
+    store_acc_global<float>(static_cast<float*>(p.dg) + base, (int64_t)H * K, dg, 16 * wave, 16 * ct, ci.len, lane);
     col += __shfl_xor(col, 16);
     col += __shfl_xor(col, 32);
     if (lane < 16) s_col[wave][16 * ct + lane] = col;
@@ -533,6 +538,7 @@ int gate_common(const pkda_gate_args* a, GateParams& p) {
   p.gcum = a->gcum;
   p.dgcum = a->dgcum;
   p.dg = a->dg;
+  p.dg_dtype = a->dg_dtype;
   p.dA_log_part = a->dA_log_part;
   p.ddt_bias_part = a->ddt_bias_part;
   p.up_weight = a->up_weight;
@@ -581,6 +587,10 @@ extern "C" int pkda_gate_bwd(const pkda_gate_args* a, void* stream) {
   int st = gate_common(a, p);
   if (st) return st;
   PKDA_REQUIRE(a->dgcum && a->dg, PKDA_EINVAL, "gate backward needs dgcum and dg");
+  PKDA_REQUIRE(a->dg_dtype == PKDA_F32 ||
+                   (a->dg_dtype == a->g_dtype &&
+                    (a->gate_kind == PKDA_GATE_LOG_CHANNEL || a->gate_kind == PKDA_GATE_RAW_CHANNEL)),
+               PKDA_EUNSUPPORTED, "dg_dtype %d: FP32, or g's dtype for the per-channel gate forms", a->dg_dtype);
   const bool raw = a->gate_kind >= PKDA_GATE_RAW_CHANNEL;
   PKDA_REQUIRE(!raw || (a->g && a->dA_log_part && a->ddt_bias_part && a->dA_log && a->ddt_bias), PKDA_EINVAL,
                "raw gate backward needs g and the dA_log / ddt_bias buffers");

@@ -60,6 +60,7 @@ struct PrecondParams {
   const float* dA_T;
   const int32_t* slot;  // forward: document -> A-state row, or null
   float* lam_chunk;
+  void* dk_final;  // backward: dk + the terms here in k's dtype (dk untouched), or null
 };
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
@@ -225,6 +226,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
   const T* __restrict__ k = static_cast<const T*>(p.k);
   const float* __restrict__ dkw_p = p.dkw;
   float* __restrict__ dk_p = p.dk;
+  T* __restrict__ dk_fin = static_cast<T*>(p.dk_final);
   const float* __restrict__ g_atk = p.g_atk;
   const float* __restrict__ beta_atk = p.beta_atk;
   const int64_t row = ((int64_t)j * H + h) * D + cc;
@@ -294,7 +296,11 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       const float lam_t = lam + dr / (at + eps);
       if (APPLY) {
         dcen -= dr;
-        if (active && in) dk_p[th * D + cc] = rdk[u] + (dkw * f + 2.f * beta_atk[th] * kc * lam_t);
+        if (active && in) {
+          const float dkt = rdk[u] + (dkw * f + 2.f * beta_atk[th] * kc * lam_t);
+          if (dk_fin) io<T>::store(dk_fin + th * D + cc, dkt);
+          else dk_p[th * D + cc] = dkt;
+        }
         const float a_prev = u > 0 ? ra[u - 1] : a_b;
         const float vg = row_sum16(lam_t * eg * a_prev);
         const float vb = row_sum16(lam_t * kc * kc);
@@ -415,6 +421,7 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
   p.dA_T = a->dA_T;
   p.slot = a->slot_idx;
   p.lam_chunk = a->lam_chunk;
+  p.dk_final = a->dk_final;
   PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed A states need pool_size > 0");
   return 0;
 }

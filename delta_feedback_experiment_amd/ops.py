@@ -164,13 +164,15 @@ def pkda_recurrence_backward(
         gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False,
                             grad_dtype=qf.dtype, key_grad_dtype=torch.float32)
         pstate = pre.PrecondState(kw, a_chunk, None, None)
+        dk = torch.empty_like(kf)  # the preconditioner's scan writes the final dk in k's dtype
         dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(
-            plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, pstate, gr.dkw, gr.dk, None, False)
-        dg, dA_log, ddt_bias = gate_backward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gr.dgcum)
+            plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, pstate, gr.dkw, gr.dk, None, False,
+            dk_final=dk)
+        dg, dA_log, ddt_bias = gate_backward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gr.dgcum, dg_dtype=gf.dtype)
     shape = tuple(q.shape)
     lead = shape[:3]
     return [
-        gr.dq.reshape(shape).to(q.dtype), gr.dk.reshape(shape).to(k.dtype), gr.dv.reshape(v.shape).to(v.dtype),
+        gr.dq.reshape(shape).to(q.dtype), dk.reshape(shape).to(k.dtype), gr.dv.reshape(v.shape).to(v.dtype),
         dg.reshape(g.shape).to(g.dtype), dg_atk.reshape(lead).to(g_atk.dtype),
         dbeta_atk.reshape(lead).to(beta_atk.dtype), gr.dbeta.reshape(lead).to(beta.dtype),
         dA_log.reshape(A_log.shape).to(A_log.dtype), ddt_bias.reshape(dt_bias.shape).to(dt_bias.dtype),

@@ -68,10 +68,12 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
 
 
 def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
-                     state: PrecondState, dkw: Tensor, dk: Tensor, dA_T: Tensor | None, want_dA0: bool):
+                     state: PrecondState, dkw: Tensor, dk: Tensor, dA_T: Tensor | None, want_dA0: bool,
+                     dk_final: Tensor | None = None):
     """Reverse scan: adds the preconditioner's terms into ``dk`` (FP32, in
-    place) and returns ``(dg_atk [N_tok,H], dbeta_atk [N_tok,H], dcenter [H],
-    dA0 [N,H,K] or None)``, all FP32."""
+    place) -- or, with ``dk_final`` (``kf``'s shape and dtype), writes the
+    sum there and leaves ``dk`` alone -- and returns ``(dg_atk [N_tok,H],
+    dbeta_atk [N_tok,H], dcenter [H], dA0 [N,H,K] or None)``, all FP32."""
     dev = kf.device
     H, K, N = plan.heads, plan.head_dim, plan.num_seqs
     ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
@@ -89,7 +91,10 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
         squash_x=float(x), squash_eps=float(eps), a_chunk=_ptr(state.a_chunk), num_chunks=plan.num_chunks,
         dkw=_ptr(dkw), dk=_ptr(dk), dg_atk=_ptr(dg_atk), dbeta_atk=_ptr(dbeta_atk),
         dcenter_part=_ptr(dcenter_part), dcenter=_ptr(dcenter), dA0=_ptr(dA0), dA_T=_ptr(dAT),
-        table=_ptr(plan.table), lam_chunk=_ptr(lam_chunk),
+        table=_ptr(plan.table), lam_chunk=_ptr(lam_chunk), dk_final=_ptr(dk_final),
     )
+    if dk_final is not None and (dk_final.shape != kf.shape or dk_final.dtype != kf.dtype
+                                 or not dk_final.is_contiguous()):
+        raise ValueError("dk_final must be contiguous with k's shape and dtype")
     _lib.call("pkda_precond_bwd", args, _stream(dev))
     return dg_atk, dbeta_atk, dcenter, dA0

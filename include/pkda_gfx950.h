@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 6
+#define PKDA_ABI_VERSION 7
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -178,7 +178,7 @@ typedef struct pkda_gate_args {
   const float* dt_bias;
   float* gcum;              /* forward output */
   const float* dgcum;       /* backward input */
-  float* dg;                /* backward output, FP32, shape of g; PKDA_GATE_LOW_RANK: the
+  void* dg;                 /* backward output in dg_dtype, shape of g; PKDA_GATE_LOW_RANK: the
                                gradient of the raw gate [N_tok, H, K] (the host turns it into
                                the decay hidden's and up_weight's gradients with two GEMMs) */
   float* dA_log_part;       /* [num_chunks, H]   workspace (raw and low-rank gates) */
@@ -193,6 +193,7 @@ typedef struct pkda_gate_args {
   const void* up_weight;
   int32_t rank;
   int32_t g_stride;
+  int32_t dg_dtype;         /* PKDA_F32 (0), or g_dtype for the per-channel forms */
 } pkda_gate_args;
 
 int pkda_gate_fwd(const pkda_gate_args* args, void* stream);
@@ -248,6 +249,8 @@ typedef struct pkda_precond_args {
   const int32_t* slot_idx;
   int64_t pool_size;
   float* lam_chunk;              /* backward workspace [num_chunks, H, K] */
+  void* dk_final;                /* backward, optional: dk + the preconditioner's terms
+                                    written here in dtype, dk left as it came in */
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
