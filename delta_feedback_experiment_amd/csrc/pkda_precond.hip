@@ -208,8 +208,8 @@ __device__ __forceinline__ float row_sum16(float v) {
 // Backward launches 1 (APPLY = false: lambda's local value before the chunk
 // from a zero start after it, into lam_chunk) and 3 (APPLY: from the lambda
 // entering the chunk, the gradients).  The chunk is walked in reverse in
-// sub-blocks of 16 tokens: a first forward pass keeps A at each sub-block's
-// start, and each sub-block recomputes its 16 A_t from there (the same
+// sub-blocks of 8 tokens: a first forward pass keeps A at each sub-block's
+// start, and each sub-block recomputes its 8 A_t from there (the same
 // arithmetic, so the same values) with its k, dkw and dk rows in registers.
 // Loads clamp as in the forward.  The per-token channel sums leave each
 // 16-lane row in lane (t mod 16) of that row (register t / 16), then cross
@@ -218,8 +218,9 @@ template <typename T, int D, bool APPLY, bool FULL>
 __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j, int h, int start, int len,
                                                   float (*sRow)[C][PrecondThreads<D>::v / 16 + 1], float* sCen) {
   constexpr int NR = PrecondThreads<D>::v / 16;  // 16-lane rows
-  constexpr int G = 16;                          // tokens per sub-block
+  constexpr int G = 8;                           // tokens per sub-block
   constexpr int NB = C / G;
+  constexpr int NQ = C / 16;                     // per-token sum registers
   const int H = p.H, c = threadIdx.x, lane16 = c & 15;
   const bool active = c < D;
   const int cc = active ? c : 0;  // channel the lane reads (idle lanes mirror channel 0, contribute 0)
@@ -256,9 +257,9 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
     }
   }
   float dcen = 0.f;
-  float sg[NB], sb[NB];
+  float sg[NQ], sb[NQ];
 #pragma unroll
-  for (int q = 0; q < NB; ++q) sg[q] = sb[q] = 0.f;
+  for (int q = 0; q < NQ; ++q) sg[q] = sb[q] = 0.f;
 #pragma unroll 1
   for (int b = NB - 1; b >= 0; --b) {
     const int g0 = b * G;
@@ -305,8 +306,8 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
         const float vg = row_sum16(lam_t * eg * a_prev);
         const float vb = row_sum16(lam_t * kc * kc);
 #pragma unroll
-        for (int q = 0; q < NB; ++q) {
-          const bool mine = q == b && lane16 == u;
+        for (int q = 0; q < NQ; ++q) {
+          const bool mine = q == (t >> 4) && lane16 == (t & 15);
           sg[q] = mine ? vg : sg[q];
           sb[q] = mine ? vb : sb[q];
         }
@@ -319,7 +320,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
     return;
   }
 #pragma unroll
-  for (int q = 0; q < NB; ++q) {
+  for (int q = 0; q < NQ; ++q) {
     sRow[0][16 * q + lane16][c >> 4] = sg[q];
     sRow[1][16 * q + lane16][c >> 4] = sb[q];
   }
