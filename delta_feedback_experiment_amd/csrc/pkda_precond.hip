@@ -208,8 +208,8 @@ __device__ __forceinline__ float row_sum16(float v) {
 // Backward launches 1 (APPLY = false: lambda's local value before the chunk
 // from a zero start after it, into lam_chunk) and 3 (APPLY: from the lambda
 // entering the chunk, the gradients).  The chunk is walked in reverse in
-// sub-blocks of 8 tokens: a first forward pass keeps A at each sub-block's
-// start, and each sub-block recomputes its 8 A_t from there (the same
+// sub-blocks of 4 (apply) or 8 (local) tokens: a first forward pass keeps A at each sub-block's
+// start, and each sub-block recomputes its A_t from there (the same
 // arithmetic, so the same values) with its k, dkw and dk rows in registers.
 // Loads clamp as in the forward.  The per-token channel sums leave each
 // 16-lane row in lane (t mod 16) of that row (register t / 16), then cross
@@ -218,7 +218,7 @@ template <typename T, int D, bool APPLY, bool FULL>
 __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j, int h, int start, int len,
                                                   float (*sRow)[C][PrecondThreads<D>::v / 16 + 1], float* sCen) {
   constexpr int NR = PrecondThreads<D>::v / 16;  // 16-lane rows
-  constexpr int G = 8;                           // tokens per sub-block
+  constexpr int G = APPLY ? 4 : 8;               // tokens per sub-block (measured best for each pass)
   constexpr int NB = C / G;
   constexpr int NQ = C / 16;                     // per-token sum registers
   const int H = p.H, c = threadIdx.x, lane16 = c & 15;
