@@ -133,13 +133,13 @@ __device__ __forceinline__ float chunk_scan(const PrecondParams& p, float* buf, 
 }
 
 // Forward launches 1 (APPLY = false: local end A from zero into a_chunk) and
-// 3 (APPLY: A from a_chunk, kw out).  The chunk runs in sub-blocks of 16
+// 3 (APPLY: A from a_chunk, kw out).  The chunk runs in sub-blocks of 8
 // tokens whose k rows load before their chain runs; a short chunk
 // (FULL = false) clamps its loads to its last token and leaves the state
 // unchanged past it, so no load sits behind a branch.
 template <typename T, int D, bool APPLY, bool FULL>
 __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j, int h, int start, int len) {
-  constexpr int G = 16;
+  constexpr int G = 8;
   const int H = p.H, c = threadIdx.x;
   const T* __restrict__ k = static_cast<const T*>(p.k);
   T* __restrict__ kw = static_cast<T*>(p.kw);
