@@ -920,7 +920,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       const int rq = 4 * (lane >> 4);  // this lane's rows r0 + rq + e
       float ex[4] = {0.f, 0.f, 0.f, 0.f};
       float gnext = 0.f;
-#pragma unroll 1
+#pragma unroll 2
       for (int xo = 15; xo >= 0; --xo) {  // x as the column of rows r > x
         const int x = r0 + xo;
         const float gx = sG[x * L::LDG + c];
@@ -940,7 +940,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       float gprev = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) ex[e] = 0.f;
-#pragma unroll 1
+#pragma unroll 2
       for (int xo = 0; xo < 16; ++xo) {  // x as the row of columns r < x
         const int x = r0 + xo;
         const float gx = sG[x * L::LDG + c];
