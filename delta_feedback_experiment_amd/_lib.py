@@ -68,7 +68,7 @@ class PrecondArgs(ctypes.Structure):
         ("dkw", c_void_p), ("dk", c_void_p), ("dg_atk", c_void_p), ("dbeta_atk", c_void_p),
         ("dcenter_part", c_void_p), ("dcenter", c_void_p), ("dA0", c_void_p), ("dA_T", c_void_p),
         ("table", c_void_p), ("slot_idx", c_void_p), ("pool_size", c_int64), ("lam_chunk", c_void_p),
-        ("dk_final", c_void_p),
+        ("dk_final", c_void_p), ("kw32", c_void_p),
     ]
 
 
@@ -98,7 +98,7 @@ class ChunkBwdArgs(ctypes.Structure):
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
         ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p), ("grad_dtype", c_int32),
-        ("key_grad_dtype", c_int32),
+        ("key_grad_dtype", c_int32), ("kw32", c_void_p),
     ]
 
 

@@ -163,12 +163,15 @@ def chunk_backward(
     plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor, scale: float,
     initial_state: Tensor | None, saved: FwdSaved, do: Tensor, dht: Tensor | None, want_dh0: bool,
     grad_dtype: torch.dtype = torch.float32, key_grad_dtype: torch.dtype | None = None,
+    kw32: Tensor | None = None,
 ) -> BwdGrads:
     """Chunk backward on flat operands.  ``dq, dv`` come in ``grad_dtype``
     (FP32, or ``q.dtype``: the FP32 value rounded once in the kernel), ``dk,
     dkw`` in ``key_grad_dtype`` (default ``grad_dtype``; FP32 with a
     ``q.dtype`` ``grad_dtype`` for a caller that adds the preconditioner's
-    terms into them); the other gradients are FP32."""
+    terms into them); the other gradients are FP32.  ``kw32``: the write keys
+    in FP32 (per-channel gates with a BF16 write key), which the in-block
+    pair sums of the gate gradient then read."""
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
     ntok = plan.num_tokens
@@ -202,7 +205,10 @@ def chunk_backward(
         dh0=_ptr(dh0), qg=_ptr(saved.qg), kg=_ptr(saved.kg),
         grad_dtype=_lib.PKDA_F32 if grad_dtype == torch.float32 else _dtype_code(q),
         key_grad_dtype=_lib.PKDA_F32 if key_grad_dtype == torch.float32 else _dtype_code(q),
+        kw32=_ptr(kw32),
     )
+    if kw32 is not None and (kw32.dtype != torch.float32 or kw32.shape != kw.shape or not kw32.is_contiguous()):
+        raise ValueError("kw32 must be a contiguous float32 tensor of kw's shape")
     _lib.call("pkda_chunk_bwd", args, _stream(dev))
     return BwdGrads(dq, dk, dkw, dv, dbeta, dgcum, dh0)
 
@@ -285,29 +291,36 @@ class _ChunkPKDA(torch.autograd.Function):
         s0 = _f32(initial_state)
         gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32, decay_up)
         precond = g_atk is not None
+        needs_grad = any(ctx.needs_input_grad)
         if precond:
-            pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, x, eps, initial_A_state)
+            pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, x, eps, initial_A_state,
+                                         want_kw32=needs_grad and gcum.dim() == 3)
             kwf, A_T = pstate.kw, pstate.final_A
         else:
             pstate, kwf, A_T = None, kf, None
-        needs_grad = any(ctx.needs_input_grad)
         o, S_T, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, scale, s0,
                                       output_final_state, save_states=needs_grad and not lean)
         if needs_grad:
             ctx.plan, ctx.kind, ctx.scale, ctx.lean, ctx.x, ctx.eps = plan, kind, scale, lean, x, eps
             ctx.per_head_raw = use_gate and decay_up is None and g.dim() == q.dim() - 1
             ctx.g_shape = tuple(g.shape)
-            ctx.decay_up = decay_up
+            ctx.precond = precond
             ctx.up_dtype = None if decay_up is None else decay_up.dtype
             ctx.dtypes = tuple(None if t is None else t.dtype for t in (q, k, v, g, beta, g_atk, beta_atk,
                                                                           A_log, dt_bias, log_atk_scale,
                                                                           initial_state, initial_A_state))
-            ctx.saved_fwd = None if lean else saved
-            ctx.pstate = pstate
+            # every tensor the backward reads goes through save_for_backward
+            # (none through ctx attributes: A_T is an output, and keeping the
+            # scan state on ctx would tie output -> grad_fn -> ctx -> output)
+            fwd = (None,) * 7 if lean else (saved.w, saved.u, saved.aqk, saved.akk, saved.h, saved.qg, saved.kg)
             ctx.save_for_backward(qf, kf, kwf, vf, gcum, beta32, s0, g_used, A_log32, dt32,
                                   None if g_atk is None else _f32(g_atk),
                                   None if beta_atk is None else _f32(beta_atk),
-                                  None if log_atk_scale is None else _f32(log_atk_scale))
+                                  None if log_atk_scale is None else _f32(log_atk_scale),
+                                  decay_up,
+                                  None if pstate is None else pstate.a_chunk,
+                                  None if pstate is None else pstate.kw32,
+                                  *fwd)
         o = o.reshape(v.shape)
         return o, S_T, A_T
 
@@ -316,11 +329,13 @@ class _ChunkPKDA(torch.autograd.Function):
         from . import precond as pre
 
         (qf, kf, kwf, vf, gcum, beta32, s0, g_used, A_log32, dt32,
-         g_atk32, beta_atk32, center32) = ctx.saved_tensors
+         g_atk32, beta_atk32, center32, decay_up, a_chunk, kw32, *fwd) = ctx.saved_tensors
         plan = ctx.plan
-        saved = ctx.saved_fwd
-        if saved is None:  # lean: rebuild the chunk quantities
+        if ctx.lean:  # rebuild the chunk quantities
             _, _, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, False, True)
+        else:
+            saved = FwdSaved(*fwd)
+        pstate = pre.PrecondState(kwf, a_chunk, None, None, kw32) if ctx.precond else None
         dof = _flat(do.to(qf.dtype).contiguous(), plan)
         dht = None if dS_T is None else dS_T.float().contiguous()
         want_dh0 = ctx.needs_input_grad[10]
@@ -328,19 +343,19 @@ class _ChunkPKDA(torch.autograd.Function):
         # dtype, which the kernel then does; dk too unless the preconditioner
         # adds its terms into it (then FP32, as is dkw)
         direct = ctx.dtypes[0] == qf.dtype and ctx.dtypes[2] == qf.dtype
-        key_direct = direct and ctx.pstate is None and ctx.dtypes[1] == qf.dtype
+        key_direct = direct and pstate is None and ctx.dtypes[1] == qf.dtype
         gr = chunk_backward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, saved, dof, dht, want_dh0,
                             grad_dtype=qf.dtype if direct else torch.float32,
-                            key_grad_dtype=qf.dtype if key_direct else torch.float32)
+                            key_grad_dtype=qf.dtype if key_direct else torch.float32, kw32=kw32)
         dk = gr.dk
         dg_atk = dbeta_atk = dcenter = dA0 = None
-        if ctx.pstate is not None:
-            pg = pre.precond_backward(plan, kf, g_atk32, beta_atk32, center32, ctx.x, ctx.eps, ctx.pstate,
+        if pstate is not None:
+            pg = pre.precond_backward(plan, kf, g_atk32, beta_atk32, center32, ctx.x, ctx.eps, pstate,
                                       gr.dkw, dk, None if dA_T is None else dA_T.float().contiguous(),
                                       want_dA0=ctx.needs_input_grad[11])
             dg_atk, dbeta_atk, dcenter, dA0 = pg
         dg, dA_log, ddt_bias = gate_backward(plan, _flat(g_used, plan), ctx.kind, A_log32, dt32, gr.dgcum,
-                                             ctx.decay_up)
+                                             decay_up)
         shape = tuple(do.shape)
         dt = ctx.dtypes
 
@@ -352,7 +367,7 @@ class _ChunkPKDA(torch.autograd.Function):
 
         d_up = None
         if ctx.kind == _lib.GATE_LOW_RANK:
-            dg, d_up = low_rank_grads(dg, g_used, ctx.decay_up)
+            dg, d_up = low_rank_grads(dg, g_used, decay_up)
             dg = dg.reshape(ctx.g_shape)
             d_up = d_up.to(ctx.up_dtype) if ctx.needs_input_grad[13] else None
         else:

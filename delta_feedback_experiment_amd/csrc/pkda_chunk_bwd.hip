@@ -15,7 +15,13 @@
 // the gradients themselves: for every row r,
 //   dG_r = sum_c (q dq + k dk - kw dkw)[r, c]
 // with dk the read-key and dkw the write-key gradient of this chunk, plus, on
-// the chunk's last row, e^{G_C} sum(S0 * dS_C) + sum(Kg * dKg).
+// the chunk's last row, e^{G_C} sum(S0 * dS_C) + sum(Kg * dKg).  Two parts of
+// that sum are O(1) and cancel exactly: the diagonal pairs of Aqk (decay
+// e^0; s dAqk[t,t] q_t kw_t enters q dq and kw dkw alike) and the last row's
+// kw dKg (decay e^{G_C - G_C}; it enters -kw dkw and sum(Kg * dKg) alike).
+// Both are left out of dG, which then sums only terms that carry a decay
+// factor: under strong decay dG is ~e^g smaller than its terms were, and
+// forming it as the difference would lose that factor in FP32 rounding.
 //
 // Two kernels:
 //   state_bwd -- per (document, head, BV value columns), reverse over chunks,
@@ -63,6 +69,7 @@ struct BwdParams {
   bool kw_is_k;
   const void* qg;  // per-channel gates: s e^G q
   const void* kg;  // per-channel gates: e^{G_last - G} kw
+  const float* kw32;  // per-channel gates: kw in FP32 (BF16 kw otherwise), or null
 };
 
 // Deterministic sum of one value per thread over an NT-thread workgroup.
@@ -301,7 +308,8 @@ struct FusedBwdLayout {
   static constexpr int off_P1 = off_P2 + CT;            // beta_t dAkk E
   static constexpr int off_gam = off_P1 + CT;
   static constexpr int off_beta = off_gam + C * 4;
-  static constexpr int off_red = off_beta + C * 4;      // [kFW] floats
+  static constexpr int off_p2d = off_beta + C * 4;      // [64] s dAqk[t,t], FP32
+  static constexpr int off_red = off_p2d + C * 4;       // [kFW] floats
   static constexpr int bytes = off_red + kFW * 4;
 };
 
@@ -338,6 +346,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   E* sP1 = reinterpret_cast<E*>(smem + L::off_P1);
   float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+  float* sP2d = reinterpret_cast<float*>(smem + L::off_p2d);
   float* sRed = reinterpret_cast<float*>(smem + L::off_red);
 
   const T* hsrc = static_cast<const T*>(p.h) + ((int64_t)cid * H + hh) * D * D;
@@ -414,8 +423,11 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
-      const float val = (s <= t && t < len) ? scale * exp_fast(sGam[t] - sGam[s]) * acc[e] : 0.f;
+      // the diagonal (decay e^0) is kept apart, in FP32: its two halves of
+      // the gate gradient (q dq and kw dkw) cancel exactly and stay out of it
+      const float val = (s < t && t < len) ? scale * exp_fast(sGam[t] - sGam[s]) * acc[e] : 0.f;
       sP2[t * L::LDC + s] = to_e<E>(val);
+      if (s == t) sP2d[t] = t < len ? scale * acc[e] : 0.f;
     }
   }
   __syncthreads();
@@ -519,12 +531,18 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
       const float qv = from_e<E>(sQ[r * L::LD + c]);
       const float wv = from_e<E>(sKWr[r * L::LD + c]);
       const float tk = dkb[j][e] + ak[e];  // e^G dBw + sum_x P1r kw
+      const float pd = sP2d[r];
       dk[e] = sBeta[r] * tk;
       db[e] += kv * tk;
       dq[j][e] += aq[e];
-      dkw[e] = dkws[j][e] + aw[e];
-      kgd += wv * dkws[j][e];
-      gsum[e] += qv * dq[j][e] + kv * dk[e] - wv * dkw[e];
+      // Every term of the gate gradient carries a decay factor: the Aqk
+      // diagonal and the last row's state-path term (e^{G_C - G_C} = 1)
+      // appear once with each sign and are left out of both.
+      const float dkwg = (r == len - 1 ? 0.f : dkws[j][e]) + aw[e];
+      if (r != len - 1) kgd += wv * dkws[j][e];
+      gsum[e] += qv * dq[j][e] + kv * dk[e] - wv * dkwg;
+      dq[j][e] += pd * wv;
+      dkw[e] = dkws[j][e] + aw[e] + pd * qv;
     }
     if constexpr (kStage) {  // S0's and dBv's regions are free: stage for 16-byte stores
       store_acc_lds(sH, L::LD, dq[j], r0, 16 * ct, lane);
@@ -583,17 +601,20 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 // fused per-chunk backward, per-channel gate (G [64][D] per chunk).
 //
-// Same phases as the per-head kernel, with the decay inside every key
-// contraction:
+// The WY backward of the per-head kernel (dBv = T^T dU, dBw = -dBv S0^T,
+// dAkk = -dBv U^T), with the decay inside every key contraction:
 //   dq  = s e^G (dO S0^T) + sum_{x<=t} s dAqk[t,x] kw[x] e^{G[t]-G[x]}
-//   dk  = beta e^G (T^T dW) + beta_t sum_{x<t} dAkk[t,x] kw[x] e^{G[t]-G[x]}
+//   dk  = beta e^G dBw + beta_t sum_{x<t} dAkk[t,x] kw[x] e^{G[t]-G[x]}
 //   dkw = e^{G_C-G} (U dS_C^T) + sum_{t>x} beta_t dAkk[t,x] k[t] e^{G[t]-G[x]}
 //                              + sum_{t>=x} s dAqk[t,x] q[t] e^{G[t]-G[x]}
 // (channel by channel).  Pairs in different 16-row blocks go through MFMA
 // with the decay split at the block boundary -- every factor <= 1 -- and
-// pairs inside a block are summed exactly.  dG[t,c] = q dq + k dk - kw dkw
+// pairs inside a block are summed exactly (dAqk's blocks there in FP32, the
+// write key in FP32 when the caller has it).  dG[t,c] = q dq + k dk - kw dkw
 // per element, plus e^{G_C[c]} sum_v S0[c,v] dS_C[c,v] + sum_t kg dkg on the
-// last row.
+// last row, with the two parts that cancel exactly (the Aqk diagonal and
+// the last row's kg dkg) left out, and each pair's two halves formed from
+// the same rounded factors.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 struct FusedBwdPcLayout {
@@ -602,28 +623,37 @@ struct FusedBwdPcLayout {
   static constexpr int LDG = D + 4;
   static constexpr int RT = C * LD * (int)sizeof(T);
   static constexpr int CT = C * LDC * (int)sizeof(T);
-  static constexpr int off_U = 0;                       // U, then V          } phase 4: G [64][LDG]
-  static constexpr int off_T = off_U + RT;              // T                  }   (then KW when D = 64)
-  static constexpr int off_dT = off_T + CT;             //                    }
-  static constexpr int off_X = off_dT + CT;             //                    }
-  static constexpr int off_dO = off_X + CT;             // dO, then Bw, then K
-  static constexpr int off_dU = off_dO + RT;            // dU
-  static constexpr int off_dW = off_dU + RT;            // dW, then P1r
-  static constexpr int off_H = off_dW + RT;             // h, dH; then Q (| KW at D = 128)
-  static constexpr int off_P2 = off_H + D * LD * (int)sizeof(T);
-  static constexpr int off_beta = off_P2 + CT;
-  static constexpr int off_hd = off_beta + C * 4;       // [D]
+  static constexpr int HT = D * LD * (int)sizeof(T);
+  static constexpr int LDW = D + 4;                     // FP32 write-key tile
+  static constexpr int KWF_BYTES = C * LDW * 4;
+  static constexpr bool KWF_IN_H = KWF_BYTES <= HT;
+  static constexpr int off_U = 0;                       // U      } phase 3: G [64][LDG], then the
+  static constexpr int off_V = off_U + RT;              // V      }   transposed diagonal blocks
+  static constexpr int off_T = off_V + RT;              // T      }
+  static constexpr int off_dO = off_T + CT;             // dO, then K
+  static constexpr int off_dU = off_dO + RT;            // dU, then dBv, then Q
+  static constexpr int off_H = off_dU + RT;             // h, then dH, then kw in FP32 (when it fits)
+  static constexpr int off_P2 = off_H + HT;             // s dAqk (strictly lower)
+  static constexpr int off_P1 = off_P2 + CT;            // dAkk (strictly lower)
+  static constexpr int off_beta = off_P1 + CT;
+  static constexpr int off_p2d = off_beta + C * 4;      // [64] s dAqk[t,t], FP32
+  static constexpr int off_hd = off_p2d + C * 4;        // [D]
   static constexpr int off_kg = off_hd + D * 4;         // [4][D]
   static constexpr int off_red = off_kg + 4 * D * 4;    // [kFW]
-  static constexpr int bytes = off_red + kFW * 4;
-  // phase 4, over dU: the diagonal 16 x 16 blocks of dAkk and dAqk transposed, [4][16 x][16 t] each
-  static constexpr int off_P1T = off_dU;
-  static constexpr int off_P2T = off_P1T + 4 * 256 * (int)sizeof(T);
-  static_assert(8 * 256 * (int)sizeof(T) <= RT, "transposed blocks fit the dU region");
+  // BF16: s dAqk's diagonal 16 x 16 blocks also in FP32, [4][16 t][16 x] then
+  // [4][16 x][16 t] (FP32 tiles read them from P2 and its transposed copy)
+  static constexpr bool P2B = sizeof(T) < 4;
+  static constexpr int off_P2B = off_red + kFW * 4;
+  static constexpr int off_KWf = KWF_IN_H ? off_H : off_P2B + (P2B ? 2 * 4 * 256 * 4 : 0);
+  static constexpr int bytes = off_P2B + (P2B ? 2 * 4 * 256 * 4 : 0) + (KWF_IN_H ? 0 : KWF_BYTES);
+  static constexpr int off_Q = off_dU;
+  // phase 3, after G: the diagonal 16 x 16 blocks of dAkk and dAqk transposed, [4][16 x][16 t] each
   static constexpr int G_BYTES = C * LDG * 4;
-  static constexpr int off_KW = D == 2 * C ? off_H + C * LD * (int)sizeof(T) : off_U + G_BYTES;
-  static_assert(G_BYTES <= off_dO, "G fits the U..X region");
-  static_assert(D == 2 * C || G_BYTES + RT <= off_dO, "KW fits after G");
+  static constexpr int off_P1T = off_U + G_BYTES;
+  static constexpr int off_P2T = off_P1T + 4 * 256 * (int)sizeof(T);
+  static_assert(G_BYTES + 8 * 256 * (int)sizeof(T) <= off_dO, "G and the transposed blocks fit the U..T region");
+  static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
+  static_assert(D * (D / Vec16<T>::N) * 4 <= CT, "row partials of sum(h * dH) fit the T region");
 };
 
 template <typename T, int D, typename OT, typename OK>
@@ -644,23 +674,24 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   const int64_t row0 = (int64_t)ci.start * H + hh;
 
   E* sU = reinterpret_cast<E*>(smem + L::off_U);
-  E* sV = sU;
+  E* sV = reinterpret_cast<E*>(smem + L::off_V);
   float* sG = reinterpret_cast<float*>(smem + L::off_U);
   E* sT = reinterpret_cast<E*>(smem + L::off_T);
-  E* sdT = reinterpret_cast<E*>(smem + L::off_dT);
-  E* sX = reinterpret_cast<E*>(smem + L::off_X);
   E* sdO = reinterpret_cast<E*>(smem + L::off_dO);
-  E* sK = sdO;  // Bw in phase 3, raw K in phase 4
+  E* sK = sdO;
   E* sdU = reinterpret_cast<E*>(smem + L::off_dU);
-  E* sdW = reinterpret_cast<E*>(smem + L::off_dW);
-  E* sP1r = sdW;
+  E* sdBv = sdU;
   E* sH = reinterpret_cast<E*>(smem + L::off_H);
-  E* sQ = sH;
-  E* sKW = reinterpret_cast<E*>(smem + L::off_KW);
+  E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
+  float* sKWf = reinterpret_cast<float*>(smem + L::off_KWf);
   E* sP2 = reinterpret_cast<E*>(smem + L::off_P2);
+  E* sP1r = reinterpret_cast<E*>(smem + L::off_P1);
   E* sP1T = reinterpret_cast<E*>(smem + L::off_P1T);
   E* sP2T = reinterpret_cast<E*>(smem + L::off_P2T);
+  float* sP2B = reinterpret_cast<float*>(smem + L::off_P2B);
+  float* sP2BT = sP2B + 4 * 256;
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+  float* sP2d = reinterpret_cast<float*>(smem + L::off_p2d);
   float* sHD = reinterpret_cast<float*>(smem + L::off_hd);
   float* sKG = reinterpret_cast<float*>(smem + L::off_kg);
   float* sRed = reinterpret_cast<float*>(smem + L::off_red);
@@ -669,6 +700,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   const T* dhsrc = static_cast<const T*>(p.dh) + ((int64_t)cid * H + hh) * D * D;
   const T* kg_ = static_cast<const T*>(p.k) + row0 * D;
   const T* kwg = static_cast<const T*>(p.kw) + row0 * D;
+  const float* kw32g = p.kw32 ? p.kw32 + row0 * D : nullptr;
+  // the write key as the exact pair sums read it: FP32 when the caller has it
+  auto kwval = [&](int r, int c) { return kw32g ? kw32g[(int64_t)r * gs + c] : io<T>::load(kwg + (int64_t)r * gs + c); };
   const float* gg = p.gcum + row0 * D;        // G rows, stride gs
   const float* gC = gg + (int64_t)(len - 1) * gs;
   auto G = [&](int r, int c) { return gg[(int64_t)min(r, len - 1) * gs + c]; };
@@ -676,21 +710,31 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 
   if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
   {
-    RegTile<kFW, C, D, T> rU, rdO, rdU;
+    RegTile<kFW, C, D, T> rU, rdO, rdU, rV;
+    RegTile<kFW, C, C, T> rT;
     TiledTile<kFW, D, T> rH;
     rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
     rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
     rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
+    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
+    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rH.load(hsrc);
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
+    rV.store(sV, L::LD);
+    rT.store(sT, L::LDC);
     rH.store(sH, L::LD);
   }
   __syncthreads();
 
   f32x4 dq[HCT], dk[HCT], dkw[HCT], dv[HCT], dkws[HCT];
-  // ---- phase 1: dQg, dW, dAqk ---------------------------------------------------
+  float db[4] = {0.f, 0.f, 0.f, 0.f};
+  const int kbeg = kfloor<E>(r0);
+  // ---- phase 1: dQg = dO S0^T, dAqk = dO U^T, dBv = T^T dU ------------------------
+  // (dk's WY part goes through dBv too: with (Bv - Bw S0) = T^-1 U,
+  //   dBw = T^T dW = -dBv S0^T  and  dAkk = -T^T dT T^T = -dBv U^T,
+  // so neither dW nor dT is formed.)
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -699,9 +743,11 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
     for (int e = 0; e < 4; ++e) dq[j][e] = scale * exp_fast(G(r0 + acc_row(lane, e), c)) * acc[e];
-    f32x4 acw = zero4();
-    mma_tile<E, ROW, COL>(acw, sdU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
-    store_acc_lds(sdW, L::LD, -acw, r0, 16 * ct, lane);
+    f32x4 acv = zero4();
+    mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
+    dv[j] = acv;  // dBv until it is in LDS
+#pragma unroll
+    for (int e = 0; e < 4; ++e) db[e] += acv[e] * from_e<E>(sV[(r0 + acc_row(lane, e)) * L::LD + c]);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -711,18 +757,63 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
-      sP2[t * L::LDC + s] = to_e<E>((s <= t && t < len) ? scale * acc[e] : 0.f);
+      // the diagonal is kept apart in FP32 (its gate-gradient terms cancel)
+      const float val = (s < t && t < len) ? scale * acc[e] : 0.f;
+      sP2[t * L::LDC + s] = to_e<E>(val);
+      if (s == t) sP2d[t] = t < len ? scale * acc[e] : 0.f;
+      // In-block pairs are summed exactly from FP32 values: their gate terms
+      // carry the largest decay factors, and a BF16 copy of dAqk there moves
+      // dA_log by ~1e-2.
+      if (L::P2B && ct == rb) {
+        sP2B[(16 * rb + t - r0) * 16 + s - r0] = val;
+        sP2BT[(16 * rb + s - r0) * 16 + t - r0] = val;
+      }
     }
   }
   __syncthreads();
-  // ---- phase 2: dH replaces h; per-row sum(h * dH) ----------------------------
-  // (dH arrives tile-major: per-piece partial sums go through the dT region,
-  // which phase 3 fills only later, and are summed per row in a fixed order)
+  // dBv over dU (every wave has read dU); dv = beta dBv
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    store_acc_lds(sdBv, L::LD, dv[j], r0, 16 * (ch * HCT + j), lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dv[j][e] *= sBeta[r0 + acc_row(lane, e)];
+  }
+  __syncthreads();
+  // ---- phase 2: dBw = -dBv S0^T (-> dk), dAkk = -dBv U^T ------------------------
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int ct = ch * HCT + j;
+    const int c = 16 * ct + acc_col(lane);
+    f32x4 acc = zero4();
+    mma_tile<E, ROW, COL>(acc, sdBv, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = r0 + acc_row(lane, e);
+      const float eg = exp_fast(G(s, c));
+      const float kv = s < len ? io<T>::load(kg_ + s * gs + c) : 0.f;
+      dk[j][e] = -sBeta[s] * eg * acc[e];
+      db[e] -= acc[e] * eg * kv;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ct = 2 * ch + j;
+    f32x4 acc = zero4();
+    if (ct <= rb) mma_tile<E, ROW, COL>(acc, sdBv, L::LD, r0, sU, L::LD, 16 * ct, D, lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
+      sP1r[t * L::LDC + s] = to_e<E>((s < t && t < len) ? -acc[e] : 0.f);  // dAkk
+    }
+  }
+  __syncthreads();
+  // ---- phase 2b: dH replaces S0; per-row sum(S0 * dH); dKg = U dH^T --------------
+  // (dH arrives tile-major: per-piece partial sums go through the T region,
+  // dead since phase 1, and are summed per row in a fixed order)
   {
     constexpr int V = Vec16<T>::N;
     constexpr int PPR = D / V;  // pieces per row
-    float* sPart = reinterpret_cast<float*>(smem + L::off_dT);
-    static_assert(D * PPR * 4 <= L::CT, "row partials fit the dT region");
+    float* sPart = reinterpret_cast<float*>(smem + L::off_T);
     TiledTile<kFW, D, T> rdH;
     rdH.load(dhsrc);
 #pragma unroll
@@ -745,7 +836,6 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       sHD[tid] = sum;
     }
   }
-  __syncthreads();
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -757,114 +847,128 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     for (int e = 0; e < 4; ++e) {
       const int s = r0 + acc_row(lane, e);
       dkws[j][e] = exp_fast(gC[c] - G(s, c)) * acc[e];
-      if (s < len) col += io<T>::load(kwg + s * gs + c) * dkws[j][e];
+      // the last row's term (decay e^0) cancels against its own -kw dkw
+      if (s < len - 1) col += kwval(s, c) * dkws[j][e];
     }
     col += __shfl_xor(col, 16);
     col += __shfl_xor(col, 32);
     if (lane < 16) sKG[rb * D + 16 * ct + lane] = col;
   }
   __syncthreads();
-  // ---- phase 3: WY backward ----------------------------------------------------
-  {
-    RegTile<kFW, C, D, T> rV, rK, rQ;
-    RegTile<kFW, C, C, T> rT;
-    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
-    rK.load(kg_, gs, len);
-    rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
-    rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
-    rV.store(sV, L::LD);
-    rK.store(sK, L::LD, [&](int r, int c, float x) { return sBeta[r] * exp_fast(G(r, c)) * x; });  // Bw
-    rT.store(sT, L::LDC);
-    rQ.store(sQ, L::LD);
-  }
-  if (!p.kw_is_k && D == 2 * C) load_tile<kFW, C, D>(sKW, L::LD, kwg, gs, len, Ident());
-  __syncthreads();
-  const int kbeg = kfloor<E>(r0);
-  float db[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < HCT; ++j) {
-    const int ct = ch * HCT + j;
-    const int c = 16 * ct + acc_col(lane);
-    f32x4 acc = zero4();
-    mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdW, L::LD, 16 * ct, kbeg, C, lane);  // dBw = T^T dW
-    f32x4 acv = zero4();
-    mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int s = r0 + acc_row(lane, e);
-      const float eg = exp_fast(G(s, c));
-      const float kv = s < len ? io<T>::load(kg_ + s * gs + c) : 0.f;
-      const float vv = from_e<E>(sV[s * L::LD + c]);
-      dk[j][e] = sBeta[s] * eg * acc[e];
-      dv[j][e] = sBeta[s] * acv[e];
-      db[e] += acc[e] * eg * kv + acv[e] * vv;
-    }
-  }
-  // dT = dW Bw^T + (dU V^T) diag(beta)
-  f32x4 dTacc[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ct = 2 * ch + j;
-    f32x4 a1 = zero4(), a2 = zero4();
-    mma_tile<E, ROW, COL>(a1, sdW, L::LD, r0, sK, L::LD, 16 * ct, D, lane);
-    mma_tile<E, ROW, COL>(a2, sdU, L::LD, r0, sV, L::LD, 16 * ct, D, lane);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) dTacc[j][e] = a1[e] + sBeta[16 * ct + acc_col(lane)] * a2[e];
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) store_acc_lds(sdT, L::LDC, dTacc[j], r0, 16 * (2 * ch + j), lane);
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ct = 2 * ch + j;
-    f32x4 acc = zero4();
-    mma_tile_range<E, COL, ROW>(acc, sT, L::LDC, r0, sdT, L::LDC, 16 * ct, kbeg, C, lane);  // X = T^T dT
-    store_acc_lds(sX, L::LDC, acc, r0, 16 * ct, lane);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ct = 2 * ch + j;
-    f32x4 acc = zero4();
-    if (ct <= rb) mma_tile_range<E, ROW, COL>(acc, sX, L::LDC, r0, sT, L::LDC, 16 * ct, 0, kceil<E>(16 * ct + 16), lane);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = r0 + acc_row(lane, e), s = 16 * ct + acc_col(lane);
-      const float raw = (s < t && t < len) ? -acc[e] : 0.f;  // dAkk
-      sP1r[t * L::LDC + s] = to_e<E>(raw);
-    }
-  }
-  __syncthreads();
-  // ---- phase 4: pairwise terms with the decay inside the contraction ----------
+  // ---- phase 3: pairwise terms with the decay inside the contraction ----------
   // dAkk is held once (unscaled); beta_t multiplies the other factor, so the
   // two halves of each (t, x) pair's gate term see the same rounded value.
   load_tile<kFW, C, D>(sK, L::LD, kg_, gs, len, Ident());
+  load_tile<kFW, C, D>(sQ, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, len, Ident());
   for (int i = tid; i < C * (D / 4); i += kFW) {
     const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
     *reinterpret_cast<float4*>(sG + r * L::LDG + c) =
         *reinterpret_cast<const float4*>(gg + (int64_t)min(r, len - 1) * gs + c);
   }
-  if (!p.kw_is_k && D != 2 * C) load_tile<kFW, C, D>(sKW, L::LD, kwg, gs, len, Ident());
-  if (ch == 0) {  // this row block's diagonal blocks, transposed (dU is dead)
+  // the write key in FP32 (kw32, else kw or k widened); zero rows past the chunk
+  for (int i = tid; i < C * (D / 4); i += kFW) {
+    const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
+    float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < len) {
+      if (kw32g) {
+        w = *reinterpret_cast<const float4*>(kw32g + (int64_t)r * gs + c);
+      } else {
+        const T* src = (p.kw_is_k ? kg_ : kwg) + (int64_t)r * gs + c;
+        w = make_float4(io<T>::load(src), io<T>::load(src + 1), io<T>::load(src + 2), io<T>::load(src + 3));
+      }
+    }
+    *reinterpret_cast<float4*>(sKWf + r * L::LDW + c) = w;
+  }
+  if (ch == 0) {  // this row block's diagonal blocks, transposed
     for (int i = lane; i < 256; i += 64) {
       const int xo = i >> 4, to = i & 15;
       sP1T[(16 * rb + xo) * 16 + to] = sP1r[(r0 + to) * L::LDC + r0 + xo];
-      sP2T[(16 * rb + xo) * 16 + to] = sP2[(r0 + to) * L::LDC + r0 + xo];
+      if (!L::P2B) sP2T[(16 * rb + xo) * 16 + to] = sP2[(r0 + to) * L::LDC + r0 + xo];
     }
   }
   __syncthreads();
-  const E* sKWr = p.kw_is_k ? sK : sKW;
   const int rlo = r0 - 1;   // last row before this row block (G[-1] = 0)
-  const int rhi = r0 + 15;  // last row of this row block
-  float gsum[4] = {0.f, 0.f, 0.f, 0.f};
+  // Pairs (t, x) in different row blocks go through MFMA with the decay split
+  // at R = (first row of t's block) - 1: e^{G[t]-G[x]} = e^{G[t]-G[R]} e^{G[R]-G[x]},
+  // each factor <= 1.  The row side (t) takes kw[x] e^{G[R]-G[x]} as its B
+  // operand, the column side (x) takes q[t] e^{G[t]-G[R]} (or beta k) -- both
+  // rounded to the MFMA's input type.  The gate gradient of a pair enters row t
+  // and row x with opposite signs and must cancel in the chunk's reverse sum:
+  // both halves are formed from the same two rounded factors (a row half
+  // a(t) * sum_x P b(x), a column half b(x) * sum_t P a(t)).  Formed from the
+  // unrounded factor on one side, the halves differ by the operand's rounding
+  // and dA_log, a sum of the gate gradient over the whole head, moves by ~4e-2.
+  auto rnd = [](float x) { return from_e<E>(to_e<E>(x)); };
 #pragma unroll 1
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
-    const int nn = 16 * ct + (lane & 15);  // this lane's B column
-    // (a) rows t of this block, x in earlier blocks: split at rlo
-    f32x4 akA = zero4(), aqP = zero4();
+    const int nn = 16 * ct + (lane & 15);  // this lane's B column (== c)
+    const int rq = 4 * (lane >> 4);        // this lane's rows r0 + rq + e
+    float gr[4], kv[4], qv[4], wv[4];
+    f32x4 dg;
+    {
+      float kgc = 0.f;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) kgc += sKG[b * D + c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r0 + rq + e;
+        gr[e] = sG[r * L::LDG + c];
+        kv[e] = from_e<E>(sK[r * L::LD + c]);
+        qv[e] = from_e<E>(sQ[r * L::LD + c]);
+        wv[e] = sKWf[r * L::LDW + c];
+        const float pd = sP2d[r];
+        // terms without a pair: the state parts of dq, dk and dkw; the Aqk
+        // diagonal and the last row's state-path write-key term (decay e^0)
+        // enter two of q dq, kw dkw and sum(kg dkg) with opposite signs and
+        // are left out of the gate gradient
+        dg[e] = qv[e] * dq[j][e] + kv[e] * dk[j][e] - (r == len - 1 ? 0.f : wv[e] * dkws[j][e]);
+        if (r == len - 1) dg[e] += exp_fast(gC[c]) * sHD[c] + kgc;
+        dq[j][e] += pd * wv[e];
+        dkw[j][e] = dkws[j][e] + pd * qv[e];
+      }
+    }
+    // (1) rows t of this block, x < t inside it: exactly, e^{G[t]-G[x]} as the
+    // running product of the per-token decays e^{G[y]-G[y-1]} (each <= 1)
+    // from x + 1 to t, started at 1 on the diagonal and 0 past it.  dAkk and
+    // dAqk are zero off their triangles (dAqk's diagonal is held apart), so
+    // no pair needs a mask.
+    {
+      f32x4 ak = zero4(), aq = zero4();
+      float ex[4] = {0.f, 0.f, 0.f, 0.f};
+      float gnext = 0.f;
+#pragma unroll 2
+      for (int xo = 15; xo >= 0; --xo) {
+        const int x = r0 + xo;
+        const float gx = sG[x * L::LDG + c];
+        const float d = xo < 15 ? exp_fast(gnext - gx) : 0.f;  // decay of token x + 1
+        gnext = gx;
+        const float kwx = sKWf[x * L::LDW + c];
+        float p1[4], p2[4];
+        lds4(sP1T + (16 * rb + xo) * 16 + rq, p1);
+        if constexpr (L::P2B) lds4(sP2BT + (16 * rb + xo) * 16 + rq, p2);
+        else lds4(sP2T + (16 * rb + xo) * 16 + rq, p2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool diag = xo == rq + e;
+          ex[e] = diag ? 1.f : ex[e] * d;
+          ak[e] += p1[e] * kwx * ex[e];
+          aq[e] += diag ? 0.f : p2[e] * kwx * ex[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float bk = sBeta[r0 + rq + e] * ak[e];
+        dk[j][e] += bk;
+        db[e] += kv[e] * ak[e];
+        dq[j][e] += aq[e];
+        dg[e] += qv[e] * aq[e] + kv[e] * bk;
+      }
+    }
+    // (2) rows t of this block, x in earlier blocks: split at rlo
     if (rb > 0) {
+      f32x4 akX = zero4(), aqX = zero4();
       const float grlo = sG[rlo * L::LDG + nn];
       for (int k0 = 0; k0 < kceil<E>(r0); k0 += Mma<E>::KS) {
         const int kk = k0 + F::off(lane);
@@ -874,72 +978,28 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
           const int x = kk + jj;
           a1[jj] = from_e<E>(sP1r[(r0 + (lane & 15)) * L::LDC + x]);
           a2[jj] = from_e<E>(sP2[(r0 + (lane & 15)) * L::LDC + x]);
-          bx[jj] = x <= rlo ? from_e<E>(sKWr[x * L::LD + nn]) * exp_fast(grlo - sG[x * L::LDG + nn]) : 0.f;
+          bx[jj] = x <= rlo ? sKWf[x * L::LDW + nn] * exp_fast(grlo - sG[x * L::LDG + nn]) : 0.f;
         }
-        F::mfma(akA, a1, bx);
-        F::mfma(aqP, a2, bx);
+        F::mfma(akX, a1, bx);
+        F::mfma(aqX, a2, bx);
+      }
+      const float grlo_c = sG[rlo * L::LDG + c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float sb = sBeta[r0 + rq + e];
+        const float dlo = exp_fast(gr[e] - grlo_c);  // e^{G[t]-G[R]}
+        dk[j][e] += sb * dlo * akX[e];
+        db[e] += kv[e] * dlo * akX[e];
+        dq[j][e] += dlo * aqX[e];
+        // the column side's B operands of these pairs: beta k e^{G[t]-G[R]}, q e^{G[t]-G[R]}
+        dg[e] += rnd(sb * kv[e] * dlo) * akX[e] + rnd(qv[e] * dlo) * aqX[e];
       }
     }
-    // (c) rows x of this block, t in later blocks: split at rhi
-    f32x4 awA = zero4(), awP = zero4();
-    if (rb < 3) {
-      const float grhi = sG[rhi * L::LDG + nn];
-      for (int k0 = kfloor<E>(r0 + 16); k0 < C; k0 += Mma<E>::KS) {
-        const int kk = k0 + F::off(lane);
-        float a1[F::N], a2[F::N], b1[F::N], b2[F::N];
-#pragma unroll
-        for (int jj = 0; jj < F::N; ++jj) {
-          const int t = kk + jj;
-          a1[jj] = from_e<E>(sP1r[t * L::LDC + r0 + (lane & 15)]);
-          a2[jj] = from_e<E>(sP2[t * L::LDC + r0 + (lane & 15)]);
-          const float f = t > rhi ? exp_fast(sG[t * L::LDG + nn] - grhi) : 0.f;
-          b1[jj] = sBeta[t] * from_e<E>(sK[t * L::LD + nn]) * f;  // beta_t on the key, dAkk unscaled
-          b2[jj] = from_e<E>(sQ[t * L::LD + nn]) * f;
-        }
-        F::mfma(awA, a1, b1);
-        F::mfma(awP, a2, b2);
-      }
-    }
-    // split factors back onto the output rows, plus the in-block pairs exactly
-    const float grlo_c = rb > 0 ? sG[rlo * L::LDG + c] : 0.f;
-    const float grhi_c = sG[rhi * L::LDG + c];
-    float gr[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      gr[e] = sG[(r0 + acc_row(lane, e)) * L::LDG + c];
-      akA[e] *= exp_fast(gr[e] - grlo_c);
-      aqP[e] *= exp_fast(gr[e] - grlo_c);
-      awA[e] *= exp_fast(grhi_c - gr[e]);
-      awP[e] *= exp_fast(grhi_c - gr[e]);
-    }
-    // Pairs inside the row block, exactly: e^{G[a]-G[b]} (a >= b) is the
-    // running product of the per-token decays e^{G[y]-G[y-1]} (each <= 1)
-    // from b + 1 to a, started at 1 on the diagonal and 0 past it.  dAkk and
-    // dAqk are zero off their triangles, so no pair needs a mask.
+    // (3) rows x of this block, t > x inside it: exactly, as (1)
     {
-      const int rq = 4 * (lane >> 4);  // this lane's rows r0 + rq + e
+      f32x4 aw = zero4();
       float ex[4] = {0.f, 0.f, 0.f, 0.f};
-      float gnext = 0.f;
-#pragma unroll 2
-      for (int xo = 15; xo >= 0; --xo) {  // x as the column of rows r > x
-        const int x = r0 + xo;
-        const float gx = sG[x * L::LDG + c];
-        const float d = xo < 15 ? exp_fast(gnext - gx) : 0.f;  // decay of token x + 1
-        gnext = gx;
-        const float kwx = from_e<E>(sKWr[x * L::LD + c]);
-        float p1[4], p2[4];
-        lds4(sP1T + (16 * rb + xo) * 16 + rq, p1);
-        lds4(sP2T + (16 * rb + xo) * 16 + rq, p2);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ex[e] = xo == rq + e ? 1.f : ex[e] * d;
-          akA[e] += p1[e] * kwx * ex[e];
-          aqP[e] += p2[e] * kwx * ex[e];
-        }
-      }
       float gprev = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ex[e] = 0.f;
 #pragma unroll 2
       for (int xo = 0; xo < 16; ++xo) {  // x as the row of columns r < x
         const int x = r0 + xo;
@@ -950,50 +1010,58 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         const float qx = from_e<E>(sQ[x * L::LD + c]);
         float p1[4], p2[4];
         lds4(sP1r + x * L::LDC + r0 + rq, p1);
-        lds4(sP2 + x * L::LDC + r0 + rq, p2);
+        if constexpr (L::P2B) lds4(sP2B + (16 * rb + xo) * 16 + rq, p2);
+        else lds4(sP2 + x * L::LDC + r0 + rq, p2);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          ex[e] = xo == rq + e ? 1.f : ex[e] * d;
-          awA[e] += p1[e] * kx * ex[e];
-          awP[e] += p2[e] * qx * ex[e];
+          const bool diag = xo == rq + e;
+          ex[e] = diag ? 1.f : ex[e] * d;
+          aw[e] += p1[e] * kx * ex[e] + (diag ? 0.f : p2[e] * qx * ex[e]);
         }
       }
-    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = r0 + acc_row(lane, e);
-      const float kv = from_e<E>(sK[r * L::LD + c]);
-      const float qv = from_e<E>(sQ[r * L::LD + c]);
-      const float wv = from_e<E>(sKWr[r * L::LD + c]);
-      dk[j][e] += sBeta[r] * akA[e];
-      db[e] += kv * akA[e];
-      dq[j][e] += aqP[e];
-      dkw[j][e] = dkws[j][e] + awA[e] + awP[e];
+      for (int e = 0; e < 4; ++e) {
+        dkw[j][e] += aw[e];
+        dg[e] -= wv[e] * aw[e];
+      }
     }
+    // (4) rows x of this block, t in each later block bi: split at 16 bi - 1
+    for (int bi = rb + 1; bi < 4; ++bi) {
+      const int R = 16 * bi - 1;
+      const float gR = sG[R * L::LDG + nn];
+      f32x4 aw = zero4();
+      for (int k0 = kfloor<E>(16 * bi); k0 < 16 * bi + 16; k0 += Mma<E>::KS) {
+        const int kk = k0 + F::off(lane);
+        float a1[F::N], a2[F::N], b1[F::N], b2[F::N];
+#pragma unroll
+        for (int jj = 0; jj < F::N; ++jj) {
+          const int t = kk + jj;
+          a1[jj] = from_e<E>(sP1r[t * L::LDC + r0 + (lane & 15)]);
+          a2[jj] = from_e<E>(sP2[t * L::LDC + r0 + (lane & 15)]);
+          const float f = t > R && t <= R + 16 ? exp_fast(sG[t * L::LDG + nn] - gR) : 0.f;
+          b1[jj] = sBeta[t] * from_e<E>(sK[t * L::LD + nn]) * f;  // beta_t on the key, dAkk unscaled
+          b2[jj] = from_e<E>(sQ[t * L::LD + nn]) * f;
+        }
+        F::mfma(aw, a1, b1);
+        F::mfma(aw, a2, b2);
+      }
+      const float gRc = sG[R * L::LDG + c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float dec = exp_fast(gRc - gr[e]);  // e^{G[R]-G[x]}
+        dkw[j][e] += dec * aw[e];
+        dg[e] -= rnd(wv[e] * dec) * aw[e];  // the row side's B operand kw e^{G[R]-G[x]}
+      }
+    }
+    store_acc_global<float>(p.dgcum + row0 * D, gs, dg, r0, 16 * ct, len, lane);
   }
   // ---- outputs -------------------------------------------------------------
   OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
   OK* dko = static_cast<OK*>(p.dk) + row0 * D;
   OT* dvo = static_cast<OT*>(p.dv) + row0 * D;
-  float* dgo = p.dgcum + row0 * D;
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
-    const int c = 16 * ct + acc_col(lane);
-    float kgc = 0.f;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) kgc += sKG[b * D + c];
-    f32x4 dg;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = r0 + acc_row(lane, e);
-      const float kv = from_e<E>(sK[r * L::LD + c]);
-      const float qv = from_e<E>(sQ[r * L::LD + c]);
-      const float wv = from_e<E>(sKWr[r * L::LD + c]);
-      dg[e] = qv * dq[j][e] + kv * dk[j][e] - wv * dkw[j][e];
-      if (r == len - 1) dg[e] += exp_fast(gC[c]) * sHD[c] + kgc;
-    }
-    store_acc_global<float>(dgo, gs, dg, r0, 16 * ct, len, lane);
     store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
     store_acc_global<OT>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
     if (p.kw_is_k) {
@@ -1369,6 +1437,7 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   p.kw_is_k = kw_is_k;
   p.qg = a->gate_per_channel ? a->qg : nullptr;
   p.kg = a->gate_per_channel ? a->kg : nullptr;
+  p.kw32 = a->gate_per_channel && !kw_is_k && a->dtype == PKDA_BF16 ? a->kw32 : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   if (a->dtype == PKDA_BF16) {

@@ -61,6 +61,7 @@ struct PrecondParams {
   const int32_t* slot;  // forward: document -> A-state row, or null
   float* lam_chunk;
   void* dk_final;  // backward: dk + the terms here in k's dtype (dk untouched), or null
+  float* kw32;     // forward: kw also in FP32, or null
 };
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
@@ -163,7 +164,10 @@ __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j,
       if (APPLY) {
         const float r = logf(a + p.eps) - center;
         const float w = kc[u] * expf(-p.log_x * (r / (1.f + fabsf(r))));
-        if (FULL || t < len) io<T>::store(kw + th * D + c, w);
+        if (FULL || t < len) {
+          io<T>::store(kw + th * D + c, w);
+          if (p.kw32) p.kw32[th * D + c] = w;
+        }
       }
     }
   }
@@ -423,6 +427,7 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
   p.slot = a->slot_idx;
   p.lam_chunk = a->lam_chunk;
   p.dk_final = a->dk_final;
+  p.kw32 = a->kw32;
   PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed A states need pool_size > 0");
   return 0;
 }

@@ -29,6 +29,11 @@ SAVED_ALWAYS = ("k_write", "a_chunk")
 """Saved by every forward: the preconditioned write keys and the
 preconditioner state entering each chunk."""
 
+SAVED_WIDE_KEY = "k_write32"
+"""Saved after ``k_write`` when the activations are narrower than FP32: the
+write keys in FP32, from which the backward sums the gate gradient's
+in-block pairs."""
+
 SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h", "qg", "kg")
 """Saved as well unless ``lean``: W, the corrected values U, the intra-chunk
 query-key products, the inverted WY matrix, the chunk-entry states and the
@@ -42,10 +47,10 @@ def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int
     chunks = -(-T // CHUNK_SIZE)
     act = q.dtype
     ntok = B * T
-    meta = [
-        ((ntok, H, K), act),                      # k_write
-        ((B * chunks, H, K), torch.float32),      # a_chunk
-    ]
+    meta = [((ntok, H, K), act)]                  # k_write
+    if act != torch.float32:
+        meta.append(((ntok, H, K), torch.float32))  # k_write32
+    meta.append(((B * chunks, H, K), torch.float32))  # a_chunk
     if not lean:
         meta += [
             ((ntok, H, K), act),                  # w
@@ -59,9 +64,15 @@ def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int
     return tuple(meta)
 
 
+def saved_names(q: Tensor, lean: bool) -> tuple[str, ...]:
+    """Names of the saved intermediates, in the order of :func:`intermediate_meta`."""
+    wide = (SAVED_WIDE_KEY,) if q.dtype != torch.float32 else ()
+    return SAVED_ALWAYS[:1] + wide + SAVED_ALWAYS[1:] + (() if lean else SAVED_RETAINED)
+
+
 def _check_saved(saved: list[Tensor], q: Tensor, v: Tensor, lean: bool) -> None:
     expected = intermediate_meta(q, v, lean)
-    names = SAVED_ALWAYS + (() if lean else SAVED_RETAINED)
+    names = saved_names(q, lean)
     if len(saved) != len(expected):
         raise RuntimeError(f"pkda_recurrence saved {len(saved)} tensors, not {len(expected)}")
     for name, t, (shape, dtype) in zip(names, saved, expected):
@@ -96,7 +107,8 @@ def _forward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, s
         gf = gf.float()
     A32, dt32 = _f32(A_log), _f32(dt_bias)
     gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)
-    pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, None)
+    pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, None,
+                                 want_kw32=True)
     beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
     o, _, fs = chunk_forward(plan, qf, kf, pstate.kw, vf, gcum, beta32, scale, None, False, save_states=save_all)
     return plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs
@@ -119,7 +131,7 @@ def pkda_recurrence(
         (plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs) = _forward(
             q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, scale, squash_x, squash_eps,
             save_all=not lean)
-    saved = [pstate.kw, pstate.a_chunk]
+    saved = [pstate.kw] + ([] if pstate.kw32 is None else [pstate.kw32]) + [pstate.a_chunk]
     if not lean:
         saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h, fs.qg, fs.kg]
     _check_saved(saved, q, v, lean)
@@ -153,16 +165,17 @@ def pkda_recurrence_backward(
         A32, dt32 = _f32(A_log), _f32(dt_bias)
         beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
         gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)  # relaunched, as the forward ran it
-        kw, a_chunk = saved[0], saved[1]
+        named = dict(zip(saved_names(q, lean), saved))
+        kw, kw32, a_chunk = named["k_write"], named.get(SAVED_WIDE_KEY), named["a_chunk"]
         if lean:
             _, _, fs = chunk_forward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, False, save_states=True)
         else:
-            fs = FwdSaved(*saved[2:9])
+            fs = FwdSaved(*(named[n] for n in SAVED_RETAINED))
         dof = flat(do.to(q.dtype))
         # dq, dv leave the kernel in the input dtype; dk, dkw stay FP32 for the
         # preconditioner's terms
         gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False,
-                            grad_dtype=qf.dtype, key_grad_dtype=torch.float32)
+                            grad_dtype=qf.dtype, key_grad_dtype=torch.float32, kw32=kw32)
         pstate = pre.PrecondState(kw, a_chunk, None, None)
         dk = torch.empty_like(kf)  # the preconditioner's scan writes the final dk in k's dtype
         dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(

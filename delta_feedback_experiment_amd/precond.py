@@ -25,8 +25,9 @@ from .pkda import _dtype_code, _f32, _ptr, _stream
 class PrecondState:
     kw: Tensor            # [N_tok, H, K], dtype of k
     a_chunk: Tensor       # [num_chunks, H, K] FP32, A entering each chunk
-    final_A: Tensor       # [N, H, K] FP32
+    final_A: Tensor | None  # [N, H, K] FP32
     initial_A: Tensor | None
+    kw32: Tensor | None = None  # kw in FP32 as well (when k is narrower and it was asked for)
 
 
 def _flat2(t: Tensor, plan) -> Tensor:
@@ -35,12 +36,15 @@ def _flat2(t: Tensor, plan) -> Tensor:
 
 def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
                     initial_A_state: Tensor | None, *, slot_idx: Tensor | None = None,
-                    final_A: Tensor | None = None) -> PrecondState:
+                    final_A: Tensor | None = None, want_kw32: bool = False) -> PrecondState:
     """Write keys for flat ``kf [N_tok, H, K]``; returns the scan's state.
 
     With ``slot_idx`` the A states are rows of a pool: ``initial_A_state``
     (zero when ``None``) and ``final_A`` are contiguous FP32 ``[P, H, K]``,
-    used in place (no conversion copy), document ``n`` at row ``slot_idx[n]``."""
+    used in place (no conversion copy), document ``n`` at row ``slot_idx[n]``.
+    ``want_kw32`` also returns the write keys in FP32 when ``kf`` is narrower
+    (the chunk backward with per-channel gates sums its in-block pairs from
+    them)."""
     dev = kf.device
     H, K, N = plan.heads, plan.head_dim, plan.num_seqs
     ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
@@ -53,6 +57,7 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
         if a0 is not None and tuple(a0.shape) != (N, H, K):
             raise ValueError(f"initial_A_state must be {(N, H, K)}")
     kw = torch.empty_like(kf)
+    kw32 = torch.empty(kf.shape, device=dev, dtype=torch.float32) if want_kw32 and kf.dtype != torch.float32 else None
     a_chunk = torch.empty(plan.num_chunks, H, K, device=dev, dtype=torch.float32)
     if final_A is None:
         final_A = torch.empty(N, H, K, device=dev, dtype=torch.float32)
@@ -61,10 +66,10 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
         cu_seqlens=_ptr(plan.cu_seqlens), k=_ptr(kf), g_atk=_ptr(ga), beta_atk=_ptr(ba), center=_ptr(cen),
         squash_x=float(x), squash_eps=float(eps), initial_A_state=_ptr(a0), final_A_state=_ptr(final_A),
         kw=_ptr(kw), a_chunk=_ptr(a_chunk), num_chunks=plan.num_chunks, table=_ptr(plan.table),
-        slot_idx=_ptr(slot_idx), pool_size=final_A.shape[0] if slot_idx is not None else 0,
+        slot_idx=_ptr(slot_idx), pool_size=final_A.shape[0] if slot_idx is not None else 0, kw32=_ptr(kw32),
     )
     _lib.call("pkda_precond_fwd", args, _stream(dev))
-    return PrecondState(kw, a_chunk, final_A, a0)
+    return PrecondState(kw, a_chunk, final_A, a0, kw32)
 
 
 def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,

@@ -251,6 +251,8 @@ typedef struct pkda_precond_args {
   float* lam_chunk;              /* backward workspace [num_chunks, H, K] */
   void* dk_final;                /* backward, optional: dk + the preconditioner's terms
                                     written here in dtype, dk left as it came in */
+  float* kw32;                   /* forward, optional: kw [N_tok,H,K] also in FP32 (the
+                                    chunk backward's exact in-block pair sums read it) */
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
@@ -365,6 +367,12 @@ typedef struct pkda_chunk_bwd_args {
   const void *qg, *kg;         /* per-channel gates only: the forward's qg, kg */
   int32_t grad_dtype;          /* dq, dv: PKDA_F32 or dtype (one rounding of the FP32 value) */
   int32_t key_grad_dtype;      /* dk, dkw: grad_dtype, or PKDA_F32 when grad_dtype is dtype */
+  /* Optional, per-channel gates with a separate write key in BF16: kw in FP32
+   * [N_tok,H,K] (pkda_precond_args.kw32).  The gate gradient's largest terms
+   * are the in-block query/key pairs, summed exactly; formed from the BF16
+   * write key they move dA_log (a sum of the gate gradient over a whole head)
+   * by ~1e-2.  NULL: the BF16 kw serves. */
+  const float* kw32;
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);

@@ -335,15 +335,14 @@ def _grad_case_pc(dev, B, T, H, D, dtype, seed, cu=None, all_strong=False):
 
 def test_chunk_per_channel_saturating_decay(dev):
     """Every token decays by e^-8 on every channel (e^-128 across a block):
-    no overflow anywhere, and every output matches the FP32 oracle to 1e-5
-    except dg.  dg is the reverse chunk-local sum of per-token terms
-    q.dq + k.dk - kw.dkw that are each O(1) while |dg| ~ 1e-3 here, so FP32
-    rounding of the terms is amplified ~2000x (the FP32 oracle itself agrees
-    with FP64 to 1e-7 on this case); its bound is 1e-3."""
+    no overflow anywhere, and every output matches the FP32 oracle to 1e-5.
+    dg is ~e^-8 of the O(1) per-token terms (q.dq, k.dk, kw.dkw) it would be
+    the difference of: this case fails if the kernel forms it that way
+    rather than from the decay-carrying terms alone."""
     print("[gpu] chunk per-channel saturating decay", flush=True)
     res = _grad_case_pc(dev, 1, 130, 2, 64, torch.float32, seed=5, all_strong=True)
     for name, val in res.items():
-        assert val < (1e-3 if name == "dg" else FP32_TOL), (name, val)
+        assert val < FP32_TOL, (name, val)
 
 
 def test_chunk_per_channel_varlen(dev):
@@ -407,28 +406,24 @@ def test_chunk_production_gate_matches_oracle(dev, D, dtype):
         res["d" + n] = rel_l2(a.float(), b)
     print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
     tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
-    # The gate's own gradients (raw g, A_log, dt_bias) come from the
-    # chunk-local gate gradient, a difference of O(1) per-token terms that is
-    # far smaller than they are under the production gate's strong decays, then
-    # summed again over all tokens; in FP32 they land at ~1e-5..5e-5 while the
-    # FP32 oracle agrees with FP64 to ~2e-7.  Bound: 1e-4 for those three.
-    gate_grads = ("dg", "dA_log", "ddt_bias")
     for n, val in res.items():
-        assert val < (max(tol, 1e-4) if n in gate_grads else tol), (n, val)
+        assert val < tol, (n, val)
 
 
-@pytest.mark.parametrize("lean", [False, True])
-def test_pkda_recurrence_op_matches_oracle(dev, lean):
+@pytest.mark.parametrize("lean,seed", [(False, 41), (True, 41), (False, 2), (False, 6)])
+def test_pkda_recurrence_op_matches_oracle(dev, lean, seed):
     """The training custom op exactly as PreconditionedKDA._cuda_recurrence
     calls it (delta_feedback_experiment/pkda.py:429-449): bf16 activations,
     raw per-channel gate, preconditioner, all ten gradients in their input
-    dtypes."""
+    dtypes.  dA_log sums the gate gradient over a whole head and is the
+    tightest of them; seeds 2 and 6 are the ones that moved it most while the
+    gate gradient's pair terms were formed from differently rounded halves."""
     from delta_feedback_experiment_amd import pkda_recurrence
 
-    print(f"[gpu] pkda_recurrence op lean={lean}", flush=True)
+    print(f"[gpu] pkda_recurrence op lean={lean} seed={seed}", flush=True)
     B, T, H, D = 2, 192, 2, 128
     (q, k, v, g_raw, beta, A_log, dt_bias, g_atk, beta_atk, center) = _production_inputs(
-        B, T, H, D, torch.bfloat16, 41)
+        B, T, H, D, torch.bfloat16, seed)
     do = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
     base = (q, k, v, g_raw, g_atk, beta_atk, beta, A_log, dt_bias, center)
     names = ("q", "k", "v", "g", "g_atk", "beta_atk", "beta", "A_log", "dt_bias", "log_atk_scale")
@@ -440,15 +435,6 @@ def test_pkda_recurrence_op_matches_oracle(dev, lean):
         return o_, torch.autograd.grad((o_ * do.float()).sum(), t)
 
     o_r, g_r = oracle_grads([x.float() for x in base])
-    # The oracle's own sensitivity: the same FP32 computation with q, k, v, g
-    # moved by bf16 half-ulp noise (relative 2^-9).  Reductions over every
-    # token and channel (dA_log above all) cancel heavily and move by ~2e-2
-    # under that noise, so no bf16 computation can pin them tighter.
-    noise = torch.Generator().manual_seed(11)
-    pert = [x.float() * (1 + 2.0 ** -9 * torch.randn(x.shape, generator=noise)) if i < 4 else x.float()
-            for i, x in enumerate(base)]
-    _, g_p = oracle_grads(pert)
-    spread = {"d" + n: rel_l2(a, b) for n, a, b in zip(names, g_p, g_r)}
     leaves = [x.to(dev).clone().requires_grad_() for x in base]
     o, saved = pkda_recurrence(*leaves, D ** -0.5, 1.5, 1e-6, lean)
     g_d = torch.autograd.grad((o.float() * do.to(dev).float()).sum(), leaves)
@@ -459,6 +445,5 @@ def test_pkda_recurrence_op_matches_oracle(dev, lean):
         assert a.dtype == x.dtype, (n, a.dtype, x.dtype)
         res["d" + n] = rel_l2(a.float(), b)
     print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
-    print("  spread " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in spread.items()), flush=True)
     for n, val in res.items():
-        assert val < max(BF16_TOL, 2 * spread.get(n, 0.0)), (n, val, spread.get(n))
+        assert val < BF16_TOL, (n, val)

@@ -148,25 +148,9 @@ def test_decay_expansion_in_the_gate_matches_the_oracle(dev, dtype, D):
     for n, a, b in zip(names, g_d, g_r):
         res["d" + n] = rel_l2(a.float(), b)
     print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
-    # Gradients that reach the gate (the raw decay's, hence the packed
-    # projection's and decay_up's, and A_log's, dt_bias's) are differences of
-    # O(1) per-token terms summed again over every token.  FP32: bound 1e-4,
-    # as for the gate gradients of the chunk tests' production case.  BF16:
-    # the oracle's own spread under bf16 half-ulp noise on the activations
-    # and weights, as the training-op test measures it.
-    gate_reached = ("dpacked", "ddecay_up", "dA_log", "ddt_bias")
-    if dtype == torch.float32:
-        for name, val in res.items():
-            assert val < (1e-4 if name in gate_reached else FP32_TOL), (name, val)
-        return
-    noise = torch.Generator().manual_seed(13)
-    pert = [x.float() * (1 + 2.0 ** -9 * torch.randn(x.shape, generator=noise)) if i < 5 else x.float()
-            for i, x in enumerate(base)]
-    _, g_p = run([x.clone().requires_grad_() for x in pert], None)
-    spread = {"d" + n: rel_l2(a, b) for n, a, b in zip(names, g_p, g_r)}
-    print("  spread " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in spread.items()), flush=True)
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
     for name, val in res.items():
-        assert val < max(BF16_TOL, 2 * spread.get(name, 0.0)), (name, val, spread.get(name))
+        assert val < tol, (name, val)
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.bfloat16, 64), (torch.float32, 64)])

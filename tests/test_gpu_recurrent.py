@@ -151,6 +151,67 @@ def test_decode_step_pool_matches_oracle(dev, precond):
         assert torch.equal(a_d.cpu()[untouched], a_pool[untouched])
 
 
+@pytest.mark.parametrize("P,N,H,D,precond", [
+    (512, 256, 32, 128, False),   # 8,192 (slot, head) items
+    (512, 256, 32, 128, True),
+    (256, 200, 32, 64, True),     # D = 64: 6,400 items
+])
+def test_decode_step_pool_full_size_matches_oracle(dev, P, N, H, D, precond):
+    """The decode pool at the benchmark's own size.  The kernel's grid stops
+    at 12 workgroups per compute unit (3,072 on 256 CUs); past that each
+    workgroup walks several (slot, head) items and hands the next item's
+    prefetched state and inputs over to the next iteration.  Three steps in a
+    row, each with a fresh random slot subset, each checked against the
+    oracle's step on the same pool, with every other slot bitwise unchanged."""
+    from delta_feedback_experiment_amd import pkda_decode_step_
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert N * H > 12 * cus, "the case must exercise the multi-item path"
+    print(f"[gpu] decode full size P={P} N={N} H={H} D={D} precond={precond} items={N * H}", flush=True)
+    gen = torch.Generator().manual_seed(1000 + D + int(precond))
+    pool = 0.02 * torch.randn(P, H, D, D, generator=gen)
+    a_pool = 0.1 * torch.randn(P, H, D, generator=gen).abs()
+    pool_d = pool.to(dev)
+    a_d = a_pool.to(dev)
+    center = torch.full((H,), -0.2)
+    for step in range(3):
+        slots = torch.randperm(P, generator=gen)[:N].to(torch.int32)
+        q, k, v, g, beta = _inputs(N, 1, H, D, torch.bfloat16, seed=2000 + step)
+        q, k, v, g, beta = q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0]
+        extra = {}
+        if precond:
+            extra = dict(g_atk=-F.softplus(torch.randn(N, H, generator=gen)),
+                         beta_atk=torch.sigmoid(torch.randn(N, H, generator=gen)),
+                         log_atk_scale=center, x=1.5)
+        before = pool.clone()
+        a_before = a_pool.clone()
+        o_ref = oracle.decode_step_reference(q, k, v, g, beta, pool, slots,
+                                             a_pool=a_pool if precond else None, **extra)
+        o = pkda_decode_step_(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), pool_d, slots.to(dev),
+                              a_pool=a_d if precond else None,
+                              **{kk: (vv.to(dev) if torch.is_tensor(vv) else vv) for kk, vv in extra.items()})
+        torch.cuda.synchronize()
+        got = pool_d.cpu()
+        sl = slots.long()
+        untouched = torch.ones(P, dtype=torch.bool)
+        untouched[sl] = False
+        e_o = rel_l2(o.float(), o_ref.float())
+        e_s = rel_l2(got[sl], pool[sl])
+        print(f"  step {step}: o={e_o:.2e} S={e_s:.2e}", flush=True)
+        assert e_o < BF16_TOL
+        assert e_s < FP32_TOL
+        assert torch.equal(got[untouched], before[untouched])
+        if precond:
+            a_got = a_d.cpu()
+            assert rel_l2(a_got[sl], a_pool[sl]) < FP32_TOL
+            assert torch.equal(a_got[untouched], a_before[untouched])
+        # carry the GPU's pool forward so later steps start from the same state
+        pool.copy_(got)
+        if precond:
+            a_pool.copy_(a_d.cpu())
+        del got, before, a_before
+
+
 def test_decode_rejects_repeated_slots(dev):
     from delta_feedback_experiment_amd import pkda_decode_step_
 

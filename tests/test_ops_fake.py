@@ -13,7 +13,7 @@ import pytest
 import torch
 from torch.fx.experimental.proxy_tensor import make_fx
 
-from delta_feedback_experiment_amd.ops import intermediate_meta, pkda_recurrence
+from delta_feedback_experiment_amd.ops import intermediate_meta, pkda_recurrence, saved_names
 
 B, T, H, D = 2, 100, 3, 64
 
@@ -32,8 +32,18 @@ def test_fake_forward_shapes(lean):
     assert o.shape == (B, T, H, D) and o.dtype == torch.bfloat16
     meta = intermediate_meta(torch.empty(B, T, H, D, dtype=torch.bfloat16), torch.empty(B, T, H, D), lean)
     assert [(tuple(s.shape), s.dtype) for s in saved] == [m for m in meta]
+    named = dict(zip(saved_names(torch.empty(1, dtype=torch.bfloat16), lean), saved))
     # T = 100 -> two chunks per row
-    assert saved[1].shape == (B * 2, H, D)
+    assert named["a_chunk"].shape == (B * 2, H, D)
+    # BF16 activations also keep the write keys in FP32
+    assert named["k_write"].dtype == torch.bfloat16 and named["k_write32"].dtype == torch.float32
+    assert len(saved) == (3 if lean else 10)
+
+
+def test_fp32_activations_save_one_write_key():
+    meta = intermediate_meta(torch.empty(B, T, H, D), torch.empty(B, T, H, D), True)
+    assert saved_names(torch.empty(1), True) == ("k_write", "a_chunk")
+    assert [dt for _, dt in meta] == [torch.float32, torch.float32]
 
 
 def test_forward_and_backward_trace_as_two_opaque_ops():
