@@ -23,7 +23,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class RecurrentArgs(ctypes.Structure):

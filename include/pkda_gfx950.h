@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 7
+#define PKDA_ABI_VERSION 8
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
