@@ -183,7 +183,7 @@ def lib() -> ctypes.CDLL:
         fn.restype = c_int32
         fn.argtypes = [POINTER(RecurrentArgs), c_void_p]
     for name, struct in (
-        ("pkda_gate_fwd", GateArgs), ("pkda_gate_bwd", GateArgs),
+        ("pkda_gate_fwd", GateArgs), ("pkda_gate_bwd", GateArgs), ("pkda_gate_bwd_noalloc", GateArgs),
         ("pkda_precond_fwd", PrecondArgs), ("pkda_precond_bwd", PrecondArgs),
         ("pkda_chunk_fwd", ChunkFwdArgs), ("pkda_chunk_bwd", ChunkBwdArgs),
         ("pkda_qkv_conv_fwd", QkvConvArgs), ("pkda_qkv_conv_bwd", QkvConvArgs),

@@ -6,6 +6,8 @@
 //   PKDA_GATE_LOG_CHANNEL  glog[t,h,c] = g[t,h,c]
 //   PKDA_GATE_RAW_CHANNEL  glog[t,h,c] = -exp(A_log[h]) softplus(g[t,h,c] + dt_bias[h*K+c])
 //                          (delta_feedback_experiment/pkda.py:375-377)
+#include <mutex>
+
 #include "pkda_chunk_common.h"
 
 namespace pkda {
@@ -582,19 +584,27 @@ extern "C" int pkda_gate_fwd(const pkda_gate_args* a, void* stream) {
   return launch_status("pkda_gate_fwd");
 }
 
-extern "C" int pkda_gate_bwd(const pkda_gate_args* a, void* stream) {
+namespace pkda {
+namespace {
+
+// The gate backward.  For the raw and low-rank forms the per-chunk partials
+// of dA_log [num_chunks, H] and ddt_bias [num_chunks, H*K] go to dA_part and
+// ddt_part: every slot is written on every call (empty chunks write zeros), so
+// nothing there needs clearing first.
+int gate_bwd_impl(const pkda_gate_args* a, float* dA_part, float* ddt_part, hipStream_t s) {
   GateParams p;
   int st = gate_common(a, p);
   if (st) return st;
+  p.dA_log_part = dA_part;
+  p.ddt_bias_part = ddt_part;
   PKDA_REQUIRE(a->dgcum && a->dg, PKDA_EINVAL, "gate backward needs dgcum and dg");
   PKDA_REQUIRE(a->dg_dtype == PKDA_F32 ||
                    (a->dg_dtype == a->g_dtype &&
                     (a->gate_kind == PKDA_GATE_LOG_CHANNEL || a->gate_kind == PKDA_GATE_RAW_CHANNEL)),
                PKDA_EUNSUPPORTED, "dg_dtype %d: FP32, or g's dtype for the per-channel gate forms", a->dg_dtype);
   const bool raw = a->gate_kind >= PKDA_GATE_RAW_CHANNEL;
-  PKDA_REQUIRE(!raw || (a->g && a->dA_log_part && a->ddt_bias_part && a->dA_log && a->ddt_bias), PKDA_EINVAL,
+  PKDA_REQUIRE(!raw || (a->g && dA_part && ddt_part && a->dA_log && a->ddt_bias), PKDA_EINVAL,
                "raw gate backward needs g and the dA_log / ddt_bias buffers");
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->num_chunks > 0) {
     if (a->gate_kind == PKDA_GATE_LOW_RANK) {
       if (int e = dispatch_low_rank(p, a->num_chunks, true, s)) return e;
@@ -606,10 +616,68 @@ extern "C" int pkda_gate_bwd(const pkda_gate_args* a, void* stream) {
   }
   if (raw) {
     const int nH = a->heads, nHK = a->heads * a->head_dim;
-    hipLaunchKernelGGL(sum_partials_tree_kernel, dim3(nH), dim3(256), 0, s, a->dA_log_part, a->num_chunks, nH,
-                       a->dA_log);
-    hipLaunchKernelGGL(sum_partials_tree_kernel, dim3(nHK), dim3(256), 0, s, a->ddt_bias_part, a->num_chunks, nHK,
+    hipLaunchKernelGGL(sum_partials_tree_kernel, dim3(nH), dim3(256), 0, s, dA_part, a->num_chunks, nH, a->dA_log);
+    hipLaunchKernelGGL(sum_partials_tree_kernel, dim3(nHK), dim3(256), 0, s, ddt_part, a->num_chunks, nHK,
                        a->ddt_bias);
   }
   return launch_status("pkda_gate_bwd");
+}
+
+// ---- the gate backward without a caller workspace ------------------------------
+// pkda_gate_bwd_noalloc keeps the partials in this device array instead of
+// the caller's dA_log_part / ddt_bias_part.  Each device holds its own copy
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// not the device address: the address comes from hipGetSymbolAddress, once
+// per device with that device current, and only that address is used.
+constexpr int64_t kGateScratchFloats = PKDA_GATE_BWD_NOALLOC_MAX_FLOATS;
+static __device__ __align__(256) float scratch[kGateScratchFloats];
+
+constexpr int kMaxDevices = 64;
+float* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+int device_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("hipGetDevice: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  PKDA_REQUIRE(dev >= 0 && dev < kMaxDevices, PKDA_EUNSUPPORTED, "device %d (at most %d devices)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      return e != hipSuccess ? static_cast<int>(e) : static_cast<int>(hipErrorInvalidSymbol);
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace pkda
+
+extern "C" int pkda_gate_bwd(const pkda_gate_args* a, void* stream) {
+  PKDA_REQUIRE(a != nullptr, PKDA_EINVAL, "null args");
+  return gate_bwd_impl(a, a->dA_log_part, a->ddt_bias_part, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pkda_gate_bwd_noalloc(const pkda_gate_args* a, void* stream) {
+  PKDA_REQUIRE(a != nullptr, PKDA_EINVAL, "null args");
+  PKDA_REQUIRE(a->num_chunks >= 0 && a->heads > 0 && a->head_dim > 0, PKDA_EINVAL, "sizes");
+  if (a->gate_kind < PKDA_GATE_RAW_CHANNEL)  // no partials: nothing to place
+    return gate_bwd_impl(a, nullptr, nullptr, static_cast<hipStream_t>(stream));
+  const int64_t nH = (int64_t)a->num_chunks * a->heads;
+  const int64_t need = nH * (1 + (int64_t)a->head_dim);
+  PKDA_REQUIRE(need <= pkda::kGateScratchFloats, PKDA_ERANGE,
+               "pkda_gate_bwd_noalloc: num_chunks * heads * (head_dim + 1) = %lld floats exceeds its scratch of "
+               "%lld floats; use pkda_gate_bwd with a workspace",
+               (long long)need, (long long)pkda::kGateScratchFloats);
+  float* base = nullptr;
+  if (int st = pkda::device_scratch(&base)) return st;
+  return gate_bwd_impl(a, base, base + nH, static_cast<hipStream_t>(stream));
 }

@@ -22,8 +22,9 @@
  *    and decode kernels as well).
  *  - `stream` is a hipStream_t passed as void*.  Calls only enqueue work: the
  *    library never allocates or frees device memory, never synchronises the
- *    host and keeps no state besides the last error message, so a caller may
- *    capture every call into a HIP graph.
+ *    host and keeps no state besides the last error message (and the static
+ *    device array of pkda_gate_bwd_noalloc), so a caller may capture every
+ *    call into a HIP graph.
  *  - Return value: 0 on success; < 0 for an argument rejected before any
  *    launch (PKDA_E*); > 0 is the hipError_t of a failed launch.  The
  *    message of the last failure on the calling thread is pkda_last_error().
@@ -198,6 +199,21 @@ typedef struct pkda_gate_args {
 
 int pkda_gate_fwd(const pkda_gate_args* args, void* stream);
 int pkda_gate_bwd(const pkda_gate_args* args, void* stream);
+
+/* pkda_gate_bwd without a caller workspace.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture that may not allocate, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as pkda_gate_bwd except that
+ * dA_log_part / ddt_bias_part are ignored: the per-chunk partials go to a
+ * static device array of PKDA_GATE_BWD_NOALLOC_MAX_FLOATS floats (16 MiB),
+ * one per device, held until the process ends.  Calls with
+ * num_chunks * heads * (head_dim + 1) above that return PKDA_ERANGE; the call
+ * allocates nothing.  Every call on one device shares that device's array,
+ * so calls that overlap on one device (concurrent streams, threads) race;
+ * serialise them.  Each call writes every partial it reads, so nothing left
+ * by an earlier call leaks into a result. */
+#define PKDA_GATE_BWD_NOALLOC_MAX_FLOATS ((int64_t)1 << 22)
+int pkda_gate_bwd_noalloc(const pkda_gate_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Preconditioner scan (forward) and its reverse scan (backward).
