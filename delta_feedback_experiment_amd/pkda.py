@@ -175,6 +175,37 @@ def fused_recurrent_pkda(
     return o, S_T, A_T
 
 
+def _require_device(*tensors: Tensor | None) -> torch.device:
+    """Device of the given tensors for the in-place serving operators: a HIP
+    device, or the fake device of a trace (``torch.compile`` and ``make_fx``
+    run the custom ops' fake implementations there).  CPU tensors are
+    refused: there is no CPU fallback."""
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not (t.is_cuda or t.is_meta):
+            raise RuntimeError("PKDA operators need tensors on a HIP device; there is no CPU fallback")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"tensors on different devices: {device} and {t.device}")
+    return device
+
+
+def check_slot_indices(slot_idx: Tensor, pool_size: int) -> None:
+    """Host-side range and uniqueness check of slot indices (synchronises):
+    the pools are updated in place, so a repeated slot would race."""
+    host = slot_idx.cpu().tolist()
+    seen = set()
+    for i, s in enumerate(host):
+        if s < 0 or s >= pool_size:
+            raise IndexError(f"slot_idx[{i}] = {s} is out of range [0, {pool_size})")
+        if s in seen:
+            raise ValueError(f"slot_idx[{i}] = {s} is repeated: the pool is updated in place")
+        seen.add(s)
+
+
 def pkda_decode_step_(
     q: Tensor,
     k: Tensor,
@@ -204,9 +235,13 @@ def pkda_decode_step_(
     device (``None`` = slots ``0..N-1``).  Slots must be unique: the update is
     in place.  ``check_slots`` copies the indices to the host and verifies
     range and uniqueness first (a synchronising debug check).
+
+    The launch is the custom op ``pkda_mi355x::decode_step_``, which declares
+    ``state_pool``, ``a_pool`` and the output buffer as mutated, so
+    ``torch.compile`` and functionalization see the in-place update.
     """
     _check_common(q, k, v, beta)
-    device = _require_cuda(q, k, v, g, beta, state_pool, slot_idx, a_pool)
+    _require_device(q, k, v, g, beta, state_pool, slot_idx, a_pool)
     N, H, D = q.shape
     if scale is None:
         scale = D ** -0.5
@@ -217,22 +252,40 @@ def pkda_decode_step_(
     if a_pool is not None and (a_pool.dtype != torch.float32 or not a_pool.is_contiguous()
                                or tuple(a_pool.shape) != (state_pool.shape[0], H, D)):
         raise ValueError("a_pool must be a contiguous float32 [P, H, D] tensor")
-    gate_kind, g = gate_form(g, q.shape[:-1], D, use_gate_in_kernel, A_log, dt_bias)
-    idx = None
-    host_idx = None
+    gate_form(g, q.shape[:-1], D, use_gate_in_kernel, A_log, dt_bias)  # shape check
     if slot_idx is not None:
         if slot_idx.dtype != torch.int32 or slot_idx.shape != (N,):
             raise ValueError("slot_idx must be int32 [N]")
-        idx = slot_idx.contiguous()
         if check_slots:
-            host_idx = idx.cpu()
+            check_slot_indices(slot_idx, state_pool.shape[0])
     elif N > state_pool.shape[0]:
         raise ValueError("more sequences than pool slots")
+    o = out if out is not None else torch.empty_like(v)
+    if o.shape != v.shape or o.dtype != v.dtype or not o.is_contiguous():
+        raise ValueError(f"out must be a contiguous {v.dtype} {tuple(v.shape)} tensor")
+    decode_step_op(q, k, v, g, beta, state_pool, slot_idx, a_pool, g_atk, beta_atk, log_atk_scale, A_log, dt_bias,
+                   bool(use_gate_in_kernel), float(scale), float(x), float(eps), o)
+    return o
+
+
+@torch.library.custom_op("pkda_mi355x::decode_step_", mutates_args=("state_pool", "a_pool", "o"),
+                         device_types="cuda")
+def decode_step_op(
+    q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state_pool: Tensor, slot_idx: Tensor | None,
+    a_pool: Tensor | None, g_atk: Tensor | None, beta_atk: Tensor | None, log_atk_scale: Tensor | None,
+    A_log: Tensor | None, dt_bias: Tensor | None, use_gate_in_kernel: bool, scale: float, x: float, eps: float,
+    o: Tensor,
+) -> None:
+    """The decode step's launch (arguments checked by :func:`pkda_decode_step_`):
+    writes ``o`` and the indexed slots of ``state_pool`` / ``a_pool``."""
+    device = _require_cuda(q, k, v, g, beta, state_pool, slot_idx, a_pool, o)
+    N, H, D = q.shape
+    gate_kind, g = gate_form(g, q.shape[:-1], D, use_gate_in_kernel, A_log, dt_bias)
+    idx = None if slot_idx is None else slot_idx.contiguous()
     q, k, v, g = q.contiguous(), k.contiguous(), v.contiguous(), g.contiguous()
     if g.dtype not in (torch.float32, torch.bfloat16):
         g = g.float()
     beta32 = _f32(beta)
-    o = out if out is not None else torch.empty_like(v)
     A_log32, dt32, gatk32, batk32, center32 = map(_f32, (A_log, dt_bias, g_atk, beta_atk, log_atk_scale))
     args = _lib.RecurrentArgs(
         dtype=_dtype_code(q), num_seqs=N, seqlen=1, heads=H, head_dim=D,
@@ -241,10 +294,13 @@ def pkda_decode_step_(
         g_atk=_ptr(gatk32), beta_atk=_ptr(batk32), center=_ptr(center32),
         squash_x=float(x), squash_eps=float(eps),
         state_pool=_ptr(state_pool), a_pool=_ptr(a_pool), pool_size=state_pool.shape[0],
-        slot_idx=_ptr(idx),
-        slot_idx_host=None if host_idx is None else host_idx.data_ptr(),
-        check_slots=int(check_slots), o=_ptr(o),
+        slot_idx=_ptr(idx), o=_ptr(o),
     )
     with torch.cuda.device(device):
         _lib.call("pkda_decode_step", args, _stream(device))
-    return o
+
+
+@decode_step_op.register_fake
+def _decode_step_fake(q, k, v, g, beta, state_pool, slot_idx, a_pool, g_atk, beta_atk, log_atk_scale, A_log,
+                      dt_bias, use_gate_in_kernel, scale, x, eps, o) -> None:
+    return None

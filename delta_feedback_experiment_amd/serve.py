@@ -35,7 +35,8 @@ from torch import Tensor
 
 from . import _lib
 from .chunk import ChunkPlan, _flat, chunk_forward, gate_forward
-from .pkda import _check_common, _dtype_code, _f32, _ptr, _require_cuda, _stream, gate_form
+from .pkda import (_check_common, _dtype_code, _f32, _ptr, _require_cuda, _require_device, _stream,
+                   check_slot_indices, gate_form)
 
 
 @dataclass
@@ -60,17 +61,11 @@ class DecodePool:
         )
 
 
-def _slots(slot_idx: Tensor, n: int, pool_size: int, check: bool) -> Tensor:
+def _slots(slot_idx: Tensor, n: int, pool_size: int, check: bool) -> None:
     if slot_idx.dtype != torch.int32 or tuple(slot_idx.shape) != (n,):
         raise ValueError(f"slot_idx must be int32 [{n}]")
-    idx = slot_idx.contiguous()
     if check:
-        host = idx.cpu()
-        if n and (int(host.min()) < 0 or int(host.max()) >= pool_size):
-            raise IndexError(f"slot index out of range [0, {pool_size})")
-        if host.unique().numel() != n:
-            raise ValueError("slot indices must be unique: the pool is updated in place")
-    return idx
+        check_slot_indices(slot_idx, pool_size)
 
 
 def pkda_prefill_(
@@ -110,8 +105,8 @@ def pkda_prefill_(
     host first (synchronising).
     """
     _check_common(q, k, v, beta)
-    device = _require_cuda(q, k, v, g, beta, state_pool, slot_idx, a_pool, cu_seqlens, g_atk, beta_atk,
-                           log_atk_scale, A_log, dt_bias)
+    _require_device(q, k, v, g, beta, state_pool, slot_idx, a_pool, cu_seqlens, g_atk, beta_atk,
+                    log_atk_scale, A_log, dt_bias)
     B, T, H, D = q.shape
     if state_pool.dtype != torch.float32 or not state_pool.is_contiguous() or tuple(state_pool.shape[1:]) != (H, D, D):
         raise ValueError(f"state_pool must be a contiguous float32 [P, {H}, {D}, {D}] tensor")
@@ -124,10 +119,32 @@ def pkda_prefill_(
     if a_pool is not None and (a_pool.dtype != torch.float32 or not a_pool.is_contiguous()
                                or tuple(a_pool.shape) != (P, H, D)):
         raise ValueError(f"a_pool must be a contiguous float32 [{P}, {H}, {D}] tensor")
+    if cu_seqlens is not None and B != 1:
+        raise ValueError("cu_seqlens requires batch size 1")
+    gate_form(g, q.shape[:-1], D, use_gate_in_kernel, A_log, dt_bias)  # shape check
     N = B if cu_seqlens is None else cu_seqlens.numel() - 1
-    idx = _slots(slot_idx, N, P, check_slots)
+    _slots(slot_idx, N, P, check_slots)
     if scale is None:
         scale = D ** -0.5
+    o = torch.empty_like(v)
+    prefill_op(q, k, v, g, beta, state_pool, slot_idx, a_pool, bool(continue_state), cu_seqlens, g_atk, beta_atk,
+               log_atk_scale, A_log, dt_bias, bool(use_gate_in_kernel), float(scale), float(x), float(eps), o)
+    return o
+
+
+@torch.library.custom_op("pkda_mi355x::prefill_", mutates_args=("state_pool", "a_pool", "o"), device_types="cuda")
+def prefill_op(
+    q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state_pool: Tensor, slot_idx: Tensor,
+    a_pool: Tensor | None, continue_state: bool, cu_seqlens: Tensor | None, g_atk: Tensor | None,
+    beta_atk: Tensor | None, log_atk_scale: Tensor | None, A_log: Tensor | None, dt_bias: Tensor | None,
+    use_gate_in_kernel: bool, scale: float, x: float, eps: float, o: Tensor,
+) -> None:
+    """The prefill's launches (arguments checked by :func:`pkda_prefill_`):
+    writes ``o`` and the final S (and A) of every document into its slot."""
+    device = _require_cuda(q, k, v, g, beta, state_pool, slot_idx, a_pool, cu_seqlens, g_atk, beta_atk,
+                           log_atk_scale, A_log, dt_bias, o)
+    H, D = q.shape[2], q.shape[3]
+    idx = slot_idx.contiguous()
     from . import precond as pre
 
     with torch.no_grad(), torch.cuda.device(device):
@@ -145,10 +162,15 @@ def pkda_prefill_(
             pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, x, eps,
                                          a_pool if continue_state else None, slot_idx=idx, final_A=a_pool)
             kwf = pstate.kw
-        o, _, _ = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, float(scale),
-                                state_pool if continue_state else None, True, False,
-                                slot_idx=idx, final_state=state_pool)
-    return o.reshape(v.shape)
+        chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, float(scale),
+                      state_pool if continue_state else None, True, False,
+                      slot_idx=idx, final_state=state_pool, out=_flat(o, plan))
+
+
+@prefill_op.register_fake
+def _prefill_fake(q, k, v, g, beta, state_pool, slot_idx, a_pool, continue_state, cu_seqlens, g_atk, beta_atk,
+                  log_atk_scale, A_log, dt_bias, use_gate_in_kernel, scale, x, eps, o) -> None:
+    return None
 
 
 def pkda_qkv_conv_cached_(
@@ -173,7 +195,7 @@ def pkda_qkv_conv_cached_(
     last ``conv_size - 1`` rows of history ++ x.  ``T = 1`` is the decode
     token.  Returns ``(q, k, v)`` ``[B, T, width]`` as :func:`pkda_qkv_conv`.
     """
-    _require_cuda(x, weight, conv_pool, slot_idx)
+    _require_device(x, weight, conv_pool, slot_idx)
     if x.dim() != 3 or weight.dim() != 2 or x.shape[-1] != weight.shape[0] or x.shape[-1] % 3:
         raise ValueError(f"x [B, T, 3 * width] and weight [3 * width, conv_size] expected, got "
                          f"{tuple(x.shape)} and {tuple(weight.shape)}")
@@ -185,11 +207,27 @@ def pkda_qkv_conv_cached_(
             or tuple(conv_pool.shape[1:]) != (W - 1, Cx)):
         raise ValueError(f"conv_pool must be a contiguous {x.dtype} [P, {W - 1}, {Cx}] tensor")
     P = conv_pool.shape[0]
-    idx = None
     if slot_idx is not None:
-        idx = _slots(slot_idx, B, P, check_slots)
+        _slots(slot_idx, B, P, check_slots)
     elif B > P:
         raise ValueError("more rows than pool slots")
+    return qkv_conv_cached_op(x, weight, int(head_dim), int(norm_channels), float(eps), conv_pool, slot_idx,
+                              bool(continue_state))
+
+
+@torch.library.custom_op("pkda_mi355x::qkv_conv_cached_", mutates_args=("conv_pool",), device_types="cuda")
+def qkv_conv_cached_op(
+    x: Tensor, weight: Tensor, head_dim: int, norm_channels: int, eps: float, conv_pool: Tensor,
+    slot_idx: Tensor | None, continue_state: bool,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """The cached convolution's launch (arguments checked by
+    :func:`pkda_qkv_conv_cached_`): returns ``(q, k, v)`` and leaves each
+    slot's new history in ``conv_pool``."""
+    _require_cuda(x, weight, conv_pool, slot_idx)
+    B, T, Cx = x.shape
+    W = weight.shape[1]
+    P = conv_pool.shape[0]
+    idx = None if slot_idx is None else slot_idx.contiguous()
     x, weight = x.contiguous(), weight.contiguous()
     q, k, v = (torch.empty(B, T, Cx // 3, device=x.device, dtype=x.dtype) for _ in range(3))
     args = _lib.QkvConvArgs(
@@ -202,3 +240,9 @@ def pkda_qkv_conv_cached_(
     with torch.no_grad(), torch.cuda.device(x.device):
         _lib.call("pkda_qkv_conv_fwd", args, _stream(x.device))
     return q, k, v
+
+
+@qkv_conv_cached_op.register_fake
+def _qkv_conv_cached_fake(x, weight, head_dim, norm_channels, eps, conv_pool, slot_idx, continue_state):
+    B, T, Cx = x.shape
+    return tuple(x.new_empty(B, T, Cx // 3) for _ in range(3))

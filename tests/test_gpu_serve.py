@@ -221,3 +221,36 @@ def test_prefill_rejects_bad_slots(dev):
         pkda_prefill_(q, k, v, g, beta, pool, torch.tensor([0, 4], dtype=torch.int32, device=dev), check_slots=True)
     with pytest.raises(ValueError):
         pkda_prefill_(q, k, v, g, beta, pool, torch.tensor([0, 1], dtype=torch.int64, device=dev))
+
+
+def test_serving_custom_ops_pass_opcheck(dev):
+    """torch.library.opcheck on the three in-place serving ops with real
+    launches: the schema's mutation marks match what the kernels write, and
+    the fake implementations agree with the real ones in shape and dtype."""
+    print("[gpu] serving ops opcheck", flush=True)
+    gen = torch.Generator().manual_seed(7)
+    N, P, H, D, T = 3, 6, 2, 64, 70
+    q, k, v, g, beta = (t.to(dev) for t in make_inputs(N, T, H, D, torch.bfloat16, seed=3))
+    pool = (0.02 * torch.randn(P, H, D, D, generator=gen)).to(dev)
+    a_pool = (0.1 * torch.randn(P, H, D, generator=gen).abs()).to(dev)
+    idx = torch.tensor([5, 1, 3], dtype=torch.int32, device=dev)
+    g_atk = -torch.nn.functional.softplus(torch.randn(N, T, H, generator=gen)).to(dev)
+    beta_atk = torch.sigmoid(torch.randn(N, T, H, generator=gen)).to(dev)
+    center = torch.full((H,), -0.2, device=dev)
+    o = torch.empty_like(v)
+    utils = ("test_schema", "test_faketensor")
+    torch.library.opcheck(torch.ops.pkda_mi355x.prefill_.default,
+                          (q, k, v, g, beta, pool, idx, a_pool, False, None, g_atk, beta_atk, center, None, None,
+                           False, D ** -0.5, 1.5, 1e-6, o), test_utils=utils)
+    qd, kd, vd, gd, bd = (t[:, 0].contiguous() for t in (q, k, v, g, beta))
+    od = torch.empty_like(vd)
+    torch.library.opcheck(torch.ops.pkda_mi355x.decode_step_.default,
+                          (qd, kd, vd, gd, bd, pool, idx, a_pool, g_atk[:, 0].contiguous(),
+                           beta_atk[:, 0].contiguous(), center, None, None, False, D ** -0.5, 1.5, 1e-6, od),
+                          test_utils=utils)
+    C = 3 * H * D
+    x = torch.randn(N, 5, C, generator=gen).to(torch.bfloat16).to(dev)
+    w = (0.5 * torch.randn(C, 4, generator=gen)).to(dev)
+    conv = torch.randn(P, 3, C, generator=gen).to(torch.bfloat16).to(dev)
+    torch.library.opcheck(torch.ops.pkda_mi355x.qkv_conv_cached_.default,
+                          (x, w, D, 2 * H * D, 1e-6, conv, idx, True), test_utils=utils)

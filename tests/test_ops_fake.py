@@ -82,3 +82,64 @@ def test_operator_validates_shapes():
     args = _args(device="cpu")
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _check_inputs(*args)
+
+
+def _serving_args(N=3, P=8, H=2, D=64, T=40):
+    def mk(*s, dt=torch.float32):
+        return torch.randn(*s, dtype=dt, device="meta")
+
+    dec = (mk(N, H, D, dt=torch.bfloat16), mk(N, H, D, dt=torch.bfloat16), mk(N, H, D, dt=torch.bfloat16),
+           mk(N, H), mk(N, H), mk(P, H, D, D), torch.zeros(N, dtype=torch.int32, device="meta"))
+    pre = (mk(N, T, H, D, dt=torch.bfloat16), mk(N, T, H, D, dt=torch.bfloat16), mk(N, T, H, D, dt=torch.bfloat16),
+           mk(N, T, H), mk(N, T, H))
+    return dec, pre
+
+
+def test_serving_ops_trace_as_mutating_custom_ops():
+    """Prefill into pool slots, then a decode step: both trace as opaque
+    custom ops whose schema marks the pools as mutated (SURVEY's drop-in
+    boundary asks for mutates_args on the in-place serving operators)."""
+    from delta_feedback_experiment_amd import pkda_decode_step_, pkda_prefill_
+
+    (q, k, v, g, beta, pool, idx), (pq, pk, pv, pg, pb) = _serving_args()
+
+    def serve(pq, pk, pv, pg, pb, q, k, v, g, beta, pool, idx):
+        o_pre = pkda_prefill_(pq, pk, pv, pg, pb, pool, idx)
+        o_dec = pkda_decode_step_(q, k, v, g, beta, pool, idx)
+        return o_pre, o_dec
+
+    gm = make_fx(serve, tracing_mode="fake")(pq, pk, pv, pg, pb, q, k, v, g, beta, pool, idx)
+    targets = [str(n.target) for n in gm.graph.nodes if n.op == "call_function"]
+    assert "pkda_mi355x.prefill_.default" in targets
+    assert "pkda_mi355x.decode_step_.default" in targets
+    for name in ("decode_step_", "prefill_"):
+        schema = getattr(torch.ops.pkda_mi355x, name).default._schema
+        mutated = {a.name for a in schema.arguments if a.alias_info is not None and a.alias_info.is_write}
+        assert mutated == {"state_pool", "a_pool", "o"}, (name, mutated)
+    schema = torch.ops.pkda_mi355x.qkv_conv_cached_.default._schema
+    assert {a.name for a in schema.arguments if a.alias_info is not None and a.alias_info.is_write} == {"conv_pool"}
+
+
+def test_serving_ops_compile_fullgraph():
+    """torch.compile(fullgraph=True) over prefill + decode (functionalized
+    by AOT autograd): no graph break, outputs of the documented shapes."""
+    from delta_feedback_experiment_amd import pkda_decode_step_, pkda_prefill_
+
+    (q, k, v, g, beta, pool, idx), (pq, pk, pv, pg, pb) = _serving_args()
+
+    def serve(pq, pk, pv, pg, pb, q, k, v, g, beta, pool, idx):
+        o_pre = pkda_prefill_(pq, pk, pv, pg, pb, pool, idx)
+        return o_pre, pkda_decode_step_(q, k, v, g, beta, pool, idx)
+
+    torch._dynamo.reset()
+    o_pre, o_dec = torch.compile(serve, fullgraph=True, backend="aot_eager")(pq, pk, pv, pg, pb, q, k, v, g, beta,
+                                                                              pool, idx)
+    assert o_pre.shape == pv.shape and o_dec.shape == v.shape and o_dec.dtype == torch.bfloat16
+
+
+def test_serving_ops_refuse_cpu_tensors():
+    from delta_feedback_experiment_amd import pkda_decode_step_
+
+    q = torch.zeros(2, 1, 64)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkda_decode_step_(q, q, q, torch.zeros(2, 1), torch.zeros(2, 1), torch.zeros(4, 1, 64, 64), None)
