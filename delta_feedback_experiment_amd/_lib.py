@@ -23,7 +23,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class RecurrentArgs(ctypes.Structure):
@@ -201,7 +201,7 @@ def lib() -> ctypes.CDLL:
     handle.pkda_controls_workspace.restype = c_int64
     handle.pkda_controls_workspace.argtypes = [c_int64, c_int32]
     handle.pkda_chunk_table.restype = c_int32
-    handle.pkda_chunk_table.argtypes = [c_void_p, c_int32, c_int32, c_void_p, c_void_p]
+    handle.pkda_chunk_table.argtypes = [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]
     if handle.pkda_abi_version() != ABI_VERSION:
         raise RuntimeError(f"libpkda ABI {handle.pkda_abi_version()} != binding ABI {ABI_VERSION}")
     for kind, struct in _ARG_KINDS.items():

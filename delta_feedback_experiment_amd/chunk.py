@@ -38,7 +38,12 @@ class ChunkPlan:
     table: Tensor | None
 
     @staticmethod
-    def make(q: Tensor, cu_seqlens: Tensor | None) -> "ChunkPlan":
+    def make(q: Tensor, cu_seqlens: Tensor | None, check: bool = False) -> "ChunkPlan":
+        """The geometry of ``q [B, T, H, D]``; with ``cu_seqlens`` the chunk
+        table is built on the device.  A malformed ``cu_seqlens`` is clamped
+        there (every kernel reads the table's sanitised copy, so no access
+        leaves the tensors) and flagged; ``check`` reads the flag back
+        (synchronising) and raises."""
         B, T, H, D = q.shape
         if cu_seqlens is None:
             nt = -(-T // CHUNK_SIZE)
@@ -50,14 +55,32 @@ class ChunkPlan:
         if N < 0:
             raise ValueError("cu_seqlens needs at least one element")
         bound = -(-T // CHUNK_SIZE) + N
-        table = torch.empty(4 * bound + 2 * N + 1, device=q.device, dtype=torch.int32)
+        table = torch.empty(4 * bound + 3 * N + 3, device=q.device, dtype=torch.int32)
         with torch.cuda.device(q.device):
             status = _lib.lib().pkda_chunk_table(
-                _ptr(cu), N, bound, _ptr(table), _stream(q.device)
+                _ptr(cu), N, T, bound, _ptr(table), _stream(q.device)
             )
         if status != 0:
             raise RuntimeError(f"pkda_chunk_table failed ({status}): {_lib.lib().pkda_last_error().decode()}")
-        return ChunkPlan(N, 0, H, D, T, bound, cu, table)
+        plan = ChunkPlan(N, 0, H, D, T, bound, cu, table)
+        if check and not plan.cu_seqlens_ok():
+            raise ValueError(f"cu_seqlens must rise from 0 to the packed length {T} without decreasing")
+        return plan
+
+    @property
+    def sanitized_cu(self) -> Tensor | None:
+        """The table's copy of ``cu_seqlens`` that the kernels read: the running
+        maximum clamped to ``[0, N_tok]`` (equal to the input when it is well
+        formed), int32 ``[N + 1]`` on the device."""
+        if self.table is None:
+            return None
+        off = 4 * self.num_chunks + 2 * self.num_seqs + 1
+        return self.table[off:off + self.num_seqs + 1]
+
+    def cu_seqlens_ok(self) -> bool:
+        """Whether ``cu_seqlens`` was well formed (reads the table's flag
+        back: synchronises)."""
+        return self.table is None or int(self.table[-1].item()) == 0
 
     def common(self) -> dict:
         return dict(

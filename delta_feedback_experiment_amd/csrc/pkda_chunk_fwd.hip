@@ -1008,11 +1008,12 @@ int chunk_geom_from(const int32_t* cu, int num_seqs, int seqlen, int num_chunks,
   PKDA_REQUIRE(num_seqs >= 0 && num_chunks >= 0, PKDA_EINVAL, "sizes");
   g.num_seqs = num_seqs;
   g.seqlen = seqlen;
-  g.cu = cu;
   g.nt = cu ? 0 : (seqlen + C - 1) / C;
   g.table = reinterpret_cast<const int4*>(table);
   g.offsets = table ? table + 4 * num_chunks : nullptr;
   g.order = table ? g.offsets + num_seqs + 1 : nullptr;
+  // packed documents: the kernels read the table's sanitised copy of cu
+  g.cu = cu && table ? g.order + num_seqs : nullptr;
   g.num_chunks = num_chunks;
   PKDA_REQUIRE(!cu || table, PKDA_EINVAL, "packed documents need the chunk table (pkda_chunk_table)");
   PKDA_REQUIRE(cu || num_chunks == num_seqs * g.nt, PKDA_EINVAL, "num_chunks %d != num_seqs * ceil(seqlen / 64) = %d",

@@ -14,16 +14,52 @@ namespace pkda {
 namespace {
 
 // ---- chunk table -------------------------------------------------------------
-__global__ __launch_bounds__(kWG) void chunk_offsets_kernel(const int32_t* cu, int N, int32_t* offsets) {
+// One workgroup.  The caller's cu_seqlens is read here only: the table keeps a
+// sanitised copy scu (nondecreasing, within [0, num_tokens]: the running
+// maximum of cu clamped to that range), which every later kernel reads, so a
+// malformed cu_seqlens cannot move any access outside the token tensors or
+// the table.  flag = 1 when cu is not 0 = cu[0] <= ... <= cu[N] = num_tokens.
+// Chunk counts come from scu and sum to at most ceil(num_tokens / 64) + N,
+// the table's bound.
+__global__ __launch_bounds__(kWG) void chunk_offsets_kernel(const int32_t* cu, int N, int num_tokens,
+                                                            int32_t* offsets, int32_t* scu, int32_t* flag) {
   __shared__ int s_scan[kWG];
-  int carry = 0;
+  __shared__ int s_max[kWG];
+  __shared__ int s_bad;
+  const int c0 = cu[0];
+  const int first = min(max(c0, 0), num_tokens);
+  if (threadIdx.x == 0) {
+    s_bad = (c0 != 0) || (N == 0 && num_tokens != 0);
+    scu[0] = first;
+  }
+  __syncthreads();  // s_bad's first value before any thread sets it
+  int carry = 0;         // chunks before this tile
+  int carry_max = first; // scu before this tile
   for (int base = 0; base < N; base += kWG) {
     const int n = base + threadIdx.x;
+    int hi = carry_max;
+    if (n < N) {
+      const int a = cu[n], b = cu[n + 1];
+      if (b < a || (n == N - 1 && b != num_tokens)) s_bad = 1;
+      hi = min(max(b, 0), num_tokens);
+    }
+    s_max[threadIdx.x] = hi;
+    __syncthreads();
+    for (int off = 1; off < kWG; off <<= 1) {  // Hillis-Steele inclusive prefix maximum
+      const int m = threadIdx.x >= off ? s_max[threadIdx.x - off] : hi;
+      __syncthreads();
+      hi = max(hi, m);
+      s_max[threadIdx.x] = hi;
+      __syncthreads();
+    }
+    const int end = max(hi, carry_max);                                          // scu[n + 1]
+    const int start = threadIdx.x > 0 ? max(s_max[threadIdx.x - 1], carry_max) : carry_max;  // scu[n]
     int cnt = 0;
     if (n < N) {
-      const int len = cu[n + 1] - cu[n];
-      cnt = len > 0 ? (len + C - 1) / C : 0;
+      scu[n + 1] = end;
+      cnt = (end - start + C - 1) / C;
     }
+    __syncthreads();
     s_scan[threadIdx.x] = cnt;
     __syncthreads();
     for (int off = 1; off < kWG; off <<= 1) {  // Hillis-Steele inclusive scan
@@ -34,12 +70,16 @@ __global__ __launch_bounds__(kWG) void chunk_offsets_kernel(const int32_t* cu, i
     }
     if (n < N) offsets[n] = carry + s_scan[threadIdx.x] - cnt;
     carry += s_scan[kWG - 1];
+    carry_max = max(carry_max, s_max[kWG - 1]);
     __syncthreads();
   }
-  if (threadIdx.x == 0) offsets[N] = carry;
+  if (threadIdx.x == 0) {
+    offsets[N] = carry;
+    *flag = s_bad;
+  }
 }
 
-__global__ __launch_bounds__(kWG) void chunk_fill_kernel(const int32_t* cu, int N, const int32_t* offsets,
+__global__ __launch_bounds__(kWG) void chunk_fill_kernel(const int32_t* scu, int N, const int32_t* offsets,
                                                          int num_chunks, int4* table) {
   const int c = blockIdx.x * kWG + threadIdx.x;
   if (c >= num_chunks) return;
@@ -51,8 +91,8 @@ __global__ __launch_bounds__(kWG) void chunk_fill_kernel(const int32_t* cu, int 
       if (offsets[mid] <= c) lo = mid; else hi = mid - 1;
     }
     const int j = c - offsets[lo];
-    const int start = cu[lo] + j * C;
-    e = make_int4(lo, start, min(C, cu[lo + 1] - start), 0);
+    const int start = scu[lo] + j * C;
+    e = make_int4(lo, start, min(C, scu[lo + 1] - start), 0);
   }
   table[c] = e;
 }
@@ -60,7 +100,7 @@ __global__ __launch_bounds__(kWG) void chunk_fill_kernel(const int32_t* cu, int 
 // Documents by length, longest first, ties by index: order[rank] = document.
 // Each thread ranks its document against all others (a strict total order,
 // so the ranks are a permutation), reading the lengths in LDS tiles.
-__global__ __launch_bounds__(kWG) void chunk_order_kernel(const int32_t* cu, int N, int32_t* order) {
+__global__ __launch_bounds__(kWG) void chunk_order_kernel(const int32_t* cu, int N, int32_t* order) {  // cu: the sanitised copy
   __shared__ int s_len[kWG];
   const int n = blockIdx.x * kWG + threadIdx.x;
   const int len = n < N ? cu[n + 1] - cu[n] : 0;
@@ -523,10 +563,10 @@ int gate_common(const pkda_gate_args* a, GateParams& p) {
   p.geom.num_seqs = a->num_seqs;
   p.geom.seqlen = a->seqlen;
   p.geom.nt = a->cu_seqlens ? 0 : (a->seqlen + C - 1) / C;
-  p.geom.cu = a->cu_seqlens;
   p.geom.table = reinterpret_cast<const int4*>(a->table);
   p.geom.offsets = a->table ? a->table + 4 * a->num_chunks : nullptr;
   p.geom.order = a->table ? p.geom.offsets + a->num_seqs + 1 : nullptr;
+  p.geom.cu = a->cu_seqlens && a->table ? p.geom.order + a->num_seqs : nullptr;  // the table's sanitised copy
   p.geom.num_chunks = a->num_chunks;
   PKDA_REQUIRE(a->cu_seqlens || a->num_chunks == a->num_seqs * p.geom.nt, PKDA_EINVAL,
                "num_chunks %d != num_seqs * ceil(seqlen / 64)", a->num_chunks);
@@ -554,18 +594,24 @@ int gate_common(const pkda_gate_args* a, GateParams& p) {
 
 using namespace pkda;
 
-extern "C" int pkda_chunk_table(const int32_t* cu_seqlens, int32_t num_seqs, int32_t num_chunks_max, int32_t* table,
-                                void* stream) {
-  PKDA_REQUIRE(cu_seqlens && table && num_seqs >= 0 && num_chunks_max >= 0, PKDA_EINVAL, "chunk table arguments");
+extern "C" int pkda_chunk_table(const int32_t* cu_seqlens, int32_t num_seqs, int32_t num_tokens,
+                                int32_t num_chunks_max, int32_t* table, void* stream) {
+  PKDA_REQUIRE(cu_seqlens && table && num_seqs >= 0 && num_tokens >= 0 && num_chunks_max >= 0, PKDA_EINVAL,
+               "chunk table arguments");
+  PKDA_REQUIRE(num_chunks_max >= (num_tokens + C - 1) / C + num_seqs, PKDA_EINVAL,
+               "num_chunks_max %d < ceil(num_tokens / 64) + num_seqs", num_chunks_max);
   hipStream_t s = static_cast<hipStream_t>(stream);
   int32_t* offsets = table + 4 * num_chunks_max;
-  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kWG), 0, s, cu_seqlens, num_seqs, offsets);
+  int32_t* order = offsets + num_seqs + 1;
+  int32_t* scu = order + num_seqs;
+  int32_t* flag = scu + num_seqs + 1;
+  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kWG), 0, s, cu_seqlens, num_seqs, num_tokens, offsets, scu,
+                     flag);
   if (num_chunks_max > 0)
-    hipLaunchKernelGGL(chunk_fill_kernel, dim3((num_chunks_max + kWG - 1) / kWG), dim3(kWG), 0, s, cu_seqlens,
-                       num_seqs, offsets, num_chunks_max, reinterpret_cast<int4*>(table));
+    hipLaunchKernelGGL(chunk_fill_kernel, dim3((num_chunks_max + kWG - 1) / kWG), dim3(kWG), 0, s, scu, num_seqs,
+                       offsets, num_chunks_max, reinterpret_cast<int4*>(table));
   if (num_seqs > 0)
-    hipLaunchKernelGGL(chunk_order_kernel, dim3((num_seqs + kWG - 1) / kWG), dim3(kWG), 0, s, cu_seqlens, num_seqs,
-                       offsets + num_seqs + 1);
+    hipLaunchKernelGGL(chunk_order_kernel, dim3((num_seqs + kWG - 1) / kWG), dim3(kWG), 0, s, scu, num_seqs, order);
   return launch_status("pkda_chunk_table");
 }
 

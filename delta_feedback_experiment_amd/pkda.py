@@ -133,7 +133,12 @@ def fused_recurrent_pkda(
     if cu_seqlens is not None:
         if B != 1:
             raise ValueError("cu_seqlens requires batch size 1")
-        cu = cu_seqlens.to(torch.int32).contiguous()
+        from .chunk import ChunkPlan
+
+        # the kernel reads document bounds from the chunk table's sanitised
+        # copy: a malformed cu_seqlens cannot send it past the token tensors
+        with torch.cuda.device(device):
+            cu = ChunkPlan.make(q, cu_seqlens).sanitized_cu
         N = cu.numel() - 1
         seqlen = 0
     else:

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 8
+#define PKDA_ABI_VERSION 9
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -144,17 +144,25 @@ int pkda_decode_step(const pkda_recurrent_args* args, void* stream);
  * Chunks of PKDA_CHUNK tokens start at every document's first token.  With
  * cu_seqlens the chunk list depends on the data, so it is built on the device
  * into a caller-provided int32 workspace `table` of
- *   4 * num_chunks_max + 2 * num_seqs + 1 elements
- * (per chunk {document, first token, length, -}, each document's first chunk
- * id plus the total, and the documents ordered by length, longest first: the
- * per-document passes start the longest documents first),
- * num_chunks_max = ceil(N_tok / 64) + num_seqs (an upper bound the host knows
- * without reading cu_seqlens).  Every chunked entry point below takes the same
- * table; launches sized by num_chunks_max skip the unused tail.  Equal-length
- * rows need no table (pass NULL).  cu_seqlens must be nondecreasing from 0.
+ *   4 * num_chunks_max + 3 * num_seqs + 3 elements
+ * (per chunk {document, first token, length, -}; each document's first chunk
+ * id plus the total; the documents ordered by length, longest first: the
+ * per-document passes start the longest documents first; a sanitised copy of
+ * cu_seqlens; a flag), num_chunks_max >= ceil(num_tokens / 64) + num_seqs (an
+ * upper bound the host knows without reading cu_seqlens).  Every chunked
+ * entry point below takes the same table and reads document bounds only from
+ * its sanitised copy: the running maximum of cu_seqlens clamped to
+ * [0, num_tokens].  A malformed cu_seqlens (cu[0] != 0, a decrease, or
+ * cu[num_seqs] != num_tokens) therefore cannot move an access outside the
+ * token tensors or the table; it sets the flag (the table's last element) to
+ * 1, which a caller may read back.  Launches sized by num_chunks_max skip the
+ * unused tail.  Equal-length rows need no table (pass NULL).
+ * pkda_recurrent_fwd reads cu_seqlens directly: pass it the table's
+ * sanitised copy (at 4 * num_chunks_max + 2 * num_seqs + 1) when the values
+ * are not known to be well formed.
  * ------------------------------------------------------------------------- */
-int pkda_chunk_table(const int32_t* cu_seqlens, int32_t num_seqs, int32_t num_chunks_max, int32_t* table,
-                     void* stream);
+int pkda_chunk_table(const int32_t* cu_seqlens, int32_t num_seqs, int32_t num_tokens, int32_t num_chunks_max,
+                     int32_t* table, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Gate: chunk-local cumulative log-decay, and its backward.

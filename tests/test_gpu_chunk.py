@@ -49,7 +49,9 @@ def test_chunk_table_documents_longest_first(dev):
     plan = ChunkPlan.make(q, cu.to(dev))
     table = plan.table.cpu()
     bound = plan.num_chunks
-    assert table.numel() == 4 * bound + 2 * N + 1
+    assert table.numel() == 4 * bound + 3 * N + 3
+    assert plan.cu_seqlens_ok()
+    assert torch.equal(plan.sanitized_cu.cpu(), cu)
     counts = [-(-n // 64) for n in lens]
     offsets = table[4 * bound:4 * bound + N + 1].tolist()
     assert offsets == [sum(counts[:n]) for n in range(N + 1)]
@@ -58,9 +60,47 @@ def test_chunk_table_documents_longest_first(dev):
         for j in range(counts[n]):
             doc, start, ln = entries[offsets[n] + j, :3].tolist()
             assert (doc, start, ln) == (n, int(cu[n]) + 64 * j, min(64, lens[n] - 64 * j))
-    order = table[4 * bound + N + 1:].tolist()
+    order = table[4 * bound + N + 1:4 * bound + 2 * N + 1].tolist()
     assert order == sorted(range(N), key=lambda n: (-lens[n], n))
 
+
+
+@pytest.mark.parametrize("cu,ok", [
+    ([0, 17, 17, 100, 164], True),
+    ([0, 17, 9, 100, 164], False),       # a decrease
+    ([5, 17, 40, 100, 164], False),      # cu[0] != 0
+    ([0, 17, 40, 100, 150], False),      # ends before the packed length
+    ([0, 17, 40, 100, 900], False),      # ends past it
+    ([0, -30, 40, 2000, 90], False),     # negative and huge values
+])
+def test_chunk_table_sanitises_cu_seqlens(dev, cu, ok):
+    """The table kernels read the caller's cu_seqlens once and keep a
+    sanitised copy -- the running maximum clamped to [0, N_tok] -- that every
+    later kernel reads; the chunk list stays inside the tokens and the
+    table's bound, and a malformed input raises the table's flag.  Only the
+    table kernels run here (their reads of cu are cu[0..N], their writes stay
+    in the table)."""
+    from delta_feedback_experiment_amd.chunk import ChunkPlan
+
+    print(f"[gpu] chunk table sanitises {cu}", flush=True)
+    T = 164
+    cu_t = torch.tensor(cu, dtype=torch.int32)
+    q = torch.empty(1, T, 1, 64, device=dev, dtype=torch.bfloat16)
+    plan = ChunkPlan.make(q, cu_t.to(dev))
+    assert plan.cu_seqlens_ok() == ok
+    expect = cu_t.cummax(0).values.clamp(0, T)
+    scu = plan.sanitized_cu.cpu()
+    assert torch.equal(scu, expect), (scu.tolist(), expect.tolist())
+    N, bound = len(cu) - 1, plan.num_chunks
+    table = plan.table.cpu()
+    offsets = table[4 * bound:4 * bound + N + 1]
+    lens = (scu[1:] - scu[:-1]).tolist()
+    assert offsets.tolist() == [sum(-(-n // 64) for n in lens[:i]) for i in range(N + 1)]
+    entries = table[:4 * bound].reshape(bound, 4)[:int(offsets[-1])]
+    assert int(entries[:, 1].min()) >= 0 and int((entries[:, 1] + entries[:, 2]).max()) <= T
+    if not ok:
+        with pytest.raises(ValueError, match="cu_seqlens"):
+            ChunkPlan.make(q, cu_t.to(dev), check=True)
 
 def test_state_pass_forms_agree_bitwise(dev):
     """Every kernel works per head and the state passes per value column, so
