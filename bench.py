@@ -16,11 +16,21 @@ Printed as ONE JSON line:
   roofline        the dominant kernel of the step, timed with HIP events on
                   the stream it runs on, against bf16 dense MFMA peak, with its
                   algorithmic flops per launch (per token-head figures below);
+  median_ms/min_ms  the median and fastest of the K replays (each between
+                  its own events; value uses the K replays back to back);
+  checks          before timing: every output and gradient finite, and two
+                  backwards accumulated in FP32 and halved equal to one;
+  agreement       before timing: the GPU step on a slice of the workload's
+                  own inputs against the CPU oracle, relative L2 <= 2e-2 for
+                  o and every gradient (a failed check exits non-zero);
   cpu_baseline    the CPU oracle (a restatement of the reference's portable
-                  recurrence) timed on this host over a bounded sample;
+                  recurrence) timed on this host over a bounded sample, with
+                  BASELINE configs 1 (whole forward) and 4 (decode steps);
+  c3, c5          the packed-document and long-context workloads, timed as
+                  the headline step;
   decode          the batched slot-pool decode step (B=256 live sequences in
-                  a 512-slot [512, 32, 128, 128] FP32 pool, 1000 steps),
-                  achieved HBM GB/s against 8 TB/s;
+                  a 512-slot [512, 32, 128, 128] FP32 pool, 1000 steps with
+                  1000 distinct slot subsets), achieved HBM GB/s against 8 TB/s;
   qkv_conv        the recurrence's producer (fused Q/K/V short convolution +
                   SiLU + L2 norm), forward and backward at the screen
                   geometry, achieved HBM GB/s against 8 TB/s;
@@ -106,19 +116,49 @@ STAGE_KERNEL = {
 TRAFFIC_PROFILE = ROOT / "profiles" / "pkda_chunk_c2_decode_c4_hbm_traffic.md"
 
 
+def kernel_source_hash() -> str:
+    """SHA-256 over the library's kernel sources and C ABI header (sorted by
+    name): what a committed counter summary was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted((ROOT / "delta_feedback_experiment_amd" / "csrc").glob("*.hip"))
+    files += sorted((ROOT / "delta_feedback_experiment_amd" / "csrc").glob("*.h"))
+    files += sorted((ROOT / "include").glob("*.h"))
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def profiled_traffic(kernel: str) -> dict | None:
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE passes, scaled by the counters of a 1 GiB copy),
-    or None when the summary has no row for this kernel."""
+    (FETCH_SIZE and WRITE_SIZE passes, scaled by the counters of a 1 GiB copy).
+    None when the summary has no row for this kernel; a summary measured on
+    other kernel sources than these (its ``source hash`` line) is refused and
+    reported as stale instead of as bytes."""
     if not TRAFFIC_PROFILE.exists():
         return None
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
+    text = TRAFFIC_PROFILE.read_text()
+    recorded = None
+    for line in text.splitlines():
+        if line.lower().startswith("source hash:"):
+            recorded = line.split(":", 1)[1].strip().strip("`")
+    current = kernel_source_hash()
+    for line in text.splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) == 4 and cells[0].strip("`").startswith(kernel + "("):
+            if recorded != current:
+                return {"stale": True, "profile_source_hash": recorded, "source_hash": current,
+                        "source": TRAFFIC_PROFILE.name}
             read_mib, write_mib = float(cells[2]), float(cells[3])
             return {"bytes": (read_mib + write_mib) * 2**20, "read_MiB": read_mib, "written_MiB": write_mib,
-                    "source": TRAFFIC_PROFILE.name}
+                    "source": TRAFFIC_PROFILE.name, "source_hash": recorded}
     return None
+
+
+def traffic_bytes(t: dict | None) -> float | None:
+    return None if t is None or t.get("stale") else t["bytes"]
 
 
 def l2norm(t: torch.Tensor) -> torch.Tensor:
@@ -196,12 +236,16 @@ def time_step(inp: dict, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def time_step_graph(inp: dict, steps: int, warmup: int) -> tuple[float, bool]:
+def time_step_graph(inp: dict, steps: int, warmup: int) -> dict:
     """Captured: one fwd+bwd step recorded into a HIP graph after warm-up on a
-    side stream, replayed K times between two events (the reference's
-    ``captured_run``, scripts/pkda_bench.py:239-285).  Every replay's
-    gradients are checked bitwise against the eager step first.
-    Returns (ms per step, replays agree)."""
+    side stream, replayed K times back to back, each replay between its own
+    pair of events (the reference's ``captured_run``,
+    scripts/pkda_bench.py:239-285).  Every replay's gradients are checked
+    bitwise against the eager step.  Returns ms per step over the K replays
+    (first event to last), the median and minimum replay, the samples, and
+    whether the replays agree."""
+    import statistics
+
     names = ["q", "k", "v", "g", "beta"] + (["s0"] if inp["s0"] is not None else [])
     leaves = [inp[n].detach().requires_grad_() for n in names]
     eager = [gr.clone() for gr in fwd_bwd(inp, leaves)]
@@ -221,14 +265,43 @@ def time_step_graph(inp: dict, steps: int, warmup: int) -> tuple[float, bool]:
         agree &= all(torch.equal(a, b) for a, b in zip(static_grads, eager))
         fwd_bwd(inp, leaves)
         torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        graph.replay()
-    end.record()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
+    for e0, e1 in events:
+        e0.record()
+        graph.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    samples = [a.elapsed_time(b) for a, b in events]
     agree &= all(torch.equal(a, b) for a, b in zip(static_grads, eager))
-    return start.elapsed_time(end) / steps, agree
+    return {"ms_per_step": events[0][0].elapsed_time(events[-1][1]) / steps,
+            "median_ms": statistics.median(samples), "min_ms": min(samples), "samples_ms": samples,
+            "agree": agree}
+
+
+def step_checks(inp: dict) -> dict:
+    """Before timing: every output and gradient of one eager step is finite,
+    and two independent backwards accumulated in FP32 buffers and halved give
+    the single step's gradients (the reference's ``accumulation_check``,
+    scripts/pkda_bench.py:224-236; these kernels are deterministic, so the
+    deviation is FP32 rounding of the sum)."""
+    from delta_feedback_experiment_amd import chunk_pkda
+
+    names = ["q", "k", "v", "g", "beta"] + (["s0"] if inp["s0"] is not None else [])
+    leaves = [inp[n].detach().requires_grad_() for n in names]
+    s0 = leaves[5] if len(leaves) > 5 else None
+    o, S, _ = chunk_pkda(*leaves[:5], initial_state=s0, output_final_state=s0 is not None, cu_seqlens=inp["cu"])
+    outs = [o] if S is None else [o, S]
+    first = torch.autograd.grad(outs, leaves, [inp["do"]] + ([torch.zeros_like(S)] if S is not None else []))
+    finite = all(bool(torch.isfinite(t).all()) for t in (*outs, *first))
+    sinks = [g.detach().float().clone() for g in first]
+    for sink, g in zip(sinks, fwd_bwd(inp, leaves)):
+        sink.add_(g.float())
+    dev = 0.0
+    for name, sink, g in zip(names, sinks, first):
+        ref = g.float()
+        dev = max(dev, float((sink * 0.5 - ref).norm() / ref.norm().clamp_min(1e-30)))
+    return {"finite": finite, "accumulation_max_rel": dev, "accumulation_ok": dev <= 1e-6}
 
 
 def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
@@ -325,9 +398,10 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
     t1.record()
     torch.cuda.synchronize()
     wall_ms = t0.elapsed_time(t1)
-    # captured: G steps (each with its own slot indices) in one HIP graph,
-    # replayed until `steps` steps have run; one launch per step
-    G = min(100, steps)
+    # captured: all `steps` steps, each with its own slot permutation, in one
+    # HIP graph (one launch per step), replayed `reps` times
+    import statistics
+
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -335,17 +409,20 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
         pkda_decode_step_(*sets[0], pool, idx[0], out=out)
     torch.cuda.current_stream().wait_stream(side)
     with torch.cuda.graph(graph):
-        for i in range(G):
+        for i in range(steps):
             pkda_decode_step_(*sets[i % 4], pool, idx[i], out=out)
-    reps = max(1, steps // G)
     graph.replay()
     torch.cuda.synchronize()
-    t0.record()
+    reps = 5
+    samples = []
     for _ in range(reps):
+        t0.record()
         graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    kern_ms = t0.elapsed_time(t1) / (reps * G)
+        t1.record()
+        torch.cuda.synchronize()
+        samples.append(t0.elapsed_time(t1) / steps)
+    kern_ms = statistics.median(samples)
+    finite = bool(torch.isfinite(out).all()) and bool(torch.isfinite(pool).all())
     nbytes = 2 * N * H * D * D * 4 + N * H * (2 * (2 * D + D) + 2 * 2) + N * H * D * 2 + 4 * N
     traffic = profiled_traffic(STAGE_KERNEL["decode"])
     return {
@@ -355,7 +432,11 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
         "ms_per_step_eager": wall_ms / steps,
         "tokens_per_s": N / (kern_ms / 1e3),
         "kernel_us": kern_ms * 1e3,
-        "timing": "HIP graph of 100 steps replayed; kernel_us = replay time / steps (launch gaps included)",
+        "min_us": min(samples) * 1e3,
+        "distinct_slot_permutations": steps,
+        "finite": finite,
+        "timing": f"HIP graph of {steps} steps (each its own random slot subset), replayed {reps} times; "
+                  "kernel_us = median replay time / steps (launch gaps included)",
         "bytes_per_step": nbytes,
         "roofline": {
             "bound": "hbm",
@@ -364,7 +445,7 @@ def bench_decode(dev: torch.device, steps: int, warmup: int = 10, seed: int = 7)
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": nbytes / (kern_ms / 1e3) / HBM_PEAK,
-            "traffic": None if traffic is None else traffic["bytes"],
+            "traffic": traffic_bytes(traffic),
             "traffic_detail": traffic,
         },
     }
@@ -639,15 +720,99 @@ def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> 
             "GBps": 2 * nbytes / (ms / 1e3) / 1e9}
 
 
-def cpu_baseline(D: int = 128, H: int = 16, T: int = 512, seed: int = 3, budget_s: float = 12.0,
-                 max_rows: int = 32) -> dict:
-    """The CPU oracle's fwd+bwd over B=1 row slices of the workload (FP32, all
-    host cores): rows of T tokens are run one after another until ``budget_s``
-    seconds or ``max_rows`` rows, and the token rate is over all of them."""
+def workload_line(name: str, dev: torch.device, steps: int, warmup: int) -> dict:
+    """One more workload's fwd+bwd step (c3 packed documents, c5 long
+    context), captured and replayed as the headline step, with the same
+    pre-timing checks."""
+    w = WORKLOADS[name]
+    inp = make_chunk_inputs(w, dev)
+    checks = step_checks(inp)
+    g = time_step_graph(inp, steps, warmup)
+    ntok = w["B"] * w["T"]
+    flops = ntok * w["H"] * step_flops_convention(w["D"])
+    line = {
+        "workload": f"{name}: " + {"c3": "one packed row of 32,768 tokens, geometric documents (mean 1,024), "
+                                          "state reset per document",
+                                   "c5": "B2 T16384, S0 ~ N(0, 0.02), 10% of tokens g = -8"}[name]
+                    + f", H{w['H']} d{w['D']} bf16 fwd+bwd",
+        "ms_per_step": g["ms_per_step"], "median_ms": g["median_ms"], "min_ms": g["min_ms"],
+        "tokens_per_s": ntok / (g["median_ms"] / 1e3),
+        "mfma_frac_step": flops / (g["median_ms"] / 1e3) / MFMA_BF16_PEAK,
+        "graph_replays_agree": g["agree"], **checks,
+    }
+    if w["varlen"]:
+        line["documents"] = int(inp["cu"].numel() - 1)
+    return line
+
+
+def _slice_inputs(inp: dict, T_s: int) -> dict:
+    """The first row's first ``T_s`` tokens of a workload's inputs (packed
+    documents cut at ``T_s``), on the host in FP32 (the BF16 values as they
+    are), and the same on the device in the workload's dtypes."""
+    out = {}
+    for n in ("q", "k", "v", "g", "beta", "do"):
+        out[n] = inp[n][:1, :T_s].contiguous()
+    out["s0"] = None if inp["s0"] is None else inp["s0"][:1].contiguous()
+    out["cu"] = None
+    if inp["cu"] is not None:
+        cu = [c for c in inp["cu"].tolist() if c < T_s] + [T_s]
+        out["cu"] = torch.tensor(cu, dtype=torch.int32, device=inp["q"].device)
+        if out["s0"] is not None:
+            out["s0"] = inp["s0"][:len(cu) - 1].contiguous()
+    return out
+
+
+def cpu_baseline(inp: dict, D: int = 128, H: int = 16, T: int = 512, seed: int = 3, budget_s: float = 12.0,
+                 max_rows: int = 32, agree_tokens: int = 512, c4_seconds: float = 10.0) -> tuple[dict, dict]:
+    """The CPU leg: the oracle (a CPU restatement of the reference's portable
+    recurrence, pkda.py:355-410) as the checker and the host baseline.
+
+    agreement -- before any timing, the GPU step on a slice of the workload's
+      own inputs (first row, first ``agree_tokens`` tokens) against the
+      oracle in FP32 on the same BF16-rounded inputs: relative L2 of o and
+      every gradient <= 2e-2 (the reference checks agreement before it keeps
+      a timing, scripts/pkda_bench.py:343-353);
+    value -- the oracle's fwd+bwd over B=1 row slices of the workload (all
+      host cores) until ``budget_s`` seconds or ``max_rows`` rows;
+    c1_forward -- BASELINE config 1 (B1 T256 H4 d64 FP32) forward, whole;
+    c4_decode -- BASELINE config 4 decode steps on the host (256 live of a
+      512-slot [512, 32, 128, 128] FP32 pool) until ``c4_seconds``."""
+    from delta_feedback_experiment_amd import chunk_pkda
     from oracle import pkda_oracle as oracle
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
+
+    # -- agreement on a slice of the workload, before timing
+    sl = _slice_inputs(inp, agree_tokens)
+    names = ["q", "k", "v", "g", "beta"] + (["s0"] if sl["s0"] is not None else [])
+    dl = [sl[n].detach().clone().requires_grad_() for n in names]
+    s0 = dl[5] if len(dl) > 5 else None
+    o, S, _ = chunk_pkda(*dl[:5], initial_state=s0, output_final_state=s0 is not None, cu_seqlens=sl["cu"])
+    dS = torch.zeros_like(S) if S is not None else None
+    got = torch.autograd.grad([o] + ([S] if S is not None else []), dl, [sl["do"]] + ([dS] if dS is not None else []))
+    cl = [sl[n].detach().float().cpu().clone().requires_grad_() for n in names]
+    o_r, S_r, _ = oracle.pkda_reference(*cl[:5], initial_state=cl[5] if len(cl) > 5 else None,
+                                        output_final_state=S is not None,
+                                        cu_seqlens=None if sl["cu"] is None else sl["cu"].cpu(),
+                                        out_dtype=torch.float32)
+    ref = torch.autograd.grad([o_r] + ([S_r] if S_r is not None else []), cl,
+                              [sl["do"].float().cpu()] + ([torch.zeros_like(S_r)] if S_r is not None else []))
+
+    def rel(a, b):
+        a, b = a.detach().double().cpu(), b.detach().double()
+        return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+    errs = {"o": rel(o.float(), o_r)}
+    errs.update({"d" + n: rel(a.float(), b) for n, a, b in zip(names, got, ref)})
+    finite = all(bool(torch.isfinite(t).all()) for t in (o, *got))
+    agreement = {"slice": f"row 0, tokens 0..{agree_tokens - 1}" + (" (documents cut there)" if sl["cu"] is not None
+                                                                     else ""),
+                 "bar": 2e-2, "rel_l2": errs, "finite": finite, "ok": finite and max(errs.values()) <= 2e-2}
+    print(f"[bench] agreement vs oracle: {json.dumps({k: f'{v:.2e}' for k, v in errs.items()})}", file=sys.stderr,
+          flush=True)
+
+    # -- the oracle's fwd+bwd rate over row slices
     gen = torch.Generator().manual_seed(seed)
     total = 0.0
     rows = 0
@@ -664,7 +829,40 @@ def cpu_baseline(D: int = 128, H: int = 16, T: int = 512, seed: int = 3, budget_
         torch.autograd.grad(o, leaves, do)
         total += time.perf_counter() - t0
         rows += 1
-    return {
+
+    # -- the whole forward
+    with torch.no_grad():
+        q1 = l2norm(torch.randn(1, 256, 4, 64, generator=gen))
+        k1 = l2norm(torch.randn(1, 256, 4, 64, generator=gen))
+        v1 = torch.randn(1, 256, 4, 64, generator=gen)
+        b1 = torch.sigmoid(torch.randn(1, 256, 4, generator=gen))
+        g1 = -F.softplus(torch.randn(1, 256, 4, generator=gen))
+        oracle.pkda_reference(q1, k1, v1, g1, b1)  # warm
+        t0 = time.perf_counter()
+        reps1 = 0
+        while reps1 < 3 or time.perf_counter() - t0 < 2.0:
+            oracle.pkda_reference(q1, k1, v1, g1, b1, output_final_state=True)
+            reps1 += 1
+        c1_ms = (time.perf_counter() - t0) / reps1 * 1e3
+
+    # -- decode steps on the host
+    with torch.no_grad():
+        P, N4, H4, D4 = 512, 256, 32, 128
+        pool = 0.02 * torch.randn(P, H4, D4, D4, generator=gen)
+        steps4, t4 = 0, 0.0
+        while steps4 < 20 and t4 < c4_seconds:
+            idx = torch.randperm(P, generator=gen)[:N4].to(torch.int32)
+            q4 = l2norm(torch.randn(N4, H4, D4, generator=gen)).to(torch.bfloat16)
+            k4 = l2norm(torch.randn(N4, H4, D4, generator=gen)).to(torch.bfloat16)
+            v4 = torch.randn(N4, H4, D4, generator=gen).to(torch.bfloat16)
+            b4 = torch.sigmoid(torch.randn(N4, H4, generator=gen))
+            g4 = -F.softplus(torch.randn(N4, H4, generator=gen))
+            t0 = time.perf_counter()
+            oracle.decode_step_reference(q4, k4, v4, g4, b4, pool, idx)
+            t4 += time.perf_counter() - t0
+            steps4 += 1
+        del pool
+    base = {
         "value": rows * T / total,
         "unit": "tokens/s",
         "cores": threads,
@@ -673,7 +871,12 @@ def cpu_baseline(D: int = 128, H: int = 16, T: int = 512, seed: int = 3, budget_
                   f"d={D} ({total:.1f} s); same per-token work as one row of the GPU workload",
         "seconds": total,
         "token_heads_per_s": rows * T * H / total,
+        "c1_forward": {"workload": "BASELINE config 1: B1 T256 H4 d64 FP32 forward (with final state)",
+                       "ms": c1_ms, "tokens_per_s": 256 / (c1_ms / 1e3), "repeats": reps1},
+        "c4_decode": {"workload": "BASELINE config 4 on the host: 256 live of 512 FP32 slots [512,32,128,128]",
+                      "steps": steps4, "ms_per_step": t4 / steps4 * 1e3, "tokens_per_s": N4 * steps4 / t4},
     }
+    return base, agreement
 
 
 def main() -> None:
@@ -690,6 +893,7 @@ def main() -> None:
     ap.add_argument("--no-serve", action="store_true", help="skip the slot-pool prefill and conv-token lines")
     ap.add_argument("--no-production", action="store_true",
                     help="skip the production-operator line (per-channel gate + preconditioner)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the c3 and c5 lines")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -710,16 +914,24 @@ def main() -> None:
     print(f"[bench] workload {args.workload} {w}", file=sys.stderr, flush=True)
     inp = make_chunk_inputs(w, dev)
     ntok = w["B"] * w["T"]
+    # before any timing: the CPU leg (oracle agreement on a slice, host
+    # baselines) and the step's own checks (finite, FP32 accumulation)
+    base = agreement = None
+    if not args.no_cpu:
+        base, agreement = cpu_baseline(inp, D=w["D"], H=w["H"], T=args.cpu_tokens, budget_s=args.cpu_seconds)
+    checks = step_checks(inp)
+    print(f"[bench] checks {json.dumps(checks)}", file=sys.stderr, flush=True)
     ms_eager = time_step(inp, args.steps, args.warmup)
     print(f"[bench] fwd+bwd eager {ms_eager:.3f} ms/step", file=sys.stderr, flush=True)
-    ms, graph_ok, timing = ms_eager, None, "eager"
+    ms, graph_ok, timing, graph = ms_eager, None, "eager", None
     if not args.no_graph:
         try:
-            ms_graph, graph_ok = time_step_graph(inp, args.steps, args.warmup)
-            print(f"[bench] fwd+bwd graph {ms_graph:.3f} ms/step (replays agree: {graph_ok})", file=sys.stderr,
-                  flush=True)
+            graph = time_step_graph(inp, args.steps, args.warmup)
+            graph_ok = graph["agree"]
+            print(f"[bench] fwd+bwd graph {graph['ms_per_step']:.3f} ms/step, median {graph['median_ms']:.3f}, "
+                  f"min {graph['min_ms']:.3f} (replays agree: {graph_ok})", file=sys.stderr, flush=True)
             if graph_ok:
-                ms, timing = ms_graph, "HIP graph replay"
+                ms, timing = graph["ms_per_step"], f"HIP graph, {args.steps} replays back to back"
         except RuntimeError as exc:  # capture unsupported here: report eager
             print(f"[bench] graph capture failed ({exc}); reporting eager timing", file=sys.stderr, flush=True)
     per_th = stage_flops(w["D"])
@@ -743,7 +955,11 @@ def main() -> None:
         "ms_per_step": ms,
         "ms_per_step_eager": ms_eager,
         "timing": timing,
+        "median_ms": None if graph is None else graph["median_ms"],
+        "min_ms": None if graph is None else graph["min_ms"],
         "graph_replays_agree": graph_ok,
+        "checks": checks,
+        "agreement": agreement,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -762,9 +978,10 @@ def main() -> None:
             "peak": MFMA_BF16_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK,
-            "traffic": None if dom_traffic is None else dom_traffic["bytes"],
+            "traffic": traffic_bytes(dom_traffic),
             "traffic_detail": dom_traffic,
-            "hbm_GBps": None if dom_traffic is None else dom_traffic["bytes"] / (stage_ms[dom] / 1e3) / 1e9,
+            "hbm_GBps": None if traffic_bytes(dom_traffic) is None
+            else traffic_bytes(dom_traffic) / (stage_ms[dom] / 1e3) / 1e9,
         },
         "stage_ms": stage_ms,
     }
@@ -802,14 +1019,35 @@ def main() -> None:
         print(f"[bench] production operator {c['ms_per_step']:.3f} ms/step "
               f"({c['tokens_per_s'] / 1e6:.2f} M tok/s)", file=sys.stderr, flush=True)
         inp = None
+    if not args.no_extra and args.workload == "c2":
+        del inp
+        torch.cuda.empty_cache()
+        for extra in ("c3", "c5"):
+            result[extra] = workload_line(extra, dev, args.steps, args.warmup)
+            c = result[extra]
+            print(f"[bench] {extra} {c['median_ms']:.3f} ms/step median ({c['tokens_per_s'] / 1e6:.1f} M tok/s, "
+                  f"{100 * c['mfma_frac_step']:.1f}% MFMA)", file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
+        inp = None
     if not args.no_decode:
         del inp
         torch.cuda.empty_cache()
         result["decode"] = bench_decode(dev, args.decode_steps)
         print(f"[bench] decode {result['decode']['kernel_us']:.1f} us/step", file=sys.stderr, flush=True)
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(D=w["D"], H=w["H"], T=args.cpu_tokens, budget_s=args.cpu_seconds)
+    if base is not None:
+        result["cpu_baseline"] = base
+    ok = checks["finite"] and checks["accumulation_ok"] and graph_ok is not False
+    ok &= agreement is None or agreement["ok"]
+    for extra in ("c3", "c5"):
+        if extra in result:
+            ok &= result[extra]["finite"] and result[extra]["graph_replays_agree"]
+    if "decode" in result:
+        ok &= result["decode"]["finite"]
     print(json.dumps(result), flush=True)
+    if not ok:
+        print("[bench] a correctness check failed (see checks / agreement); the timing above is not valid",
+              file=sys.stderr, flush=True)
+        sys.exit(1)
 
 
 if __name__ == "__main__":
