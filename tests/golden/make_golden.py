@@ -17,6 +17,10 @@ copied.  Cases:
 * ``prod_grad`` -- production PKDA (squash_x=1.5, per-channel raw gate,
                    nonzero S0/A0, T=80 not a multiple of 64), all gradients.
 * ``decode_t1`` -- B3 T1 H2 d64 production step from nonzero S0/A0.
+* ``module_fwd`` -- the whole mixer, ``PreconditionedKDA.forward``
+                   (pkda.py:477-559) on its CPU path: B2 T80 hidden 96, H2
+                   d64, squash_x=1.5, randomised parameters, the output, the
+                   final S and A, and the gradients of x and every parameter.
 """
 
 from __future__ import annotations
@@ -106,6 +110,34 @@ def run_case(PreconditionedKDA, name, *, B, T, H, d, squash_x, seed, per_channel
     print(name, {k: v.shape for k, v in out.items() if hasattr(v, "shape") and v.ndim})
 
 
+def run_module_case(PreconditionedKDA, name, *, B, T, hidden, H, d, seed):
+    torch.manual_seed(seed)
+    m = PreconditionedKDA(hidden_size=hidden, num_heads=H, head_dim=d, squash_x=1.5, squash_eps=1e-6)
+    gen = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():  # parameters the default init leaves trivial
+        m.output_norm.copy_(1 + 0.3 * torch.randn(m.output_norm.shape, generator=gen))
+        m.output_gate_up.bias.copy_(0.3 * torch.randn(m.output_gate_up.bias.shape, generator=gen))
+        m.dt_bias.copy_(0.1 * torch.randn(m.dt_bias.shape, generator=gen))
+        m.log_precond_center.copy_(-0.2 + 0.1 * torch.randn(H, generator=gen))
+    x = torch.randn(B, T, hidden, generator=gen).requires_grad_()
+    out, S, A, _conv = m(x, output_final_state=True)
+    dout = torch.randn(out.shape, generator=gen)
+    dS = torch.randn(S.shape, generator=gen)
+    dA = torch.randn(A.shape, generator=gen)
+    params = dict(m.named_parameters())
+    loss = (out * dout).sum() + (S * dS).sum() + (A * dA).sum()
+    got = torch.autograd.grad(loss, [x] + list(params.values()))
+    rec = dict(in_x=x.detach().numpy(), out_o=out.detach().numpy(), out_S=S.detach().numpy(),
+               out_A=A.detach().numpy(), cot_o=dout.numpy(), cot_S=dS.numpy(), cot_A=dA.numpy(),
+               grad_x=got[0].numpy())
+    for (n, prm), gval in zip(params.items(), got[1:]):
+        key = n.replace(".", "__")
+        rec[f"param_{key}"] = prm.detach().numpy()
+        rec[f"grad_{key}"] = gval.numpy()
+    np.savez_compressed(HERE / f"{name}.npz", **rec)
+    print(name, sorted(k for k in rec if k.startswith("param_")))
+
+
 def main():
     root = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
     sys.path.insert(0, str(root))
@@ -120,6 +152,7 @@ def main():
              per_channel=True, nonzero_state=True, grads=True)
     run_case(PreconditionedKDA, "decode_t1", B=3, T=1, H=2, d=64, squash_x=1.5, seed=4,
              per_channel=True, nonzero_state=True, grads=False)
+    run_module_case(PreconditionedKDA, "module_fwd", B=2, T=80, hidden=96, H=2, d=64, seed=5)
 
 
 if __name__ == "__main__":

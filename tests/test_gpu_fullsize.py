@@ -157,3 +157,95 @@ def test_full_size_gradients_stay_in_their_row_and_head(dev):
         xs, ys = x.transpose(1, 2)[keep], y.transpose(1, 2)[keep]
         assert torch.equal(xs, ys), f"{name} changed outside row 3 head 7"
         assert not torch.equal(x.transpose(1, 2)[3, 7], y.transpose(1, 2)[3, 7]), f"{name} ignores dO"
+
+
+def test_c3_full_size_gradients_per_document(dev):
+    """c3 (one packed row of 32,768 tokens, geometric documents, H16 d128 bf16),
+    forward and backward at full size.
+
+    * Document independence, bitwise: the gradients of three documents (the
+      first, the longest and the last) equal those of the same document run
+      on its own -- chunks start at document boundaries and every state
+      resets there, so the arithmetic is the same.
+    * The leading documents (those ending by token 1,024) against the CPU
+      oracle's FP32 autograd on the same BF16-rounded values."""
+    from delta_feedback_experiment_amd import chunk_pkda
+
+    T, H, D = 32768, 16, 128
+    q, k, v, g, beta = make_inputs(dev, 1, T, H, D, seed=41)
+    cu = geometric_cu_seqlens(T, seed=42).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(43)
+    do = torch.randn(1, T, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    print(f"[gpu] c3 full-size gradients ({cu.numel() - 1} documents)", flush=True)
+
+    def run(sl, cu_part):
+        leaves = [t[:, sl].detach().clone().requires_grad_() for t in (q, k, v, g, beta)]
+        o, _, _ = chunk_pkda(*leaves, cu_seqlens=cu_part)
+        return (o, *torch.autograd.grad(o, leaves, do[:, sl]))
+
+    full = run(slice(0, T), cu)
+    cuh = cu.cpu().tolist()
+    lens = [b - a for a, b in zip(cuh, cuh[1:])]
+    for n in sorted({0, max(range(len(lens)), key=lambda i: lens[i]), len(lens) - 1}):
+        a, b = cuh[n], cuh[n + 1]
+        one = run(slice(a, b), torch.tensor([0, b - a], dtype=torch.int32, device=dev))
+        for name, x, y in zip(("o", "dq", "dk", "dv", "dg", "dbeta"), full, one):
+            assert torch.equal(x[:, a:b], y), f"document {n}: {name} differs from its own run"
+    lead = max(i for i in range(len(cuh)) if cuh[i] <= 1024)
+    end = cuh[lead]
+    assert end > 0
+    leaves = [t[:, :end].detach().cpu().float().requires_grad_() for t in (q, k, v, g, beta)]
+    o_r, _, _ = oracle.pkda_reference(*leaves, cu_seqlens=torch.tensor(cuh[:lead + 1]), out_dtype=torch.float32)
+    ref = torch.autograd.grad(o_r, leaves, do[:, :end].cpu().float())
+    errs = {"o": rel_l2(full[0][:, :end].float(), o_r)}
+    errs.update({n: rel_l2(a[:, :end].float(), b) for n, a, b in zip(("dq", "dk", "dv", "dg", "dbeta"),
+                                                                        full[1:], ref)})
+    print(f"  documents 0..{lead - 1} (tokens 0..{end - 1}): " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()),
+          flush=True)
+    bad = {n: e for n, e in errs.items() if not e < BF16_TOL}
+    assert not bad, bad
+
+
+def test_c5_full_size_gradients_with_initial_state(dev):
+    """c5 (B2 T16384 H32 d128 bf16, S0 ~ N(0, 0.02), 10% of tokens g = -8),
+    forward and backward at full size including dS0.
+
+    * Row independence, bitwise: row 1 run alone gives row 1's gradients
+      and dS0 of the batch run.
+    * A slice against the oracle: with these decays (g <= -softplus(.)
+      everywhere) a token's influence on S0's gradient, and the later tokens'
+      influence on the first 256 tokens' gradients, fall below e^-150 within
+      a few hundred tokens, so dS0 and the gradients of tokens 0..255 of the
+      full run equal those of the oracle's run over the first 1,024 tokens
+      (loss on those outputs only) to far below the BF16 bar."""
+    from delta_feedback_experiment_amd import chunk_pkda
+
+    B, T, H, D = 2, 16384, 32, 128
+    q, k, v, g, beta = make_inputs(dev, B, T, H, D, seed=51, strong=True)
+    gen = torch.Generator(device=dev).manual_seed(52)
+    s0 = 0.02 * torch.randn(B, H, D, D, generator=gen, device=dev)
+    do = torch.randn(B, T, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    dS = torch.randn(B, H, D, D, generator=gen, device=dev)
+    print("[gpu] c5 full-size gradients with dS0", flush=True)
+
+    def run(rows):
+        leaves = [t[rows].detach().clone().requires_grad_() for t in (q, k, v, g, beta, s0)]
+        o, S, _ = chunk_pkda(*leaves[:5], initial_state=leaves[5], output_final_state=True)
+        return (o, S, *torch.autograd.grad([o, S], leaves, [do[rows], dS[rows]]))
+
+    full = run(slice(0, B))
+    alone = run(slice(1, 2))
+    for name, x, y in zip(("o", "S", "dq", "dk", "dv", "dg", "dbeta", "dS0"), full, alone):
+        assert torch.equal(x[1:2], y), f"row 1: {name} differs from its own run"
+    Ts, keep = 1024, 256
+    cut = [t[:1, :Ts].detach().cpu().float() for t in (q, k, v, g, beta)]
+    leaves = [t.clone().requires_grad_() for t in cut] + [s0[:1].detach().cpu().clone().requires_grad_()]
+    o_r, _, _ = oracle.pkda_reference(*leaves[:5], initial_state=leaves[5], out_dtype=torch.float32)
+    ref = torch.autograd.grad(o_r, leaves, do[:1, :Ts].cpu().float())
+    errs = {"o": rel_l2(full[0][:1, :Ts].float(), o_r)}
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta"), full[2:7], ref[:5]):
+        errs[name] = rel_l2(a[:1, :keep].float(), b[:, :keep])
+    errs["dS0"] = rel_l2(full[7][:1], ref[5])
+    print("  row 0, tokens 0..255 and dS0: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    bad = {n: e for n, e in errs.items() if not e < BF16_TOL}
+    assert not bad, bad
