@@ -667,7 +667,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   if (ci.len <= 0) return;
   const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int rb = wave & 3, ch = wave >> 2;
+  // waves w and w + 4 share a SIMD: they take row blocks rb and 3 - rb, whose
+  // cross-block pair work (later blocks for small rb, earlier ones for large)
+  // adds up to the same on every SIMD
+  const int ch = wave >> 2, rb = ch ? 3 - (wave & 3) : (wave & 3);
   const int r0 = 16 * rb;
   const int len = ci.len;
   const int64_t gs = (int64_t)H * D;
@@ -705,10 +708,18 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   auto kwval = [&](int r, int c) { return kw32g ? kw32g[(int64_t)r * gs + c] : io<T>::load(kwg + (int64_t)r * gs + c); };
   const float* gg = p.gcum + row0 * D;        // G rows, stride gs
   const float* gC = gg + (int64_t)(len - 1) * gs;
-  auto G = [&](int r, int c) { return gg[(int64_t)min(r, len - 1) * gs + c]; };
   const float scale = p.scale;
 
   if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
+  // G at this lane's accumulator positions (rows r0 + 4 (lane / 16) + e,
+  // column 16 (ch HCT + j) + lane % 16) is read there by phases 1 to 2b: loaded
+  // where phase 1 first needs it and kept.  K waits in registers behind the
+  // first tiles and takes dO's region once phase 1 is done with it.  (A wait
+  // for a load covers every load issued before it, so loads go in the order
+  // they are needed.)
+  const int rq = 4 * (lane >> 4);
+  float Gl[HCT][4], gCl[HCT];
+  RegTile<kFW, C, D, T> rK;
   {
     RegTile<kFW, C, D, T> rU, rdO, rdU, rV;
     RegTile<kFW, C, C, T> rT;
@@ -719,6 +730,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
     rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rH.load(hsrc);
+    rK.load(kg_, gs, len);
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
@@ -740,9 +752,11 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     f32x4 acc = zero4();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Gl[j][e] = gg[(int64_t)min(r0 + rq + e, len - 1) * gs + c];
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dq[j][e] = scale * exp_fast(G(r0 + acc_row(lane, e), c)) * acc[e];
+    for (int e = 0; e < 4; ++e) dq[j][e] = scale * exp_fast(Gl[j][e]) * acc[e];
     f32x4 acv = zero4();
     mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
     dv[j] = acv;  // dBv until it is in LDS
@@ -771,6 +785,23 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     }
   }
   __syncthreads();
+  // the next phases' operands start their way in: G_C, dH and the write key at
+  // this lane's positions (0 on the last row and past it, whose terms cancel)
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) gCl[j] = gC[16 * (ch * HCT + j) + (lane & 15)];
+  TiledTile<kFW, D, T> rdH;
+  rdH.load(dhsrc);
+  float Wl[HCT][4];
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int c = 16 * (ch * HCT + j) + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + rq + e;
+      Wl[j][e] = r < len - 1 ? kwval(r, c) : 0.f;
+    }
+  }
+  rK.store(sK, L::LD);  // dO's region: phase 1 is done with it
   // dBv over dU (every wave has read dU); dv = beta dBv
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
@@ -789,10 +820,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int s = r0 + acc_row(lane, e);
-      const float eg = exp_fast(G(s, c));
-      const float kv = s < len ? io<T>::load(kg_ + s * gs + c) : 0.f;
+      const float eg = exp_fast(Gl[j][e]);
       dk[j][e] = -sBeta[s] * eg * acc[e];
-      db[e] -= acc[e] * eg * kv;
+      db[e] -= acc[e] * eg * from_e<E>(sK[s * L::LD + c]);
     }
   }
 #pragma unroll
@@ -808,14 +838,15 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   __syncthreads();
   // ---- phase 2b: dH replaces S0; per-row sum(S0 * dH); dKg = U dH^T --------------
+  // phase 3's Q starts its way in (its region, dBv's, is dead)
+  RegTile<kFW, C, D, T> rQ;
+  rQ.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
   // (dH arrives tile-major: per-piece partial sums go through the T region,
   // dead since phase 1, and are summed per row in a fixed order)
   {
     constexpr int V = Vec16<T>::N;
     constexpr int PPR = D / V;  // pieces per row
     float* sPart = reinterpret_cast<float*>(smem + L::off_T);
-    TiledTile<kFW, D, T> rdH;
-    rdH.load(dhsrc);
 #pragma unroll
     for (int i = 0; i < TiledTile<kFW, D, T>::ITER; ++i) {
       int r, c;
@@ -839,45 +870,47 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
-    const int c = 16 * ct + acc_col(lane);
     f32x4 acc = zero4();
     mma_tile<E, ROW, COL>(acc, sU, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
     float col = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int s = r0 + acc_row(lane, e);
-      dkws[j][e] = exp_fast(gC[c] - G(s, c)) * acc[e];
-      // the last row's term (decay e^0) cancels against its own -kw dkw
-      if (s < len - 1) col += kwval(s, c) * dkws[j][e];
+      dkws[j][e] = exp_fast(gCl[j] - Gl[j][e]) * acc[e];
+      // the last row's term (decay e^0) cancels against its own -kw dkw (Wl is 0 there)
+      col += Wl[j][e] * dkws[j][e];
     }
     col += __shfl_xor(col, 16);
     col += __shfl_xor(col, 32);
     if (lane < 16) sKG[rb * D + 16 * ct + lane] = col;
   }
+  // G (rows past the chunk repeat its last) and the write key in FP32 (kw32,
+  // else kw or k widened; zero rows past the chunk) for phase 3
+  RegTile<kFW, C, D, float> rG, rW32;
+  RegTile<kFW, C, D, T> rWn;
+  rG.load_clamped(gg, gs, len);
+  if (kw32g) rW32.load(kw32g, gs, len);
+  else rWn.load(p.kw_is_k ? kg_ : kwg, gs, len);
   __syncthreads();
   // ---- phase 3: pairwise terms with the decay inside the contraction ----------
   // dAkk is held once (unscaled); beta_t multiplies the other factor, so the
   // two halves of each (t, x) pair's gate term see the same rounded value.
-  load_tile<kFW, C, D>(sK, L::LD, kg_, gs, len, Ident());
-  load_tile<kFW, C, D>(sQ, L::LD, static_cast<const T*>(p.q) + row0 * D, gs, len, Ident());
-  for (int i = tid; i < C * (D / 4); i += kFW) {
-    const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
-    *reinterpret_cast<float4*>(sG + r * L::LDG + c) =
-        *reinterpret_cast<const float4*>(gg + (int64_t)min(r, len - 1) * gs + c);
-  }
-  // the write key in FP32 (kw32, else kw or k widened); zero rows past the chunk
-  for (int i = tid; i < C * (D / 4); i += kFW) {
-    const int r = i / (D / 4), c = (i - r * (D / 4)) * 4;
-    float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (r < len) {
-      if (kw32g) {
-        w = *reinterpret_cast<const float4*>(kw32g + (int64_t)r * gs + c);
-      } else {
-        const T* src = (p.kw_is_k ? kg_ : kwg) + (int64_t)r * gs + c;
-        w = make_float4(io<T>::load(src), io<T>::load(src + 1), io<T>::load(src + 2), io<T>::load(src + 3));
-      }
+  rQ.store(sQ, L::LD);
+  rG.store(sG, L::LDG);
+  if (kw32g) {
+    rW32.store(sKWf, L::LDW);
+  } else {
+    using RW = RegTile<kFW, C, D, T>;
+#pragma unroll
+    for (int i = 0; i < RW::ITER; ++i) {
+      const int idx = tid + i * kFW;
+      if (RW::TOTAL % kFW != 0 && idx >= RW::TOTAL) break;
+      const int r = idx / RW::PER_ROW, c = (idx - r * RW::PER_ROW) * RW::V;
+      float x[RW::V];
+      Vec16<T>::unpack(rWn.r[i], x);
+#pragma unroll
+      for (int v = 0; v < RW::V; v += 4)
+        *reinterpret_cast<float4*>(sKWf + r * L::LDW + c + v) = make_float4(x[v], x[v + 1], x[v + 2], x[v + 3]);
     }
-    *reinterpret_cast<float4*>(sKWf + r * L::LDW + c) = w;
   }
   if (ch == 0) {  // this row block's diagonal blocks, transposed
     for (int i = lane; i < 256; i += 64) {
@@ -904,7 +937,6 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     const int nn = 16 * ct + (lane & 15);  // this lane's B column (== c)
-    const int rq = 4 * (lane >> 4);        // this lane's rows r0 + rq + e
     float gr[4], kv[4], qv[4], wv[4];
     f32x4 dg;
     {
@@ -924,41 +956,60 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         // enter two of q dq, kw dkw and sum(kg dkg) with opposite signs and
         // are left out of the gate gradient
         dg[e] = qv[e] * dq[j][e] + kv[e] * dk[j][e] - (r == len - 1 ? 0.f : wv[e] * dkws[j][e]);
-        if (r == len - 1) dg[e] += exp_fast(gC[c]) * sHD[c] + kgc;
+        if (r == len - 1) dg[e] += exp_fast(sG[(C - 1) * L::LDG + c]) * sHD[c] + kgc;
         dq[j][e] += pd * wv[e];
         dkw[j][e] = dkws[j][e] + pd * qv[e];
       }
     }
-    // (1) rows t of this block, x < t inside it: exactly, e^{G[t]-G[x]} as the
-    // running product of the per-token decays e^{G[y]-G[y-1]} (each <= 1)
-    // from x + 1 to t, started at 1 on the diagonal and 0 past it.  dAkk and
-    // dAqk are zero off their triangles (dAqk's diagonal is held apart), so
-    // no pair needs a mask.
+    // (1) rows t_e = r0 + rq + e of this block, x <= t_e inside it, exactly
+    // (pairs with x > t_e vanish: dAkk and dAqk are zero on and above the
+    // diagonal, dAqk's diagonal being held apart).  For x <= t_0 the decay
+    // factors as e^{G[t_e]-G[x]} = R_e E(x), R_e = e^{G[t_e]-G[t_0]},
+    // E(x) = e^{G[t_0]-G[x]} the running product of the per-token decays
+    // e^{G[y]-G[y-1]} from x + 1 to t_0 (every factor <= 1, so no overflow for
+    // any gate); the pairs with x in (t_0, t_e] take their factor directly.
     {
       f32x4 ak = zero4(), aq = zero4();
-      float ex[4] = {0.f, 0.f, 0.f, 0.f};
-      float gnext = 0.f;
-#pragma unroll 2
-      for (int xo = 15; xo >= 0; --xo) {
+#pragma unroll
+      for (int u = 1; u < 3; ++u) {  // x = t_u, rows e > u
+        float p1[4], p2[4];
+        lds4(sP1T + (16 * rb + rq + u) * 16 + rq, p1);
+        if constexpr (L::P2B) lds4(sP2BT + (16 * rb + rq + u) * 16 + rq, p2);
+        else lds4(sP2T + (16 * rb + rq + u) * 16 + rq, p2);
+#pragma unroll
+        for (int e = u + 1; e < 4; ++e) {
+          const float w = wv[u] * exp_fast(gr[e] - gr[u]);
+          ak[e] += p1[e] * w;
+          aq[e] += p2[e] * w;
+        }
+      }
+      float ak0[4] = {0.f, 0.f, 0.f, 0.f}, aq0[4] = {0.f, 0.f, 0.f, 0.f};
+      float ep = 1.f, gprev = gr[0];
+      for (int xo = rq; xo >= 0; --xo) {  // x = r0 + xo <= t_0
         const int x = r0 + xo;
-        const float gx = sG[x * L::LDG + c];
-        const float d = xo < 15 ? exp_fast(gnext - gx) : 0.f;  // decay of token x + 1
-        gnext = gx;
-        const float kwx = sKWf[x * L::LDW + c];
+        float kwx = wv[0];
+        if (xo < rq) {
+          const float gx = sG[x * L::LDG + c];
+          ep *= exp_fast(gprev - gx);  // decay of token x + 1
+          gprev = gx;
+          kwx = sKWf[x * L::LDW + c];
+        }
         float p1[4], p2[4];
         lds4(sP1T + (16 * rb + xo) * 16 + rq, p1);
         if constexpr (L::P2B) lds4(sP2BT + (16 * rb + xo) * 16 + rq, p2);
         else lds4(sP2T + (16 * rb + xo) * 16 + rq, p2);
+        const float w = kwx * ep;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const bool diag = xo == rq + e;
-          ex[e] = diag ? 1.f : ex[e] * d;
-          ak[e] += p1[e] * kwx * ex[e];
-          aq[e] += diag ? 0.f : p2[e] * kwx * ex[e];
+          ak0[e] += p1[e] * w;
+          aq0[e] += p2[e] * w;
         }
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
+        const float R = e == 0 ? 1.f : exp_fast(gr[e] - gr[0]);
+        ak[e] += R * ak0[e];
+        aq[e] += R * aq0[e];
         const float bk = sBeta[r0 + rq + e] * ak[e];
         dk[j][e] += bk;
         db[e] += kv[e] * ak[e];
@@ -995,32 +1046,42 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         dg[e] += rnd(sb * kv[e] * dlo) * akX[e] + rnd(qv[e] * dlo) * aqX[e];
       }
     }
-    // (3) rows x of this block, t > x inside it: exactly, as (1)
+    // (3) rows x_e = r0 + rq + e of this block as the key, t > x_e inside it,
+    // exactly, as (1): for t > t_3, e^{G[t]-G[x_e]} = E'(t) R'_e with
+    // E'(t) = e^{G[t]-G[t_3]} (running product from t_3 + 1) and
+    // R'_e = e^{G[t_3]-G[x_e]}; t in (x_e, t_3] directly.
     {
       f32x4 aw = zero4();
-      float ex[4] = {0.f, 0.f, 0.f, 0.f};
-      float gprev = 0.f;
-#pragma unroll 2
-      for (int xo = 0; xo < 16; ++xo) {  // x as the row of columns r < x
-        const int x = r0 + xo;
-        const float gx = sG[x * L::LDG + c];
-        const float d = xo > 0 ? exp_fast(gx - gprev) : 0.f;  // decay of token x
-        gprev = gx;
-        const float kx = sBeta[x] * from_e<E>(sK[x * L::LD + c]);
-        const float qx = from_e<E>(sQ[x * L::LD + c]);
-        float p1[4], p2[4];
-        lds4(sP1r + x * L::LDC + r0 + rq, p1);
-        if constexpr (L::P2B) lds4(sP2B + (16 * rb + xo) * 16 + rq, p2);
-        else lds4(sP2 + x * L::LDC + r0 + rq, p2);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool diag = xo == rq + e;
-          ex[e] = diag ? 1.f : ex[e] * d;
-          aw[e] += p1[e] * kx * ex[e] + (diag ? 0.f : p2[e] * qx * ex[e]);
-        }
+      for (int u = 1; u < 4; ++u) {  // t = t_u, keys e < u
+        const int t = r0 + rq + u;
+        float p1[4], p2[4];
+        lds4(sP1r + t * L::LDC + r0 + rq, p1);
+        if constexpr (L::P2B) lds4(sP2B + (16 * rb + rq + u) * 16 + rq, p2);
+        else lds4(sP2 + t * L::LDC + r0 + rq, p2);
+        const float kx = sBeta[t] * kv[u], qx = qv[u];
+#pragma unroll
+        for (int e = 0; e < u; ++e) aw[e] += (p1[e] * kx + p2[e] * qx) * exp_fast(gr[u] - gr[e]);
+      }
+      float aw0[4] = {0.f, 0.f, 0.f, 0.f};
+      float ep = 1.f, gprev = gr[3];
+      for (int xo = rq + 4; xo < 16; ++xo) {  // t = r0 + xo > t_3
+        const int t = r0 + xo;
+        const float gt = sG[t * L::LDG + c];
+        ep *= exp_fast(gt - gprev);  // decay of token t
+        gprev = gt;
+        const float kx = sBeta[t] * from_e<E>(sK[t * L::LD + c]) * ep;
+        const float qx = from_e<E>(sQ[t * L::LD + c]) * ep;
+        float p1[4], p2[4];
+        lds4(sP1r + t * L::LDC + r0 + rq, p1);
+        if constexpr (L::P2B) lds4(sP2B + (16 * rb + xo) * 16 + rq, p2);
+        else lds4(sP2 + t * L::LDC + r0 + rq, p2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) aw0[e] += p1[e] * kx + p2[e] * qx;
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
+        aw[e] += (e == 3 ? 1.f : exp_fast(gr[3] - gr[e])) * aw0[e];
         dkw[j][e] += aw[e];
         dg[e] -= wv[e] * aw[e];
       }
