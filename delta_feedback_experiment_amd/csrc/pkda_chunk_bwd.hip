@@ -1021,7 +1021,24 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     if (rb > 0) {
       f32x4 akX = zero4(), aqX = zero4();
       const float grlo = sG[rlo * L::LDG + nn];
-      for (int k0 = 0; k0 < kceil<E>(r0); k0 += Mma<E>::KS) {
+      if constexpr (sizeof(E) == 2) {
+        // 16-deep steps cover exactly the earlier blocks: A = rows of dAkk and
+        // s dAqk (four consecutive x, one 8-byte read each), B = kw e^{G[R]-G[x]}
+        for (int k0 = 0; k0 < r0; k0 += 16) {
+          const int kk = k0 + 4 * (lane >> 4);
+          const s16x4_t a1 = *reinterpret_cast<const s16x4_t*>(sP1r + (r0 + (lane & 15)) * L::LDC + kk);
+          const s16x4_t a2 = *reinterpret_cast<const s16x4_t*>(sP2 + (r0 + (lane & 15)) * L::LDC + kk);
+          float bx[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int x = kk + jj;
+            bx[jj] = sKWf[x * L::LDW + nn] * exp_fast(grlo - sG[x * L::LDG + nn]);
+          }
+          const s16x4_t b = pack_bf16x4(bx);
+          mfma16_bf16(akX, a1, b);
+          mfma16_bf16(aqX, a2, b);
+        }
+      } else for (int k0 = 0; k0 < kceil<E>(r0); k0 += Mma<E>::KS) {
         const int kk = k0 + F::off(lane);
         float a1[F::N], a2[F::N], bx[F::N];
 #pragma unroll
@@ -1091,7 +1108,25 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       const int R = 16 * bi - 1;
       const float gR = sG[R * L::LDG + nn];
       f32x4 aw = zero4();
-      for (int k0 = kfloor<E>(16 * bi); k0 < 16 * bi + 16; k0 += Mma<E>::KS) {
+      if constexpr (sizeof(E) == 2) {
+        // one 16-deep step over block bi: A = dAkk and s dAqk columns x (their
+        // rows t k-major: transposed reads), B = beta k e^{G[t]-G[R]} and
+        // q e^{G[t]-G[R]} from K and Q read the same way
+        const s16x4_t a1 = lds_read_kmajor4(sP1r + r0, L::LDC, 16 * bi, lane);
+        const s16x4_t a2 = lds_read_kmajor4(sP2 + r0, L::LDC, 16 * bi, lane);
+        const s16x4_t kt = lds_read_kmajor4(sK + 16 * ct, L::LD, 16 * bi, lane);
+        const s16x4_t qt = lds_read_kmajor4(sQ + 16 * ct, L::LD, 16 * bi, lane);
+        float b1[4], b2[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int t = 16 * bi + 4 * (lane >> 4) + jj;
+          const float f = exp_fast(sG[t * L::LDG + nn] - gR);
+          b1[jj] = sBeta[t] * bf16_to_f32(static_cast<bf16_t>(kt[jj])) * f;  // beta_t on the key, dAkk unscaled
+          b2[jj] = bf16_to_f32(static_cast<bf16_t>(qt[jj])) * f;
+        }
+        mfma16_bf16(aw, a1, pack_bf16x4(b1));
+        mfma16_bf16(aw, a2, pack_bf16x4(b2));
+      } else for (int k0 = kfloor<E>(16 * bi); k0 < 16 * bi + 16; k0 += Mma<E>::KS) {
         const int kk = k0 + F::off(lane);
         float a1[F::N], a2[F::N], b1[F::N], b2[F::N];
 #pragma unroll

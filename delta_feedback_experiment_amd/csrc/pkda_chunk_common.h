@@ -137,6 +137,27 @@ __device__ __forceinline__ s16x8_t lds_read_kmajor(const bf16_t* p, int ld, int 
   return s16x8_t{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
 }
 
+// Four k-consecutive bf16 of one column of a k-major LDS tile (element (k, n)
+// at p[k * ld + n]), as the operand of a 16x16x16 MFMA step: lane 16q + i
+// receives column i, rows k0 + 4q .. k0 + 4q + 3 (one ds_read_b64_tr_b16).
+__device__ __forceinline__ s16x4_t lds_read_kmajor4(const bf16_t* p, int ld, int k0, int lane) {
+  const int i = lane & 15, q = lane >> 4;
+  const bf16_t* src = p + (k0 + 4 * q + (i >> 2)) * ld + 4 * (i & 3);
+  return __builtin_bit_cast(s16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(src)));
+}
+
+// acc += A B over one 16-deep k-step (bf16 operands, four k per lane: lane
+// 16q + i holds row / column i, k = 4q .. 4q + 3).
+__device__ __forceinline__ void mfma16_bf16(f32x4& acc, const s16x4_t& a, const s16x4_t& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+}
+
+// Four floats rounded to bf16 (nearest even), packed as an operand.
+__device__ __forceinline__ s16x4_t pack_bf16x4(const float* x) {
+  return s16x4_t{static_cast<short>(f32_to_bf16(x[0])), static_cast<short>(f32_to_bf16(x[1])),
+                 static_cast<short>(f32_to_bf16(x[2])), static_cast<short>(f32_to_bf16(x[3]))};
+}
+
 // Operand fragments of one MFMA k-step, loaded on their own (frag_a / frag_b
 // on tiles already offset to row m0 / column n0) so a phase can hold
 // operands that several products share, and mfma() on them.
