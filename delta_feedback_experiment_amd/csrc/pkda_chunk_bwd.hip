@@ -886,32 +886,16 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   // G (rows past the chunk repeat its last) and the write key in FP32 (kw32,
   // else kw or k widened; zero rows past the chunk) for phase 3
   RegTile<kFW, C, D, float> rG, rW32;
-  RegTile<kFW, C, D, T> rWn;
   rG.load_clamped(gg, gs, len);
   if (kw32g) rW32.load(kw32g, gs, len);
-  else rWn.load(p.kw_is_k ? kg_ : kwg, gs, len);
   __syncthreads();
   // ---- phase 3: pairwise terms with the decay inside the contraction ----------
   // dAkk is held once (unscaled); beta_t multiplies the other factor, so the
   // two halves of each (t, x) pair's gate term see the same rounded value.
   rQ.store(sQ, L::LD);
   rG.store(sG, L::LDG);
-  if (kw32g) {
-    rW32.store(sKWf, L::LDW);
-  } else {
-    using RW = RegTile<kFW, C, D, T>;
-#pragma unroll
-    for (int i = 0; i < RW::ITER; ++i) {
-      const int idx = tid + i * kFW;
-      if (RW::TOTAL % kFW != 0 && idx >= RW::TOTAL) break;
-      const int r = idx / RW::PER_ROW, c = (idx - r * RW::PER_ROW) * RW::V;
-      float x[RW::V];
-      Vec16<T>::unpack(rWn.r[i], x);
-#pragma unroll
-      for (int v = 0; v < RW::V; v += 4)
-        *reinterpret_cast<float4*>(sKWf + r * L::LDW + c + v) = make_float4(x[v], x[v + 1], x[v + 2], x[v + 3]);
-    }
-  }
+  if (kw32g) rW32.store(sKWf, L::LDW);
+  else load_tile<kFW, C, D>(sKWf, L::LDW, p.kw_is_k ? kg_ : kwg, gs, len, Ident());  // widened to FP32
   if (ch == 0) {  // this row block's diagonal blocks, transposed
     for (int i = lane; i < 256; i += 64) {
       const int xo = i >> 4, to = i & 15;

@@ -466,13 +466,16 @@ struct RegTile {
     }
   }
   // rows r >= nvalid (nvalid >= 1) repeat row nvalid - 1
+  // (every piece is assigned on every path: a conditionally assigned piece
+  // keeps the array out of registers)
   __device__ __forceinline__ void load_clamped(const T* g, int64_t gstride, int nvalid) {
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
       const int idx = threadIdx.x + i * NT;
       const int row = min(idx / PER_ROW, nvalid - 1);
       const int c = (idx % PER_ROW) * V;
-      if (idx < TOTAL) r[i] = *reinterpret_cast<const uint4*>(g + row * gstride + c);
+      r[i] = (TOTAL % NT == 0 || idx < TOTAL) ? *reinterpret_cast<const uint4*>(g + row * gstride + c)
+                                              : make_uint4(0u, 0u, 0u, 0u);
     }
   }
   __device__ __forceinline__ void store(T* lds, int ld) const { store_as(threadIdx.x, lds, ld); }
