@@ -969,20 +969,34 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       }
       float ak0[4] = {0.f, 0.f, 0.f, 0.f}, aq0[4] = {0.f, 0.f, 0.f, 0.f};
       float ep = 1.f, gprev = gr[0];
-      for (int xo = rq; xo >= 0; --xo) {  // x = r0 + xo <= t_0
-        const int x = r0 + xo;
-        float kwx = wv[0];
-        if (xo < rq) {
-          const float gx = sG[x * L::LDG + c];
-          ep *= exp_fast(gprev - gx);  // decay of token x + 1
-          gprev = gx;
-          kwx = sKWf[x * L::LDW + c];
+      {  // x = t_0: the product starts at 1
+        float p1[4], p2[4];
+        lds4(sP1T + (16 * rb + rq) * 16 + rq, p1);
+        if constexpr (L::P2B) lds4(sP2BT + (16 * rb + rq) * 16 + rq, p2);
+        else lds4(sP2T + (16 * rb + rq) * 16 + rq, p2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ak0[e] += p1[e] * wv[0];
+          aq0[e] += p2[e] * wv[0];
         }
+      }
+      // x = t_0 - i, i = 1 .. 12: the same count for every lane (lanes whose
+      // x would fall below the block read its first row and add nothing), so
+      // the loop unrolls and a step's reads go out with its neighbours
+#pragma unroll 4
+      for (int i = 1; i < 13; ++i) {
+        const bool in = i <= rq;
+        const int xo = in ? rq - i : 0;
+        const int x = r0 + xo;
+        const float gx = sG[x * L::LDG + c];
+        const float kwx = sKWf[x * L::LDW + c];
         float p1[4], p2[4];
         lds4(sP1T + (16 * rb + xo) * 16 + rq, p1);
         if constexpr (L::P2B) lds4(sP2BT + (16 * rb + xo) * 16 + rq, p2);
         else lds4(sP2T + (16 * rb + xo) * 16 + rq, p2);
-        const float w = kwx * ep;
+        ep = in ? ep * exp_fast(gprev - gx) : ep;  // decay of token x + 1
+        gprev = in ? gx : gprev;
+        const float w = in ? kwx * ep : 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           ak0[e] += p1[e] * w;
@@ -1066,17 +1080,22 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       }
       float aw0[4] = {0.f, 0.f, 0.f, 0.f};
       float ep = 1.f, gprev = gr[3];
-      for (int xo = rq + 4; xo < 16; ++xo) {  // t = r0 + xo > t_3
+      // t = t_3 + i, i = 1 .. 12, the same count for every lane (as in (1))
+#pragma unroll 4
+      for (int i = 1; i < 13; ++i) {
+        const bool in = rq + 3 + i < 16;
+        const int xo = in ? rq + 3 + i : 15;
         const int t = r0 + xo;
         const float gt = sG[t * L::LDG + c];
-        ep *= exp_fast(gt - gprev);  // decay of token t
-        gprev = gt;
-        const float kx = sBeta[t] * from_e<E>(sK[t * L::LD + c]) * ep;
-        const float qx = from_e<E>(sQ[t * L::LD + c]) * ep;
+        const float kt = sBeta[t] * from_e<E>(sK[t * L::LD + c]);
+        const float qt = from_e<E>(sQ[t * L::LD + c]);
         float p1[4], p2[4];
         lds4(sP1r + t * L::LDC + r0 + rq, p1);
         if constexpr (L::P2B) lds4(sP2B + (16 * rb + xo) * 16 + rq, p2);
         else lds4(sP2 + t * L::LDC + r0 + rq, p2);
+        ep = in ? ep * exp_fast(gt - gprev) : ep;  // decay of token t
+        gprev = in ? gt : gprev;
+        const float kx = in ? kt * ep : 0.f, qx = in ? qt * ep : 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) aw0[e] += p1[e] * kx + p2[e] * qx;
       }
