@@ -66,6 +66,40 @@ struct PrecondParams {
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
 
+// The per-(chunk, head) passes: CH consecutive channels per lane (two at
+// D = 128, so a chunk is one wave), read and written as one 4- or 8-byte
+// access per row, each channel its own chain.
+template <int D> struct PrecondChunk {
+  static constexpr int CH = D >= 128 ? 2 : 1;
+  static constexpr int NT = D / CH < 64 ? 64 : D / CH;
+};
+template <typename T, int CH> struct ChanIO;
+template <typename T> struct ChanIO<T, 1> {
+  __device__ __forceinline__ static void load(const T* p, float* x) { x[0] = io<T>::load(p); }
+  __device__ __forceinline__ static void store(T* p, const float* x) { io<T>::store(p, x[0]); }
+};
+template <> struct ChanIO<float, 2> {
+  __device__ __forceinline__ static void load(const float* p, float* x) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    x[0] = v.x;
+    x[1] = v.y;
+  }
+  __device__ __forceinline__ static void store(float* p, const float* x) {
+    *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+  }
+};
+template <> struct ChanIO<bf16_t, 2> {
+  __device__ __forceinline__ static void load(const bf16_t* p, float* x) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    x[0] = __uint_as_float(v << 16);
+    x[1] = __uint_as_float(v & 0xffff0000u);
+  }
+  __device__ __forceinline__ static void store(bf16_t* p, const float* x) {
+    *reinterpret_cast<uint32_t*>(p) =
+        static_cast<uint32_t>(f32_to_bf16(x[0])) | (static_cast<uint32_t>(f32_to_bf16(x[1])) << 16);
+  }
+};
+
 // Per-(chunk, head) launches: workgroup b takes chunk b / H of head b % H, so
 // neighbouring workgroups read neighbouring head slices of the same tokens.
 struct ChunkHead {
@@ -140,44 +174,54 @@ __device__ __forceinline__ float chunk_scan(const PrecondParams& p, float* buf, 
 // unchanged past it, so no load sits behind a branch.
 template <typename T, int D, bool APPLY, bool FULL>
 __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j, int h, int start, int len) {
-  constexpr int G = 8;
-  const int H = p.H, c = threadIdx.x;
+  constexpr int G = 8, CH = PrecondChunk<D>::CH;
+  using IO = ChanIO<T, CH>;
+  using FIO = ChanIO<float, CH>;
+  const int H = p.H, c0 = CH * threadIdx.x;
   const T* __restrict__ k = static_cast<const T*>(p.k);
   T* __restrict__ kw = static_cast<T*>(p.kw);
   const float* __restrict__ g_atk = p.g_atk;
   const float* __restrict__ beta_atk = p.beta_atk;
-  float* slot = p.a_chunk + ((int64_t)j * H + h) * D + c;
-  float a = APPLY ? *slot : 0.f;
+  float* slot = p.a_chunk + ((int64_t)j * H + h) * D + c0;
+  float a[CH];
+#pragma unroll
+  for (int q = 0; q < CH; ++q) a[q] = 0.f;
+  if (APPLY) FIO::load(slot, a);
   const float center = APPLY ? p.center[h] : 0.f;
   auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
 #pragma unroll 1
   for (int g0 = 0; g0 < C; g0 += G) {
-    float kc[G];
+    float kc[G][CH];
 #pragma unroll
-    for (int u = 0; u < G; ++u) kc[u] = io<T>::load(k + tok(g0 + u) * D + c);
+    for (int u = 0; u < G; ++u) IO::load(k + tok(g0 + u) * D + c0, kc[u]);
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       const int t = g0 + u;
       const int64_t th = tok(t);
-      const float an = expf(g_atk[th]) * a + beta_atk[th] * (kc[u] * kc[u]);
-      a = (FULL || t < len) ? an : a;
-      if (APPLY) {
-        const float r = logf(a + p.eps) - center;
-        const float w = kc[u] * expf(-p.log_x * (r / (1.f + fabsf(r))));
-        if (FULL || t < len) {
-          io<T>::store(kw + th * D + c, w);
-          if (p.kw32) p.kw32[th * D + c] = w;
+      const float eg = expf(g_atk[th]), bt = beta_atk[th];
+      float w[CH];
+#pragma unroll
+      for (int q = 0; q < CH; ++q) {
+        const float an = eg * a[q] + bt * (kc[u][q] * kc[u][q]);
+        a[q] = (FULL || t < len) ? an : a[q];
+        if (APPLY) {
+          const float r = logf(a[q] + p.eps) - center;
+          w[q] = kc[u][q] * expf(-p.log_x * (r / (1.f + fabsf(r))));
         }
+      }
+      if (APPLY && (FULL || t < len)) {
+        IO::store(kw + th * D + c0, w);
+        if (p.kw32) FIO::store(p.kw32 + th * D + c0, w);
       }
     }
   }
-  if (!APPLY) *slot = a;
+  if (!APPLY) FIO::store(slot, a);
 }
 
 template <typename T, int D, bool APPLY>
-__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_fwd_chunk_kernel(PrecondParams p) {
+__global__ __launch_bounds__(PrecondChunk<D>::NT) void precond_fwd_chunk_kernel(PrecondParams p) {
   const ChunkHead ch = chunk_head(p.H);
-  if (threadIdx.x >= D) return;
+  if (threadIdx.x * PrecondChunk<D>::CH >= D) return;
   const ChunkInfo ci = chunk_info(p.geom, ch.j);
   if (ci.len == C)
     precond_fwd_chunk<T, D, APPLY, true>(p, ch.j, ch.h, ci.start, C);
@@ -220,44 +264,64 @@ __device__ __forceinline__ float row_sum16(float v) {
 // the rows through LDS.
 template <typename T, int D, bool APPLY, bool FULL>
 __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j, int h, int start, int len,
-                                                  float (*sRow)[C][PrecondThreads<D>::v / 16 + 1], float* sCen) {
-  constexpr int NR = PrecondThreads<D>::v / 16;  // 16-lane rows
+                                                  float (*sRow)[C][PrecondChunk<D>::NT / 16 + 1], float* sCen) {
+  constexpr int CH = PrecondChunk<D>::CH;
+  constexpr int NR = PrecondChunk<D>::NT / 16;  // 16-lane rows
   constexpr int G = APPLY ? 4 : 8;               // tokens per sub-block (measured best for each pass)
   constexpr int NB = C / G;
   constexpr int NQ = C / 16;                     // per-token sum registers
+  using IO = ChanIO<T, CH>;
+  using FIO = ChanIO<float, CH>;
   const int H = p.H, c = threadIdx.x, lane16 = c & 15;
-  const bool active = c < D;
-  const int cc = active ? c : 0;  // channel the lane reads (idle lanes mirror channel 0, contribute 0)
+  const bool active = c * CH < D;
+  const int c0 = active ? c * CH : 0;  // first channel the lane reads (idle lanes mirror 0, contribute 0)
   const T* __restrict__ k = static_cast<const T*>(p.k);
   const float* __restrict__ dkw_p = p.dkw;
   float* __restrict__ dk_p = p.dk;
   T* __restrict__ dk_fin = static_cast<T*>(p.dk_final);
   const float* __restrict__ g_atk = p.g_atk;
   const float* __restrict__ beta_atk = p.beta_atk;
-  const int64_t row = ((int64_t)j * H + h) * D + cc;
-  const float a_in = active ? p.a_chunk[row] : 0.f;
-  float lam = (APPLY && active) ? p.lam_chunk[row] : 0.f;
+  const int64_t row = ((int64_t)j * H + h) * D + c0;
+  float a_in[CH], lam[CH];
+#pragma unroll
+  for (int q = 0; q < CH; ++q) a_in[q] = lam[q] = 0.f;
+  if (active) FIO::load(p.a_chunk + row, a_in);
+  if (APPLY && active) FIO::load(p.lam_chunk + row, lam);
   const float center = p.center[h], lx = p.log_x, eps = p.eps;
   auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
-  auto step = [&](int t, float a, float kc) -> float {
+  // one token of the forward's A recurrence, channel by channel (the same
+  // arithmetic as the forward pass, so the same values)
+  auto step = [&](int t, float* a, const float* kc) {
     const int64_t th = tok(t);
-    const float an = expf(g_atk[th]) * a + beta_atk[th] * (kc * kc);
-    return (FULL || t < len) ? an : a;
+    const float eg = expf(g_atk[th]), bt = beta_atk[th];
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      const float an = eg * a[q] + bt * (kc[q] * kc[q]);
+      a[q] = (FULL || t < len) ? an : a[q];
+    }
   };
   // Register arrays indexed by the (rolled) sub-block number go through
   // compile-time selects so they stay in registers.
-  float a_blk[NB];  // A entering each sub-block
+  float a_blk[NB][CH];  // A entering each sub-block
   {
-    float a = a_in;
+    float a[CH];
+#pragma unroll
+    for (int q = 0; q < CH; ++q) a[q] = a_in[q];
 #pragma unroll 1
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
-      for (int q = 0; q < NB; ++q) a_blk[q] = q == b ? a : a_blk[q];
-      float kb[G];
+      for (int r = 0; r < NB; ++r)
 #pragma unroll
-      for (int u = 0; u < G; ++u) kb[u] = io<T>::load(k + tok(b * G + u) * D + cc);
+        for (int q = 0; q < CH; ++q) a_blk[r][q] = r == b ? a[q] : a_blk[r][q];
+      float kb[G][CH];
 #pragma unroll
-      for (int u = 0; u < G; ++u) a = step(b * G + u, a, active ? kb[u] : 0.f);
+      for (int u = 0; u < G; ++u) {
+        IO::load(k + tok(b * G + u) * D + c0, kb[u]);
+#pragma unroll
+        for (int q = 0; q < CH; ++q) kb[u][q] = active ? kb[u][q] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < G; ++u) step(b * G + u, a, kb[u]);
     }
   }
   float dcen = 0.f;
@@ -267,23 +331,31 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
 #pragma unroll 1
   for (int b = NB - 1; b >= 0; --b) {
     const int g0 = b * G;
-    float a_b = a_blk[0];
+    float a_b[CH];
 #pragma unroll
-    for (int q = 1; q < NB; ++q) a_b = q == b ? a_blk[q] : a_b;
-    float rk[G], ra[G], rdkw[G], rdk[G];
+    for (int q = 0; q < CH; ++q) {
+      a_b[q] = a_blk[0][q];
+#pragma unroll
+      for (int r = 1; r < NB; ++r) a_b[q] = r == b ? a_blk[r][q] : a_b[q];
+    }
+    float rk[G][CH], ra[G][CH], rdkw[G][CH], rdk[G][CH];
 #pragma unroll
     for (int u = 0; u < G; ++u) {
-      rk[u] = io<T>::load(k + tok(g0 + u) * D + cc);
-      rdkw[u] = dkw_p[tok(g0 + u) * D + cc];
-      if (APPLY) rdk[u] = dk_p[tok(g0 + u) * D + cc];
+      IO::load(k + tok(g0 + u) * D + c0, rk[u]);
+      FIO::load(dkw_p + tok(g0 + u) * D + c0, rdkw[u]);
+      if (APPLY) FIO::load(dk_p + tok(g0 + u) * D + c0, rdk[u]);
     }
     {
-      float a = a_b;
+      float a[CH];
+#pragma unroll
+      for (int q = 0; q < CH; ++q) a[q] = a_b[q];
 #pragma unroll
       for (int u = 0; u < G; ++u) {
-        rk[u] = active ? rk[u] : 0.f;
-        a = step(g0 + u, a, rk[u]);
-        ra[u] = a;
+#pragma unroll
+        for (int q = 0; q < CH; ++q) rk[u][q] = active ? rk[u][q] : 0.f;
+        step(g0 + u, a, rk[u]);
+#pragma unroll
+        for (int q = 0; q < CH; ++q) ra[u][q] = a[q];
       }
     }
 #pragma unroll
@@ -291,24 +363,33 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       const int t = g0 + u;
       const bool in = FULL || t < len;
       const int64_t th = tok(t);
-      const float kc = rk[u], at = ra[u];
       const float eg = expf(g_atk[th]);
-      const float r = logf(at + eps) - center;
-      const float den = 1.f + fabsf(r);
-      const float f = expf(-lx * (r / den));
-      const float dkw = active && in ? rdkw[u] : 0.f;
-      const float dr = dkw * kc * f * (-lx) / (den * den);
-      const float lam_t = lam + dr / (at + eps);
-      if (APPLY) {
-        dcen -= dr;
-        if (active && in) {
-          const float dkt = rdk[u] + (dkw * f + 2.f * beta_atk[th] * kc * lam_t);
-          if (dk_fin) io<T>::store(dk_fin + th * D + cc, dkt);
-          else dk_p[th * D + cc] = dkt;
+      float vg = 0.f, vb = 0.f, dkt[CH];
+#pragma unroll
+      for (int q = 0; q < CH; ++q) {
+        const float kc = rk[u][q], at = ra[u][q];
+        const float r = logf(at + eps) - center;
+        const float den = 1.f + fabsf(r);
+        const float f = expf(-lx * (r / den));
+        const float dkw = active && in ? rdkw[u][q] : 0.f;
+        const float dr = dkw * kc * f * (-lx) / (den * den);
+        const float lam_t = lam[q] + dr / (at + eps);
+        if (APPLY) {
+          dcen -= dr;
+          dkt[q] = rdk[u][q] + (dkw * f + 2.f * beta_atk[th] * kc * lam_t);
+          const float a_prev = u > 0 ? ra[u - 1][q] : a_b[q];
+          vg += lam_t * eg * a_prev;
+          vb += lam_t * kc * kc;
         }
-        const float a_prev = u > 0 ? ra[u - 1] : a_b;
-        const float vg = row_sum16(lam_t * eg * a_prev);
-        const float vb = row_sum16(lam_t * kc * kc);
+        lam[q] = in ? lam_t * eg : lam[q];  // carry to A_{t-1}
+      }
+      if (APPLY) {
+        if (active && in) {
+          if (dk_fin) IO::store(dk_fin + th * D + c0, dkt);
+          else FIO::store(dk_p + th * D + c0, dkt);
+        }
+        vg = row_sum16(vg);
+        vb = row_sum16(vb);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           const bool mine = q == (t >> 4) && lane16 == (t & 15);
@@ -316,11 +397,10 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
           sb[q] = mine ? vb : sb[q];
         }
       }
-      lam = in ? lam_t * eg : lam;  // carry to A_{t-1}
     }
   }
   if (!APPLY) {
-    if (active) p.lam_chunk[row] = lam;
+    if (active) FIO::store(p.lam_chunk + row, lam);
     return;
   }
 #pragma unroll
@@ -351,9 +431,9 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
 }
 
 template <typename T, int D, bool APPLY>
-__global__ __launch_bounds__(PrecondThreads<D>::v) void precond_bwd_chunk_kernel(PrecondParams p) {
-  __shared__ float sRow[2][C][PrecondThreads<D>::v / 16 + 1];
-  __shared__ float sCen[PrecondThreads<D>::v / 16];
+__global__ __launch_bounds__(PrecondChunk<D>::NT) void precond_bwd_chunk_kernel(PrecondParams p) {
+  __shared__ float sRow[2][C][PrecondChunk<D>::NT / 16 + 1];
+  __shared__ float sCen[PrecondChunk<D>::NT / 16];
   const ChunkHead ch = chunk_head(p.H);
   const ChunkInfo ci = chunk_info(p.geom, ch.j);
   if (ci.len == C)
@@ -434,18 +514,18 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
 
 template <typename T, int D>
 int launch_precond(const PrecondParams& p, bool backward, hipStream_t s) {
-  constexpr int NT = PrecondThreads<D>::v;
+  constexpr int NT = PrecondThreads<D>::v, NTC = PrecondChunk<D>::NT;
   const dim3 chunks((unsigned)((int64_t)p.geom.num_chunks * p.H));
   const dim3 docs = doc_grid(p.geom.num_seqs, p.H, 1);
   const bool any = p.geom.num_chunks > 0;
   if (backward) {
-    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, false>), chunks, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, false>), chunks, dim3(NTC), 0, s, p);
     hipLaunchKernelGGL((precond_bwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
-    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, true>), chunks, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, true>), chunks, dim3(NTC), 0, s, p);
   } else {
-    if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, false>), chunks, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, false>), chunks, dim3(NTC), 0, s, p);
     hipLaunchKernelGGL((precond_fwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
-    if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, true>), chunks, dim3(NT), 0, s, p);
+    if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, true>), chunks, dim3(NTC), 0, s, p);
   }
   return launch_status(backward ? "pkda_precond_bwd" : "pkda_precond_fwd");
 }
