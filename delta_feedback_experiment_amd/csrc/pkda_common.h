@@ -50,6 +50,12 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
 // kernels take it on decay factors e^(G_t - G_s) <= 1.
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
+// ln x as log2(x) ln 2 on the hardware log2 (v_log_f32), for x > 0 normal.
+__device__ __forceinline__ float log_fast(float x) { return __builtin_amdgcn_logf(x) * 0.693147180559945309f; }
+
+// a / b as a * (1 / b) on the hardware reciprocal (v_rcp_f32, 1 ulp).
+__device__ __forceinline__ float div_fast(float a, float b) { return a * __builtin_amdgcn_rcpf(b); }
+
 template <typename T> struct io;
 template <> struct io<float> {
   static constexpr int dtype = PKDA_F32;
