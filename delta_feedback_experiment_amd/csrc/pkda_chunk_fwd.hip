@@ -370,19 +370,25 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   __syncthreads();
 
   // ---- diagonal blocks, exactly: one (t, s) pair, s <= t, per lane -----------
-  // The 4 x 136 pairs are numbered block by block; waves 0-3 take pairs
-  // 0..511 (two per lane), and waves 6 and 7, which hold one off-diagonal
-  // block each (waves 4 and 5 hold two), take the last 32 after it.
-  auto diag_pair = [&](int pg) {
+  // The 4 x 136 pairs are numbered block by block.  Every wave takes pairs
+  // lane + 64 wave (0..511); waves 2-7 then take one off-diagonal block each
+  // and wave 0 the last 32 pairs, each split over two lanes (channels 0-63
+  // and 64-127, summed by a lane exchange), so no wave carries more than one
+  // pair pass and one block's worth of work.
+  auto pair_of = [&](int pg, int& t, int& s) {
     const int tb = pg / 136;
     int tl = 0, rest = pg - tb * 136;
     while (rest > tl) {
       rest -= tl + 1;
       ++tl;
     }
-    const int t = 16 * tb + tl, s = 16 * tb + rest;
-    float akk = 0.f, aqk = 0.f;
-    for (int c = 0; c < D; c += V) {
+    t = 16 * tb + tl;
+    s = 16 * tb + rest;
+  };
+  auto pair_sums = [&](int t, int s, int c0, int c1, float& akk, float& aqk) {
+    akk = 0.f;
+    aqk = 0.f;
+    for (int c = c0; c < c1; c += V) {
       float kx[V], qx[V], wx[V];
       lds_vec<V>(sK + t * L::LD + c, kx);
       lds_vec<V>(sQ + t * L::LD + c, qx);
@@ -394,43 +400,56 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
         aqk += qx[j] * wx[j] * e;
       }
     }
+  };
+  auto pair_store = [&](int t, int s, float akk, float aqk) {
     sA[t * L::LDF + s] = (s < t && t < len) ? sBeta[t] * akk : 0.f;
     sAqk[t * L::LDC + s] = to_e<E>(t < len ? p.scale * aqk : 0.f);
   };
-  if (wave < 4) {
-    diag_pair(lane + 64 * wave);
-    diag_pair(lane + 64 * (wave + 4));
-  } else {
+  {
+    int t, s;
+    float akk, aqk;
+    pair_of(lane + 64 * wave, t, s);
+    pair_sums(t, s, 0, D, akk, aqk);
+    pair_store(t, s, akk, aqk);
+  }
+  if (wave == 0) {
+    int t, s;
+    float akk, aqk;
+    pair_of(512 + (lane & 31), t, s);
+    const int half = lane >> 5;
+    pair_sums(t, s, half * (D / 2), (half + 1) * (D / 2), akk, aqk);
+    akk += __shfl_xor(akk, 32);
+    aqk += __shfl_xor(aqk, 32);
+    if (half == 0) pair_store(t, s, akk, aqk);
+  } else if (wave >= 2) {
     // ---- off-diagonal blocks (tb > sb) with the split decay --------------------
-    for (int blk = wave - 4; blk < 6; blk += 4) {
-      const int tb = blk < 1 ? 1 : blk < 3 ? 2 : 3;
-      const int sb = blk - (tb - 1) * tb / 2;
-      const int r = 16 * tb - 1;
-      const int t = 16 * tb + (lane & 15), s = 16 * sb + (lane & 15);
-      f32x4 akk = zero4(), aqk = zero4();
-      for (int k0 = 0; k0 < D; k0 += Mma<E>::KS) {
-        const int kk = k0 + F::off(lane);
-        float ak[F::N], aq[F::N], bw[F::N];
+    const int blk = wave - 2;
+    const int tb = blk < 1 ? 1 : blk < 3 ? 2 : 3;
+    const int sb = blk - (tb - 1) * tb / 2;
+    const int r = 16 * tb - 1;
+    const int t = 16 * tb + (lane & 15), s = 16 * sb + (lane & 15);
+    f32x4 akk = zero4(), aqk = zero4();
+    for (int k0 = 0; k0 < D; k0 += Mma<E>::KS) {
+      const int kk = k0 + F::off(lane);
+      float ak[F::N], aq[F::N], bw[F::N];
 #pragma unroll
-        for (int j = 0; j < F::N; ++j) {
-          const float gr = sG[r * L::LDG + kk + j];
-          const float fa = exp_fast(sG[t * L::LDG + kk + j] - gr);
-          const float fb = exp_fast(gr - sG[s * L::LDG + kk + j]);
-          ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
-          aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
-          bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
-        }
-        F::mfma(akk, ak, bw);
-        F::mfma(aqk, aq, bw);
+      for (int j = 0; j < F::N; ++j) {
+        const float gr = sG[r * L::LDG + kk + j];
+        const float fa = exp_fast(sG[t * L::LDG + kk + j] - gr);
+        const float fb = exp_fast(gr - sG[s * L::LDG + kk + j]);
+        ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
+        aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
+        bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int tt = 16 * tb + acc_row(lane, e), ss = 16 * sb + acc_col(lane);
-        sA[tt * L::LDF + ss] = tt < len ? sBeta[tt] * akk[e] : 0.f;
-        sAqk[tt * L::LDC + ss] = to_e<E>(tt < len ? p.scale * aqk[e] : 0.f);
-      }
+      F::mfma(akk, ak, bw);
+      F::mfma(aqk, aq, bw);
     }
-    if (wave >= 6 && lane < 16) diag_pair(512 + 16 * (wave - 6) + lane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tt = 16 * tb + acc_row(lane, e), ss = 16 * sb + acc_col(lane);
+      sA[tt * L::LDF + ss] = tt < len ? sBeta[tt] * akk[e] : 0.f;
+      sAqk[tt * L::LDC + ss] = to_e<E>(tt < len ? p.scale * aqk[e] : 0.f);
+    }
   }
   // ---- qg = s e^G q and kg = e^{G_last - G} kw, straight to global -----------
   T* qg_out = static_cast<T*>(p.qg) + row0 * D;
