@@ -11,7 +11,7 @@ the preconditioner, the output gate GEMM, RMSNorm with the sigmoid gate
 (the reference's ``sink_linear`` without sinks is one).
 
 * CPU: the oracle's restatements of each piece composed -- pins them,
-  together, to the reference module (FP32, relative L2 <= 1e-5).
+  together, to the reference module (FP32, relative L2 <= 1e-6).
 * GPU (``gpu``): this package's operators composed -- conv, controls,
   ``chunk_pkda(decay_up=...)``, norm gate -- FP32, relative L2 <= 1e-5 on the
   output, final S and A and the gradients of x and every parameter but the
