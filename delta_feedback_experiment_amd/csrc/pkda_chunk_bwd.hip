@@ -786,7 +786,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   __syncthreads();
   // the next phases' operands start their way in: G_C, dH and the write key at
-  // this lane's positions (0 on the last row and past it, whose terms cancel)
+  // this lane's positions (0 past the chunk).  The eight waves' Gl and Wl
+  // cover the [64 x D] tiles once, so phase 3 takes its LDS copies of G and
+  // the write key from them rather than from global memory again.
 #pragma unroll
   for (int j = 0; j < HCT; ++j) gCl[j] = gC[16 * (ch * HCT + j) + (lane & 15)];
   TiledTile<kFW, D, T> rdH;
@@ -798,7 +800,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = r0 + rq + e;
-      Wl[j][e] = r < len - 1 ? kwval(r, c) : 0.f;
+      Wl[j][e] = r < len ? kwval(r, c) : 0.f;
     }
   }
   rK.store(sK, L::LD);  // dO's region: phase 1 is done with it
@@ -876,26 +878,29 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       dkws[j][e] = exp_fast(gCl[j] - Gl[j][e]) * acc[e];
-      // the last row's term (decay e^0) cancels against its own -kw dkw (Wl is 0 there)
-      col += Wl[j][e] * dkws[j][e];
+      // the last row's term (decay e^0) cancels against its own -kw dkw: left out
+      col += (r0 + rq + e == len - 1 ? 0.f : Wl[j][e]) * dkws[j][e];
     }
     col += __shfl_xor(col, 16);
     col += __shfl_xor(col, 32);
     if (lane < 16) sKG[rb * D + 16 * ct + lane] = col;
   }
-  // G (rows past the chunk repeat its last) and the write key in FP32 (kw32,
-  // else kw or k widened; zero rows past the chunk) for phase 3
-  RegTile<kFW, C, D, float> rG, rW32;
-  rG.load_clamped(gg, gs, len);
-  if (kw32g) rW32.load(kw32g, gs, len);
   __syncthreads();
   // ---- phase 3: pairwise terms with the decay inside the contraction ----------
   // dAkk is held once (unscaled); beta_t multiplies the other factor, so the
   // two halves of each (t, x) pair's gate term see the same rounded value.
+  // G (rows past the chunk repeat its last) and the write key in FP32 (kw32,
+  // else kw or k widened; zero rows past the chunk) from this lane's Gl, Wl.
   rQ.store(sQ, L::LD);
-  rG.store(sG, L::LDG);
-  if (kw32g) rW32.store(sKWf, L::LDW);
-  else load_tile<kFW, C, D>(sKWf, L::LDW, p.kw_is_k ? kg_ : kwg, gs, len, Ident());  // widened to FP32
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) {
+    const int c = 16 * (ch * HCT + j) + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sG[(r0 + rq + e) * L::LDG + c] = Gl[j][e];
+      sKWf[(r0 + rq + e) * L::LDW + c] = Wl[j][e];
+    }
+  }
   if (ch == 0) {  // this row block's diagonal blocks, transposed
     for (int i = lane; i < 256; i += 64) {
       const int xo = i >> 4, to = i & 15;
