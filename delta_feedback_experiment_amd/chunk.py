@@ -363,20 +363,24 @@ class _ChunkPKDA(torch.autograd.Function):
         dht = None if dS_T is None else dS_T.float().contiguous()
         want_dh0 = ctx.needs_input_grad[10]
         # nothing consumes dq, dv after the kernel but the cast to the input
-        # dtype, which the kernel then does; dk too unless the preconditioner
-        # adds its terms into it (then FP32, as is dkw)
+        # dtype, which the kernel then does; dk and dkw too (the
+        # preconditioner's reverse scan reads them in that dtype and writes
+        # the final dk)
         direct = ctx.dtypes[0] == qf.dtype and ctx.dtypes[2] == qf.dtype
-        key_direct = direct and pstate is None and ctx.dtypes[1] == qf.dtype
+        key_direct = direct and ctx.dtypes[1] == qf.dtype
         gr = chunk_backward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, saved, dof, dht, want_dh0,
                             grad_dtype=qf.dtype if direct else torch.float32,
                             key_grad_dtype=qf.dtype if key_direct else torch.float32, kw32=kw32)
         dk = gr.dk
         dg_atk = dbeta_atk = dcenter = dA0 = None
         if pstate is not None:
+            dk_final = torch.empty_like(kf) if dk.dtype != torch.float32 else None
             pg = pre.precond_backward(plan, kf, g_atk32, beta_atk32, center32, ctx.x, ctx.eps, pstate,
                                       gr.dkw, dk, None if dA_T is None else dA_T.float().contiguous(),
-                                      want_dA0=ctx.needs_input_grad[11])
+                                      want_dA0=ctx.needs_input_grad[11], dk_final=dk_final)
             dg_atk, dbeta_atk, dcenter, dA0 = pg
+            if dk_final is not None:
+                dk = dk_final
         dg, dA_log, ddt_bias = gate_backward(plan, _flat(g_used, plan), ctx.kind, A_log32, dt32, gr.dgcum,
                                              decay_up)
         shape = tuple(do.shape)

@@ -740,7 +740,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   __syncthreads();
 
-  f32x4 dq[HCT], dk[HCT], dkw[HCT], dv[HCT], dkws[HCT];
+  f32x4 dq[HCT], dk[HCT], dv[HCT], dkws[HCT];
   float db[4] = {0.f, 0.f, 0.f, 0.f};
   const int kbeg = kfloor<E>(r0);
   // ---- phase 1: dQg = dO S0^T, dAqk = dO U^T, dBv = T^T dU ------------------------
@@ -921,13 +921,21 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   // unrounded factor on one side, the halves differ by the operand's rounding
   // and dA_log, a sum of the gate gradient over the whole head, moves by ~4e-2.
   auto rnd = [](float x) { return from_e<E>(to_e<E>(x)); };
+  OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
+  OK* dko = static_cast<OK*>(p.dk) + row0 * D;
+  OK* dkwo = p.dkw ? static_cast<OK*>(p.dkw) + row0 * D : nullptr;
+  OT* dvo = static_cast<OT*>(p.dv) + row0 * D;
+#pragma unroll
+  for (int j = 0; j < HCT; ++j) store_acc_global<OT>(dvo, gs, dv[j], r0, 16 * (ch * HCT + j), len, lane);
+  // Each pass works on slot 0 of dq, dk and dkws, which hold column tile
+  // ch HCT + j at pass j.
 #pragma unroll 1
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     const int nn = 16 * ct + (lane & 15);  // this lane's B column (== c)
     float gr[4], kv[4], qv[4], wv[4];
-    f32x4 dg;
+    f32x4 dg, dkwj;
     {
       float kgc = 0.f;
 #pragma unroll
@@ -944,10 +952,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         // diagonal and the last row's state-path write-key term (decay e^0)
         // enter two of q dq, kw dkw and sum(kg dkg) with opposite signs and
         // are left out of the gate gradient
-        dg[e] = qv[e] * dq[j][e] + kv[e] * dk[j][e] - (r == len - 1 ? 0.f : wv[e] * dkws[j][e]);
+        dg[e] = qv[e] * dq[0][e] + kv[e] * dk[0][e] - (r == len - 1 ? 0.f : wv[e] * dkws[0][e]);
         if (r == len - 1) dg[e] += exp_fast(sG[(C - 1) * L::LDG + c]) * sHD[c] + kgc;
-        dq[j][e] += pd * wv[e];
-        dkw[j][e] = dkws[j][e] + pd * qv[e];
+        dq[0][e] += pd * wv[e];
+        dkwj[e] = dkws[0][e] + pd * qv[e];
       }
     }
     // (1) rows t_e = r0 + rq + e of this block, x <= t_e inside it, exactly
@@ -1014,9 +1022,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         ak[e] += R * ak0[e];
         aq[e] += R * aq0[e];
         const float bk = sBeta[r0 + rq + e] * ak[e];
-        dk[j][e] += bk;
+        dk[0][e] += bk;
         db[e] += kv[e] * ak[e];
-        dq[j][e] += aq[e];
+        dq[0][e] += aq[e];
         dg[e] += qv[e] * aq[e] + kv[e] * bk;
       }
     }
@@ -1059,9 +1067,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const float sb = sBeta[r0 + rq + e];
         const float dlo = exp_fast(gr[e] - grlo_c);  // e^{G[t]-G[R]}
-        dk[j][e] += sb * dlo * akX[e];
+        dk[0][e] += sb * dlo * akX[e];
         db[e] += kv[e] * dlo * akX[e];
-        dq[j][e] += dlo * aqX[e];
+        dq[0][e] += dlo * aqX[e];
         // the column side's B operands of these pairs: beta k e^{G[t]-G[R]}, q e^{G[t]-G[R]}
         dg[e] += rnd(sb * kv[e] * dlo) * akX[e] + rnd(qv[e] * dlo) * aqX[e];
       }
@@ -1107,7 +1115,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         aw[e] += (e == 3 ? 1.f : exp_fast(gr[3] - gr[e])) * aw0[e];
-        dkw[j][e] += aw[e];
+        dkwj[e] += aw[e];
         dg[e] -= wv[e] * aw[e];
       }
     }
@@ -1153,26 +1161,26 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float dec = exp_fast(gRc - gr[e]);  // e^{G[R]-G[x]}
-        dkw[j][e] += dec * aw[e];
+        dkwj[e] += dec * aw[e];
         dg[e] -= rnd(wv[e] * dec) * aw[e];  // the row side's B operand kw e^{G[R]-G[x]}
       }
     }
     store_acc_global<float>(p.dgcum + row0 * D, gs, dg, r0, 16 * ct, len, lane);
-  }
-  // ---- outputs -------------------------------------------------------------
-  OT* dqo = static_cast<OT*>(p.dq) + row0 * D;
-  OK* dko = static_cast<OK*>(p.dk) + row0 * D;
-  OT* dvo = static_cast<OT*>(p.dv) + row0 * D;
-#pragma unroll
-  for (int j = 0; j < HCT; ++j) {
-    const int ct = ch * HCT + j;
-    store_acc_global<OT>(dqo, gs, dq[j], r0, 16 * ct, len, lane);
-    store_acc_global<OT>(dvo, gs, dv[j], r0, 16 * ct, len, lane);
+    // this column tile's dq, dk and dkw are final
+    store_acc_global<OT>(dqo, gs, dq[0], r0, 16 * ct, len, lane);
     if (p.kw_is_k) {
-      store_acc_global<OK>(dko, gs, dk[j] + dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OK>(dko, gs, dk[0] + dkwj, r0, 16 * ct, len, lane);
     } else {
-      store_acc_global<OK>(dko, gs, dk[j], r0, 16 * ct, len, lane);
-      store_acc_global<OK>(static_cast<OK*>(p.dkw) + row0 * D, gs, dkw[j], r0, 16 * ct, len, lane);
+      store_acc_global<OK>(dko, gs, dk[0], r0, 16 * ct, len, lane);
+      store_acc_global<OK>(dkwo, gs, dkwj, r0, 16 * ct, len, lane);
+    }
+    // the next tile's accumulators move into slot 0 (fixed registers: a
+    // runtime index into the arrays would go through indexed register moves)
+#pragma unroll
+    for (int t = 0; t + 1 < HCT; ++t) {
+      dq[t] = dq[t + 1];
+      dk[t] = dk[t + 1];
+      dkws[t] = dkws[t + 1];
     }
   }
   float* sRowB = sRed;  // [2][64]

@@ -37,6 +37,8 @@
 // inside the chunk from a_chunk with the same arithmetic, so the backward
 // sees exactly the A the forward squashed.  Channel sums (dg_atk, dbeta_atk,
 // dcenter) reduce in a fixed order: lanes of a 16-lane row, then rows.
+#include <type_traits>
+
 #include "pkda_chunk_common.h"
 
 namespace pkda {
@@ -54,8 +56,8 @@ struct PrecondParams {
   float* aT;
   void* kw;
   float* a_chunk;
-  const float* dkw;
-  float* dk;
+  const void* dkw;  // backward: FP32, or k's dtype when narrow_grads
+  void* dk;
   float* dg_atk;
   float* dbeta_atk;
   float* dcenter_part;
@@ -65,6 +67,7 @@ struct PrecondParams {
   float* lam_chunk;
   void* dk_final;  // backward: dk + the terms here in k's dtype (dk untouched), or null
   float* kw32;     // forward: kw also in FP32, or null
+  bool narrow_grads;  // backward: dkw and dk in k's dtype (dk read only, dk_final written)
 };
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
@@ -265,7 +268,7 @@ __device__ __forceinline__ float row_sum16(float v) {
 // Loads clamp as in the forward.  The per-token channel sums leave each
 // 16-lane row in lane (t mod 16) of that row (register t / 16), then cross
 // the rows through LDS.
-template <typename T, int D, bool APPLY, bool FULL>
+template <typename T, int D, bool APPLY, bool FULL, typename GT>
 __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j, int h, int start, int len,
                                                   float (*sRow)[C][PrecondChunk<D>::NT / 16 + 1], float* sCen) {
   constexpr int CH = PrecondChunk<D>::CH;
@@ -275,12 +278,13 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
   constexpr int NQ = C / 16;                     // per-token sum registers
   using IO = ChanIO<T, CH>;
   using FIO = ChanIO<float, CH>;
+  using GIO = ChanIO<GT, CH>;  // dkw and dk as they come in
   const int H = p.H, c = threadIdx.x, lane16 = c & 15;
   const bool active = c * CH < D;
   const int c0 = active ? c * CH : 0;  // first channel the lane reads (idle lanes mirror 0, contribute 0)
   const T* __restrict__ k = static_cast<const T*>(p.k);
-  const float* __restrict__ dkw_p = p.dkw;
-  float* __restrict__ dk_p = p.dk;
+  const GT* __restrict__ dkw_p = static_cast<const GT*>(p.dkw);
+  GT* __restrict__ dk_p = static_cast<GT*>(p.dk);
   T* __restrict__ dk_fin = static_cast<T*>(p.dk_final);
   const float* __restrict__ g_atk = p.g_atk;
   const float* __restrict__ beta_atk = p.beta_atk;
@@ -345,8 +349,8 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       IO::load(k + tok(g0 + u) * D + c0, rk[u]);
-      FIO::load(dkw_p + tok(g0 + u) * D + c0, rdkw[u]);
-      if (APPLY) FIO::load(dk_p + tok(g0 + u) * D + c0, rdk[u]);
+      GIO::load(dkw_p + tok(g0 + u) * D + c0, rdkw[u]);
+      if (APPLY) GIO::load(dk_p + tok(g0 + u) * D + c0, rdk[u]);
     }
     {
       float a[CH];
@@ -389,8 +393,12 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       }
       if (APPLY) {
         if (active && in) {
-          if (dk_fin) IO::store(dk_fin + th * D + c0, dkt);
-          else FIO::store(dk_p + th * D + c0, dkt);
+          if constexpr (std::is_same<GT, float>::value) {
+            if (dk_fin) IO::store(dk_fin + th * D + c0, dkt);
+            else FIO::store(dk_p + th * D + c0, dkt);
+          } else {
+            IO::store(dk_fin + th * D + c0, dkt);  // narrow gradients always leave through dk_final
+          }
         }
         vg = row_sum16(vg);
         vb = row_sum16(vb);
@@ -434,16 +442,16 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
   }
 }
 
-template <typename T, int D, bool APPLY>
+template <typename T, int D, bool APPLY, typename GT>
 __global__ __launch_bounds__(PrecondChunk<D>::NT) void precond_bwd_chunk_kernel(PrecondParams p) {
   __shared__ float sRow[2][C][PrecondChunk<D>::NT / 16 + 1];
   __shared__ float sCen[PrecondChunk<D>::NT / 16];
   const ChunkHead ch = chunk_head(p.H);
   const ChunkInfo ci = chunk_info(p.geom, ch.j);
   if (ci.len == C)
-    precond_bwd_chunk<T, D, APPLY, true>(p, ch.j, ch.h, ci.start, C, sRow, sCen);
+    precond_bwd_chunk<T, D, APPLY, true, GT>(p, ch.j, ch.h, ci.start, C, sRow, sCen);
   else if (ci.len > 0)
-    precond_bwd_chunk<T, D, APPLY, false>(p, ch.j, ch.h, ci.start, ci.len, sRow, sCen);
+    precond_bwd_chunk<T, D, APPLY, false, GT>(p, ch.j, ch.h, ci.start, ci.len, sRow, sCen);
   else if (APPLY && threadIdx.x == 0)
     p.dcenter_part[(int64_t)ch.j * p.H + ch.h] = 0.f;
 }
@@ -512,8 +520,20 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
   p.lam_chunk = a->lam_chunk;
   p.dk_final = a->dk_final;
   p.kw32 = a->kw32;
+  p.narrow_grads = a->grad_dtype != PKDA_F32;
   PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed A states need pool_size > 0");
   return 0;
+}
+
+template <typename T, int D, typename GT>
+void launch_precond_bwd_chunks(const PrecondParams& p, hipStream_t s) {
+  constexpr int NT = PrecondThreads<D>::v, NTC = PrecondChunk<D>::NT;
+  const dim3 chunks((unsigned)((int64_t)p.geom.num_chunks * p.H));
+  const dim3 docs = doc_grid(p.geom.num_seqs, p.H, 1);
+  const bool any = p.geom.num_chunks > 0;
+  if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, false, GT>), chunks, dim3(NTC), 0, s, p);
+  hipLaunchKernelGGL((precond_bwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
+  if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, true, GT>), chunks, dim3(NTC), 0, s, p);
 }
 
 template <typename T, int D>
@@ -523,9 +543,8 @@ int launch_precond(const PrecondParams& p, bool backward, hipStream_t s) {
   const dim3 docs = doc_grid(p.geom.num_seqs, p.H, 1);
   const bool any = p.geom.num_chunks > 0;
   if (backward) {
-    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, false>), chunks, dim3(NTC), 0, s, p);
-    hipLaunchKernelGGL((precond_bwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
-    if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, true>), chunks, dim3(NTC), 0, s, p);
+    if (p.narrow_grads) launch_precond_bwd_chunks<T, D, T>(p, s);
+    else launch_precond_bwd_chunks<T, D, float>(p, s);
   } else {
     if (any) hipLaunchKernelGGL((precond_fwd_chunk_kernel<T, D, false>), chunks, dim3(NTC), 0, s, p);
     hipLaunchKernelGGL((precond_fwd_scan_kernel<D>), docs, dim3(NT), 0, s, p);
@@ -567,6 +586,10 @@ extern "C" int pkda_precond_bwd(const pkda_precond_args* a, void* stream) {
   if (a->num_seqs > 0) {
     PKDA_REQUIRE(a->a_chunk && a->lam_chunk && a->dkw && a->dk && a->dg_atk && a->dbeta_atk, PKDA_EINVAL,
                  "preconditioner backward needs a_chunk, lam_chunk, dkw, dk, dg_atk and dbeta_atk");
+    PKDA_REQUIRE(a->grad_dtype == PKDA_F32 || a->grad_dtype == a->dtype, PKDA_EUNSUPPORTED,
+                 "grad_dtype %d (FP32 or the dtype of k)", a->grad_dtype);
+    PKDA_REQUIRE(a->grad_dtype == PKDA_F32 || a->dk_final, PKDA_EINVAL,
+                 "dkw and dk in the dtype of k need dk_final");
     const int st = a->dtype == PKDA_F32 ? dispatch_precond<float>(p, a->head_dim, true, s)
                                         : dispatch_precond<bf16_t>(p, a->head_dim, true, s);
     if (st) return st;

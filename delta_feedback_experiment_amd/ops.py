@@ -11,8 +11,9 @@ The saved list is this library's own (the caller treats it as opaque,
 ``pkda.py:433``): the write keys and the preconditioner's chunk checkpoints
 always; the WY factors, corrected values, intra-chunk products and chunk
 states as well unless ``lean``, in which case the backward rebuilds them with
-the same kernels the forward ran.  The gate cumsum is relaunched in the
-backward either way, as the reference does.
+the same kernels the forward ran.  The gate's chunk cumsum is one of the
+retained tensors; under ``lean`` the backward relaunches the gate, as the
+reference's backward always does (``fla_ops.py:423-432``).
 """
 
 from __future__ import annotations
@@ -34,10 +35,11 @@ SAVED_WIDE_KEY = "k_write32"
 write keys in FP32, from which the backward sums the gate gradient's
 in-block pairs."""
 
-SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h", "qg", "kg")
+SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h", "qg", "kg", "gcum")
 """Saved as well unless ``lean``: W, the corrected values U, the intra-chunk
-query-key products, the inverted WY matrix, the chunk-entry states and the
-gated query and write key."""
+query-key products, the inverted WY matrix, the chunk-entry states, the
+gated query and write key, and the gate's chunk-local cumulative log-decay
+(FP32)."""
 
 
 def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int, ...], torch.dtype], ...]:
@@ -60,6 +62,7 @@ def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int
             ((B * chunks, H, K, V), act),         # h
             ((ntok, H, K), act),                  # qg
             ((ntok, H, K), act),                  # kg
+            ((ntok, H, K), torch.float32),        # gcum
         ]
     return tuple(meta)
 
@@ -133,7 +136,7 @@ def pkda_recurrence(
             save_all=not lean)
     saved = [pstate.kw] + ([] if pstate.kw32 is None else [pstate.kw32]) + [pstate.a_chunk]
     if not lean:
-        saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h, fs.qg, fs.kg]
+        saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h, fs.qg, fs.kg, gcum]
     _check_saved(saved, q, v, lean)
     return o.reshape(*q.shape[:3], v.shape[-1]).to(q.dtype), saved
 
@@ -164,18 +167,20 @@ def pkda_recurrence_backward(
             gf = gf.float()
         A32, dt32 = _f32(A_log), _f32(dt_bias)
         beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
-        gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)  # relaunched, as the forward ran it
         named = dict(zip(saved_names(q, lean), saved))
         kw, kw32, a_chunk = named["k_write"], named.get(SAVED_WIDE_KEY), named["a_chunk"]
-        if lean:
+        if lean:  # the gate and the chunk quantities again, as the forward ran them
+            gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)
             _, _, fs = chunk_forward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, False, save_states=True)
         else:
-            fs = FwdSaved(*(named[n] for n in SAVED_RETAINED))
+            gcum = named["gcum"]
+            fs = FwdSaved(*(named[n] for n in SAVED_RETAINED[:-1]))
         dof = flat(do.to(q.dtype))
-        # dq, dv leave the kernel in the input dtype; dk, dkw stay FP32 for the
-        # preconditioner's terms
+        # every gradient leaves the kernel in the input dtype; the
+        # preconditioner's reverse scan reads dk, dkw that way and writes the
+        # final dk
         gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False,
-                            grad_dtype=qf.dtype, key_grad_dtype=torch.float32, kw32=kw32)
+                            grad_dtype=qf.dtype, key_grad_dtype=qf.dtype, kw32=kw32)
         pstate = pre.PrecondState(kw, a_chunk, None, None)
         dk = torch.empty_like(kf)  # the preconditioner's scan writes the final dk in k's dtype
         dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(

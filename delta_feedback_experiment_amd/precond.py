@@ -78,7 +78,11 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
     """Reverse scan: adds the preconditioner's terms into ``dk`` (FP32, in
     place) -- or, with ``dk_final`` (``kf``'s shape and dtype), writes the
     sum there and leaves ``dk`` alone -- and returns ``(dg_atk [N_tok,H],
-    dbeta_atk [N_tok,H], dcenter [H], dA0 [N,H,K] or None)``, all FP32."""
+    dbeta_atk [N_tok,H], dcenter [H], dA0 [N,H,K] or None)``, all FP32.
+
+    ``dkw`` and ``dk`` come in FP32, or both in ``kf``'s dtype (the chunk
+    backward's key gradients as it rounds them once); the narrow form needs
+    ``dk_final``."""
     dev = kf.device
     H, K, N = plan.heads, plan.head_dim, plan.num_seqs
     ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
@@ -90,6 +94,11 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
     dcenter = torch.empty(H, **f32)
     dA0 = torch.empty(N, H, K, **f32) if want_dA0 else None
     dAT = None if dA_T is None else _f32(dA_T)
+    narrow = dkw.dtype != torch.float32
+    if narrow and (dkw.dtype != kf.dtype or dk.dtype != kf.dtype or dk_final is None):
+        raise ValueError("dkw and dk must be FP32, or both in k's dtype with dk_final given")
+    if not narrow and dk.dtype != torch.float32:
+        raise ValueError("dk must be FP32 when dkw is")
     args = _lib.PrecondArgs(
         dtype=_dtype_code(kf), num_seqs=N, seqlen=plan.seqlen, heads=H, head_dim=K,
         cu_seqlens=_ptr(plan.cu_seqlens), k=_ptr(kf), g_atk=_ptr(ga), beta_atk=_ptr(ba), center=_ptr(cen),
@@ -97,6 +106,7 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
         dkw=_ptr(dkw), dk=_ptr(dk), dg_atk=_ptr(dg_atk), dbeta_atk=_ptr(dbeta_atk),
         dcenter_part=_ptr(dcenter_part), dcenter=_ptr(dcenter), dA0=_ptr(dA0), dA_T=_ptr(dAT),
         table=_ptr(plan.table), lam_chunk=_ptr(lam_chunk), dk_final=_ptr(dk_final),
+        grad_dtype=_dtype_code(dkw) if narrow else _lib.PKDA_F32,
     )
     if dk_final is not None and (dk_final.shape != kf.shape or dk_final.dtype != kf.dtype
                                  or not dk_final.is_contiguous()):

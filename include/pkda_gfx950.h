@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 9
+#define PKDA_ABI_VERSION 10
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -231,7 +231,8 @@ int pkda_gate_bwd_noalloc(const pkda_gate_args* args, void* stream);
  * 441-479); math of delta_feedback_experiment/pkda.py:392-398.
  *   forward:  kw [N_tok,H,K] (dtype), A at every chunk start a_chunk
  *             [num_chunks, H, K] FP32 (backward checkpoint), final A.
- *   backward: dkw (FP32 [N_tok,H,K]) -> dk (FP32, accumulated: dk += ...),
+ *   backward: dkw ([N_tok,H,K], FP32 or dtype: grad_dtype) -> dk (accumulated:
+ *             dk += ..., or written to dk_final),
  *             dg_atk, dbeta_atk [N_tok,H] FP32, dcenter [H] (through
  *             per-document partials dcenter_part [num_seqs, H], summed in a
  *             fixed order), dA0 [N,H,K] when dA0 != NULL; dA_T optional
@@ -259,8 +260,9 @@ typedef struct pkda_precond_args {
   void* kw;                      /* forward output [N_tok,H,K] dtype */
   float* a_chunk;                /* [num_chunks, H, K] */
   int32_t num_chunks;
-  const float* dkw;              /* backward input */
-  float* dk;                     /* backward: accumulated into */
+  const void* dkw;               /* backward input, grad_dtype */
+  void* dk;                      /* backward: accumulated into (FP32), or read only (grad_dtype
+                                    narrower than FP32, with dk_final) */
   float* dg_atk;
   float* dbeta_atk;
   float* dcenter_part;           /* [num_chunks, H] workspace */
@@ -277,6 +279,10 @@ typedef struct pkda_precond_args {
                                     written here in dtype, dk left as it came in */
   float* kw32;                   /* forward, optional: kw [N_tok,H,K] also in FP32 (the
                                     chunk backward's exact in-block pair sums read it) */
+  int32_t grad_dtype;            /* backward: dtype of dkw and dk, PKDA_F32 or `dtype`; the
+                                    narrow form needs dk_final (the chunk backward hands its
+                                    key gradients over in the activation dtype: half the bytes
+                                    for it to write and for both reverse-scan passes to read) */
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);

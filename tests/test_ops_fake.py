@@ -37,7 +37,9 @@ def test_fake_forward_shapes(lean):
     assert named["a_chunk"].shape == (B * 2, H, D)
     # BF16 activations also keep the write keys in FP32
     assert named["k_write"].dtype == torch.bfloat16 and named["k_write32"].dtype == torch.float32
-    assert len(saved) == (3 if lean else 10)
+    assert len(saved) == (3 if lean else 11)
+    if not lean:  # the gate's chunk cumsum is retained for the backward
+        assert named["gcum"].shape == (B * T, H, D) and named["gcum"].dtype == torch.float32
 
 
 def test_fp32_activations_save_one_write_key():
