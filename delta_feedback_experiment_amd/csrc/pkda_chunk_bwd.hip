@@ -599,6 +599,449 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// fused per-chunk backward, BF16 with a per-head gate and kw = k: the
+// four-wave form, two workgroups per compute unit.
+//
+// The same products and gate-gradient terms as chunk_fused_bwd_kernel with
+// the work laid out so that a workgroup needs ~64 KB of LDS instead of
+// ~132 KB: while one workgroup waits for its tiles, the other computes.
+//   * Wave w owns output columns [D w / 4, D (w + 1) / 4) of every row, so
+//     the contractions over the value index (dO S0^T, dBv S0^T, U dS_C^T)
+//     take S0 and dS_C rows of its own columns only: they come from the
+//     tile-major checkpoints straight into registers as MFMA B operands
+//     (never through LDS), and sum(S0 * dS_C) is formed there too.
+//   * dv = beta dBv and sum_c dBv V (the value part of dbeta) are formed on
+//     the loaded registers: V and dv never touch LDS.
+//   * Two [64 x D] LDS regions hold U and dO, then U and dBv, then K and Q;
+//     the pair matrices (s dAqk E, dAkk E, beta dAkk E) have their own.
+// Passes: (1) dQg = dO S0^T, dAqk = dO U^T -> P2;  (2) dBw = -dBv S0^T,
+// dAkk = -dBv U^T -> P1r, P1, dKg = U dS_C^T;  (3) the pair terms with K and
+// Q, row block by row block, and the outputs.
+// ---------------------------------------------------------------------------
+constexpr int kW4 = 256;
+
+template <int D>
+struct FusedW4Layout {
+  static constexpr int LD = D + Pad<bf16_t>::v;
+  static constexpr int LDC = C + Pad<bf16_t>::v;
+  static constexpr int RT = C * LD * 2;
+  static constexpr int CT = C * LDC * 2;
+  static constexpr int off_R0 = 0;               // U, then K
+  static constexpr int off_R1 = off_R0 + RT;     // dO, then dBv, then Q
+  static constexpr int off_P2 = off_R1 + RT;     // s dAqk E (strictly lower)
+  static constexpr int off_P1r = off_P2 + CT;    // dAkk E (strictly lower)
+  static constexpr int off_P1 = off_P1r + CT;    // beta_t dAkk E
+  static constexpr int off_gam = off_P1 + CT;    // [64] G
+  static constexpr int off_beta = off_gam + C * 4;
+  static constexpr int off_p2d = off_beta + C * 4;   // [64] s dAqk[t,t], FP32
+  static constexpr int off_db1 = off_p2d + C * 4;    // [64] sum_c dBv V
+  static constexpr int off_rowg = off_db1 + C * 4;   // [4][64] per-wave row sums of the gate gradient
+  static constexpr int off_rowb = off_rowg + 4 * C * 4;  // [4][64] per-wave row sums of dbeta
+  static constexpr int off_wave = off_rowb + 4 * C * 4;  // [2][4] sum(S0 dS_C), sum(kw dKg) per wave
+  // dq's last PARK tiles (row blocks 2-3) between passes 1 and 3 (FP32, one
+  // 16-byte slot per lane and tile): at D = 128 the accumulators of passes 2
+  // and 3 fit the 256 registers of two workgroups per compute unit only
+  // without them
+  static constexpr int PARK = D == 128 ? 3 : 0;  // tiles per wave
+  static constexpr int off_park = off_wave + 8 * 4;
+  static constexpr int bytes = off_park + 4 * PARK * 64 * 16;
+  static_assert(2 * bytes <= 160 * 1024, "two workgroups per compute unit");
+};
+
+// The lower 16 x 16 tiles (tb >= sb) of a [64 x 64] chunk matrix, numbered
+// 0..9, dealt to the four waves as w, w + 4, w + 8.
+__device__ __forceinline__ void lower_tile(int i, int& tb, int& sb) {
+  tb = i < 1 ? 0 : i < 3 ? 1 : i < 6 ? 2 : 3;
+  sb = i - tb * (tb + 1) / 2;
+}
+
+template <int D>
+__global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p) {
+  using L = FusedW4Layout<D>;
+  using E = bf16_t;
+  using M = Mma<bf16_t>;
+  constexpr int NJ = D / 64;  // column tiles per wave
+  constexpr int KV = D / 32;  // k steps over the value index
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len <= 0) return;
+  const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, il = lane & 15;
+  const int len = ci.len;
+  const int64_t gs = (int64_t)H * D;
+  const int64_t row0 = (int64_t)ci.start * H + hh;
+  const float scale = p.scale;
+
+  E* sR0 = reinterpret_cast<E*>(smem + L::off_R0);
+  E* sR1 = reinterpret_cast<E*>(smem + L::off_R1);
+  E* sP2 = reinterpret_cast<E*>(smem + L::off_P2);
+  E* sP1r = reinterpret_cast<E*>(smem + L::off_P1r);
+  E* sP1 = reinterpret_cast<E*>(smem + L::off_P1);
+  float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
+  float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+  float* sP2d = reinterpret_cast<float*>(smem + L::off_p2d);
+  float* sDb1 = reinterpret_cast<float*>(smem + L::off_db1);
+  float* sRowG = reinterpret_cast<float*>(smem + L::off_rowg);
+  float* sRowB = reinterpret_cast<float*>(smem + L::off_rowb);
+  float* sWave = reinterpret_cast<float*>(smem + L::off_wave);
+  f32x4* sPark = reinterpret_cast<f32x4*>(smem + L::off_park) + wave * L::PARK * 64 + lane;
+
+  if (tid < C) {
+    const int64_t idx = (int64_t)(ci.start + min(tid, len - 1)) * H + hh;
+    sGam[tid] = p.gcum[idx];  // rows past the end repeat the last gate
+    sBeta[tid] = tid < len ? p.beta[idx] : 0.f;
+  }
+  // the first passes' loads go out before the first LDS store, in the order
+  // the passes need them
+  RegTile<kW4, C, D, E> rU, rdO, rdBv, rV, rK, rQ;
+  s16x8_t S0f[NJ][KV], dSf[NJ][KV];  // B operands: rows of this wave's columns, k over the value index
+  const E* hsrc = static_cast<const E*>(p.h) + ((int64_t)cid * H + hh) * D * D;
+  const E* dhsrc = static_cast<const E*>(p.dh) + ((int64_t)cid * H + hh) * D * D;
+  rU.load(static_cast<const E*>(p.u) + row0 * D, gs, len);
+  rdO.load(static_cast<const E*>(p.dO) + row0 * D, gs, len);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int kk = 0; kk < KV; ++kk) {
+      // tile-major [D x D]: B[k = v][n = c] = S0[c][v], c = 16 ct + il, v = 32 kk + 8 q .. + 7
+      const int ct = NJ * wave + j;
+      const int64_t off = tile_offset(D, ct, 2 * kk + (q >> 1)) + il * 16 + 8 * (q & 1);
+      S0f[j][kk] = *reinterpret_cast<const s16x8_t*>(hsrc + off);
+    }
+  rdBv.load(static_cast<const E*>(p.du) + row0 * D, gs, len);
+  rV.load(static_cast<const E*>(p.v) + row0 * D, gs, len);
+  rU.store(sR0, L::LD);
+  rdO.store(sR1, L::LD);
+  __syncthreads();
+
+  // dv = beta dBv (final) and sum_c dBv V on the registers: the 16 pieces of
+  // a row sit in 16 consecutive lanes
+  {
+    constexpr int V = Vec16<E>::N;
+    constexpr int PER_ROW = D / V;
+    static_assert(PER_ROW == 16 || PER_ROW == 8, "row pieces fill 16 or 8 lanes");
+    E* dvo = static_cast<E*>(p.dv) + row0 * D;
+#pragma unroll
+    for (int i = 0; i < RegTile<kW4, C, D, E>::ITER; ++i) {
+      const int idx = tid + i * kW4;
+      const int r = idx / PER_ROW, c = (idx % PER_ROW) * V;
+      float b[V], v[V];
+      Vec16<E>::unpack(rdBv.r[i], b);
+      Vec16<E>::unpack(rV.r[i], v);
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) part += b[e] * v[e];
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      part += __shfl_xor(part, 4);
+      if constexpr (PER_ROW == 16) part += __shfl_xor(part, 8);
+      if (idx % PER_ROW == 0) sDb1[r] = part;
+      const float br = sBeta[r];
+#pragma unroll
+      for (int e = 0; e < V; ++e) b[e] *= br;
+      if (r < len) store_vec<V>(dvo + r * gs + c, b);
+    }
+  }
+
+  // ---- pass 1: dQg = dO S0^T (-> s e^G dQg), dAqk = dO U^T -> P2, P2d ---------
+  f32x4 dq[4][NJ];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dq[rb][j] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < KV; ++kk) {
+      const s16x8_t a = M::frag_a<ROW>(sR1 + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) M::mfma(dq[rb][j], a, S0f[j][kk]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float f = scale * exp_fast(sGam[16 * rb + 4 * q + e]);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dq[rb][j][e] *= f;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {  // parked until pass 3 (this lane's own slots)
+      const int slot = rb * NJ + j - (4 * NJ - L::PARK);
+      if (slot >= 0) sPark[slot * 64] = dq[rb][j];
+    }
+  }
+  // pair tiles of this wave: lower tiles w, w + 4, w + 8; waves 2 and 3 also
+  // write the six upper tiles' zeros (of P2 here, of P1r and P1 in pass 2)
+  auto upper_zero = [&](E* P) {
+    if (wave >= 2) {
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        const int k = 3 * (wave - 2) + u;  // 0..5: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+        const int tb = k < 3 ? 0 : k < 5 ? 1 : 2;
+        const int sb = k < 3 ? k + 1 : k < 5 ? k - 1 : 3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) P[(16 * tb + 4 * q + e) * L::LDC + 16 * sb + il] = to_e<E>(0.f);
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int i = wave + 4 * u;
+    if (i < 10) {
+      int tb, sb;
+      lower_tile(i, tb, sb);
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kk = 0; kk < KV; ++kk)
+        M::mfma(acc, M::frag_a<ROW>(sR1 + 16 * tb * L::LD, L::LD, 32 * kk, lane),
+                M::frag_b<COL>(sR0 + 16 * sb * L::LD, L::LD, 32 * kk, lane));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 16 * tb + 4 * q + e, s = 16 * sb + il;
+        // the diagonal (decay e^0) is kept apart, in FP32: its two halves of
+        // the gate gradient (q dq and kw dkw) cancel exactly and stay out of it
+        const float val = (s < t && t < len) ? scale * exp_fast(sGam[t] - sGam[s]) * acc[e] : 0.f;
+        sP2[t * L::LDC + s] = to_e<E>(val);
+        if (s == t) sP2d[t] = t < len ? scale * acc[e] : 0.f;
+      }
+    }
+  }
+  upper_zero(sP2);
+  __syncthreads();  // every wave is done with dO
+  rdBv.store(sR1, L::LD);
+  __syncthreads();
+
+  // ---- pass 2: dBw = -dBv S0^T (-> -e^G dBv S0^T), dAkk = -dBv U^T -> P1r, P1,
+  //      dKg = U dS_C^T (-> e^{G_C - G} dKg), sum(S0 dS_C) ----------------------
+  f32x4 tk[4][NJ], dkws[4][NJ];
+  const float gC = sGam[C - 1];
+  // dS_C's rows of this wave's columns (loaded here: S0's and dS_C's operands
+  // are not in registers together through pass 1)
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int kk = 0; kk < KV; ++kk) {
+      const int ct = NJ * wave + j;
+      const int64_t off = tile_offset(D, ct, 2 * kk + (q >> 1)) + il * 16 + 8 * (q & 1);
+      dSf[j][kk] = *reinterpret_cast<const s16x8_t*>(dhsrc + off);
+    }
+  // tk from S0 first; sum(S0 dS_C) is S0's last use, before dS_C's products
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) tk[rb][j] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < KV; ++kk) {
+      const s16x8_t a = M::frag_a<ROW>(sR1 + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) M::mfma(tk[rb][j], a, S0f[j][kk]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float fb = -exp_fast(sGam[16 * rb + 4 * q + e]);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) tk[rb][j][e] *= fb;  // e^G dBw
+    }
+  }
+  float hd = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int kk = 0; kk < KV; ++kk) {
+      const uint4 a = __builtin_bit_cast(uint4, S0f[j][kk]), b = __builtin_bit_cast(uint4, dSf[j][kk]);
+      float x[8], y[8];
+      Vec16<E>::unpack(a, x);
+      Vec16<E>::unpack(b, y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hd += x[e] * y[e];
+    }
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dkws[rb][j] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < KV; ++kk) {
+      const s16x8_t u = M::frag_a<ROW>(sR0 + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) M::mfma(dkws[rb][j], u, dSf[j][kk]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float fs = exp_fast(gC - sGam[16 * rb + 4 * q + e]);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dkws[rb][j][e] *= fs;
+    }
+  }
+  // K and Q go out now (in registers until U's and dBv's regions free); the
+  // fence keeps the scheduler from hoisting them into the loops above, where
+  // their registers would push the pass past 256
+  __builtin_amdgcn_sched_barrier(0);
+  rK.load(static_cast<const E*>(p.k) + row0 * D, gs, len);
+  rQ.load(static_cast<const E*>(p.q) + row0 * D, gs, len);
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int i = wave + 4 * u;
+    if (i < 10) {
+      int tb, sb;
+      lower_tile(i, tb, sb);
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kk = 0; kk < KV; ++kk)
+        M::mfma(acc, M::frag_a<ROW>(sR1 + 16 * tb * L::LD, L::LD, 32 * kk, lane),
+                M::frag_b<COL>(sR0 + 16 * sb * L::LD, L::LD, 32 * kk, lane));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 16 * tb + 4 * q + e, s = 16 * sb + il;
+        const float raw = (s < t && t < len) ? -acc[e] * exp_fast(sGam[t] - sGam[s]) : 0.f;
+        sP1r[t * L::LDC + s] = to_e<E>(raw);
+        sP1[t * L::LDC + s] = to_e<E>(sBeta[t] * raw);
+      }
+    }
+  }
+  upper_zero(sP1r);
+  upper_zero(sP1);
+  hd = wave_sum(hd);
+  __syncthreads();  // every wave is done with U and dBv; the pair matrices are complete
+  rK.store(sR0, L::LD);
+  rQ.store(sR1, L::LD);
+  __syncthreads();
+
+  // ---- pass 3: pair terms, row block by row block; outputs ----------------------
+  //   (a) dq += P2 K -> dq out, its gate-gradient term q dq;
+  //   (b) tk += P1r K (tk = e^G dBw + sum_x P1r kw; dk = beta tk) and
+  //       dkw = dkws + P1^T K + P2^T Q -> dk + dkw out, the other terms
+  E* dqo = static_cast<E*>(p.dq) + row0 * D;
+  E* dko = static_cast<E*>(p.dk) + row0 * D;
+  s16x8_t Kf[2][NJ];  // B operands K[x][c] over the chunk's tokens
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) Kf[kt][j] = M::frag_b<ROW>(sR0 + 16 * (NJ * wave + j), L::LD, 32 * kt, lane);
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int r0 = 16 * rb;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int slot = rb * NJ + j - (4 * NJ - L::PARK);
+      if (slot >= 0) dq[rb][j] = sPark[slot * 64];
+    }
+    // P2 is zero above the diagonal: rows of block rb reach k < 16 rb + 16
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      if (32 * kt < r0 + 16) {
+        const s16x8_t a2 = M::frag_a<ROW>(sP2 + r0 * L::LDC, L::LDC, 32 * kt, lane);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) M::mfma(dq[rb][j], a2, Kf[kt][j]);
+      }
+    }
+    float gq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = 16 * (NJ * wave + j) + il;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r0 + 4 * q + e;
+        gq[e] += from_e<E>(sR1[r * L::LD + c]) * dq[rb][j][e];
+        dq[rb][j][e] += sP2d[r] * from_e<E>(sR0[r * L::LD + c]);  // the diagonal, after the gate term
+      }
+      store_acc_global<E>(dqo, gs, dq[rb][j], r0, 16 * (NJ * wave + j), len, lane);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g = group16_sum(gq[e]);
+      if (il == 0) sRowG[wave * C + r0 + 4 * q + e] = g;
+    }
+  }
+  s16x8_t Qf[2][NJ];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) Qf[kt][j] = M::frag_b<ROW>(sR1 + 16 * (NJ * wave + j), L::LD, 32 * kt, lane);
+  float kgd = 0.f;
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int r0 = 16 * rb;
+    f32x4 aw[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) aw[j] = zero4();
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      if (32 * kt < r0 + 16) {
+        const s16x8_t a1 = M::frag_a<ROW>(sP1r + r0 * L::LDC, L::LDC, 32 * kt, lane);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) M::mfma(tk[rb][j], a1, Kf[kt][j]);
+      }
+      // columns x of block rb take rows t > x: k >= 16 rb
+      if (32 * kt + 32 > r0) {
+        const s16x8_t b1 = M::frag_a<COL>(sP1 + r0, L::LDC, 32 * kt, lane);
+        const s16x8_t b2 = M::frag_a<COL>(sP2 + r0, L::LDC, 32 * kt, lane);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          M::mfma(aw[j], b1, Kf[kt][j]);
+          M::mfma(aw[j], b2, Qf[kt][j]);
+        }
+      }
+    }
+    float gsum[4] = {0.f, 0.f, 0.f, 0.f}, db[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = 16 * (NJ * wave + j) + il;
+      f32x4 dk, dkw;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r0 + 4 * q + e;
+        const float kv = from_e<E>(sR0[r * L::LD + c]);
+        const float qv = from_e<E>(sR1[r * L::LD + c]);
+        const float t_ = tk[rb][j][e];
+        dk[e] = sBeta[r] * t_;
+        db[e] += kv * t_;
+        // Every term of the gate gradient carries a decay factor: the Aqk
+        // diagonal and the last row's state-path term (e^{G_C - G_C} = 1)
+        // appear once with each sign and are left out of both.
+        const float dkwg = (r == len - 1 ? 0.f : dkws[rb][j][e]) + aw[j][e];
+        if (r != len - 1) kgd += kv * dkws[rb][j][e];
+        gsum[e] += kv * dk[e] - kv * dkwg;
+        dkw[e] = dkws[rb][j][e] + aw[j][e] + sP2d[r] * qv;
+      }
+      store_acc_global<E>(dko, gs, dk + dkw, r0, 16 * (NJ * wave + j), len, lane);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g = group16_sum(gsum[e]);
+      const float b = group16_sum(db[e]);
+      if (il == 0) {
+        sRowG[wave * C + r0 + 4 * q + e] += g;  // this lane wrote the q dq part in (a)
+        sRowB[wave * C + r0 + 4 * q + e] = b;
+      }
+    }
+  }
+  kgd = wave_sum(kgd);
+  if (lane == 0) {
+    sWave[wave] = hd;
+    sWave[4 + wave] = kgd;
+  }
+  __syncthreads();
+  if (tid < len) {
+    const int64_t idx = (int64_t)(ci.start + tid) * H + hh;
+    float g = 0.f, b = sDb1[tid];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      g += sRowG[w * C + tid];
+      b += sRowB[w * C + tid];
+    }
+    if (tid == len - 1) {
+      float hd_sum = 0.f, kg_sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        hd_sum += sWave[w];
+        kg_sum += sWave[4 + w];
+      }
+      g += exp_fast(gC) * hd_sum + kg_sum;
+    }
+    p.dgcum[idx] = g;
+    p.dbeta[idx] = b;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fused per-chunk backward, per-channel gate (G [64][D] per chunk).
 //
 // The WY backward of the per-head kernel (dBv = T^T dU, dBw = -dBv S0^T,
@@ -1498,6 +1941,15 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   }
   if (num_chunks == 0) return 0;
   if (all || (stages & PKDA_STAGE_BWD_CHUNK)) {
+    if constexpr (implicit_w<T>() && std::is_same<OT, bf16_t>::value && std::is_same<OK, bf16_t>::value) {
+      if (!p.qg && p.kw_is_k) {  // BF16, per-head gate, kw = k: the four-wave form
+        auto kern = chunk_fused_bwd_w4_kernel<D>;
+        constexpr int bytes = FusedW4Layout<D>::bytes;
+        if (int st = set_smem(kern, bytes)) return st;
+        hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kW4), bytes, s, p);
+        return launch_status("pkda_chunk_bwd(chunk)");
+      }
+    }
     auto kern = p.qg ? chunk_fused_bwd_pc_kernel<T, D, OT, OK>
                      : (p.kw_is_k ? chunk_fused_bwd_kernel<T, D, OT, OK, true>
                                   : chunk_fused_bwd_kernel<T, D, OT, OK, false>);
