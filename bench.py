@@ -110,7 +110,7 @@ STAGE_KERNEL = {
     "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true, false>",
     "fwd_state": "chunk_state_fwd_rr_kernel<128, 64, true>",
     "bwd_state": "chunk_state_bwd_rr_kernel<128, 64, true>",
-    "bwd_chunk": "chunk_fused_bwd_kernel<bf16, 128, bf16, bf16, true>",
+    "bwd_chunk": "chunk_fused_bwd_w4_kernel<128>",
     "decode": "decode_kernel<bf16, 128, 512>",
 }
 TRAFFIC_PROFILE = ROOT / "profiles" / "pkda_chunk_c2_decode_c4_hbm_traffic.md"
