@@ -169,11 +169,21 @@ struct IntraLayout {
   static constexpr int off_beta = off_A + AR;
   static constexpr int off_gam = off_beta + C * 4;
   static constexpr int bytes = off_gam + C * 4;
+  // Without W and u (the state passes form them from T) and where it fits:
+  // Akk waits in the accumulators until every wave is done with K, then takes
+  // K's region, so the workgroup needs no region of its own for it (four per
+  // compute unit at D = 128 BF16 instead of three).
+  static constexpr bool lean_fits = C * LDF * 4 <= RT && SCR <= RT;
+  static constexpr int off_A_lean = off_K;
+  static constexpr int off_beta_lean = off_KW + (ALIAS ? 0 : RT);
+  static constexpr int off_gam_lean = off_beta_lean + C * 4;
+  static constexpr int bytes_lean = off_gam_lean + C * 4;
 };
 
 template <typename T, int D, bool ALIAS, bool WU>
 __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   using L = IntraLayout<T, D, ALIAS>;
+  constexpr bool LEAN = !WU && L::lean_fits;  // Akk over K's region
   using E = T;
   constexpr int HCT = D / 32;  // column tiles per wave of W / u
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -191,10 +201,10 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   E* sTw = sQ;                 // T diag(beta e^G)
   E* sTu = sQ + C * L::LDC;    // T diag(beta)
   E* sKW = ALIAS ? sK : reinterpret_cast<E*>(smem + L::off_KW);
-  float* sA = reinterpret_cast<float*>(smem + L::off_A);
+  float* sA = reinterpret_cast<float*>(smem + (LEAN ? L::off_A_lean : L::off_A));
   E* sV = reinterpret_cast<E*>(smem + L::off_A);
-  float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
-  float* sGam = reinterpret_cast<float*>(smem + L::off_gam);
+  float* sBeta = reinterpret_cast<float*>(smem + (LEAN ? L::off_beta_lean : L::off_beta));
+  float* sGam = reinterpret_cast<float*>(smem + (LEAN ? L::off_gam_lean : L::off_gam));
 
   const T* q = static_cast<const T*>(p.q) + row0 * D;
   const T* k = static_cast<const T*>(p.k) + row0 * D;
@@ -221,8 +231,13 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   __syncthreads();
 
   // ---- Akk, Aqk: lower blocks 0..9 on MFMA, upper blocks 10..15 zero ----------
+  // (block blk = wave + 8 u of this wave; without W and u the Akk values wait
+  // in registers until every wave is done with K, whose region they take)
   T* aqk_out = static_cast<T*>(p.aqk) + row0 * C;
-  for (int blk = wave; blk < 16; blk += 8) {
+  f32x4 akk_keep[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int blk = wave + 8 * u;
     if (blk < 10) {
       const int tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
       const int sb = blk - tb * (tb + 1) / 2;
@@ -234,17 +249,49 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
         const int t = 16 * tb + acc_row(lane, j);
         const int s = 16 * sb + acc_col(lane);
         const float dec = (s <= t && t < len) ? exp_fast(sGam[t] - sGam[s]) : 0.f;
-        sA[t * L::LDF + s] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
+        akk[j] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
         aqk[j] = p.scale * dec * aqk[j];
       }
       store_acc_global<T>(aqk_out, (int64_t)H * C, aqk, 16 * tb, 16 * sb, len, lane);
+      akk_keep[u] = akk;
     } else {  // (tb, sb) above the diagonal
-      const int u = blk - 10;  // 0..5: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
-      const int tb = u < 3 ? 0 : u < 5 ? 1 : 2;
-      const int sb = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
+      const int v = blk - 10;  // 0..5: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+      const int tb = v < 3 ? 0 : v < 5 ? 1 : 2;
+      const int sb = v < 3 ? v + 1 : v < 5 ? v - 1 : 3;
       store_acc_global<T>(aqk_out, (int64_t)H * C, zero4(), 16 * tb, 16 * sb, len, lane);
+      akk_keep[u] = zero4();
+    }
+    if (!LEAN) {  // Akk has a region of its own
+      const int b = blk;
+      int tb, sb;
+      if (b < 10) {
+        tb = b < 1 ? 0 : b < 3 ? 1 : b < 6 ? 2 : 3;
+        sb = b - tb * (tb + 1) / 2;
+      } else {
+        const int v = b - 10;
+        tb = v < 3 ? 0 : v < 5 ? 1 : 2;
+        sb = v < 3 ? v + 1 : v < 5 ? v - 1 : 3;
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sA[(16 * tb + acc_row(lane, j)) * L::LDF + 16 * sb + acc_col(lane)] = 0.f;
+      for (int j = 0; j < 4; ++j) sA[(16 * tb + acc_row(lane, j)) * L::LDF + 16 * sb + acc_col(lane)] = akk_keep[u][j];
+    }
+  }
+  if (LEAN) {
+    __syncthreads();  // every wave is done with K
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int b = wave + 8 * u;
+      int tb, sb;
+      if (b < 10) {
+        tb = b < 1 ? 0 : b < 3 ? 1 : b < 6 ? 2 : 3;
+        sb = b - tb * (tb + 1) / 2;
+      } else {
+        const int v = b - 10;
+        tb = v < 3 ? 0 : v < 5 ? 1 : 2;
+        sb = v < 3 ? v + 1 : v < 5 ? v - 1 : 3;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sA[(16 * tb + acc_row(lane, j)) * L::LDF + 16 * sb + acc_col(lane)] = akk_keep[u][j];
     }
   }
   __syncthreads();
@@ -1002,7 +1049,9 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
     auto kern = p.qg ? (alias ? chunk_intra_fwd_pc_kernel<T, D, true> : chunk_intra_fwd_pc_kernel<T, D, false>)
                      : (alias ? chunk_intra_fwd_kernel<T, D, true, WU> : chunk_intra_fwd_kernel<T, D, false, WU>);
     const int bytes = p.qg ? (alias ? IntraPcLayout<T, D, true>::bytes : IntraPcLayout<T, D, false>::bytes)
-                           : (alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes);
+                           : (WU || !IntraLayout<T, D, true>::lean_fits)
+                                 ? (alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes)
+                                 : (alias ? IntraLayout<T, D, true>::bytes_lean : IntraLayout<T, D, false>::bytes_lean);
     if (int st = set_smem(kern, bytes)) return st;
     if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kIW), bytes, s, p);
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
