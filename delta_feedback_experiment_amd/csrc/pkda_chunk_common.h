@@ -567,27 +567,44 @@ __device__ __forceinline__ uint32_t quad_swap(uint32_t x, int ctrl_is_pair) {
 
 // 4 x 4 transpose of 16-bit elements in a quad: in, lane t holds column t as
 // (v0 = rows 0,1; v1 = rows 2,3); out, row t as (v0 = cols 0,1; v1 = cols 2,3).
+// Branch-free: the lane-dependent halves are picked by a byte permute
+// (v_perm_b32 with a per-lane selector) and bit masks, so no divergent
+// if/else splits the caller's code around every store.
 __device__ __forceinline__ void quad_transpose_b16(uint32_t& v0, uint32_t& v1, int lane) {
-  const bool odd = lane & 1, hi = lane & 2;
+  // v_perm_b32(a, b, sel): byte i of the result is byte sel_i of {b (0..3), a (4..7)}
+  //   even lane: own low half, then the partner's low half   -> bytes 0 1 4 5
+  //   odd lane:  the partner's high half, then own high half -> bytes 6 7 2 3
+  const uint32_t sel = (lane & 1) ? 0x03020706u : 0x05040100u;
+  const uint32_t hm = (lane & 2) ? 0xffffffffu : 0u;
   const uint32_t p0 = quad_swap(v0, 1), p1 = quad_swap(v1, 1);
-  v0 = odd ? ((p0 >> 16) | (v0 & 0xffff0000u)) : ((v0 & 0xffffu) | (p0 << 16));
-  v1 = odd ? ((p1 >> 16) | (v1 & 0xffff0000u)) : ((v1 & 0xffffu) | (p1 << 16));
-  const uint32_t s = quad_swap(hi ? v0 : v1, 0);
-  if (hi) v0 = s; else v1 = s;
+  v0 = __builtin_amdgcn_perm(p0, v0, sel);
+  v1 = __builtin_amdgcn_perm(p1, v1, sel);
+  const uint32_t s = quad_swap((v0 & hm) | (v1 & ~hm), 0);
+  v0 = (s & hm) | (v0 & ~hm);
+  v1 = (v1 & hm) | (s & ~hm);
 }
 
 // 4 x 4 transpose of 32-bit elements in a quad (a[j] = row j of column t in,
 // column j of row t out).
 __device__ __forceinline__ void quad_transpose_b32(float* a, int lane) {
-  const bool odd = lane & 1, hi = lane & 2;
-  const uint32_t r0 = quad_swap(__float_as_uint(odd ? a[0] : a[1]), 1);
-  const uint32_t r1 = quad_swap(__float_as_uint(odd ? a[2] : a[3]), 1);
-  if (odd) { a[0] = __uint_as_float(r0); a[2] = __uint_as_float(r1); }
-  else { a[1] = __uint_as_float(r0); a[3] = __uint_as_float(r1); }
-  const uint32_t s0 = quad_swap(__float_as_uint(hi ? a[0] : a[2]), 0);
-  const uint32_t s1 = quad_swap(__float_as_uint(hi ? a[1] : a[3]), 0);
-  if (hi) { a[0] = __uint_as_float(s0); a[1] = __uint_as_float(s1); }
-  else { a[2] = __uint_as_float(s0); a[3] = __uint_as_float(s1); }
+  // every lane-dependent choice is a bit-mask select (no divergent branches)
+  const uint32_t om = (lane & 1) ? 0xffffffffu : 0u, hm = (lane & 2) ? 0xffffffffu : 0u;
+  auto sel = [](uint32_t m, uint32_t x, uint32_t y) { return (x & m) | (y & ~m); };  // m ? x : y
+  uint32_t u[4] = {__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]), __float_as_uint(a[3])};
+  const uint32_t r0 = quad_swap(sel(om, u[0], u[1]), 1);
+  const uint32_t r1 = quad_swap(sel(om, u[2], u[3]), 1);
+  u[0] = sel(om, r0, u[0]);
+  u[1] = sel(om, u[1], r0);
+  u[2] = sel(om, r1, u[2]);
+  u[3] = sel(om, u[3], r1);
+  const uint32_t s0 = quad_swap(sel(hm, u[0], u[2]), 0);
+  const uint32_t s1 = quad_swap(sel(hm, u[1], u[3]), 0);
+  u[0] = sel(hm, s0, u[0]);
+  u[1] = sel(hm, s1, u[1]);
+  u[2] = sel(hm, u[2], s0);
+  u[3] = sel(hm, u[3], s1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = __uint_as_float(u[j]);
 }
 
 // Row and first column of the lane's piece after the transpose.
@@ -595,12 +612,15 @@ __device__ __forceinline__ int quad_row(int lane) { return 4 * (lane >> 4) + (la
 __device__ __forceinline__ int quad_col(int lane) { return 4 * ((lane >> 2) & 3); }
 
 // Store packed bf16 pairs of an accumulator-layout tile (v0 = rows 4q, 4q+1;
-// v1 = rows 4q+2, 4q+3 of column lane & 15) by rows.
+// v1 = rows 4q+2, 4q+3 of column lane & 15) by rows.  FULL: every row is
+// valid (a whole chunk), so no row test splits the caller's code into
+// branches.
+template <bool FULL = false>
 __device__ __forceinline__ void store_packed_rows(bf16_t* g, int64_t gstride, uint32_t v0, uint32_t v1, int m0, int n0,
                                                   int nvalid, int lane) {
   quad_transpose_b16(v0, v1, lane);
   const int r = m0 + quad_row(lane);
-  if (r < nvalid) {
+  if (FULL || r < nvalid) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     *reinterpret_cast<u32x2*>(g + r * gstride + n0 + quad_col(lane)) = u32x2{v0, v1};
   }
@@ -625,26 +645,37 @@ __device__ __forceinline__ void store_acc_tile(float* tile, const f32x4& acc, in
 }
 __device__ __forceinline__ int64_t tile_offset(int D, int rt, int ct) { return ((int64_t)rt * (D / 16) + ct) * 256; }
 
-template <typename T>
+template <typename T, bool FULL = false>
+struct AccStore;
+template <bool FULL>
+struct AccStore<bf16_t, FULL> {
+  __device__ __forceinline__ static void run(bf16_t* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
+                                             int lane) {
+    bf16x2_t a, b;
+    a[0] = static_cast<__bf16>(acc[0]);
+    a[1] = static_cast<__bf16>(acc[1]);
+    b[0] = static_cast<__bf16>(acc[2]);
+    b[1] = static_cast<__bf16>(acc[3]);
+    store_packed_rows<FULL>(g, gstride, __builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), m0, n0,
+                            nvalid, lane);
+  }
+};
+template <bool FULL>
+struct AccStore<float, FULL> {
+  __device__ __forceinline__ static void run(float* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
+                                             int lane) {
+    float a[4] = {acc[0], acc[1], acc[2], acc[3]};
+    quad_transpose_b32(a, lane);
+    const int r = m0 + quad_row(lane);
+    if (FULL || r < nvalid)
+      *reinterpret_cast<float4*>(g + r * gstride + n0 + quad_col(lane)) = make_float4(a[0], a[1], a[2], a[3]);
+  }
+};
+// Store an accumulator tile by rows, rows >= nvalid masked (FULL: none are).
+template <typename T, bool FULL = false>
 __device__ __forceinline__ void store_acc_global(T* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
-                                                 int lane);
-template <>
-__device__ __forceinline__ void store_acc_global<bf16_t>(bf16_t* g, int64_t gstride, const f32x4& acc, int m0, int n0,
-                                                         int nvalid, int lane) {
-  bf16x2_t a, b;
-  a[0] = static_cast<__bf16>(acc[0]);
-  a[1] = static_cast<__bf16>(acc[1]);
-  b[0] = static_cast<__bf16>(acc[2]);
-  b[1] = static_cast<__bf16>(acc[3]);
-  store_packed_rows(g, gstride, __builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), m0, n0, nvalid, lane);
-}
-template <>
-__device__ __forceinline__ void store_acc_global<float>(float* g, int64_t gstride, const f32x4& acc, int m0, int n0,
-                                                        int nvalid, int lane) {
-  float a[4] = {acc[0], acc[1], acc[2], acc[3]};
-  quad_transpose_b32(a, lane);
-  const int r = m0 + quad_row(lane);
-  if (r < nvalid) *reinterpret_cast<float4*>(g + r * gstride + n0 + quad_col(lane)) = make_float4(a[0], a[1], a[2], a[3]);
+                                                 int lane) {
+  AccStore<T, FULL>::run(g, gstride, acc, m0, n0, nvalid, lane);
 }
 
 template <typename E>

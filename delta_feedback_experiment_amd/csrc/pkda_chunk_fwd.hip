@@ -871,135 +871,147 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
       S[rt][j] = p.s0 ? p.s0[((state_row(p, n) * H + h) * D + 16 * rt + q4 + j) * D + col] : 0.f;
   const float scale = p.scale;
 
-  for (int jc = 0; jc < count; ++jc) {
-    __syncthreads();
-    const char* buf = smem + (jc & 1) * L::BUF;
-    const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
-    const T* sKW = reinterpret_cast<const T*>(buf + L::off_KW);
-    const T* sK = ALIAS ? sKW : reinterpret_cast<const T*>(buf + L::off_K);
-    const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
-    const T* sT = reinterpret_cast<const T*>(buf + L::off_T);
-    const T* sV = reinterpret_cast<const T*>(buf + L::off_V);
-    const float* sG = reinterpret_cast<const float*>(buf + L::off_G);
-    const float* sB = reinterpret_cast<const float*>(buf + L::off_B);
-    const int cid = first + jc;
-    const int clen = min(C, dlen - jc * C);
-    const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+  // A whole chunk (every one of a document's but its last) stores without
+  // row tests: no branches split the step's code, so the scheduler
+  // interleaves its products, LDS reads and stores.
+  auto step = [&](int jc, auto full_t) {
+    constexpr bool FULL = decltype(full_t)::value;
+      const char* buf = smem + (jc & 1) * L::BUF;
+      const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
+      const T* sKW = reinterpret_cast<const T*>(buf + L::off_KW);
+      const T* sK = ALIAS ? sKW : reinterpret_cast<const T*>(buf + L::off_K);
+      const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
+      const T* sT = reinterpret_cast<const T*>(buf + L::off_T);
+      const T* sV = reinterpret_cast<const T*>(buf + L::off_V);
+      const float* sG = reinterpret_cast<const float*>(buf + L::off_G);
+      const float* sB = reinterpret_cast<const float*>(buf + L::off_B);
+      const int cid = first + jc;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
 
-    // S as bf16 B operands; checkpoint the entering state
-    s16x8_t SB[NKT / 2];
+      // S as bf16 B operands; checkpoint the entering state
+      s16x8_t SB[NKT / 2];
 #pragma unroll
-    for (int kk = 0; kk < NKT / 2; ++kk) SB[kk] = pack_acc_pair(S[2 * kk], S[2 * kk + 1]);
-    if (p.h) {
-      T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D;
+      for (int kk = 0; kk < NKT / 2; ++kk) SB[kk] = pack_acc_pair(S[2 * kk], S[2 * kk + 1]);
+      if (p.h) {
+        T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D;
 #pragma unroll
-      for (int kk = 0; kk < NKT / 2; ++kk) {
-        const uint4 w = __builtin_bit_cast(uint4, SB[kk]);
-        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
-        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
-      }
-    }
-    // K S and Q S: for each k step the eight tiles are independent accumulators
-    f32x4 KS[4], QS[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) KS[rb] = QS[rb] = zero4();
-#pragma unroll
-    for (int kk = 0; kk < NKT / 2; ++kk) {
-      s16x8_t ak[4], aq[4];
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        ak[rb] = lds_a_perm(sK + 16 * rb * L::LD, L::LD, 32 * kk, lane);
-        aq[rb] = lds_a_perm(sQ + 16 * rb * L::LD, L::LD, 32 * kk, lane);
-      }
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        mfma_bf16(KS[rb], ak[rb], SB[kk]);
-        mfma_bf16(QS[rb], aq[rb], SB[kk]);
-      }
-    }
-    // Y = diag(beta) (V - diag(e^G) K S) as B operands over the tokens
-    s16x8_t YB[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      f32x4 y[2];
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 32 * kt + 16 * hf + q4 + j;
-          y[hf][j] = sB[r] * (bf16_to_f32(sV[r * L::LDV + cl]) - exp_fast(sG[r]) * KS[2 * kt + hf][j]);
+        for (int kk = 0; kk < NKT / 2; ++kk) {
+          const uint4 w = __builtin_bit_cast(uint4, SB[kk]);
+          store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+          store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
         }
       }
-      YB[kt] = pack_acc_pair(y[0], y[1]);
-    }
-    // U = T Y   (T is lower triangular: row block rb needs k steps kt <= rb / 2)
-    f32x4 U[4];
-    {
-      s16x8_t at[6];
+      // K S and Q S: for each k step the eight tiles are independent accumulators
+      f32x4 KS[4], QS[4];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) at[rb] = lds_a_perm(sT + 16 * rb * L::LDC, L::LDC, 0, lane);
-      at[4] = lds_a_perm(sT + 32 * L::LDC, L::LDC, 32, lane);
-      at[5] = lds_a_perm(sT + 48 * L::LDC, L::LDC, 32, lane);
+      for (int rb = 0; rb < 4; ++rb) KS[rb] = QS[rb] = zero4();
+#pragma unroll
+      for (int kk = 0; kk < NKT / 2; ++kk) {
+        s16x8_t ak[4], aq[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          ak[rb] = lds_a_perm(sK + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+          aq[rb] = lds_a_perm(sQ + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          mfma_bf16(KS[rb], ak[rb], SB[kk]);
+          mfma_bf16(QS[rb], aq[rb], SB[kk]);
+        }
+      }
+      // Y = diag(beta) (V - diag(e^G) K S) as B operands over the tokens
+      s16x8_t YB[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        f32x4 y[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 32 * kt + 16 * hf + q4 + j;
+            y[hf][j] = sB[r] * (bf16_to_f32(sV[r * L::LDV + cl]) - exp_fast(sG[r]) * KS[2 * kt + hf][j]);
+          }
+        }
+        YB[kt] = pack_acc_pair(y[0], y[1]);
+      }
+      // U = T Y   (T is lower triangular: row block rb needs k steps kt <= rb / 2)
+      f32x4 U[4];
+      {
+        s16x8_t at[6];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) at[rb] = lds_a_perm(sT + 16 * rb * L::LDC, L::LDC, 0, lane);
+        at[4] = lds_a_perm(sT + 32 * L::LDC, L::LDC, 32, lane);
+        at[5] = lds_a_perm(sT + 48 * L::LDC, L::LDC, 32, lane);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          U[rb] = zero4();
+          mfma_bf16(U[rb], at[rb], YB[0]);
+        }
+        mfma_bf16(U[2], at[4], YB[1]);
+        mfma_bf16(U[3], at[5], YB[1]);
+      }
+      T* u_out = static_cast<T*>(p.u) + row0 * D + col0;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, FULL>(u_out, gs, U[rb], 16 * rb, 0, clen, lane);
+      const s16x8_t UB[2] = {pack_acc_pair(U[0], U[1]), pack_acc_pair(U[2], U[3])};
+      // O = diag(s e^G) Q S + Aqk U   (Aqk is lower triangular: row block rb needs k steps kt <= rb / 2)
+      f32x4 AU[4];
+      {
+        s16x8_t aa[6];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) aa[rb] = lds_a_perm(sA + 16 * rb * L::LDC, L::LDC, 0, lane);
+        aa[4] = lds_a_perm(sA + 32 * L::LDC, L::LDC, 32, lane);
+        aa[5] = lds_a_perm(sA + 48 * L::LDC, L::LDC, 32, lane);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          AU[rb] = zero4();
+          mfma_bf16(AU[rb], aa[rb], UB[0]);
+        }
+        mfma_bf16(AU[2], aa[4], UB[1]);
+        mfma_bf16(AU[3], aa[5], UB[1]);
+      }
+      T* o_out = static_cast<T*>(p.o) + row0 * D + col0;
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
-        U[rb] = zero4();
-        mfma_bf16(U[rb], at[rb], YB[0]);
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = scale * exp_fast(sG[16 * rb + q4 + j]) * QS[rb][j] + AU[rb][j];
+        store_acc_global<T, FULL>(o_out, gs, o, 16 * rb, 0, clen, lane);
       }
-      mfma_bf16(U[2], at[4], YB[1]);
-      mfma_bf16(U[3], at[5], YB[1]);
-    }
-    T* u_out = static_cast<T*>(p.u) + row0 * D + col0;
+      // S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U
+      const float gC = sG[C - 1];
+      s16x8_t UgB[2];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(u_out, gs, U[rb], 16 * rb, 0, clen, lane);
-    const s16x8_t UB[2] = {pack_acc_pair(U[0], U[1]), pack_acc_pair(U[2], U[3])};
-    // O = diag(s e^G) Q S + Aqk U   (Aqk is lower triangular: row block rb needs k steps kt <= rb / 2)
-    f32x4 AU[4];
-    {
-      s16x8_t aa[6];
+      for (int kt = 0; kt < 2; ++kt) {
+        float fa[4], fb[4];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) aa[rb] = lds_a_perm(sA + 16 * rb * L::LDC, L::LDC, 0, lane);
-      aa[4] = lds_a_perm(sA + 32 * L::LDC, L::LDC, 32, lane);
-      aa[5] = lds_a_perm(sA + 48 * L::LDC, L::LDC, 32, lane);
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        AU[rb] = zero4();
-        mfma_bf16(AU[rb], aa[rb], UB[0]);
+        for (int j = 0; j < 4; ++j) {
+          fa[j] = exp_fast(gC - sG[32 * kt + q4 + j]);
+          fb[j] = exp_fast(gC - sG[32 * kt + 16 + q4 + j]);
+        }
+        UgB[kt] = pack_acc_pair_scaled(U[2 * kt], fa, U[2 * kt + 1], fb);
       }
-      mfma_bf16(AU[2], aa[4], UB[1]);
-      mfma_bf16(AU[3], aa[5], UB[1]);
-    }
-    T* o_out = static_cast<T*>(p.o) + row0 * D + col0;
+      const float decay = exp_fast(gC);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      f32x4 o;
+      for (int rt = 0; rt < NKT; ++rt) S[rt] = S[rt] * decay;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = scale * exp_fast(sG[16 * rb + q4 + j]) * QS[rb][j] + AU[rb][j];
-      store_acc_global<T>(o_out, gs, o, 16 * rb, 0, clen, lane);
-    }
-    // S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U
-    const float gC = sG[C - 1];
-    s16x8_t UgB[2];
+      for (int kt = 0; kt < 2; ++kt) {
+        s16x8_t ak[NKT];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      float fa[4], fb[4];
+        for (int rt = 0; rt < NKT; ++rt) ak[rt] = lds_kmajor_perm(sKW + 16 * rt, L::LD, 32 * kt, lane);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        fa[j] = exp_fast(gC - sG[32 * kt + q4 + j]);
-        fb[j] = exp_fast(gC - sG[32 * kt + 16 + q4 + j]);
+        for (int rt = 0; rt < NKT; ++rt) mfma_bf16(S[rt], ak[rt], UgB[kt]);
       }
-      UgB[kt] = pack_acc_pair_scaled(U[2 * kt], fa, U[2 * kt + 1], fb);
-    }
-    const float decay = exp_fast(gC);
-#pragma unroll
-    for (int rt = 0; rt < NKT; ++rt) S[rt] = S[rt] * decay;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      s16x8_t ak[NKT];
-#pragma unroll
-      for (int rt = 0; rt < NKT; ++rt) ak[rt] = lds_kmajor_perm(sKW + 16 * rt, L::LD, 32 * kt, lane);
-#pragma unroll
-      for (int rt = 0; rt < NKT; ++rt) mfma_bf16(S[rt], ak[rt], UgB[kt]);
-    }
+  };
+  for (int jc = 0; jc + 1 < count; ++jc) {
+    __syncthreads();
+    step(jc, std::true_type{});
+  }
+  if (count > 0) {
+    __syncthreads();
+    if (dlen - (count - 1) * C == C) step(count - 1, std::true_type{});
+    else step(count - 1, std::false_type{});
   }
   if (p.sT) {
     float* sb = p.sT + (state_row(p, n) * H + h) * D * D + col0;
