@@ -633,8 +633,8 @@ struct FusedW4Layout {
   static constexpr int off_P1 = off_P1r + CT;    // beta_t dAkk E
   static constexpr int off_gam = off_P1 + CT;    // [64] G
   static constexpr int off_beta = off_gam + C * 4;
-  static constexpr int off_p2d = off_beta + C * 4;   // [64] s dAqk[t,t], FP32
-  static constexpr int off_db1 = off_p2d + C * 4;    // [64] sum_c dBv V
+  static constexpr int off_p2d = off_beta + C * 4;   // [64] s dAqk[t,t], FP32, then 64 dummy slots
+  static constexpr int off_db1 = off_p2d + 2 * C * 4;  // [64] sum_c dBv V
   static constexpr int off_rowg = off_db1 + C * 4;   // [4][64] per-wave row sums of the gate gradient
   static constexpr int off_rowb = off_rowg + 4 * C * 4;  // [4][64] per-wave row sums of dbeta
   static constexpr int off_wave = off_rowb + 4 * C * 4;  // [2][4] sum(S0 dS_C), sum(kw dKg) per wave
@@ -655,20 +655,19 @@ __device__ __forceinline__ void lower_tile(int i, int& tb, int& sb) {
   sb = i - tb * (tb + 1) / 2;
 }
 
+// The body for one chunk; `len` is a literal C for whole chunks (every chunk
+// of a document but its last), so every row test folds away and no branch
+// splits the code.
 template <int D>
-__global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p) {
+__device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo ci, const int len, char* smem) {
   using L = FusedW4Layout<D>;
   using E = bf16_t;
   using M = Mma<bf16_t>;
   constexpr int NJ = D / 64;  // column tiles per wave
   constexpr int KV = D / 32;  // k steps over the value index
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
   const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int q = lane >> 4, il = lane & 15;
-  const int len = ci.len;
   const int64_t gs = (int64_t)H * D;
   const int64_t row0 = (int64_t)ci.start * H + hh;
   const float scale = p.scale;
@@ -736,7 +735,7 @@ __global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p)
       part += __shfl_xor(part, 2);
       part += __shfl_xor(part, 4);
       if constexpr (PER_ROW == 16) part += __shfl_xor(part, 8);
-      if (idx % PER_ROW == 0) sDb1[r] = part;
+      sDb1[r] = part;  // the row's lanes all hold the sum: unconditional, no branch
       const float br = sBeta[r];
 #pragma unroll
       for (int e = 0; e < V; ++e) b[e] *= br;
@@ -800,7 +799,8 @@ __global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p)
         // the gate gradient (q dq and kw dkw) cancel exactly and stay out of it
         const float val = (s < t && t < len) ? scale * exp_fast(sGam[t] - sGam[s]) * acc[e] : 0.f;
         sP2[t * L::LDC + s] = to_e<E>(val);
-        if (s == t) sP2d[t] = t < len ? scale * acc[e] : 0.f;
+        // the diagonal lane writes P2d[t], the others their own dummy slot
+        sP2d[s == t ? t : C + lane] = t < len ? scale * acc[e] : 0.f;
       }
     }
   }
@@ -945,10 +945,7 @@ __global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p)
       store_acc_global<E>(dqo, gs, dq[rb][j], r0, 16 * (NJ * wave + j), len, lane);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float g = group16_sum(gq[e]);
-      if (il == 0) sRowG[wave * C + r0 + 4 * q + e] = g;
-    }
+    for (int e = 0; e < 4; ++e) sRowG[wave * C + r0 + 4 * q + e] = group16_sum(gq[e]);  // same value from 16 lanes
   }
   s16x8_t Qf[2][NJ];
 #pragma unroll
@@ -1007,17 +1004,15 @@ __global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p)
     for (int e = 0; e < 4; ++e) {
       const float g = group16_sum(gsum[e]);
       const float b = group16_sum(db[e]);
-      if (il == 0) {
-        sRowG[wave * C + r0 + 4 * q + e] += g;  // this lane wrote the q dq part in (a)
-        sRowB[wave * C + r0 + 4 * q + e] = b;
-      }
+      // the 16 lanes of the row all read the q dq part (a) wrote, then all
+      // write the same sum
+      sRowG[wave * C + r0 + 4 * q + e] += g;
+      sRowB[wave * C + r0 + 4 * q + e] = b;
     }
   }
   kgd = wave_sum(kgd);
-  if (lane == 0) {
-    sWave[wave] = hd;
-    sWave[4 + wave] = kgd;
-  }
+  sWave[wave] = hd;  // every lane holds the wave sums
+  sWave[4 + wave] = kgd;
   __syncthreads();
   if (tid < len) {
     const int64_t idx = (int64_t)(ci.start + tid) * H + hh;
@@ -1039,6 +1034,14 @@ __global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p)
     p.dgcum[idx] = g;
     p.dbeta[idx] = b;
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len == C) fused_bwd_w4<D>(p, ci, C, smem);
+  else if (ci.len > 0) fused_bwd_w4<D>(p, ci, ci.len, smem);
 }
 
 // ---------------------------------------------------------------------------
