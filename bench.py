@@ -113,6 +113,14 @@ STAGE_KERNEL = {
     "bwd_chunk": "chunk_fused_bwd_w4_kernel<128>",
     "decode": "decode_kernel<bf16, 128, 512>",
 }
+# The production operator's chunk kernels (per-channel gate, BF16 keys with
+# the preconditioner's write key, d = 128), by the same stage split.
+PRODUCTION_STAGE_KERNEL = {
+    "fwd_intra": "chunk_intra_fwd_pc_kernel<bf16, 128, false>",
+    "fwd_state": "chunk_state_fwd_kernel<bf16, 128, 64, true>",
+    "bwd_state": "chunk_state_bwd_kernel<bf16, 128, 64, true>",
+    "bwd_chunk": "chunk_fused_bwd_pc_kernel<bf16, 128, bf16, bf16>",
+}
 TRAFFIC_PROFILE = ROOT / "profiles" / "pkda_chunk_c2_decode_c4_hbm_traffic.md"
 
 
@@ -341,13 +349,21 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
         du=_ptr(du), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
         dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None, grad_dtype=_lib.PKDA_BF16, key_grad_dtype=_lib.PKDA_BF16,
     )
+    return _event_stages(fa, ba, _stream(dev), steps)
+
+
+def _event_stages(fa, ba, stream, steps: int) -> dict[str, float]:
+    """Average duration (ms) of each kernel of one chunked fwd+bwd, launched
+    stage by stage on ``stream`` (torch's current stream) with events around
+    each launch."""
+    from delta_feedback_experiment_amd import _lib
+
     stages = [
         ("fwd_intra", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_INTRA),
         ("fwd_state", "pkda_chunk_fwd", fa, _lib.STAGE_FWD_STATE),
         ("bwd_state", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_STATE),
         ("bwd_chunk", "pkda_chunk_bwd", ba, _lib.STAGE_BWD_CHUNK),
     ]
-    stream = _stream(dev)
     events = {name: [] for name, *_ in stages}
 
     def run(record: bool):
@@ -694,12 +710,57 @@ def bench_production(dev: torch.device, steps: int = 10, warmup: int = 3) -> dic
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    stage_ms = time_production_stages([x.detach() for x in leaves], do, D ** -0.5, steps)
+    # dominant kernel: the per-channel fused backward, priced on the products
+    # it shares with the per-head kernel (its pair terms come on top)
+    dom = max(stage_ms, key=stage_ms.get)
+    tflops = B * T * H * stage_flops(D)[dom] / (stage_ms[dom] / 1e3) / 1e12
+    traffic = profiled_traffic(PRODUCTION_STAGE_KERNEL[dom])
+    roofline = {
+        "bound": "mfma", "kernel": dom, "achieved": tflops, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+        "frac": tflops * 1e12 / MFMA_BF16_PEAK, "traffic": traffic_bytes(traffic), "traffic_detail": traffic,
+    }
+    if traffic_bytes(traffic) is not None:
+        roofline["hbm_GBps"] = traffic_bytes(traffic) / (stage_ms[dom] / 1e3) / 1e9
     return {
         "workload": "c2 geometry, production operator: B8 T4096 H16 d128 bf16, raw per-channel gate, "
                     "preconditioner x=1.5, fwd+bwd of all ten inputs",
         "ms_per_step": ms, "tokens_per_s": B * T / (ms / 1e3),
         "mfma_frac_step": B * T * H * step_flops_convention(D) / (ms / 1e3) / MFMA_BF16_PEAK,
+        "stage_ms": stage_ms, "stage_kernels": PRODUCTION_STAGE_KERNEL, "roofline": roofline,
     }
+
+
+def time_production_stages(leaves: list[torch.Tensor], do: torch.Tensor, scale: float, steps: int) -> dict:
+    """The production operator's four chunk kernels timed one by one (events
+    around each launch), on the intermediates its own forward retains."""
+    from delta_feedback_experiment_amd import _lib, ops
+    from delta_feedback_experiment_amd.pkda import _ptr, _stream
+
+    q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, center = leaves
+    with torch.no_grad():
+        plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs = ops._forward(
+            q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, center, scale, 1.5, 1e-6, save_all=True)
+    ntok, H, D = plan.num_tokens, plan.heads, plan.head_dim
+    dev = q.device
+    bf = dict(device=dev, dtype=torch.bfloat16)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dof = do.contiguous().reshape(ntok, H, D)
+    ob = torch.empty(ntok, H, D, **bf)
+    dh = torch.empty(plan.num_chunks, H, D, D, **bf)
+    du = torch.empty(ntok, H, D, **bf)
+    dq, dk, dkw, dv = (torch.empty(ntok, H, D, **bf) for _ in range(4))
+    dbeta, dgcum = torch.empty(ntok, H, **f32), torch.empty(ntok, H, D, **f32)
+    common = dict(dtype=_lib.PKDA_BF16, **plan.common(), q=_ptr(qf), k=_ptr(kf), kw=_ptr(pstate.kw), v=_ptr(vf),
+                  gcum=_ptr(gcum), gate_per_channel=1, beta=_ptr(beta32), scale=scale, initial_state=None,
+                  w=_ptr(fs.w), u=_ptr(fs.u), aqk=_ptr(fs.aqk), akk=_ptr(fs.akk), h=_ptr(fs.h),
+                  qg=_ptr(fs.qg), kg=_ptr(fs.kg))
+    fa = _lib.ChunkFwdArgs(**common, final_state=None, o=_ptr(ob))
+    ba = _lib.ChunkBwdArgs(
+        **common, do=_ptr(dof), dht=None, dh=_ptr(dh), du=_ptr(du), dq=_ptr(dq), dk=_ptr(dk), dkw=_ptr(dkw),
+        dv=_ptr(dv), dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None, grad_dtype=_lib.PKDA_BF16,
+        key_grad_dtype=_lib.PKDA_BF16, kw32=_ptr(pstate.kw32))
+    return _event_stages(fa, ba, _stream(dev), steps)
 
 
 def copy_bandwidth(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
@@ -1017,7 +1078,8 @@ def main() -> None:
         result["production"] = bench_production(dev, args.steps, args.warmup)
         c = result["production"]
         print(f"[bench] production operator {c['ms_per_step']:.3f} ms/step "
-              f"({c['tokens_per_s'] / 1e6:.2f} M tok/s)", file=sys.stderr, flush=True)
+              f"({c['tokens_per_s'] / 1e6:.2f} M tok/s); stages (ms): "
+              f"{json.dumps({n: round(t, 4) for n, t in c['stage_ms'].items()})}", file=sys.stderr, flush=True)
         inp = None
     if not args.no_extra and args.workload == "c2":
         del inp
