@@ -1677,8 +1677,14 @@ struct RrBwdLayout {
   static constexpr int off_G = off_dO + C * LDV * 2;
   static constexpr int off_B = off_G + C * 4;                     // beta (0 past the chunk's end)
   static constexpr int BUF = off_B + C * 4;
-  static constexpr int bytes = 2 * BUF;
-  static_assert(BUF % 16 == 0, "16-byte aligned stages");
+  // Output stage (where it fits): the compute waves leave each chunk's dBv
+  // rows here, double-buffered, and the loader group that is not staging
+  // inputs in that step writes them to global memory.
+  static constexpr int OUT = C * LDV * 2;
+  static constexpr bool STAGE_OUT = 2 * BUF + 2 * OUT <= 160 * 1024;
+  static constexpr int off_Out = 2 * BUF;
+  static constexpr int bytes = 2 * BUF + (STAGE_OUT ? 2 * OUT : 0);
+  static_assert(BUF % 16 == 0 && (LDV * 2) % 16 == 0, "16-byte aligned stages and rows");
   static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
 };
 
@@ -1739,6 +1745,24 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
         reinterpret_cast<float*>(buf + L::off_B)[lt] = rb;
       }
     };
+    // visit s's dBv rows from the output stage to global memory
+    auto flush = [&](int s) {
+      constexpr int SEG = BV / 8;  // 16-byte pieces of a row
+      static_assert(C * SEG % NGT == 0, "whole passes over the stage");
+      const T* so = reinterpret_cast<const T*>(smem + L::off_Out + (s & 1) * L::OUT);
+      const int jc = count - 1 - s;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+#pragma unroll
+      for (int it = 0; it < C * SEG / NGT; ++it) {
+        const int i = lt + it * NGT;
+        const int r = i / SEG, sg = i % SEG;
+        if (r < clen) {
+          const uint4 x = *reinterpret_cast<const uint4*>(so + r * L::LDV + 8 * sg);
+          *reinterpret_cast<uint4*>(static_cast<T*>(p.du) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg) = x;
+        }
+      }
+    };
     if (lgroup < count) load(lgroup);
     if (lgroup == 0 && count > 0) {
       stash(0);
@@ -1746,10 +1770,18 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
     }
     for (int s = 0; s < count; ++s) {
       __syncthreads();
-      if (((s + 1) & 1) == lgroup && s + 1 < count) {
-        stash((s + 1) & 1);
-        if (s + 3 < count) load(s + 3);
+      if (((s + 1) & 1) == lgroup) {
+        if (s + 1 < count) {
+          stash((s + 1) & 1);
+          if (s + 3 < count) load(s + 3);
+        }
+      } else if constexpr (L::STAGE_OUT) {
+        if (s > 0) flush(s - 1);
       }
+    }
+    if constexpr (L::STAGE_OUT) {
+      __syncthreads();  // the last visit's outputs
+      if ((count & 1) == lgroup && count > 0) flush(count - 1);
     }
     return;
   }
@@ -1861,9 +1893,15 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       mfma_bf16(Z[3], at[5], dUnB[1]);
     }
     // the per-chunk kernel needs dU only through dBv = T^T dU = -Z: hand it that
-    T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
+    if constexpr (L::STAGE_OUT) {
+      T* so = reinterpret_cast<T*>(smem + L::off_Out + (s & 1) * L::OUT) + 16 * wave;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(du_out, gs, -Z[rb], 16 * rb, 0, clen, lane);
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, true>(so, L::LDV, -Z[rb], 16 * rb, 0, C, lane);
+    } else {
+      T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(du_out, gs, -Z[rb], 16 * rb, 0, clen, lane);
+    }
     // dS <- e^{G_C} dS + Q^T (s e^G dO) + K^T diag(beta e^G) Z
     s16x8_t ZB[2];
 #pragma unroll
@@ -1895,6 +1933,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       }
     }
   }
+  if constexpr (L::STAGE_OUT) __syncthreads();  // the loaders' flush of the last visit
   if (p.dh0) {
     float* db = p.dh0 + ((int64_t)n * H + h) * D * D + col0;
 #pragma unroll

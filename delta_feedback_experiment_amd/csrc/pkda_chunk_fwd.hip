@@ -783,8 +783,15 @@ struct RrFwdLayout {
   static constexpr int off_G = off_V + C * LDV * 2;
   static constexpr int off_B = off_G + C * 4;                     // beta (0 past the chunk's end)
   static constexpr int BUF = off_B + C * 4;
-  static constexpr int bytes = 2 * BUF;
-  static_assert(BUF % 16 == 0, "16-byte aligned stages");
+  // Output stage (where it fits): the compute waves leave each chunk's U and
+  // O rows here, double-buffered, and the loader group that is not staging
+  // inputs in that step writes them to global memory, so the compute waves
+  // issue no global stores for them.
+  static constexpr int OUT = 2 * C * LDV * 2;  // U, then O
+  static constexpr bool STAGE_OUT = 2 * BUF + 2 * OUT <= 160 * 1024;
+  static constexpr int off_Out = 2 * BUF;
+  static constexpr int bytes = 2 * BUF + (STAGE_OUT ? 2 * OUT : 0);
+  static_assert(BUF % 16 == 0 && (LDV * 2) % 16 == 0, "16-byte aligned stages and rows");
   static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
 };
 
@@ -843,6 +850,25 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
         reinterpret_cast<float*>(buf + L::off_B)[lt] = rb;
       }
     };
+    // chunk jc's U and O rows from the output stage to global memory
+    auto flush = [&](int jc) {
+      constexpr int SEG = BV / 8;  // 16-byte pieces of a row
+      const T* so = reinterpret_cast<const T*>(smem + L::off_Out + (jc & 1) * L::OUT);
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+      static_assert(2 * C * SEG % NGT == 0, "whole passes over the stage");
+#pragma unroll
+      for (int it = 0; it < 2 * C * SEG / NGT; ++it) {
+        const int i = lt + it * NGT;
+        const int which = i / (C * SEG);
+        const int r = (i - which * C * SEG) / SEG, sg = i % SEG;
+        if (r < clen) {
+          const uint4 x = *reinterpret_cast<const uint4*>(so + (which * C + r) * L::LDV + 8 * sg);
+          T* dst = static_cast<T*>(which ? p.o : p.u) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg;
+          *reinterpret_cast<uint4*>(dst) = x;
+        }
+      }
+    };
     // group g holds chunks g, g + 2, ...; chunk 0 is staged before the loop
     if (lgroup < count) load(lgroup);
     if (lgroup == 0 && count > 0) {
@@ -851,10 +877,18 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
     }
     for (int jc = 0; jc < count; ++jc) {
       __syncthreads();
-      if (((jc + 1) & 1) == lgroup && jc + 1 < count) {
-        stash((jc + 1) & 1);
-        if (jc + 3 < count) load(jc + 3);
+      if (((jc + 1) & 1) == lgroup) {
+        if (jc + 1 < count) {
+          stash((jc + 1) & 1);
+          if (jc + 3 < count) load(jc + 3);
+        }
+      } else if constexpr (L::STAGE_OUT) {
+        if (jc > 0) flush(jc - 1);
       }
+    }
+    if constexpr (L::STAGE_OUT) {
+      __syncthreads();  // the last chunk's outputs
+      if ((count & 1) == lgroup && count > 0) flush(count - 1);
     }
     return;
   }
@@ -951,9 +985,15 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
         mfma_bf16(U[2], at[4], YB[1]);
         mfma_bf16(U[3], at[5], YB[1]);
       }
-      T* u_out = static_cast<T*>(p.u) + row0 * D + col0;
+      T* so = reinterpret_cast<T*>(smem + L::off_Out + (jc & 1) * L::OUT) + 16 * wave;
+      if constexpr (L::STAGE_OUT) {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, FULL>(u_out, gs, U[rb], 16 * rb, 0, clen, lane);
+        for (int rb = 0; rb < 4; ++rb) store_acc_global<T, true>(so, L::LDV, U[rb], 16 * rb, 0, C, lane);
+      } else {
+        T* u_out = static_cast<T*>(p.u) + row0 * D + col0;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) store_acc_global<T, FULL>(u_out, gs, U[rb], 16 * rb, 0, clen, lane);
+      }
       const s16x8_t UB[2] = {pack_acc_pair(U[0], U[1]), pack_acc_pair(U[2], U[3])};
       // O = diag(s e^G) Q S + Aqk U   (Aqk is lower triangular: row block rb needs k steps kt <= rb / 2)
       f32x4 AU[4];
@@ -977,7 +1017,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
         f32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = scale * exp_fast(sG[16 * rb + q4 + j]) * QS[rb][j] + AU[rb][j];
-        store_acc_global<T, FULL>(o_out, gs, o, 16 * rb, 0, clen, lane);
+        if constexpr (L::STAGE_OUT) store_acc_global<T, true>(so + C * L::LDV, L::LDV, o, 16 * rb, 0, C, lane);
+        else store_acc_global<T, FULL>(o_out, gs, o, 16 * rb, 0, clen, lane);
       }
       // S <- e^{G_C} S + KW^T diag(e^{G_C - G}) U
       const float gC = sG[C - 1];
@@ -1013,6 +1054,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
     if (dlen - (count - 1) * C == C) step(count - 1, std::true_type{});
     else step(count - 1, std::false_type{});
   }
+  if constexpr (L::STAGE_OUT) __syncthreads();  // the loaders' flush of the last chunk
   if (p.sT) {
     float* sb = p.sT + (state_row(p, n) * H + h) * D * D + col0;
 #pragma unroll
