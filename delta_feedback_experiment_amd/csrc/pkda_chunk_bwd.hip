@@ -1427,7 +1427,6 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
         }
       }
       float ak0[4] = {0.f, 0.f, 0.f, 0.f}, aq0[4] = {0.f, 0.f, 0.f, 0.f};
-      float ep = 1.f, gprev = gr[0];
       {  // x = t_0: the product starts at 1
         float p1[4], p2[4];
         lds4(sP1T + (16 * rb + rq) * 16 + rq, p1);
@@ -1439,27 +1438,36 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
           aq0[e] += p2[e] * wv[0];
         }
       }
-      // x = t_0 - i, i = 1 .. 12: the same count for every lane (lanes whose
-      // x would fall below the block read its first row and add nothing), so
-      // the loop unrolls and a step's reads go out with its neighbours
-#pragma unroll 4
-      for (int i = 1; i < 13; ++i) {
-        const bool in = i <= rq;
-        const int xo = in ? rq - i : 0;
-        const int x = r0 + xo;
-        const float gx = sG[x * L::LDG + c];
-        const float kwx = sKWf[x * L::LDW + c];
-        float p1[4], p2[4];
-        lds4(sP1T + (16 * rb + xo) * 16 + rq, p1);
-        if constexpr (L::P2B) lds4(sP2BT + (16 * rb + xo) * 16 + rq, p2);
-        else lds4(sP2T + (16 * rb + xo) * 16 + rq, p2);
-        ep = in ? ep * exp_fast(gprev - gx) : ep;  // decay of token x + 1
-        gprev = in ? gx : gprev;
-        const float w = in ? kwx * ep : 0.f;
+      // x in the block's earlier 4-row groups (x < t_0): FP32 MFMA steps, one
+      // per (row group g, key group j < g), the decay split at t_0 of group g:
+      // B = kw[x] e^{G[t_0(g)]-G[x]} (<= 1), A = the rows of group g (the other
+      // rows zero), so the lanes of group g receive exactly their rows' sums.
+      {
+        const int mrow = lane & 15, kq = lane >> 4, ag = mrow >> 2;
+        float g0[4];
+#pragma unroll
+        for (int g = 1; g < 4; ++g) g0[g] = sG[(r0 + 4 * g) * L::LDG + nn];
+        f32x4 mk = zero4(), mq = zero4();
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const int x = r0 + 4 * j + kq;  // this lane's B row
+          const float gx = sG[x * L::LDG + nn];
+          const float kwx = sKWf[x * L::LDW + nn];
+          const float a1 = from_e<E>(sP1r[(r0 + mrow) * L::LDC + x]);
+          float a2;
+          if constexpr (L::P2B) a2 = sP2B[(16 * rb + mrow) * 16 + 4 * j + kq];
+          else a2 = from_e<E>(sP2[(r0 + mrow) * L::LDC + x]);
+#pragma unroll
+          for (int g = j + 1; g < 4; ++g) {
+            const float bx = kwx * exp_fast(g0[g] - gx);
+            Mma<float>::mfma(mk, ag == g ? a1 : 0.f, bx);
+            Mma<float>::mfma(mq, ag == g ? a2 : 0.f, bx);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          ak0[e] += p1[e] * w;
-          aq0[e] += p2[e] * w;
+          ak0[e] += mk[e];
+          aq0[e] += mq[e];
         }
       }
 #pragma unroll
@@ -1537,26 +1545,36 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
         for (int e = 0; e < u; ++e) aw[e] += (p1[e] * kx + p2[e] * qx) * exp_fast(gr[u] - gr[e]);
       }
+      // t in the block's later 4-row groups (t > t_3): FP32 MFMA steps, one per
+      // (key group g, row group i > g), the decay split at t_3 of group g:
+      // B = beta k[t] e^{G[t]-G[t_3(g)]} and q[t] e^{G[t]-G[t_3(g)]} (<= 1),
+      // A = dAkk and s dAqk columns of group g (the other columns zero).
       float aw0[4] = {0.f, 0.f, 0.f, 0.f};
-      float ep = 1.f, gprev = gr[3];
-      // t = t_3 + i, i = 1 .. 12, the same count for every lane (as in (1))
-#pragma unroll 4
-      for (int i = 1; i < 13; ++i) {
-        const bool in = rq + 3 + i < 16;
-        const int xo = in ? rq + 3 + i : 15;
-        const int t = r0 + xo;
-        const float gt = sG[t * L::LDG + c];
-        const float kt = sBeta[t] * from_e<E>(sK[t * L::LD + c]);
-        const float qt = from_e<E>(sQ[t * L::LD + c]);
-        float p1[4], p2[4];
-        lds4(sP1r + t * L::LDC + r0 + rq, p1);
-        if constexpr (L::P2B) lds4(sP2B + (16 * rb + xo) * 16 + rq, p2);
-        else lds4(sP2 + t * L::LDC + r0 + rq, p2);
-        ep = in ? ep * exp_fast(gt - gprev) : ep;  // decay of token t
-        gprev = in ? gt : gprev;
-        const float kx = in ? kt * ep : 0.f, qx = in ? qt * ep : 0.f;
+      {
+        const int mrow = lane & 15, kq = lane >> 4, ag = mrow >> 2;
+        float g3[3];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) aw0[e] += p1[e] * kx + p2[e] * qx;
+        for (int g = 0; g < 3; ++g) g3[g] = sG[(r0 + 4 * g + 3) * L::LDG + nn];
+        f32x4 mw = zero4();
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+          const int t = r0 + 4 * i + kq;  // this lane's B row
+          const float gt = sG[t * L::LDG + nn];
+          const float kt = sBeta[t] * from_e<E>(sK[t * L::LD + nn]);
+          const float qt = from_e<E>(sQ[t * L::LD + nn]);
+          const float a1 = from_e<E>(sP1r[t * L::LDC + r0 + mrow]);
+          float a2;
+          if constexpr (L::P2B) a2 = sP2B[(16 * rb + 4 * i + kq) * 16 + mrow];
+          else a2 = from_e<E>(sP2[t * L::LDC + r0 + mrow]);
+#pragma unroll
+          for (int g = 0; g < i; ++g) {
+            const float f = exp_fast(gt - g3[g]);
+            Mma<float>::mfma(mw, ag == g ? a1 : 0.f, kt * f);
+            Mma<float>::mfma(mw, ag == g ? a2 : 0.f, qt * f);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) aw0[e] = mw[e];
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
