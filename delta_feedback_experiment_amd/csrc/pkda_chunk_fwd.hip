@@ -180,19 +180,17 @@ struct IntraLayout {
   static constexpr int bytes_lean = off_gam_lean + C * 4;
 };
 
+// The body for one chunk; `len` is a literal C for whole chunks (every row
+// test folds away, so no branch holds a load back).
 template <typename T, int D, bool ALIAS, bool WU>
-__global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
+__device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkInfo ci, const int len, char* smem) {
   using L = IntraLayout<T, D, ALIAS>;
   constexpr bool LEAN = !WU && L::lean_fits;  // Akk over K's region
   using E = T;
   constexpr int HCT = D / 32;  // column tiles per wave of W / u
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
   const int h = blockIdx.y;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int len = ci.len;
   const int64_t row0 = (int64_t)ci.start * H + h;  // token-row index of the chunk's first token
   const int64_t gs = (int64_t)H * D;               // token stride in elements
 
@@ -211,12 +209,9 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   const T* kw = static_cast<const T*>(p.kw) + row0 * D;
   const T* v = static_cast<const T*>(p.v) + row0 * D;
 
-  if (tid < C) {
-    const int64_t idx = (int64_t)(ci.start + min(tid, len - 1)) * H + h;
-    sGam[tid] = p.gcum[idx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
-    sBeta[tid] = tid < len ? p.beta[idx] : 0.f;
-  }
-  // all tiles in one memory round trip; V waits in registers until region A frees
+  // all tiles in one memory round trip (the gate and beta loads go out after
+  // them: their LDS stores wait for every load before); V waits in registers
+  // until region A frees
   RegTile<kIW, C, D, T> rV;
   {
     RegTile<kIW, C, D, T> rK, rQ, rKW;
@@ -224,6 +219,13 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
     rQ.load(q, gs, len);
     if (!ALIAS) rKW.load(kw, gs, len);
     if (WU) rV.load(v, gs, len);
+    if (tid < C) {
+      const int64_t idx = (int64_t)(ci.start + min(tid, len - 1)) * H + h;
+      const float g = p.gcum[idx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
+      const float b = tid < len ? p.beta[idx] : 0.f;
+      sGam[tid] = g;
+      sBeta[tid] = b;
+    }
     rK.store(sK, L::LD);
     rQ.store(sQ, L::LD);
     if (!ALIAS) rKW.store(sKW, L::LD);
@@ -329,6 +331,14 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
 }
 
 
+template <typename T, int D, bool ALIAS, bool WU>
+__global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len == C) intra_fwd_chunk<T, D, ALIAS, WU>(p, ci, C, smem);
+  else if (ci.len > 0) intra_fwd_chunk<T, D, ALIAS, WU>(p, ci, ci.len, smem);
+}
+
 // ---------------------------------------------------------------------------
 // intra-chunk forward, per-channel gate (G [64][D] per chunk).
 //   Akk[t,s] = beta_t sum_c k[t,c] kw[s,c] e^{G[t,c]-G[s,c]},  Aqk likewise
@@ -359,20 +369,37 @@ struct IntraPcLayout {
   static constexpr int bytes = off_beta + C * 4;
 };
 
+// One chunk's input tiles in registers.  `len` is a literal C for whole
+// chunks: the row tests of the loads fold away, so no branch (and no register
+// copy inside one) makes a load wait before the next goes out.
 template <typename T, int D, bool ALIAS>
-__global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
+struct IntraPcTiles {
+  RegTile<kIW, C, D, T> K, Q, KW, V;
+  RegTile<kIW, C, D, float> G;
+  __device__ __forceinline__ void load(const FwdParams& p, const ChunkInfo& ci, int h, const int len) {
+    const int64_t row0 = (int64_t)ci.start * p.H + h;
+    const int64_t gs = (int64_t)p.H * D;
+    K.load(static_cast<const T*>(p.k) + row0 * D, gs, len);
+    Q.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
+    if (!ALIAS) KW.load(static_cast<const T*>(p.kw) + row0 * D, gs, len);
+    // G rows past the end repeat the last row (G is non-increasing in t, so
+    // every split factor stays <= 1 there too)
+    G.load_clamped(p.gcum + row0 * D, gs, len);
+    V.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
+  }
+};
+
+// The body for one chunk (its tiles' loads already issued).
+template <typename T, int D, bool ALIAS>
+__device__ __forceinline__ void intra_pc_chunk(const FwdParams& p, const ChunkInfo ci, const int h, const int len,
+                                               const IntraPcTiles<T, D, ALIAS>& tiles, char* smem) {
   using L = IntraPcLayout<T, D, ALIAS>;
   using E = T;
   using F = FragK<E>;
   constexpr int HCT = D / 32;
   constexpr int V = Vec16<T>::N;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
-  const int h = blockIdx.y;
   const int H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int len = ci.len;
   const int64_t row0 = (int64_t)ci.start * H + h;
   const int64_t gs = (int64_t)H * D;
 
@@ -385,30 +412,13 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
 
-  const T* q = static_cast<const T*>(p.q) + row0 * D;
-  const T* k = static_cast<const T*>(p.k) + row0 * D;
-  const T* kw = static_cast<const T*>(p.kw) + row0 * D;
-  const T* v = static_cast<const T*>(p.v) + row0 * D;
-  const float* g = p.gcum + row0 * D;
-
   if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + h] : 0.f;
-  // all tiles in one memory round trip; V waits in registers until Q's slot
-  // frees.  G rows past the end repeat the last row (G is non-increasing in
-  // t, so every split factor stays <= 1 there too).
-  RegTile<kIW, C, D, T> rV;
-  {
-    RegTile<kIW, C, D, T> rK, rQ, rKW;
-    RegTile<kIW, C, D, float> rG;
-    rK.load(k, gs, len);
-    rQ.load(q, gs, len);
-    if (!ALIAS) rKW.load(kw, gs, len);
-    rG.load_clamped(g, gs, len);
-    rV.load(v, gs, len);
-    rK.store(sK, L::LD);
-    rQ.store(sQ, L::LD);
-    if (!ALIAS) rKW.store(sKW, L::LD);
-    rG.store(sG, L::LDG);
-  }
+  // V waits in registers until Q's slot frees
+  tiles.K.store(sK, L::LD);
+  tiles.Q.store(sQ, L::LD);
+  if (!ALIAS) tiles.KW.store(sKW, L::LD);
+  tiles.G.store(sG, L::LDG);
+  const RegTile<kIW, C, D, T>& rV = tiles.V;
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
     sA[r * L::LDF + c] = 0.f;
@@ -556,6 +566,22 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   __syncthreads();
   store_tile<kIW, C, D>(static_cast<T*>(p.w) + row0 * D, gs, sK, L::LD, len);
   store_tile<kIW, C, D>(static_cast<T*>(p.u) + row0 * D, gs, sQ, L::LD, len);
+}
+
+template <typename T, int D, bool ALIAS>
+__device__ __forceinline__ void intra_pc_run(const FwdParams& p, const ChunkInfo& ci, const int h, const int len,
+                                             char* smem) {
+  IntraPcTiles<T, D, ALIAS> tiles;
+  tiles.load(p, ci, h, len);
+  intra_pc_chunk<T, D, ALIAS>(p, ci, h, len, tiles, smem);
+}
+
+template <typename T, int D, bool ALIAS>
+__global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len == C) intra_pc_run<T, D, ALIAS>(p, ci, blockIdx.y, C, smem);
+  else if (ci.len > 0) intra_pc_run<T, D, ALIAS>(p, ci, blockIdx.y, ci.len, smem);
 }
 
 // ---------------------------------------------------------------------------
