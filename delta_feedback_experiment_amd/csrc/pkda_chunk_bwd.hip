@@ -686,13 +686,12 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
   float* sWave = reinterpret_cast<float*>(smem + L::off_wave);
   f32x4* sPark = reinterpret_cast<f32x4*>(smem + L::off_park) + wave * L::PARK * 64 + lane;
 
-  if (tid < C) {
-    const int64_t idx = (int64_t)(ci.start + min(tid, len - 1)) * H + hh;
-    sGam[tid] = p.gcum[idx];  // rows past the end repeat the last gate
-    sBeta[tid] = tid < len ? p.beta[idx] : 0.f;
-  }
   // the first passes' loads go out before the first LDS store, in the order
-  // the passes need them
+  // the passes need them; the gate and beta first, so that their LDS stores
+  // wait for those loads only
+  const int64_t gidx = (int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + hh;
+  const float gval = p.gcum[gidx];  // rows past the end repeat the last gate
+  const float bval = p.beta[gidx];
   RegTile<kW4, C, D, E> rU, rdO, rdBv, rV, rK, rQ;
   s16x8_t S0f[NJ][KV], dSf[NJ][KV];  // B operands: rows of this wave's columns, k over the value index
   const E* hsrc = static_cast<const E*>(p.h) + ((int64_t)cid * H + hh) * D * D;
@@ -710,6 +709,9 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
     }
   rdBv.load(static_cast<const E*>(p.du) + row0 * D, gs, len);
   rV.load(static_cast<const E*>(p.v) + row0 * D, gs, len);
+  // every thread writes (the C rows' values, repeated): no branch
+  sGam[tid & (C - 1)] = gval;
+  sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? bval : 0.f;
   rU.store(sR0, L::LD);
   rdO.store(sR1, L::LD);
   __syncthreads();
@@ -1102,15 +1104,14 @@ struct FusedBwdPcLayout {
   static_assert(D * (D / Vec16<T>::N) * 4 <= CT, "row partials of sum(h * dH) fit the T region");
 };
 
+// The body for one chunk; `len` is a literal C for whole chunks (every row
+// test of the tile loads folds away, so no branch holds a load back).
 template <typename T, int D, typename OT, typename OK>
-__global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
+__device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo ci, const int len, char* smem) {
   using L = FusedBwdPcLayout<T, D>;
   using E = T;
   using F = FragK<E>;
   constexpr int HCT = D / 32;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
   const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // waves w and w + 4 share a SIMD: they take row blocks rb and 3 - rb, whose
@@ -1118,7 +1119,6 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   // adds up to the same on every SIMD
   const int ch = wave >> 2, rb = ch ? 3 - (wave & 3) : (wave & 3);
   const int r0 = 16 * rb;
-  const int len = ci.len;
   const int64_t gs = (int64_t)H * D;
   const int64_t row0 = (int64_t)ci.start * H + hh;
 
@@ -1150,13 +1150,10 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   const T* kg_ = static_cast<const T*>(p.k) + row0 * D;
   const T* kwg = static_cast<const T*>(p.kw) + row0 * D;
   const float* kw32g = p.kw32 ? p.kw32 + row0 * D : nullptr;
-  // the write key as the exact pair sums read it: FP32 when the caller has it
-  auto kwval = [&](int r, int c) { return kw32g ? kw32g[(int64_t)r * gs + c] : io<T>::load(kwg + (int64_t)r * gs + c); };
   const float* gg = p.gcum + row0 * D;        // G rows, stride gs
   const float* gC = gg + (int64_t)(len - 1) * gs;
   const float scale = p.scale;
 
-  if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + hh] : 0.f;
   // G at this lane's accumulator positions (rows r0 + 4 (lane / 16) + e,
   // column 16 (ch HCT + j) + lane % 16) is read there by phases 1 to 2b: loaded
   // where phase 1 first needs it and kept.  K waits in registers behind the
@@ -1166,6 +1163,8 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   const int rq = 4 * (lane >> 4);
   float Gl[HCT][4], gCl[HCT];
   RegTile<kFW, C, D, T> rK;
+  // beta first: its LDS store below then waits for this load only
+  const float bval = p.beta[(int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + hh];
   {
     RegTile<kFW, C, D, T> rU, rdO, rdU, rV;
     RegTile<kFW, C, C, T> rT;
@@ -1177,6 +1176,9 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rH.load(hsrc);
     rK.load(kg_, gs, len);
+    // every thread writes (the C rows' values, repeated): no branch to hold
+    // the tile loads after it behind this load
+    sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? bval : 0.f;
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
@@ -1239,14 +1241,23 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   for (int j = 0; j < HCT; ++j) gCl[j] = gC[16 * (ch * HCT + j) + (lane & 15)];
   TiledTile<kFW, D, T> rdH;
   rdH.load(dhsrc);
+  // (rows clamped into the chunk and every load unconditional, so the
+  // sixteen go out together; rows past the chunk are zeroed where phase 3
+  // stores them)
   float Wl[HCT][4];
+  if (kw32g) {
 #pragma unroll
-  for (int j = 0; j < HCT; ++j) {
-    const int c = 16 * (ch * HCT + j) + (lane & 15);
+    for (int j = 0; j < HCT; ++j) {
+      const int c = 16 * (ch * HCT + j) + (lane & 15);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = r0 + rq + e;
-      Wl[j][e] = r < len ? kwval(r, c) : 0.f;
+      for (int e = 0; e < 4; ++e) Wl[j][e] = kw32g[(int64_t)min(r0 + rq + e, len - 1) * gs + c];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < HCT; ++j) {
+      const int c = 16 * (ch * HCT + j) + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Wl[j][e] = io<T>::load(kwg + (int64_t)min(r0 + rq + e, len - 1) * gs + c);
     }
   }
   rK.store(sK, L::LD);  // dO's region: phase 1 is done with it
@@ -1325,7 +1336,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
     for (int e = 0; e < 4; ++e) {
       dkws[j][e] = exp_fast(gCl[j] - Gl[j][e]) * acc[e];
       // the last row's term (decay e^0) cancels against its own -kw dkw: left out
-      col += (r0 + rq + e == len - 1 ? 0.f : Wl[j][e]) * dkws[j][e];
+      col += (r0 + rq + e < len - 1 ? Wl[j][e] : 0.f) * dkws[j][e];
     }
     col += __shfl_xor(col, 16);
     col += __shfl_xor(col, 32);
@@ -1344,7 +1355,7 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sG[(r0 + rq + e) * L::LDG + c] = Gl[j][e];
-      sKWf[(r0 + rq + e) * L::LDW + c] = Wl[j][e];
+      sKWf[(r0 + rq + e) * L::LDW + c] = r0 + rq + e < len ? Wl[j][e] : 0.f;
     }
   }
   if (ch == 0) {  // this row block's diagonal blocks, transposed
@@ -1655,6 +1666,14 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   }
   __syncthreads();
   if (tid < len) p.dbeta[(int64_t)(ci.start + tid) * H + hh] = sRowB[tid] + sRowB[C + tid];
+}
+
+template <typename T, int D, typename OT, typename OK>
+__global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len == C) fused_bwd_pc<T, D, OT, OK>(p, ci, C, smem);
+  else if (ci.len > 0) fused_bwd_pc<T, D, OT, OK>(p, ci, ci.len, smem);
 }
 
 template <typename K>

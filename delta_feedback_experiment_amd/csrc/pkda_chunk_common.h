@@ -454,8 +454,10 @@ struct RegTile {
   static constexpr int ITER = (TOTAL + NT - 1) / NT;
   uint4 r[ITER];
   __device__ __forceinline__ void load(const T* g, int64_t gstride, int nvalid) { load_as(threadIdx.x, g, gstride, nvalid); }
-  // as thread t of the NT that share the tile
+  // as thread t of the NT that share the tile (t < NT: with a literal nvalid of
+  // ROWS, every row test then folds away and no branch holds a load back)
   __device__ __forceinline__ void load_as(int t, const T* g, int64_t gstride, int nvalid) {
+    __builtin_assume(t >= 0 && t < NT);
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
       const int idx = t + i * NT;
@@ -469,6 +471,7 @@ struct RegTile {
   // (every piece is assigned on every path: a conditionally assigned piece
   // keeps the array out of registers)
   __device__ __forceinline__ void load_clamped(const T* g, int64_t gstride, int nvalid) {
+    __builtin_assume(threadIdx.x < NT);
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
       const int idx = threadIdx.x + i * NT;
@@ -480,6 +483,7 @@ struct RegTile {
   }
   __device__ __forceinline__ void store(T* lds, int ld) const { store_as(threadIdx.x, lds, ld); }
   __device__ __forceinline__ void store_as(int t, T* lds, int ld) const {
+    __builtin_assume(t >= 0 && t < NT);
 #pragma unroll
     for (int i = 0; i < ITER; ++i) {
       const int idx = t + i * NT;

@@ -209,23 +209,22 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
   const T* kw = static_cast<const T*>(p.kw) + row0 * D;
   const T* v = static_cast<const T*>(p.v) + row0 * D;
 
-  // all tiles in one memory round trip (the gate and beta loads go out after
-  // them: their LDS stores wait for every load before); V waits in registers
-  // until region A frees
+  // all tiles in one memory round trip (the gate and beta loads go out first,
+  // so that their LDS stores wait for those loads only); V waits in
+  // registers until region A frees
   RegTile<kIW, C, D, T> rV;
   {
+    const int64_t gidx = (int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + h;
+    const float gval = p.gcum[gidx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
+    const float bval = p.beta[gidx];
     RegTile<kIW, C, D, T> rK, rQ, rKW;
     rK.load(k, gs, len);
     rQ.load(q, gs, len);
     if (!ALIAS) rKW.load(kw, gs, len);
     if (WU) rV.load(v, gs, len);
-    if (tid < C) {
-      const int64_t idx = (int64_t)(ci.start + min(tid, len - 1)) * H + h;
-      const float g = p.gcum[idx];  // rows past the end repeat the last gate: e^{G_t-G_s} stays finite
-      const float b = tid < len ? p.beta[idx] : 0.f;
-      sGam[tid] = g;
-      sBeta[tid] = b;
-    }
+    // every thread writes (the C rows' values, repeated): no branch
+    sGam[tid & (C - 1)] = gval;
+    sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? bval : 0.f;
     rK.store(sK, L::LD);
     rQ.store(sQ, L::LD);
     if (!ALIAS) rKW.store(sKW, L::LD);
@@ -376,9 +375,12 @@ template <typename T, int D, bool ALIAS>
 struct IntraPcTiles {
   RegTile<kIW, C, D, T> K, Q, KW, V;
   RegTile<kIW, C, D, float> G;
+  float beta;  // of row threadIdx.x % C (clamped into the chunk)
   __device__ __forceinline__ void load(const FwdParams& p, const ChunkInfo& ci, int h, const int len) {
     const int64_t row0 = (int64_t)ci.start * p.H + h;
     const int64_t gs = (int64_t)p.H * D;
+    // beta first: its LDS store then waits for this load only
+    beta = p.beta[(int64_t)(ci.start + min((int)threadIdx.x & (C - 1), len - 1)) * p.H + h];
     K.load(static_cast<const T*>(p.k) + row0 * D, gs, len);
     Q.load(static_cast<const T*>(p.q) + row0 * D, gs, len);
     if (!ALIAS) KW.load(static_cast<const T*>(p.kw) + row0 * D, gs, len);
@@ -412,7 +414,7 @@ __device__ __forceinline__ void intra_pc_chunk(const FwdParams& p, const ChunkIn
   E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
 
-  if (tid < C) sBeta[tid] = tid < len ? p.beta[(int64_t)(ci.start + tid) * H + h] : 0.f;
+  sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? tiles.beta : 0.f;  // every thread: no branch
   // V waits in registers until Q's slot frees
   tiles.K.store(sK, L::LD);
   tiles.Q.store(sQ, L::LD);
