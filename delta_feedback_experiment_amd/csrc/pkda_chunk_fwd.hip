@@ -587,6 +587,296 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// The same, BF16 at head_dim 128, with the channels in two halves of 64 so
+// that a workgroup needs ~72 KB of LDS and two share a compute unit (one
+// workgroup's loads then overlap the other's products).  Every contraction
+// over the channels (the pair sums of Akk and Aqk) accumulates in registers
+// across the halves; qg, kg and the column blocks of W = T Bw and u = T Bv
+// are per half.  Both halves' tiles are loaded up front: the second half
+// waits in registers while the first computes, and the first half's K and G
+// stay there until W needs them again.
+// ---------------------------------------------------------------------------
+template <bool ALIAS>
+struct IntraPc2Layout {
+  static constexpr int DH = 64;                 // channels per half
+  static constexpr int LD = DH + Pad<bf16_t>::v;
+  static constexpr int LDG = DH + 4;
+  static constexpr int LDC = C + Pad<bf16_t>::v;
+  static constexpr int LDF = C + 4;
+  static constexpr int RT = C * LD * 2;         // a bf16 half tile
+  static constexpr int SCR = 4 * 3 * 16 * SLD * 4;
+  static constexpr int QR = ALIAS ? (RT > SCR ? RT : SCR) : RT;
+  static constexpr int off_K = 0;                          // K half, then Bw half
+  static constexpr int off_Q = off_K + RT;                 // Q half, then solve scratch (with KW), then Bv half
+  static constexpr int off_KW = off_Q + QR;                // KW half (when not aliased to K)
+  static constexpr int off_G = off_KW + (ALIAS ? 0 : RT);  // fp32 [64][LDG] half of G
+  static constexpr int off_A = off_G + C * LDG * 4;        // fp32 [64][LDF]: Akk, then T
+  static constexpr int off_Aqk = off_A + C * LDF * 4;      // bf16 Aqk, then T
+  static constexpr int off_beta = off_Aqk + C * LDC * 2;
+  static constexpr int bytes = off_beta + C * 4;
+  static_assert(ALIAS || QR + RT >= SCR, "the solve's scratch fits the Q and KW regions");
+  static_assert(2 * bytes <= 160 * 1024, "two workgroups per compute unit");
+};
+
+template <bool ALIAS>
+__device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkInfo ci, const int h, const int len,
+                                                char* smem) {
+  using L = IntraPc2Layout<ALIAS>;
+  using T = bf16_t;
+  using E = T;
+  using F = FragK<E>;
+  constexpr int D = 128, DH = L::DH;
+  constexpr int V = Vec16<T>::N;
+  const int H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t row0 = (int64_t)ci.start * H + h;
+  const int64_t gs = (int64_t)H * D;
+
+  E* sK = reinterpret_cast<E*>(smem + L::off_K);
+  E* sQ = reinterpret_cast<E*>(smem + L::off_Q);
+  E* sKW = ALIAS ? sK : reinterpret_cast<E*>(smem + L::off_KW);
+  float* sG = reinterpret_cast<float*>(smem + L::off_G);
+  float* sA = reinterpret_cast<float*>(smem + L::off_A);
+  E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
+  E* sTe = sAqk;
+  float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+
+  const T* k = static_cast<const T*>(p.k) + row0 * D;
+  const T* q = static_cast<const T*>(p.q) + row0 * D;
+  const T* kw = static_cast<const T*>(p.kw) + row0 * D;
+  const float* g = p.gcum + row0 * D;
+
+  // the first half's tiles (beta first: its LDS store waits for it only); G
+  // rows past the end repeat the last row, so every split factor stays <= 1.
+  // Each later tile set is loaded one phase ahead of its use: with two
+  // workgroups per compute unit the other one covers the wait, and the
+  // registers stay within the 128 of four waves per SIMD.
+  const float bval = p.beta[(int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + h];
+  {
+    RegTile<kIW, C, DH, T> K0, Q0, KW0;
+    RegTile<kIW, C, DH, float> G0;
+    K0.load(k, gs, len);
+    Q0.load(q, gs, len);
+    if (!ALIAS) KW0.load(kw, gs, len);
+    G0.load_clamped(g, gs, len);
+    sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? bval : 0.f;  // every thread: no branch
+    K0.store(sK, L::LD);
+    Q0.store(sQ, L::LD);
+    if (!ALIAS) KW0.store(sKW, L::LD);
+    G0.store(sG, L::LDG);
+  }
+#pragma unroll 1
+  for (int i = tid; i < C * C; i += kIW) {
+    const int r = i / C, c = i - r * C;
+    sA[r * L::LDF + c] = 0.f;
+    sAqk[r * L::LDC + c] = to_e<E>(0.f);
+  }
+
+  // the pair sums over one half's channels, accumulated in registers:
+  // diagonal blocks exactly (one (t, s) pair, s <= t, per lane: the 4 x 136
+  // pairs numbered block by block, every wave taking pairs lane + 64 wave and
+  // wave 0 also the last 32, split over two lanes), the off-diagonal blocks
+  // (tb > sb, waves 2-7, one each) on MFMA with the decay split at the row
+  // before the row block
+  auto pair_of = [&](int pg, int& t, int& s) {
+    const int tb = pg / 136;
+    int tl = 0, rest = pg - tb * 136;
+    while (rest > tl) {
+      rest -= tl + 1;
+      ++tl;
+    }
+    t = 16 * tb + tl;
+    s = 16 * tb + rest;
+  };
+  auto pair_sums = [&](int t, int s, int c0, int c1, float& akk, float& aqk) {
+    for (int c = c0; c < c1; c += V) {
+      float kx[V], qx[V], wx[V];
+      lds_vec<V>(sK + t * L::LD + c, kx);
+      lds_vec<V>(sQ + t * L::LD + c, qx);
+      lds_vec<V>(sKW + s * L::LD + c, wx);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float e = exp_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
+        akk += kx[j] * wx[j] * e;
+        aqk += qx[j] * wx[j] * e;
+      }
+    }
+  };
+  const int xh = lane >> 5;  // wave 0's extra pairs: this lane's 32 channels of each half
+  float akk1 = 0.f, aqk1 = 0.f, akk2 = 0.f, aqk2 = 0.f;
+  const int blk = wave - 2;
+  const int tb = blk < 1 ? 1 : blk < 3 ? 2 : 3;
+  const int sb = blk - (tb - 1) * tb / 2;
+  f32x4 akk4 = zero4(), aqk4 = zero4();
+  T* qg_out = static_cast<T*>(p.qg) + row0 * D;
+  T* kg_out = static_cast<T*>(p.kg) + row0 * D;
+
+  auto half_pass = [&](int hc) {  // the half of channels [hc, hc + DH) is in LDS
+    {  // (pair indices recomputed where used: nothing held across the passes)
+      int t1, s1;
+      pair_of(lane + 64 * wave, t1, s1);
+      pair_sums(t1, s1, 0, DH, akk1, aqk1);
+    }
+    if (wave == 0) {
+      int t2, s2;
+      pair_of(512 + (lane & 31), t2, s2);
+      pair_sums(t2, s2, xh * (DH / 2), (xh + 1) * (DH / 2), akk2, aqk2);
+    } else if (wave >= 2) {
+      const int r = 16 * tb - 1;
+      const int t = 16 * tb + (lane & 15), s = 16 * sb + (lane & 15);
+#pragma unroll
+      for (int k0 = 0; k0 < DH; k0 += Mma<E>::KS) {
+        const int kk = k0 + F::off(lane);
+        float ak[F::N], aq[F::N], bw[F::N];
+#pragma unroll
+        for (int j = 0; j < F::N; ++j) {
+          const float gr = sG[r * L::LDG + kk + j];
+          const float fa = exp_fast(sG[t * L::LDG + kk + j] - gr);
+          const float fb = exp_fast(gr - sG[s * L::LDG + kk + j]);
+          ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
+          aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
+          bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
+        }
+        F::mfma(akk4, ak, bw);
+        F::mfma(aqk4, aq, bw);
+      }
+    }
+    // qg = s e^G q and kg = e^{G_last - G} kw of this half, straight to global
+    {
+      const int r = tid / (DH / V), c = (tid % (DH / V)) * V;  // C x DH / V = kIW pieces: one per thread
+      if (r < len) {
+        float qx[V], wx[V];
+        lds_vec<V>(sQ + r * L::LD + c, qx);
+        lds_vec<V>(sKW + r * L::LD + c, wx);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const float gv = sG[r * L::LDG + c + j];
+          qx[j] *= p.scale * exp_fast(gv);
+          wx[j] *= exp_fast(sG[(C - 1) * L::LDG + c + j] - gv);
+        }
+        store_vec<V>(qg_out + r * gs + hc + c, qx);
+        store_vec<V>(kg_out + r * gs + hc + c, wx);
+      }
+    }
+  };
+  static_assert(C * (DH / V) == kIW, "one qg / kg piece per thread and half");
+
+  // ---- first half (the second half's loads go out first) -------------------------
+  {
+    RegTile<kIW, C, DH, T> K1, Q1, KW1;
+    RegTile<kIW, C, DH, float> G1;
+    __syncthreads();
+    half_pass(0);
+    K1.load(k + DH, gs, len);
+    Q1.load(q + DH, gs, len);
+    if (!ALIAS) KW1.load(kw + DH, gs, len);
+    G1.load_clamped(g + DH, gs, len);
+    __syncthreads();
+    // ---- second half -----------------------------------------------------------
+    K1.store(sK, L::LD);
+    Q1.store(sQ, L::LD);
+    if (!ALIAS) KW1.store(sKW, L::LD);
+    G1.store(sG, L::LDG);
+  }
+  __syncthreads();
+  half_pass(DH);
+  // ---- Akk and Aqk from the registers --------------------------------------------
+  {
+    auto pair_store = [&](int t, int s, float akk, float aqk) {
+      sA[t * L::LDF + s] = (s < t && t < len) ? sBeta[t] * akk : 0.f;
+      sAqk[t * L::LDC + s] = to_e<E>(t < len ? p.scale * aqk : 0.f);
+    };
+    int t1, s1;
+    pair_of(lane + 64 * wave, t1, s1);
+    pair_store(t1, s1, akk1, aqk1);
+    if (wave == 0) {
+      akk2 += __shfl_xor(akk2, 32);
+      aqk2 += __shfl_xor(aqk2, 32);
+      int t2, s2;
+      pair_of(512 + (lane & 31), t2, s2);
+      if (xh == 0) pair_store(t2, s2, akk2, aqk2);
+    } else if (wave >= 2) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tt = 16 * tb + acc_row(lane, e), ss = 16 * sb + acc_col(lane);
+        sA[tt * L::LDF + ss] = tt < len ? sBeta[tt] * akk4[e] : 0.f;
+        sAqk[tt * L::LDC + ss] = to_e<E>(tt < len ? p.scale * aqk4[e] : 0.f);
+      }
+    }
+  }
+  __syncthreads();
+  // ---- T = (I + Akk)^-1 in place (scratch over Q and KW); Aqk leaves first ------
+  store_tile<kIW, C, C>(static_cast<T*>(p.aqk) + row0 * C, (int64_t)H * C, sAqk, L::LDC, len);
+  solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
+  // W's operands: V, and the first half's K and G again
+  RegTile<kIW, C, D, T> rV;
+  RegTile<kIW, C, DH, T> K0;
+  RegTile<kIW, C, DH, float> G0;
+  rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
+  K0.load(k, gs, len);
+  G0.load_clamped(g, gs, len);
+  // (loops over the tile not unrolled: hoisted addresses would be held, and
+  // spilled, across the phases)
+#pragma unroll 1
+  for (int i = tid; i < C * C; i += kIW) {  // T in bf16 over Aqk (its reads ended before the solve's barriers)
+    const int r = i / C, c = i - r * C;
+    sTe[r * L::LDC + c] = to_e<E>(sA[r * L::LDF + c]);
+  }
+  // ---- W = T Bw and u = T Bv, column half by column half -------------------------
+  // Bw = diag(beta) (e^G * K), Bv = diag(beta) V; the second half's K and G
+  // are still in LDS, the first half's come back from the registers
+  const int rb = wave & 3, ch = wave >> 2;
+  const int kend = kceil<E>(16 * rb + 16);
+  T* w_out = static_cast<T*>(p.w) + row0 * D;
+  T* u_out = static_cast<T*>(p.u) + row0 * D;
+  auto wu_half = [&](int hc) {
+#pragma unroll 1
+    for (int i = tid; i < C * DH; i += kIW) {
+      const int r = i / DH, c = i - r * DH;
+      sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+    }
+    // this half's V columns from the register tile (pieces of 8 columns)
+#pragma unroll
+    for (int i = 0; i < RegTile<kIW, C, D, T>::ITER; ++i) {
+      const int idx = tid + i * kIW;
+      const int r = idx / (D / V), c = (idx % (D / V)) * V;
+      if (c >= hc && c < hc + DH) {
+        float x[V];
+        Vec16<T>::unpack(rV.r[i], x);
+#pragma unroll
+        for (int j = 0; j < V; ++j) x[j] *= sBeta[r];
+        store_vec<V>(sQ + r * L::LD + c - hc, x);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < DH / 32; ++j) {
+      const int ct = ch * (DH / 32) + j;  // column tile within the half
+      f32x4 aw = zero4(), au = zero4();
+      mma_tile_range<E, ROW, ROW>(aw, sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
+      mma_tile_range<E, ROW, ROW>(au, sTe, L::LDC, 16 * rb, sQ, L::LD, 16 * ct, 0, kend, lane);
+      store_acc_global<T>(w_out, gs, aw, 16 * rb, hc + 16 * ct, len, lane);
+      store_acc_global<T>(u_out, gs, au, 16 * rb, hc + 16 * ct, len, lane);
+    }
+  };
+  wu_half(DH);
+  __syncthreads();  // every wave is done with the second half's Bw and Bv
+  K0.store(sK, L::LD);
+  G0.store(sG, L::LDG);
+  __syncthreads();
+  wu_half(0);
+  store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
+}
+
+template <bool ALIAS>
+__global__ __launch_bounds__(kIW, 4) void chunk_intra_fwd_pc2_kernel(FwdParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  if (ci.len == C) intra_pc2_chunk<ALIAS>(p, ci, blockIdx.y, C, smem);
+  else if (ci.len > 0) intra_pc2_chunk<ALIAS>(p, ci, blockIdx.y, ci.len, smem);
+}
+
+// ---------------------------------------------------------------------------
 // per-document state pass
 //
 // One workgroup per (document, head, BV value columns).  The FP32 state slice
@@ -1134,8 +1424,19 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
                            : (WU || !IntraLayout<T, D, true>::lean_fits)
                                  ? (alias ? IntraLayout<T, D, true>::bytes : IntraLayout<T, D, false>::bytes)
                                  : (alias ? IntraLayout<T, D, true>::bytes_lean : IntraLayout<T, D, false>::bytes_lean);
-    if (int st = set_smem(kern, bytes)) return st;
-    if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kIW), bytes, s, p);
+    if constexpr (std::is_same<T, bf16_t>::value && D == 128) {
+      if (p.qg) {  // BF16 per-channel gate at d = 128: the two-half form, two workgroups per CU
+        auto kern2 = alias ? chunk_intra_fwd_pc2_kernel<true> : chunk_intra_fwd_pc2_kernel<false>;
+        const int bytes2 = alias ? IntraPc2Layout<true>::bytes : IntraPc2Layout<false>::bytes;
+        if (int st = set_smem(kern2, bytes2)) return st;
+        if (num_chunks > 0) hipLaunchKernelGGL(kern2, dim3(num_chunks, p.H), dim3(kIW), bytes2, s, p);
+        kern = nullptr;
+      }
+    }
+    if (kern) {
+      if (int st = set_smem(kern, bytes)) return st;
+      if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kIW), bytes, s, p);
+    }
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
   }
   if (all || (stages & PKDA_STAGE_FWD_STATE)) {
