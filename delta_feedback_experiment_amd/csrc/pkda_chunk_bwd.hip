@@ -1998,6 +1998,245 @@ int launch_state_bwd_rr(const BwdParams& p, hipStream_t s) {
   return p.kw_is_k ? launch_state_bwd_rr_as<D, 64, true>(p, s) : launch_state_bwd_rr_as<D, 64, false>(p, s);
 }
 
+// ---------------------------------------------------------------------------
+// reverse state pass, BF16 with a per-channel gate: register-resident form.
+// The structure of chunk_state_bwd_rr_kernel with W, qg and kg as inputs:
+//   dU = Aqk^T dO + kg dS_C            (written for the per-chunk kernel)
+//   dS <- diag(e^{G_C}) dS + qg^T dO - W^T dU.
+// Loader waves stage qg, kg, W, Aqk, the dO slice and e^{G_C}; the compute
+// waves leave dU in a double-buffered LDS output stage that the loader group
+// not staging inputs writes out.
+// ---------------------------------------------------------------------------
+template <int D, int BV>
+struct RrPcBwdLayout {
+  static constexpr int LD = D + Pad<bf16_t>::v;
+  static constexpr int LDV = BV + Pad<bf16_t>::v;
+  static constexpr int LDC = C + Pad<bf16_t>::v;
+  static constexpr int off_Q = 0;                     // qg
+  static constexpr int off_KG = off_Q + C * LD * 2;   // kg
+  static constexpr int off_W = off_KG + C * LD * 2;
+  static constexpr int off_A = off_W + C * LD * 2;    // Aqk
+  static constexpr int off_dO = off_A + C * LDC * 2;  // the dO slice
+  static constexpr int off_E = off_dO + C * LDV * 2;  // [D] e^{G_C}
+  static constexpr int BUF = off_E + D * 4;
+  static constexpr int OUT = C * LDV * 2;             // dU rows
+  static constexpr bool STAGE_OUT = 2 * BUF + 2 * OUT <= 160 * 1024;
+  static constexpr int off_Out = 2 * BUF;
+  static constexpr int bytes = 2 * BUF + (STAGE_OUT ? 2 * OUT : 0);
+  static_assert(BUF % 16 == 0 && (LDV * 2) % 16 == 0, "16-byte aligned stages and rows");
+  static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
+};
+
+template <int D, int BV>
+__global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bwd_rr_pc_kernel(BwdParams p) {
+  using L = RrPcBwdLayout<D, BV>;
+  using T = bf16_t;
+  constexpr int NC = BV / 16;
+  constexpr int NKT = D / 16;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const DocSlot ds = doc_slot(p.geom, p.H, D / BV);
+  const int n = ds.n, h = ds.h, v0 = ds.z * BV;
+  const int H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t gs = (int64_t)H * D;
+  int first, count, dstart, dlen;
+  doc_chunks(p.geom, n, first, count, dstart, dlen);
+  const bool loader = wave >= NC;
+
+  // chunks are visited in the order s = 0, 1, ... as jc = count - 1 - s
+  if (loader) {
+    constexpr int NGT = 64 * kRrLoadersBwd / 2;
+    static_assert(D <= NGT, "one loader thread per gate channel");
+    const int lgroup = (tid - 64 * NC) / NGT;  // takes visits s with s % 2 == lgroup
+    const int lt = (tid - 64 * NC) % NGT;
+    RegTile<NGT, C, D, T> rQ, rK, rW;
+    RegTile<NGT, C, C, T> rA;
+    RegTile<NGT, C, BV, T> rdO;
+    float re = 0.f;
+    auto load = [&](int s) {
+      const int jc = count - 1 - s;
+      const int cstart = dstart + jc * C;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)cstart * H + h;
+      rQ.load_as(lt, static_cast<const T*>(p.qg) + row0 * D, gs, clen);
+      rK.load_as(lt, static_cast<const T*>(p.kg) + row0 * D, gs, clen);
+      rW.load_as(lt, static_cast<const T*>(p.w) + row0 * D, gs, clen);
+      rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+      rdO.load_as(lt, static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen);
+      if (lt < D) re = p.gcum[((int64_t)(cstart + clen - 1) * H + h) * D + lt];
+    };
+    auto stash = [&](int b) {
+      char* buf = smem + b * L::BUF;
+      rQ.store_as(lt, reinterpret_cast<T*>(buf + L::off_Q), L::LD);
+      rK.store_as(lt, reinterpret_cast<T*>(buf + L::off_KG), L::LD);
+      rW.store_as(lt, reinterpret_cast<T*>(buf + L::off_W), L::LD);
+      rA.store_as(lt, reinterpret_cast<T*>(buf + L::off_A), L::LDC);
+      rdO.store_as(lt, reinterpret_cast<T*>(buf + L::off_dO), L::LDV);
+      if (lt < D) reinterpret_cast<float*>(buf + L::off_E)[lt] = exp_fast(re);
+    };
+    // visit s's dU rows from the output stage to global memory
+    auto flush = [&](int s) {
+      constexpr int SEG = BV / 8;  // 16-byte pieces of a row
+      static_assert(C * SEG % NGT == 0, "whole passes over the stage");
+      const T* so = reinterpret_cast<const T*>(smem + L::off_Out + (s & 1) * L::OUT);
+      const int jc = count - 1 - s;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+#pragma unroll
+      for (int it = 0; it < C * SEG / NGT; ++it) {
+        const int i = lt + it * NGT;
+        const int r = i / SEG, sg = i % SEG;
+        if (r < clen) {
+          const uint4 x = *reinterpret_cast<const uint4*>(so + r * L::LDV + 8 * sg);
+          *reinterpret_cast<uint4*>(static_cast<T*>(p.du) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg) = x;
+        }
+      }
+    };
+    if (lgroup < count) load(lgroup);
+    if (lgroup == 0 && count > 0) {
+      stash(0);
+      if (count > 2) load(2);
+    }
+    for (int s = 0; s < count; ++s) {
+      __syncthreads();
+      if (((s + 1) & 1) == lgroup) {
+        if (s + 1 < count) {
+          stash((s + 1) & 1);
+          if (s + 3 < count) load(s + 3);
+        }
+      } else if constexpr (L::STAGE_OUT) {
+        if (s > 0) flush(s - 1);
+      }
+    }
+    if constexpr (L::STAGE_OUT) {
+      __syncthreads();  // the last visit's outputs
+      if ((count & 1) == lgroup && count > 0) flush(count - 1);
+    }
+    return;
+  }
+
+  const int q4 = 4 * (lane >> 4), il = lane & 15;
+  const int col0 = v0 + 16 * wave;
+  f32x4 dS[NKT];
+#pragma unroll
+  for (int rt = 0; rt < NKT; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dS[rt][j] = p.dht ? p.dht[(((int64_t)n * H + h) * D + 16 * rt + q4 + j) * D + col0 + il] : 0.f;
+
+  for (int s = 0; s < count; ++s) {
+    __syncthreads();
+    const int jc = count - 1 - s;
+    const char* buf = smem + (s & 1) * L::BUF;
+    const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
+    const T* sK = reinterpret_cast<const T*>(buf + L::off_KG);
+    const T* sW = reinterpret_cast<const T*>(buf + L::off_W);
+    const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
+    const T* sdO = reinterpret_cast<const T*>(buf + L::off_dO);
+    const float* sE = reinterpret_cast<const float*>(buf + L::off_E);
+    const int cid = first + jc;
+    const int clen = min(C, dlen - jc * C);
+    const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+
+    // dS_C as bf16 B operands; checkpoint it (tile-major)
+    s16x8_t dSB[NKT / 2];
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) dSB[kk] = pack_acc_pair(dS[2 * kk], dS[2 * kk + 1]);
+    {
+      T* hb = static_cast<T*>(p.dh) + ((int64_t)cid * H + h) * D * D;
+#pragma unroll
+      for (int kk = 0; kk < NKT / 2; ++kk) {
+        const uint4 w = __builtin_bit_cast(uint4, dSB[kk]);
+        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+      }
+    }
+    // kg dS (eight independent accumulators per k step)
+    f32x4 dU[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) dU[rb] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) {
+      s16x8_t ak[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) ak[rb] = lds_a_perm(sK + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) mfma_bf16(dU[rb], ak[rb], dSB[kk]);
+    }
+    // dO of this wave's columns as B operands over the tokens
+    const s16x8_t dOB[2] = {lds_kmajor_perm(sdO + 16 * wave, L::LDV, 0, lane),
+                            lds_kmajor_perm(sdO + 16 * wave, L::LDV, 32, lane)};
+    // dU += Aqk^T dO   (Aqk^T row block rb needs k steps kt >= rb / 2)
+    {
+      s16x8_t aa[6];
+      aa[0] = lds_kmajor_perm(sA + 0, L::LDC, 0, lane);
+      aa[1] = lds_kmajor_perm(sA + 0, L::LDC, 32, lane);
+      aa[2] = lds_kmajor_perm(sA + 16, L::LDC, 0, lane);
+      aa[3] = lds_kmajor_perm(sA + 16, L::LDC, 32, lane);
+      aa[4] = lds_kmajor_perm(sA + 32, L::LDC, 32, lane);
+      aa[5] = lds_kmajor_perm(sA + 48, L::LDC, 32, lane);
+      mfma_bf16(dU[0], aa[0], dOB[0]);
+      mfma_bf16(dU[1], aa[2], dOB[0]);
+      mfma_bf16(dU[0], aa[1], dOB[1]);
+      mfma_bf16(dU[1], aa[3], dOB[1]);
+      mfma_bf16(dU[2], aa[4], dOB[1]);
+      mfma_bf16(dU[3], aa[5], dOB[1]);
+    }
+    if constexpr (L::STAGE_OUT) {
+      T* so = reinterpret_cast<T*>(smem + L::off_Out + (s & 1) * L::OUT) + 16 * wave;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, true>(so, L::LDV, dU[rb], 16 * rb, 0, C, lane);
+    } else {
+      T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(du_out, gs, dU[rb], 16 * rb, 0, clen, lane);
+    }
+    // dS <- diag(e^{G_C}) dS + qg^T dO - W^T dU
+    const s16x8_t dUnB[2] = {pack_acc_pair(-dU[0], -dU[1]), pack_acc_pair(-dU[2], -dU[3])};
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dS[rt][j] *= sE[16 * rt + q4 + j];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s16x8_t aq[NKT], aw[NKT];
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) {
+        aq[rt] = lds_kmajor_perm(sQ + 16 * rt, L::LD, 32 * kt, lane);
+        aw[rt] = lds_kmajor_perm(sW + 16 * rt, L::LD, 32 * kt, lane);
+      }
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) {
+        mfma_bf16(dS[rt], aq[rt], dOB[kt]);
+        mfma_bf16(dS[rt], aw[rt], dUnB[kt]);
+      }
+    }
+  }
+  if constexpr (L::STAGE_OUT) __syncthreads();  // the loaders' flush of the last visit
+  if (p.dh0) {
+    float* db = p.dh0 + ((int64_t)n * H + h) * D * D + col0;
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt) store_acc_global<float>(db, D, dS[rt], 16 * rt, 0, D, lane);
+  }
+}
+
+template <int D, int BV>
+int launch_state_bwd_rr_pc_as(const BwdParams& p, hipStream_t s) {
+  auto kern = chunk_state_bwd_rr_pc_kernel<D, BV>;
+  constexpr int bytes = RrPcBwdLayout<D, BV>::bytes;
+  if (int st = set_smem(kern, bytes)) return st;
+  hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoadersBwd)), bytes, s, p);
+  return launch_status("pkda_chunk_bwd(state)");
+}
+
+template <int D>
+int launch_state_bwd_rr_pc(const BwdParams& p, hipStream_t s) {
+  const int N = p.geom.num_seqs;
+  if (N <= 0) return 0;
+  const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
+  return narrow ? launch_state_bwd_rr_pc_as<D, 32>(p, s) : launch_state_bwd_rr_pc_as<D, 64>(p, s);
+}
+
 template <typename T, int D, int BV, typename OT, typename OK>
 int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const int N = p.geom.num_seqs;
@@ -2007,8 +2246,10 @@ int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
     if constexpr (std::is_same<T, bf16_t>::value) {
       if (!p.qg) {  // BF16, per-head gate: the register-resident pass
         if (int st = launch_state_bwd_rr<D>(p, s)) return st;
-        done = true;
+      } else {      // BF16, per-channel gate: its register-resident pass
+        if (int st = launch_state_bwd_rr_pc<D>(p, s)) return st;
       }
+      done = true;
     }
     if (!done) {
       auto kern = p.qg ? chunk_state_bwd_kernel<T, D, BV, true> : chunk_state_bwd_kernel<T, D, BV, false>;

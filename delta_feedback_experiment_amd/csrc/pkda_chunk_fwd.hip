@@ -1380,6 +1380,244 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
   }
 }
 
+// ---------------------------------------------------------------------------
+// per-document state pass, BF16 with a per-channel gate: register-resident
+// form.  The structure of chunk_state_fwd_rr_kernel with the intra kernel's
+// W, u, qg = s e^G q and kg = e^{G_last - G} kw as inputs:
+//   U = u - W S,   O = qg S + Aqk U,   S <- diag(e^{G_C}) S + kg^T U.
+// BV/16 compute waves each keep the S [D x 16] slice in MFMA accumulators and
+// the chunk's U [64 x 16] in registers; kRrLoaders loader waves stage qg, W,
+// kg, Aqk, the u slice and e^{G_C} (the chunk's last gate row, exponentiated
+// by the loader) one chunk ahead in a double-buffered LDS stage.
+// ---------------------------------------------------------------------------
+template <int D, int BV>
+struct RrPcFwdLayout {
+  static constexpr int LD = D + Pad<bf16_t>::v;
+  static constexpr int LDV = BV + Pad<bf16_t>::v;
+  static constexpr int LDC = C + Pad<bf16_t>::v;
+  static constexpr int off_Q = 0;                   // qg
+  static constexpr int off_W = off_Q + C * LD * 2;
+  static constexpr int off_KG = off_W + C * LD * 2;  // kg
+  static constexpr int off_A = off_KG + C * LD * 2;  // Aqk
+  static constexpr int off_U = off_A + C * LDC * 2;  // the u slice
+  static constexpr int off_E = off_U + C * LDV * 2;  // [D] e^{G_C}
+  static constexpr int BUF = off_E + D * 4;
+  // output stage (where it fits): O rows, double-buffered, written out by the
+  // loader group that is not staging inputs in that step
+  static constexpr int OUT = C * LDV * 2;
+  static constexpr bool STAGE_OUT = 2 * BUF + 2 * OUT <= 160 * 1024;
+  static constexpr int off_Out = 2 * BUF;
+  static constexpr int bytes = 2 * BUF + (STAGE_OUT ? 2 * OUT : 0);
+  static_assert(BUF % 16 == 0 && (LDV * 2) % 16 == 0, "16-byte aligned stages and rows");
+  static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
+};
+
+template <int D, int BV>
+__global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_rr_pc_kernel(FwdParams p) {
+  using L = RrPcFwdLayout<D, BV>;
+  using T = bf16_t;
+  constexpr int NC = BV / 16;   // compute waves
+  constexpr int NKT = D / 16;   // 16-row tiles of the state slice
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const DocSlot ds = doc_slot(p.geom, p.H, D / BV);
+  const int n = ds.n, h = ds.h, v0 = ds.z * BV;
+  const int H = p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t gs = (int64_t)H * D;
+  int first, count, dstart, dlen;
+  doc_chunks(p.geom, n, first, count, dstart, dlen);
+  const bool loader = wave >= NC;
+  constexpr int NGT = 64 * kRrLoaders / 2;   // threads of one loader group
+  const int lgroup = (tid - 64 * NC) / NGT;  // loader group: chunks jc with jc % 2 == lgroup
+  const int lt = (tid - 64 * NC) % NGT;
+
+  if (loader) {
+    RegTile<NGT, C, D, T> rQ, rW, rK;
+    RegTile<NGT, C, C, T> rA;
+    RegTile<NGT, C, BV, T> rU;
+    float re = 0.f;
+    auto load = [&](int jc) {
+      const int cstart = dstart + jc * C;
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)cstart * H + h;
+      rQ.load_as(lt, static_cast<const T*>(p.qg) + row0 * D, gs, clen);
+      rW.load_as(lt, static_cast<const T*>(p.w) + row0 * D, gs, clen);
+      rK.load_as(lt, static_cast<const T*>(p.kg) + row0 * D, gs, clen);
+      rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+      rU.load_as(lt, static_cast<const T*>(p.u) + row0 * D + v0, gs, clen);
+      if (lt < D) re = p.gcum[((int64_t)(cstart + clen - 1) * H + h) * D + lt];
+    };
+    auto stash = [&](int b) {
+      char* buf = smem + b * L::BUF;
+      rQ.store_as(lt, reinterpret_cast<T*>(buf + L::off_Q), L::LD);
+      rW.store_as(lt, reinterpret_cast<T*>(buf + L::off_W), L::LD);
+      rK.store_as(lt, reinterpret_cast<T*>(buf + L::off_KG), L::LD);
+      rA.store_as(lt, reinterpret_cast<T*>(buf + L::off_A), L::LDC);
+      rU.store_as(lt, reinterpret_cast<T*>(buf + L::off_U), L::LDV);
+      if (lt < D) reinterpret_cast<float*>(buf + L::off_E)[lt] = exp_fast(re);
+    };
+    static_assert(D <= NGT, "one loader thread per gate channel");
+    // chunk jc's O rows from the output stage to global memory
+    auto flush = [&](int jc) {
+      constexpr int SEG = BV / 8;  // 16-byte pieces of a row
+      static_assert(C * SEG % NGT == 0, "whole passes over the stage");
+      const T* so = reinterpret_cast<const T*>(smem + L::off_Out + (jc & 1) * L::OUT);
+      const int clen = min(C, dlen - jc * C);
+      const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+#pragma unroll
+      for (int it = 0; it < C * SEG / NGT; ++it) {
+        const int i = lt + it * NGT;
+        const int r = i / SEG, sg = i % SEG;
+        if (r < clen) {
+          const uint4 x = *reinterpret_cast<const uint4*>(so + r * L::LDV + 8 * sg);
+          *reinterpret_cast<uint4*>(static_cast<T*>(p.o) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg) = x;
+        }
+      }
+    };
+    if (lgroup < count) load(lgroup);
+    if (lgroup == 0 && count > 0) {
+      stash(0);
+      if (count > 2) load(2);
+    }
+    for (int jc = 0; jc < count; ++jc) {
+      __syncthreads();
+      if (((jc + 1) & 1) == lgroup) {
+        if (jc + 1 < count) {
+          stash((jc + 1) & 1);
+          if (jc + 3 < count) load(jc + 3);
+        }
+      } else if constexpr (L::STAGE_OUT) {
+        if (jc > 0) flush(jc - 1);
+      }
+    }
+    if constexpr (L::STAGE_OUT) {
+      __syncthreads();  // the last chunk's outputs
+      if ((count & 1) == lgroup && count > 0) flush(count - 1);
+    }
+    return;
+  }
+
+  const int q4 = 4 * (lane >> 4), il = lane & 15;
+  const int cl = 16 * wave + il;    // this lane's column within the slice
+  const int col0 = v0 + 16 * wave;  // first column of this wave's block
+  const int col = col0 + il;
+  f32x4 S[NKT];
+#pragma unroll
+  for (int rt = 0; rt < NKT; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      S[rt][j] = p.s0 ? p.s0[((state_row(p, n) * H + h) * D + 16 * rt + q4 + j) * D + col] : 0.f;
+
+  auto step = [&](int jc, auto full_t) {
+    constexpr bool FULL = decltype(full_t)::value;
+    const char* buf = smem + (jc & 1) * L::BUF;
+    const T* sQ = reinterpret_cast<const T*>(buf + L::off_Q);
+    const T* sW = reinterpret_cast<const T*>(buf + L::off_W);
+    const T* sK = reinterpret_cast<const T*>(buf + L::off_KG);
+    const T* sA = reinterpret_cast<const T*>(buf + L::off_A);
+    const T* sU = reinterpret_cast<const T*>(buf + L::off_U);
+    const float* sE = reinterpret_cast<const float*>(buf + L::off_E);
+    const int cid = first + jc;
+    const int clen = min(C, dlen - jc * C);
+    const int64_t row0 = (int64_t)(dstart + jc * C) * H + h;
+
+    // S as bf16 B operands; checkpoint the entering state
+    s16x8_t SB[NKT / 2];
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) SB[kk] = pack_acc_pair(S[2 * kk], S[2 * kk + 1]);
+    if (p.h) {
+      T* hb = static_cast<T*>(p.h) + ((int64_t)cid * H + h) * D * D;
+#pragma unroll
+      for (int kk = 0; kk < NKT / 2; ++kk) {
+        const uint4 w = __builtin_bit_cast(uint4, SB[kk]);
+        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+      }
+    }
+    // W S and qg S: for each k step the eight tiles are independent accumulators
+    f32x4 WS[4], QS[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) WS[rb] = QS[rb] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < NKT / 2; ++kk) {
+      s16x8_t aw[4], aq[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        aw[rb] = lds_a_perm(sW + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+        aq[rb] = lds_a_perm(sQ + 16 * rb * L::LD, L::LD, 32 * kk, lane);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        mfma_bf16(WS[rb], aw[rb], SB[kk]);
+        mfma_bf16(QS[rb], aq[rb], SB[kk]);
+      }
+    }
+    // U = u - W S
+    f32x4 U[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) U[rb][j] = bf16_to_f32(sU[(16 * rb + q4 + j) * L::LDV + cl]) - WS[rb][j];
+    T* u_out = static_cast<T*>(p.u) + row0 * D + col0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) store_acc_global<T, FULL>(u_out, gs, U[rb], 16 * rb, 0, clen, lane);
+    const s16x8_t UB[2] = {pack_acc_pair(U[0], U[1]), pack_acc_pair(U[2], U[3])};
+    // O = qg S + Aqk U   (Aqk is lower triangular: row block rb needs k steps kt <= rb / 2)
+    f32x4 AU[4];
+    {
+      s16x8_t aa[6];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) aa[rb] = lds_a_perm(sA + 16 * rb * L::LDC, L::LDC, 0, lane);
+      aa[4] = lds_a_perm(sA + 32 * L::LDC, L::LDC, 32, lane);
+      aa[5] = lds_a_perm(sA + 48 * L::LDC, L::LDC, 32, lane);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        AU[rb] = zero4();
+        mfma_bf16(AU[rb], aa[rb], UB[0]);
+      }
+      mfma_bf16(AU[2], aa[4], UB[1]);
+      mfma_bf16(AU[3], aa[5], UB[1]);
+    }
+    if constexpr (L::STAGE_OUT) {
+      T* so = reinterpret_cast<T*>(smem + L::off_Out + (jc & 1) * L::OUT) + 16 * wave;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, true>(so, L::LDV, QS[rb] + AU[rb], 16 * rb, 0, C, lane);
+    } else {
+      T* o_out = static_cast<T*>(p.o) + row0 * D + col0;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, FULL>(o_out, gs, QS[rb] + AU[rb], 16 * rb, 0, clen, lane);
+    }
+    // S <- diag(e^{G_C}) S + kg^T U
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[rt][j] *= sE[16 * rt + q4 + j];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s16x8_t ak[NKT];
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) ak[rt] = lds_kmajor_perm(sK + 16 * rt, L::LD, 32 * kt, lane);
+#pragma unroll
+      for (int rt = 0; rt < NKT; ++rt) mfma_bf16(S[rt], ak[rt], UB[kt]);
+    }
+  };
+  for (int jc = 0; jc + 1 < count; ++jc) {
+    __syncthreads();
+    step(jc, std::true_type{});
+  }
+  if (count > 0) {
+    __syncthreads();
+    if (dlen - (count - 1) * C == C) step(count - 1, std::true_type{});
+    else step(count - 1, std::false_type{});
+  }
+  if constexpr (L::STAGE_OUT) __syncthreads();  // the loaders' flush of the last chunk
+  if (p.sT) {
+    float* sb = p.sT + (state_row(p, n) * H + h) * D * D + col0;
+#pragma unroll
+    for (int rt = 0; rt < NKT; ++rt) store_acc_global<float>(sb, D, S[rt], 16 * rt, 0, D, lane);
+  }
+}
+
 template <typename K>
 int set_smem(K kernel, int bytes) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -1412,6 +1650,23 @@ int launch_state_fwd_rr(const FwdParams& p, hipStream_t s) {
   return alias ? launch_state_fwd_rr_as<D, 64, true>(p, s) : launch_state_fwd_rr_as<D, 64, false>(p, s);
 }
 
+template <int D, int BV>
+int launch_state_fwd_rr_pc_as(const FwdParams& p, hipStream_t s) {
+  auto kern = chunk_state_fwd_rr_pc_kernel<D, BV>;
+  constexpr int bytes = RrPcFwdLayout<D, BV>::bytes;
+  if (int st = set_smem(kern, bytes)) return st;
+  hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoaders)), bytes, s, p);
+  return launch_status("pkda_chunk_fwd(state)");
+}
+
+template <int D>
+int launch_state_fwd_rr_pc(const FwdParams& p, hipStream_t s) {
+  const int N = p.geom.num_seqs;
+  if (N <= 0) return 0;
+  const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
+  return narrow ? launch_state_fwd_rr_pc_as<D, 32>(p, s) : launch_state_fwd_rr_pc_as<D, 64>(p, s);
+}
+
 template <typename T, int D, int BV>
 int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
   const bool all = stages == 0;
@@ -1442,6 +1697,7 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
   if (all || (stages & PKDA_STAGE_FWD_STATE)) {
     if constexpr (std::is_same<T, bf16_t>::value) {
       if (!p.qg) return launch_state_fwd_rr<D>(p, s);  // BF16, per-head gate: the register-resident pass
+      return launch_state_fwd_rr_pc<D>(p, s);         // BF16, per-channel gate: its register-resident pass
     }
     auto kern = p.qg ? chunk_state_fwd_kernel<T, D, BV, true> : chunk_state_fwd_kernel<T, D, BV, false>;
     const int bytes = StateLayout<T, D, BV>::bytes;
