@@ -393,6 +393,19 @@ def test_chunk_per_channel_varlen(dev):
         assert val < BF16_TOL, (name, val)
 
 
+def test_chunk_per_channel_varlen_wide(dev):
+    """Per-channel gate at d = 128 in BF16 with 16 packed documents (empty,
+    one-token, partial and whole chunks) and 8 heads: 16 x 8 (document, head)
+    pairs run the register-resident state passes in their 64-column form,
+    and every chunk length goes through the two-half intra kernel."""
+    print("[gpu] chunk per-channel varlen d=128, wide state passes", flush=True)
+    lens = [1, 64, 65, 0, 130, 17, 64, 3, 128, 1, 70, 0, 33, 64, 100, 9]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    res = _grad_case_pc(dev, 1, int(cu[-1]), 8, 128, torch.bfloat16, seed=31, cu=cu)
+    for name, val in res.items():
+        assert val < BF16_TOL, (name, val)
+
+
 def _production_inputs(B, T, H, D, dtype, seed):
     """Production PKDA controls as the reference's bench draws them
     (scripts/pkda_bench.py:162-187): raw per-channel gate with
