@@ -116,9 +116,9 @@ STAGE_KERNEL = {
 # The production operator's chunk kernels (per-channel gate, BF16 keys with
 # the preconditioner's write key, d = 128), by the same stage split.
 PRODUCTION_STAGE_KERNEL = {
-    "fwd_intra": "chunk_intra_fwd_pc_kernel<bf16, 128, false>",
-    "fwd_state": "chunk_state_fwd_kernel<bf16, 128, 64, true>",
-    "bwd_state": "chunk_state_bwd_kernel<bf16, 128, 64, true>",
+    "fwd_intra": "chunk_intra_fwd_pc2_kernel<false>",
+    "fwd_state": "chunk_state_fwd_rr_pc_kernel<128, 64>",
+    "bwd_state": "chunk_state_bwd_rr_pc_kernel<128, 64>",
     "bwd_chunk": "chunk_fused_bwd_pc_kernel<bf16, 128, bf16, bf16>",
 }
 TRAFFIC_PROFILE = ROOT / "profiles" / "pkda_chunk_c2_decode_c4_hbm_traffic.md"
