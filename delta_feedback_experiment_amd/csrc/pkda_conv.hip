@@ -153,12 +153,25 @@ __device__ __forceinline__ const T* slab_ptr(const void* q, const void* k, const
   return base + row * P;
 }
 
+// The 8 W taps of this thread's channels are contiguous: one branch on the
+// dtype (uniform) around straight-line loads, so they go out together (a
+// per-element dtype test made each load wait for the one before).
 template <int W>
 __device__ __forceinline__ void load_weights(const ConvParams& p, int c0, float (&wt)[8][W]) {
+  const int64_t base = (int64_t)c0 * W;
+  if (p.w_dtype == PKDA_BF16) {
+    const bf16_t* w8 = static_cast<const bf16_t*>(p.weight) + base;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int w = 0; w < W; ++w) wt[j][w] = load_any(p.weight, (int64_t)(c0 + j) * W + w, p.w_dtype);
+      for (int w = 0; w < W; ++w) wt[j][w] = bf16_to_f32(w8[j * W + w]);
+  } else {
+    const float* w8 = static_cast<const float*>(p.weight) + base;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int w = 0; w < W; ++w) wt[j][w] = w8[j * W + w];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -177,17 +190,24 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_fwd_kernel(ConvParams p
   load_weights<W>(p, c0, wt);
   const T* xs = static_cast<const T*>(p.x) + (int64_t)b * p.T * p.C + c0;
   float hist[W > 1 ? W - 1 : 1][8];  // x at t - (W - 1) .. t - 1
+  {
+    // the halo rows load unconditionally (row 0 stands in before the row's
+    // start) and are replaced below where t < 0, so no branch holds them back
+    Raw8<T> hr[W > 1 ? W - 1 : 1];
 #pragma unroll
-  for (int w = 0; w < W - 1; ++w) {
-    const int t = t0 - (W - 1) + w;
-    if (t >= 0) {
-      Vec8<T>::load(xs + (int64_t)t * p.C, hist[w]);
-    } else if (p.hist_in) {  // the row's cached projections before its first token
-      const int64_t sb = p.slot ? p.slot[b] : b;
-      Vec8<T>::load(static_cast<const T*>(p.hist_in) + (sb * (W - 1) + (W - 1) + t) * p.C + c0, hist[w]);
-    } else {
+    for (int w = 0; w < W - 1; ++w) hr[w].load(xs + (int64_t)max(t0 - (W - 1) + w, 0) * p.C);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) hist[w][j] = 0.f;
+    for (int w = 0; w < W - 1; ++w) {
+      const int t = t0 - (W - 1) + w;
+      if (t >= 0) {
+        hr[w].unpack(hist[w]);
+      } else if (p.hist_in) {  // the row's cached projections before its first token
+        const int64_t sb = p.slot ? p.slot[b] : b;
+        Vec8<T>::load(static_cast<const T*>(p.hist_in) + (sb * (W - 1) + (W - 1) + t) * p.C + c0, hist[w]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hist[w][j] = 0.f;
+      }
     }
   }
   int off;
@@ -195,10 +215,9 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_fwd_kernel(ConvParams p
   // tokens in groups of kGroup rows, the next group's loads in flight while
   // the current one computes
   Raw8<T> xa[kGroup], xb[kGroup];
-  auto load_group = [&](int tg, Raw8<T> (&dst)[kGroup]) {
+  auto load_group = [&](int tg, Raw8<T> (&dst)[kGroup]) {  // rows past the tile clamp (never used)
 #pragma unroll
-    for (int i = 0; i < kGroup; ++i)
-      if (tg + i < t1) dst[i].load(xs + (int64_t)(tg + i) * p.C);
+    for (int i = 0; i < kGroup; ++i) dst[i].load(xs + (int64_t)min(tg + i, t1 - 1) * p.C);
   };
   load_group(t0, xa);
   for (int tg = t0; tg < t1; tg += kGroup) {
@@ -279,26 +298,30 @@ __global__ __launch_bounds__(kConvThreads) void qkv_conv_bwd_kernel(ConvParams p
       dwin[w][j] = 0.f;
       dw[j][w] = 0.f;
     }
+  {
+    // halo rows unconditionally (row 0 stands in before the row's start, then zeroed)
+    Raw8<T> hr[W > 1 ? W - 1 : 1];
 #pragma unroll
-  for (int w = 0; w < W - 1; ++w) {
-    const int t = t0 - (W - 1) + w;
-    if (t >= 0) {
-      Vec8<T>::load(xs + (int64_t)t * p.C, hist[w]);
-    } else {
+    for (int w = 0; w < W - 1; ++w) hr[w].load(xs + (int64_t)max(t0 - (W - 1) + w, 0) * p.C);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) hist[w][j] = 0.f;
+    for (int w = 0; w < W - 1; ++w) {
+      hr[w].unpack(hist[w]);
+      if (t0 - (W - 1) + w < 0)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hist[w][j] = 0.f;
     }
   }
   const int tend = t1 + W - 1;  // da of the W - 1 rows after the tile reaches its dx
   Raw8<T> xa[kGroupBwd], xb[kGroupBwd], na[kGroupBwd], nb[kGroupBwd];
   const int tlast = min(tend, p.T);
   auto load_group = [&](int tg, Raw8<T> (&dx_)[kGroupBwd], Raw8<T> (&dn_)[kGroupBwd]) {
+    // rows past the last clamp (never used): no branch holds a load back
 #pragma unroll
-    for (int i = 0; i < kGroupBwd; ++i)
-      if (tg + i < tlast) {
-        dx_[i].load(xs + (int64_t)(tg + i) * p.C);
-        dn_[i].load(dn_base + (int64_t)(tg + i) * p.P);
-      }
+    for (int i = 0; i < kGroupBwd; ++i) {
+      const int t = min(tg + i, tlast - 1);
+      dx_[i].load(xs + (int64_t)t * p.C);
+      dn_[i].load(dn_base + (int64_t)t * p.P);
+    }
   };
   load_group(t0, xa, na);
   for (int tg = t0; tg < tend; tg += kGroupBwd) {
