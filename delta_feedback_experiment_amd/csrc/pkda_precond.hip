@@ -197,14 +197,20 @@ __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j,
   auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
 #pragma unroll 1
   for (int g0 = 0; g0 < C; g0 += G) {
-    float kc[G][CH];
+    // the group's k rows and its per-token gate values go out together
+    float kc[G][CH], lg[G], bg[G];
 #pragma unroll
-    for (int u = 0; u < G; ++u) IO::load(k + tok(g0 + u) * D + c0, kc[u]);
+    for (int u = 0; u < G; ++u) {
+      const int64_t th = tok(g0 + u);
+      IO::load(k + th * D + c0, kc[u]);
+      lg[u] = g_atk[th];
+      bg[u] = beta_atk[th];
+    }
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       const int t = g0 + u;
       const int64_t th = tok(t);
-      const float eg = exp_fast(g_atk[th]), bt = beta_atk[th];
+      const float eg = exp_fast(lg[u]), bt = bg[u];
       float w[CH];
 #pragma unroll
       for (int q = 0; q < CH; ++q) {
@@ -298,9 +304,8 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
   auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
   // one token of the forward's A recurrence, channel by channel (the same
   // arithmetic as the forward pass, so the same values)
-  auto step = [&](int t, float* a, const float* kc) {
-    const int64_t th = tok(t);
-    const float eg = exp_fast(g_atk[th]), bt = beta_atk[th];
+  auto step = [&](int t, float* a, const float* kc, float lgv, float bt) {
+    const float eg = exp_fast(lgv);
 #pragma unroll
     for (int q = 0; q < CH; ++q) {
       const float an = eg * a[q] + bt * (kc[q] * kc[q]);
@@ -320,15 +325,20 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       for (int r = 0; r < NB; ++r)
 #pragma unroll
         for (int q = 0; q < CH; ++q) a_blk[r][q] = r == b ? a[q] : a_blk[r][q];
-      float kb[G][CH];
+      float kb[G][CH], lg[G], bg[G];  // k rows and gate values of the sub-block, loaded together
 #pragma unroll
       for (int u = 0; u < G; ++u) {
-        IO::load(k + tok(b * G + u) * D + c0, kb[u]);
-#pragma unroll
-        for (int q = 0; q < CH; ++q) kb[u][q] = active ? kb[u][q] : 0.f;
+        const int64_t th = tok(b * G + u);
+        IO::load(k + th * D + c0, kb[u]);
+        lg[u] = g_atk[th];
+        bg[u] = beta_atk[th];
       }
 #pragma unroll
-      for (int u = 0; u < G; ++u) step(b * G + u, a, kb[u]);
+      for (int u = 0; u < G; ++u) {
+#pragma unroll
+        for (int q = 0; q < CH; ++q) kb[u][q] = active ? kb[u][q] : 0.f;
+        step(b * G + u, a, kb[u], lg[u], bg[u]);
+      }
     }
   }
   float dcen = 0.f;
@@ -345,12 +355,15 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
 #pragma unroll
       for (int r = 1; r < NB; ++r) a_b[q] = r == b ? a_blk[r][q] : a_b[q];
     }
-    float rk[G][CH], ra[G][CH], rdkw[G][CH], rdk[G][CH];
+    float rk[G][CH], ra[G][CH], rdkw[G][CH], rdk[G][CH], lg[G], bg[G];
 #pragma unroll
     for (int u = 0; u < G; ++u) {
-      IO::load(k + tok(g0 + u) * D + c0, rk[u]);
-      GIO::load(dkw_p + tok(g0 + u) * D + c0, rdkw[u]);
-      if (APPLY) GIO::load(dk_p + tok(g0 + u) * D + c0, rdk[u]);
+      const int64_t th = tok(g0 + u);
+      IO::load(k + th * D + c0, rk[u]);
+      GIO::load(dkw_p + th * D + c0, rdkw[u]);
+      if (APPLY) GIO::load(dk_p + th * D + c0, rdk[u]);
+      lg[u] = g_atk[th];
+      bg[u] = beta_atk[th];
     }
     {
       float a[CH];
@@ -360,7 +373,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       for (int u = 0; u < G; ++u) {
 #pragma unroll
         for (int q = 0; q < CH; ++q) rk[u][q] = active ? rk[u][q] : 0.f;
-        step(g0 + u, a, rk[u]);
+        step(g0 + u, a, rk[u], lg[u], bg[u]);
 #pragma unroll
         for (int q = 0; q < CH; ++q) ra[u][q] = a[q];
       }
@@ -370,7 +383,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       const int t = g0 + u;
       const bool in = FULL || t < len;
       const int64_t th = tok(t);
-      const float eg = exp_fast(g_atk[th]);
+      const float eg = exp_fast(lg[u]);
       float vg = 0.f, vb = 0.f, dkt[CH];
 #pragma unroll
       for (int q = 0; q < CH; ++q) {
@@ -384,7 +397,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
         const float lam_t = lam[q] + div_fast(dr, at + eps);
         if (APPLY) {
           dcen -= dr;
-          dkt[q] = rdk[u][q] + (dkw * f + 2.f * beta_atk[th] * kc * lam_t);
+          dkt[q] = rdk[u][q] + (dkw * f + 2.f * bg[u] * kc * lam_t);
           const float a_prev = u > 0 ? ra[u - 1][q] : a_b[q];
           vg += lam_t * eg * a_prev;
           vb += lam_t * kc * kc;
