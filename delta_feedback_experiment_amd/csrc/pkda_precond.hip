@@ -127,8 +127,16 @@ __device__ __forceinline__ void chunk_decays(const PrecondParams& p, int h, int 
   if (i < nb) {
     const int t0 = dstart + (j0 + i) * C;
     const int len = min(C, dlen - (j0 + i) * C);
+    // 16 tokens' loads go out together (clamped rows, masked in the sum); the
+    // sum still runs token by token in order
     float g = 0.f;
-    for (int t = 0; t < len; ++t) g += p.g_atk[(int64_t)(t0 + t) * p.H + h];
+    for (int tb = 0; tb < len; tb += 16) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = p.g_atk[(int64_t)(t0 + min(tb + u, len - 1)) * p.H + h];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) g += tb + u < len ? v[u] : 0.f;
+    }
     s[i] = exp_fast(g);
   }
 }
