@@ -89,19 +89,34 @@ class ChunkPlan:
         )
 
 
+def wants_gcum_lo(kind: int, dtype: torch.dtype) -> bool:
+    """Whether the chunk kernels take the gate's FP64 remainder: FP32
+    activations with a per-channel gate.  There the decay between two tokens
+    of a chunk is the difference of two cumsums that reach a few hundred
+    under strong gates; from FP32 cumsums alone that difference carries their
+    rounding (~1e-5 relative to it), which the gate gradient's sums over a
+    head amplify past the FP32 tolerance."""
+    return kind != _lib.GATE_LOG_HEAD and dtype == torch.float32
+
+
 def gate_forward(plan: ChunkPlan, g: Tensor, kind: int, A_log: Tensor | None, dt_bias: Tensor | None,
-                 up_weight: Tensor | None = None) -> Tensor:
+                 up_weight: Tensor | None = None, gcum_lo: Tensor | None = None) -> Tensor:
     """Chunk-local cumulative natural-log decay, FP32, ``[N_tok, H]`` or ``[N_tok, H, K]``.
 
     The low-rank form takes ``g`` as the decay hidden rows ``[N_tok, R]``
-    (unit column stride, any row stride) and ``up_weight [H*K, R]``."""
+    (unit column stride, any row stride) and ``up_weight [H*K, R]``.  With
+    ``gcum_lo`` (per-channel forms, FP32 of gcum's shape) the cumsum is formed
+    in FP64 and ``gcum_lo`` receives its remainder past the FP32 result."""
     shape = (plan.num_tokens, plan.heads) if kind == _lib.GATE_LOG_HEAD else (plan.num_tokens, plan.heads, plan.head_dim)
     gcum = torch.empty(shape, device=g.device, dtype=torch.float32)
+    if gcum_lo is not None and (tuple(gcum_lo.shape) != shape or gcum_lo.dtype != torch.float32
+                                or not gcum_lo.is_contiguous()):
+        raise ValueError(f"gcum_lo must be a contiguous float32 tensor of shape {shape}")
     args = _lib.GateArgs(
         num_seqs=plan.num_seqs, seqlen=plan.seqlen, heads=plan.heads, head_dim=plan.head_dim,
         gate_kind=kind, g_dtype=_dtype_code(g), cu_seqlens=_ptr(plan.cu_seqlens), g=_ptr(g),
         A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), gcum=_ptr(gcum),
-        num_chunks=plan.num_chunks, table=_ptr(plan.table),
+        num_chunks=plan.num_chunks, table=_ptr(plan.table), gcum_lo=_ptr(gcum_lo),
     )
     if kind == _lib.GATE_LOW_RANK:
         args.up_weight, args.rank, args.g_stride = _ptr(up_weight), g.shape[-1], g.stride(0)
@@ -137,12 +152,14 @@ def chunk_forward(
     plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor,
     scale: float, initial_state: Tensor | None, output_final_state: bool, save_states: bool,
     *, slot_idx: Tensor | None = None, final_state: Tensor | None = None, out: Tensor | None = None,
+    gcum_lo: Tensor | None = None,
 ) -> tuple[Tensor, Tensor | None, FwdSaved]:
     """Run the chunk forward on flat ``[N_tok, H, D]`` operands.
 
     With ``slot_idx`` (int32 ``[N]``) the states are rows of a pool:
     ``initial_state`` (or zero when ``None``) and ``final_state`` are
-    ``[P, H, D, D]`` and document ``n`` uses row ``slot_idx[n]`` of each."""
+    ``[P, H, D, D]`` and document ``n`` uses row ``slot_idx[n]`` of each.
+    ``gcum_lo``: the gate's FP64 remainder (:func:`wants_gcum_lo`)."""
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
     o = torch.empty_like(v) if out is None else out
@@ -165,7 +182,7 @@ def chunk_forward(
         gate_per_channel=int(per_channel), beta=_ptr(beta32), scale=float(scale),
         initial_state=_ptr(initial_state), final_state=_ptr(S_T), o=_ptr(o),
         w=_ptr(w), u=_ptr(u), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), qg=_ptr(qg), kg=_ptr(kg),
-        slot_idx=_ptr(slot_idx), pool_size=0 if S_T is None else S_T.shape[0],
+        slot_idx=_ptr(slot_idx), pool_size=0 if S_T is None else S_T.shape[0], gcum_lo=_ptr(gcum_lo),
     )
     _lib.call("pkda_chunk_fwd", args, _stream(dev))
     return o, S_T, FwdSaved(w, u, aqk, akk, h, qg, kg)
@@ -186,7 +203,7 @@ def chunk_backward(
     plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor, scale: float,
     initial_state: Tensor | None, saved: FwdSaved, do: Tensor, dht: Tensor | None, want_dh0: bool,
     grad_dtype: torch.dtype = torch.float32, key_grad_dtype: torch.dtype | None = None,
-    kw32: Tensor | None = None,
+    kw32: Tensor | None = None, gcum_lo: Tensor | None = None,
 ) -> BwdGrads:
     """Chunk backward on flat operands.  ``dq, dv`` come in ``grad_dtype``
     (FP32, or ``q.dtype``: the FP32 value rounded once in the kernel), ``dk,
@@ -194,7 +211,8 @@ def chunk_backward(
     ``q.dtype`` ``grad_dtype`` for a caller that adds the preconditioner's
     terms into them); the other gradients are FP32.  ``kw32``: the write keys
     in FP32 (per-channel gates with a BF16 write key), which the in-block
-    pair sums of the gate gradient then read."""
+    pair sums of the gate gradient then read.  ``gcum_lo``: the gate's FP64
+    remainder, as the forward took it."""
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
     ntok = plan.num_tokens
@@ -228,7 +246,7 @@ def chunk_backward(
         dh0=_ptr(dh0), qg=_ptr(saved.qg), kg=_ptr(saved.kg),
         grad_dtype=_lib.PKDA_F32 if grad_dtype == torch.float32 else _dtype_code(q),
         key_grad_dtype=_lib.PKDA_F32 if key_grad_dtype == torch.float32 else _dtype_code(q),
-        kw32=_ptr(kw32),
+        kw32=_ptr(kw32), gcum_lo=_ptr(gcum_lo),
     )
     if kw32 is not None and (kw32.dtype != torch.float32 or kw32.shape != kw.shape or not kw32.is_contiguous()):
         raise ValueError("kw32 must be a contiguous float32 tensor of kw's shape")
@@ -312,7 +330,11 @@ class _ChunkPKDA(torch.autograd.Function):
         qf, kf, vf = (_flat(t.contiguous(), plan) for t in (q, k, v))
         beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
         s0 = _f32(initial_state)
-        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32, decay_up)
+        gcum_lo = None
+        if wants_gcum_lo(kind, q.dtype):
+            shp = (plan.num_tokens, plan.heads, plan.head_dim)
+            gcum_lo = torch.empty(shp, device=q.device, dtype=torch.float32)
+        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32, decay_up, gcum_lo=gcum_lo)
         precond = g_atk is not None
         needs_grad = any(ctx.needs_input_grad)
         if precond:
@@ -322,7 +344,7 @@ class _ChunkPKDA(torch.autograd.Function):
         else:
             pstate, kwf, A_T = None, kf, None
         o, S_T, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, scale, s0,
-                                      output_final_state, save_states=needs_grad and not lean)
+                                      output_final_state, save_states=needs_grad and not lean, gcum_lo=gcum_lo)
         if needs_grad:
             ctx.plan, ctx.kind, ctx.scale, ctx.lean, ctx.x, ctx.eps = plan, kind, scale, lean, x, eps
             ctx.per_head_raw = use_gate and decay_up is None and g.dim() == q.dim() - 1
@@ -343,7 +365,7 @@ class _ChunkPKDA(torch.autograd.Function):
                                   decay_up,
                                   None if pstate is None else pstate.a_chunk,
                                   None if pstate is None else pstate.kw32,
-                                  *fwd)
+                                  gcum_lo, *fwd)
         o = o.reshape(v.shape)
         return o, S_T, A_T
 
@@ -352,10 +374,11 @@ class _ChunkPKDA(torch.autograd.Function):
         from . import precond as pre
 
         (qf, kf, kwf, vf, gcum, beta32, s0, g_used, A_log32, dt32,
-         g_atk32, beta_atk32, center32, decay_up, a_chunk, kw32, *fwd) = ctx.saved_tensors
+         g_atk32, beta_atk32, center32, decay_up, a_chunk, kw32, gcum_lo, *fwd) = ctx.saved_tensors
         plan = ctx.plan
         if ctx.lean:  # rebuild the chunk quantities
-            _, _, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, False, True)
+            _, _, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, False, True,
+                                        gcum_lo=gcum_lo)
         else:
             saved = FwdSaved(*fwd)
         pstate = pre.PrecondState(kwf, a_chunk, None, None, kw32) if ctx.precond else None
@@ -370,7 +393,7 @@ class _ChunkPKDA(torch.autograd.Function):
         key_direct = direct and ctx.dtypes[1] == qf.dtype
         gr = chunk_backward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, saved, dof, dht, want_dh0,
                             grad_dtype=qf.dtype if direct else torch.float32,
-                            key_grad_dtype=qf.dtype if key_direct else torch.float32, kw32=kw32)
+                            key_grad_dtype=qf.dtype if key_direct else torch.float32, kw32=kw32, gcum_lo=gcum_lo)
         dk = gr.dk
         dg_atk = dbeta_atk = dcenter = dA0 = None
         if pstate is not None:

@@ -70,6 +70,7 @@ struct BwdParams {
   const void* qg;  // per-channel gates: s e^G q
   const void* kg;  // per-channel gates: e^{G_last - G} kw
   const float* kw32;  // per-channel gates: kw in FP32 (BF16 kw otherwise), or null
+  const float* gcum_lo;  // FP32 per-channel gates, optional: gcum's FP64 remainder
 };
 
 // Deterministic sum of one value per thread over an NT-thread workgroup.
@@ -1100,6 +1101,10 @@ struct FusedBwdPcLayout {
   static constexpr int off_P1T = off_U + G_BYTES;
   static constexpr int off_P2T = off_P1T + 4 * 256 * (int)sizeof(T);
   static_assert(G_BYTES + 8 * 256 * (int)sizeof(T) <= off_dO, "G and the transposed blocks fit the U..T region");
+  // FP32: the gate's FP64 remainder beside G (pair decays from hi and lo)
+  static constexpr bool GLO = sizeof(T) == 4;
+  static constexpr int off_Glo = off_P2T + 4 * 256 * (int)sizeof(T);
+  static_assert(!GLO || off_Glo + G_BYTES <= off_dO, "G's remainder fits the U..T region");
   static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
   static_assert(D * (D / Vec16<T>::N) * 4 <= CT, "row partials of sum(h * dH) fit the T region");
 };
@@ -1144,6 +1149,12 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   float* sHD = reinterpret_cast<float*>(smem + L::off_hd);
   float* sKG = reinterpret_cast<float*>(smem + L::off_kg);
   float* sRed = reinterpret_cast<float*>(smem + L::off_red);
+  float* sGlo = reinterpret_cast<float*>(smem + L::off_Glo);  // FP32, phase 3
+  // G's remainder at (row, column) of the phase 3 tile (0 unless FP32)
+  auto glo = [&](int r, int c) -> float {
+    if constexpr (L::GLO) return sGlo[r * L::LDG + c];
+    else return 0.f;
+  };
 
   const T* hsrc = static_cast<const T*>(p.h) + ((int64_t)cid * H + hh) * D * D;
   const T* dhsrc = static_cast<const T*>(p.dh) + ((int64_t)cid * H + hh) * D * D;
@@ -1151,6 +1162,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   const T* kwg = static_cast<const T*>(p.kw) + row0 * D;
   const float* kw32g = p.kw32 ? p.kw32 + row0 * D : nullptr;
   const float* gg = p.gcum + row0 * D;        // G rows, stride gs
+  const float* ggl = p.gcum_lo ? p.gcum_lo + row0 * D : nullptr;  // FP32: G's remainder
   const float* gC = gg + (int64_t)(len - 1) * gs;
   const float scale = p.scale;
 
@@ -1162,6 +1174,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   // they are needed.)
   const int rq = 4 * (lane >> 4);
   float Gl[HCT][4], gCl[HCT];
+  float Gll[HCT][4], gCll[HCT];  // FP32: the remainders (zero without gcum_lo)
   RegTile<kFW, C, D, T> rK;
   // beta first: its LDS store below then waits for this load only
   const float bval = p.beta[(int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + hh];
@@ -1201,7 +1214,10 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     const int c = 16 * ct + acc_col(lane);
     f32x4 acc = zero4();
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Gl[j][e] = gg[(int64_t)min(r0 + rq + e, len - 1) * gs + c];
+    for (int e = 0; e < 4; ++e) {
+      Gl[j][e] = gg[(int64_t)min(r0 + rq + e, len - 1) * gs + c];
+      if constexpr (L::GLO) Gll[j][e] = ggl ? ggl[(int64_t)min(r0 + rq + e, len - 1) * gs + c] : 0.f;
+    }
     mma_tile<E, ROW, COL>(acc, sdO, L::LD, r0, sH, L::LD, 16 * ct, D, lane);
 #pragma unroll
     for (int e = 0; e < 4; ++e) dq[j][e] = scale * exp_fast(Gl[j][e]) * acc[e];
@@ -1238,7 +1254,10 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   // cover the [64 x D] tiles once, so phase 3 takes its LDS copies of G and
   // the write key from them rather than from global memory again.
 #pragma unroll
-  for (int j = 0; j < HCT; ++j) gCl[j] = gC[16 * (ch * HCT + j) + (lane & 15)];
+  for (int j = 0; j < HCT; ++j) {
+    gCl[j] = gC[16 * (ch * HCT + j) + (lane & 15)];
+    if constexpr (L::GLO) gCll[j] = ggl ? ggl[(int64_t)(len - 1) * gs + 16 * (ch * HCT + j) + (lane & 15)] : 0.f;
+  }
   TiledTile<kFW, D, T> rdH;
   rdH.load(dhsrc);
   // (rows clamped into the chunk and every load unconditional, so the
@@ -1334,7 +1353,9 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     float col = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      dkws[j][e] = exp_fast(gCl[j] - Gl[j][e]) * acc[e];
+      float gdc = gCl[j] - Gl[j][e];
+      if constexpr (L::GLO) gdc += gCll[j] - Gll[j][e];
+      dkws[j][e] = exp_fast(gdc) * acc[e];
       // the last row's term (decay e^0) cancels against its own -kw dkw: left out
       col += (r0 + rq + e < len - 1 ? Wl[j][e] : 0.f) * dkws[j][e];
     }
@@ -1355,6 +1376,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sG[(r0 + rq + e) * L::LDG + c] = Gl[j][e];
+      if constexpr (L::GLO) sGlo[(r0 + rq + e) * L::LDG + c] = Gll[j][e];
       sKWf[(r0 + rq + e) * L::LDW + c] = r0 + rq + e < len ? Wl[j][e] : 0.f;
     }
   }
@@ -1391,8 +1413,13 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     const int ct = ch * HCT + j;
     const int c = 16 * ct + acc_col(lane);
     const int nn = 16 * ct + (lane & 15);  // this lane's B column (== c)
-    float gr[4], kv[4], qv[4], wv[4];
+    float gr[4], grl[4], kv[4], qv[4], wv[4];
     f32x4 dg, dkwj;
+    // the decay between two rows: G[a] - G[b] from hi and (FP32) the remainders
+    auto gdv = [&](float a, float al, float b, float bl) -> float {
+      if constexpr (L::GLO) return (a - b) + (al - bl);
+      else return a - b;
+    };
     {
       float kgc = 0.f;
 #pragma unroll
@@ -1401,6 +1428,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       for (int e = 0; e < 4; ++e) {
         const int r = r0 + rq + e;
         gr[e] = sG[r * L::LDG + c];
+        grl[e] = glo(r, c);
         kv[e] = from_e<E>(sK[r * L::LD + c]);
         qv[e] = from_e<E>(sQ[r * L::LD + c]);
         wv[e] = sKWf[r * L::LDW + c];
@@ -1432,7 +1460,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
         else lds4(sP2T + (16 * rb + rq + u) * 16 + rq, p2);
 #pragma unroll
         for (int e = u + 1; e < 4; ++e) {
-          const float w = wv[u] * exp_fast(gr[e] - gr[u]);
+          const float w = wv[u] * exp_fast(gdv(gr[e], grl[e], gr[u], grl[u]));
           ak[e] += p1[e] * w;
           aq[e] += p2[e] * w;
         }
@@ -1455,14 +1483,17 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       // rows zero), so the lanes of group g receive exactly their rows' sums.
       {
         const int mrow = lane & 15, kq = lane >> 4, ag = mrow >> 2;
-        float g0[4];
+        float g0[4], g0l[4];
 #pragma unroll
-        for (int g = 1; g < 4; ++g) g0[g] = sG[(r0 + 4 * g) * L::LDG + nn];
+        for (int g = 1; g < 4; ++g) {
+          g0[g] = sG[(r0 + 4 * g) * L::LDG + nn];
+          g0l[g] = glo(r0 + 4 * g, nn);
+        }
         f32x4 mk = zero4(), mq = zero4();
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
           const int x = r0 + 4 * j + kq;  // this lane's B row
-          const float gx = sG[x * L::LDG + nn];
+          const float gx = sG[x * L::LDG + nn], gxl = glo(x, nn);
           const float kwx = sKWf[x * L::LDW + nn];
           const float a1 = from_e<E>(sP1r[(r0 + mrow) * L::LDC + x]);
           float a2;
@@ -1470,7 +1501,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           else a2 = from_e<E>(sP2[(r0 + mrow) * L::LDC + x]);
 #pragma unroll
           for (int g = j + 1; g < 4; ++g) {
-            const float bx = kwx * exp_fast(g0[g] - gx);
+            const float bx = kwx * exp_fast(gdv(g0[g], g0l[g], gx, gxl));
             Mma<float>::mfma(mk, ag == g ? a1 : 0.f, bx);
             Mma<float>::mfma(mq, ag == g ? a2 : 0.f, bx);
           }
@@ -1483,7 +1514,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float R = e == 0 ? 1.f : exp_fast(gr[e] - gr[0]);
+        const float R = e == 0 ? 1.f : exp_fast(gdv(gr[e], grl[e], gr[0], grl[0]));
         ak[e] += R * ak0[e];
         aq[e] += R * aq0[e];
         const float bk = sBeta[r0 + rq + e] * ak[e];
@@ -1496,7 +1527,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     // (2) rows t of this block, x in earlier blocks: split at rlo
     if (rb > 0) {
       f32x4 akX = zero4(), aqX = zero4();
-      const float grlo = sG[rlo * L::LDG + nn];
+      const float grlo = sG[rlo * L::LDG + nn], grlo_l = glo(rlo, nn);
       if constexpr (sizeof(E) == 2) {
         // 16-deep steps cover exactly the earlier blocks: A = rows of dAkk and
         // s dAqk (four consecutive x, one 8-byte read each), B = kw e^{G[R]-G[x]}
@@ -1522,16 +1553,17 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           const int x = kk + jj;
           a1[jj] = from_e<E>(sP1r[(r0 + (lane & 15)) * L::LDC + x]);
           a2[jj] = from_e<E>(sP2[(r0 + (lane & 15)) * L::LDC + x]);
-          bx[jj] = x <= rlo ? sKWf[x * L::LDW + nn] * exp_fast(grlo - sG[x * L::LDG + nn]) : 0.f;
+          bx[jj] = x <= rlo ? sKWf[x * L::LDW + nn] * exp_fast(gdv(grlo, grlo_l, sG[x * L::LDG + nn], glo(x, nn)))
+                            : 0.f;
         }
         F::mfma(akX, a1, bx);
         F::mfma(aqX, a2, bx);
       }
-      const float grlo_c = sG[rlo * L::LDG + c];
+      const float grlo_c = sG[rlo * L::LDG + c], grlo_cl = glo(rlo, c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float sb = sBeta[r0 + rq + e];
-        const float dlo = exp_fast(gr[e] - grlo_c);  // e^{G[t]-G[R]}
+        const float dlo = exp_fast(gdv(gr[e], grl[e], grlo_c, grlo_cl));  // e^{G[t]-G[R]}
         dk[0][e] += sb * dlo * akX[e];
         db[e] += kv[e] * dlo * akX[e];
         dq[0][e] += dlo * aqX[e];
@@ -1554,7 +1586,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
         else lds4(sP2 + t * L::LDC + r0 + rq, p2);
         const float kx = sBeta[t] * kv[u], qx = qv[u];
 #pragma unroll
-        for (int e = 0; e < u; ++e) aw[e] += (p1[e] * kx + p2[e] * qx) * exp_fast(gr[u] - gr[e]);
+        for (int e = 0; e < u; ++e) aw[e] += (p1[e] * kx + p2[e] * qx) * exp_fast(gdv(gr[u], grl[u], gr[e], grl[e]));
       }
       // t in the block's later 4-row groups (t > t_3): FP32 MFMA steps, one per
       // (key group g, row group i > g), the decay split at t_3 of group g:
@@ -1563,14 +1595,17 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       float aw0[4] = {0.f, 0.f, 0.f, 0.f};
       {
         const int mrow = lane & 15, kq = lane >> 4, ag = mrow >> 2;
-        float g3[3];
+        float g3[3], g3l[3];
 #pragma unroll
-        for (int g = 0; g < 3; ++g) g3[g] = sG[(r0 + 4 * g + 3) * L::LDG + nn];
+        for (int g = 0; g < 3; ++g) {
+          g3[g] = sG[(r0 + 4 * g + 3) * L::LDG + nn];
+          g3l[g] = glo(r0 + 4 * g + 3, nn);
+        }
         f32x4 mw = zero4();
 #pragma unroll
         for (int i = 1; i < 4; ++i) {
           const int t = r0 + 4 * i + kq;  // this lane's B row
-          const float gt = sG[t * L::LDG + nn];
+          const float gt = sG[t * L::LDG + nn], gtl = glo(t, nn);
           const float kt = sBeta[t] * from_e<E>(sK[t * L::LD + nn]);
           const float qt = from_e<E>(sQ[t * L::LD + nn]);
           const float a1 = from_e<E>(sP1r[t * L::LDC + r0 + mrow]);
@@ -1579,7 +1614,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           else a2 = from_e<E>(sP2[t * L::LDC + r0 + mrow]);
 #pragma unroll
           for (int g = 0; g < i; ++g) {
-            const float f = exp_fast(gt - g3[g]);
+            const float f = exp_fast(gdv(gt, gtl, g3[g], g3l[g]));
             Mma<float>::mfma(mw, ag == g ? a1 : 0.f, kt * f);
             Mma<float>::mfma(mw, ag == g ? a2 : 0.f, qt * f);
           }
@@ -1589,7 +1624,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        aw[e] += (e == 3 ? 1.f : exp_fast(gr[3] - gr[e])) * aw0[e];
+        aw[e] += (e == 3 ? 1.f : exp_fast(gdv(gr[3], grl[3], gr[e], grl[e]))) * aw0[e];
         dkwj[e] += aw[e];
         dg[e] -= wv[e] * aw[e];
       }
@@ -1597,7 +1632,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     // (4) rows x of this block, t in each later block bi: split at 16 bi - 1
     for (int bi = rb + 1; bi < 4; ++bi) {
       const int R = 16 * bi - 1;
-      const float gR = sG[R * L::LDG + nn];
+      const float gR = sG[R * L::LDG + nn], gRl = glo(R, nn);
       f32x4 aw = zero4();
       if constexpr (sizeof(E) == 2) {
         // one 16-deep step over block bi: A = dAkk and s dAqk columns x (their
@@ -1625,17 +1660,17 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           const int t = kk + jj;
           a1[jj] = from_e<E>(sP1r[t * L::LDC + r0 + (lane & 15)]);
           a2[jj] = from_e<E>(sP2[t * L::LDC + r0 + (lane & 15)]);
-          const float f = t > R && t <= R + 16 ? exp_fast(sG[t * L::LDG + nn] - gR) : 0.f;
+          const float f = t > R && t <= R + 16 ? exp_fast(gdv(sG[t * L::LDG + nn], glo(t, nn), gR, gRl)) : 0.f;
           b1[jj] = sBeta[t] * from_e<E>(sK[t * L::LD + nn]) * f;  // beta_t on the key, dAkk unscaled
           b2[jj] = from_e<E>(sQ[t * L::LD + nn]) * f;
         }
         F::mfma(aw, a1, b1);
         F::mfma(aw, a2, b2);
       }
-      const float gRc = sG[R * L::LDG + c];
+      const float gRc = sG[R * L::LDG + c], gRcl = glo(R, c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float dec = exp_fast(gRc - gr[e]);  // e^{G[R]-G[x]}
+        const float dec = exp_fast(gdv(gRc, gRcl, gr[e], grl[e]));  // e^{G[R]-G[x]}
         dkwj[e] += dec * aw[e];
         dg[e] -= rnd(wv[e] * dec) * aw[e];  // the row side's B operand kw e^{G[R]-G[x]}
       }
@@ -2315,6 +2350,7 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   p.H = a->heads;
   p.q = a->q; p.k = a->k; p.kw = kw_is_k ? a->k : a->kw; p.v = a->v;
   p.gcum = a->gcum; p.beta = a->beta; p.scale = a->scale;
+  p.gcum_lo = a->gate_per_channel && a->dtype == PKDA_F32 ? a->gcum_lo : nullptr;
   p.w = a->w; p.u = a->u; p.aqk = a->aqk; p.akk = a->akk; p.h = a->h;
   p.dO = a->do_; p.dht = a->dht; p.dh = a->dh; p.du = a->du;
   p.dq = a->dq; p.dk = a->dk; p.dkw = a->dkw; p.dv = a->dv; p.dbeta = a->dbeta; p.dgcum = a->dgcum; p.dh0 = a->dh0;

@@ -51,6 +51,7 @@ struct FwdParams {
   void* qg;   // per-channel gates: s e^G q
   void* kg;   // per-channel gates: e^{G_last - G} kw
   const int32_t* slot;  // document -> state row (slot-indexed pools), or null
+  const float* gcum_lo;  // FP32 per-channel gates, optional: gcum's FP64 remainder
 };
 
 // Row of the initial/final state of document n.
@@ -365,7 +366,10 @@ struct IntraPcLayout {
   static constexpr int off_Te = off_A + C * LDF * 4;
   static constexpr int off_Aqk = off_Te + C * LDC * (int)sizeof(T);
   static constexpr int off_beta = off_Aqk + C * LDC * (int)sizeof(T);
-  static constexpr int bytes = off_beta + C * 4;
+  // FP32: the gate's FP64 remainder, [64][LDG] (pair decays from hi and lo)
+  static constexpr bool GLO = sizeof(T) == 4;
+  static constexpr int off_Glo = off_beta + C * 4;
+  static constexpr int bytes = off_Glo + (GLO ? C * LDG * 4 : 0);
 };
 
 // One chunk's input tiles in registers.  `len` is a literal C for whole
@@ -374,7 +378,7 @@ struct IntraPcLayout {
 template <typename T, int D, bool ALIAS>
 struct IntraPcTiles {
   RegTile<kIW, C, D, T> K, Q, KW, V;
-  RegTile<kIW, C, D, float> G;
+  RegTile<kIW, C, D, float> G, Glo;  // Glo: FP32 only, zero without gcum_lo
   float beta;  // of row threadIdx.x % C (clamped into the chunk)
   __device__ __forceinline__ void load(const FwdParams& p, const ChunkInfo& ci, int h, const int len) {
     const int64_t row0 = (int64_t)ci.start * p.H + h;
@@ -387,6 +391,10 @@ struct IntraPcTiles {
     // G rows past the end repeat the last row (G is non-increasing in t, so
     // every split factor stays <= 1 there too)
     G.load_clamped(p.gcum + row0 * D, gs, len);
+    if constexpr (sizeof(T) == 4) {
+      if (p.gcum_lo) Glo.load_clamped(p.gcum_lo + row0 * D, gs, len);
+      else Glo.load(p.gcum + row0 * D, gs, 0);  // zeros
+    }
     V.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
   }
 };
@@ -420,6 +428,15 @@ __device__ __forceinline__ void intra_pc_chunk(const FwdParams& p, const ChunkIn
   tiles.Q.store(sQ, L::LD);
   if (!ALIAS) tiles.KW.store(sKW, L::LD);
   tiles.G.store(sG, L::LDG);
+  float* sGlo = reinterpret_cast<float*>(smem + L::off_Glo);
+  if constexpr (L::GLO) tiles.Glo.store(sGlo, L::LDG);
+  // G[a] - G[b] at column c; FP32 adds the remainders' difference, so a
+  // difference of two large cumsums carries only its own rounding
+  auto gd = [&](int a, int b, int c) {
+    float d = sG[a * L::LDG + c] - sG[b * L::LDG + c];
+    if constexpr (L::GLO) d += sGlo[a * L::LDG + c] - sGlo[b * L::LDG + c];
+    return d;
+  };
   const RegTile<kIW, C, D, T>& rV = tiles.V;
   for (int i = tid; i < C * C; i += kIW) {
     const int r = i / C, c = i - r * C;
@@ -454,7 +471,7 @@ __device__ __forceinline__ void intra_pc_chunk(const FwdParams& p, const ChunkIn
       lds_vec<V>(sKW + s * L::LD + c, wx);
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float e = exp_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
+        const float e = exp_fast(gd(t, s, c + j));
         akk += kx[j] * wx[j] * e;
         aqk += qx[j] * wx[j] * e;
       }
@@ -493,9 +510,8 @@ __device__ __forceinline__ void intra_pc_chunk(const FwdParams& p, const ChunkIn
       float ak[F::N], aq[F::N], bw[F::N];
 #pragma unroll
       for (int j = 0; j < F::N; ++j) {
-        const float gr = sG[r * L::LDG + kk + j];
-        const float fa = exp_fast(sG[t * L::LDG + kk + j] - gr);
-        const float fb = exp_fast(gr - sG[s * L::LDG + kk + j]);
+        const float fa = exp_fast(gd(t, r, kk + j));
+        const float fb = exp_fast(gd(r, s, kk + j));
         ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
         aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
         bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
@@ -521,9 +537,8 @@ __device__ __forceinline__ void intra_pc_chunk(const FwdParams& p, const ChunkIn
       lds_vec<V>(sKW + r * L::LD + c, wx);
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float gv = sG[r * L::LDG + c + j];
-        qx[j] *= p.scale * exp_fast(gv);
-        wx[j] *= exp_fast(sG[(C - 1) * L::LDG + c + j] - gv);
+        qx[j] *= p.scale * exp_fast(sG[r * L::LDG + c + j]);
+        wx[j] *= exp_fast(gd(C - 1, r, c + j));
       }
       store_vec<V>(qg_out + r * gs + c, qx);
       store_vec<V>(kg_out + r * gs + c, wx);
@@ -1751,6 +1766,7 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   p.H = a->heads;
   p.q = a->q; p.k = a->k; p.kw = a->kw ? a->kw : a->k; p.v = a->v;
   p.gcum = a->gcum; p.beta = a->beta; p.scale = a->scale;
+  p.gcum_lo = a->gate_per_channel && a->dtype == PKDA_F32 ? a->gcum_lo : nullptr;
   p.s0 = a->initial_state; p.sT = a->final_state; p.o = a->o;
   p.w = a->w; p.u = a->u; p.aqk = a->aqk; p.akk = a->akk; p.h = a->h;
   p.qg = a->gate_per_channel ? a->qg : nullptr;

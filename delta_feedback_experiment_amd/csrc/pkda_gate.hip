@@ -134,6 +134,7 @@ struct GateParams {
   const void* up_weight;  // low-rank gate: [H*K, R]
   int rank, g_stride;
   int dg_dtype;  // per-channel backward: dg in FP32 or g's dtype
+  float* gcum_lo;  // per-channel forward, optional: the FP32 residual of an FP64 cumsum
 };
 
 // Per-head form: one wave, lane t scans the chunk.
@@ -171,6 +172,24 @@ __global__ __launch_bounds__(NT) void gate_channel_fwd_kernel(GateParams p) {
   for (int c = threadIdx.x; c < D; c += NT) {
     const float bias = RAW ? p.dt_bias[h * D + c] : 0.f;
     const int64_t base = ((int64_t)ci.start * H + h) * D + c;
+    if (p.gcum_lo) {  // FP64 cumsum, split into its FP32 rounding and the remainder
+      double acc = 0.0;
+      for (int t0 = 0; t0 < len; t0 += 16) {
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) x[u] = io<G>::load(g + base + (int64_t)min(t0 + u, len - 1) * step);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          acc += (double)(RAW ? a_scale * softplus_sigmoid_fast(x[u] + bias).softplus : x[u]);
+          const float hi = (float)acc;
+          if (t0 + u < len) {
+            out[base + (int64_t)(t0 + u) * step] = hi;
+            p.gcum_lo[base + (int64_t)(t0 + u) * step] = (float)(acc - (double)hi);
+          }
+        }
+      }
+      continue;
+    }
     float acc = 0.f;
     for (int t0 = 0; t0 < len; t0 += 16) {
       float x[16];
@@ -391,6 +410,23 @@ __device__ __forceinline__ float wave_prefix_rows(f32x4& v, int lane) {
   return __shfl(t, 48 + (lane & 15));  // group 3's inclusive value: the wave total
 }
 
+// The same inclusive prefix in FP64 (the gcum_lo form).
+__device__ __forceinline__ double wave_prefix_rows_f64(double (&v)[4], int lane) {
+  v[1] += v[0];
+  v[2] += v[1];
+  v[3] += v[2];
+  const int q = lane >> 4;
+  double t = v[3];
+  double u = __shfl_up(t, 16);
+  if (q >= 1) t += u;
+  u = __shfl_up(t, 32);
+  if (q >= 2) t += u;
+  const double carry = t - v[3];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += carry;
+  return __shfl(t, 48 + (lane & 15));
+}
+
 // Reverse (suffix) form: rows descending.
 __device__ __forceinline__ float wave_suffix_rows(f32x4& v, int lane) {
   v[2] += v[3];
@@ -411,6 +447,7 @@ __device__ __forceinline__ float wave_suffix_rows(f32x4& v, int lane) {
 template <typename T, int K, int R>
 __global__ __launch_bounds__(kWG) void gate_low_rank_fwd_kernel(GateParams p) {
   __shared__ float s_tot[4][K];
+  __shared__ double s_tot64[sizeof(T) == 4 ? 4 : 1][K];
   __shared__ __attribute__((aligned(16))) T sW[K * LrW<T, R>::LDW];
   const int h = blockIdx.y, H = p.heads;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -425,6 +462,36 @@ __global__ __launch_bounds__(kWG) void gate_low_rank_fwd_kernel(GateParams p) {
     if (ci.len <= 0) continue;
     f32x4 acc[K / 16];
     low_rank_z<T, K, R>(p, ci, h, wave, lane, sW, acc);
+    if constexpr (sizeof(T) == 4) {
+      if (p.gcum_lo) {  // FP64 cumsum, split into its FP32 rounding and the remainder
+        double v[K / 16][4];
+#pragma unroll
+        for (int ct = 0; ct < K / 16; ++ct) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[ct][j] = (double)(a_scale * softplus_sigmoid_fast(acc[ct][j]).softplus);
+          const double tot = wave_prefix_rows_f64(v[ct], lane);
+          if (lane < 16) s_tot64[wave][16 * ct + lane] = tot;
+        }
+        __syncthreads();
+        const int64_t off = ((int64_t)ci.start * H + h) * K;
+#pragma unroll
+        for (int ct = 0; ct < K / 16; ++ct) {
+          double carry = 0.0;
+          for (int w = 0; w < wave; ++w) carry += s_tot64[w][16 * ct + (lane & 15)];
+          f32x4 hi, lo;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const double x = v[ct][j] + carry;
+            hi[j] = (float)x;
+            lo[j] = (float)(x - (double)hi[j]);
+          }
+          store_acc_global<float>(p.gcum + off, (int64_t)H * K, hi, 16 * wave, 16 * ct, ci.len, lane);
+          store_acc_global<float>(p.gcum_lo + off, (int64_t)H * K, lo, 16 * wave, 16 * ct, ci.len, lane);
+        }
+        __syncthreads();  // s_tot64 is read before the next chunk writes it
+        continue;
+      }
+    }
 #pragma unroll
     for (int ct = 0; ct < K / 16; ++ct) {
 #pragma unroll
@@ -586,6 +653,7 @@ int gate_common(const pkda_gate_args* a, GateParams& p) {
   p.up_weight = a->up_weight;
   p.rank = a->rank;
   p.g_stride = a->g_stride;
+  p.gcum_lo = a->gcum_lo;
   return 0;
 }
 
@@ -620,6 +688,8 @@ extern "C" int pkda_gate_fwd(const pkda_gate_args* a, void* stream) {
   int st = gate_common(a, p);
   if (st) return st;
   PKDA_REQUIRE(a->g && a->gcum, PKDA_EINVAL, "gate forward needs g and gcum");
+  PKDA_REQUIRE(!a->gcum_lo || a->gate_kind != PKDA_GATE_LOG_HEAD, PKDA_EUNSUPPORTED,
+               "gcum_lo is formed for the per-channel gate forms");
   if (a->num_chunks == 0) return 0;
   if (a->gate_kind == PKDA_GATE_LOW_RANK)
     return dispatch_low_rank(p, a->num_chunks, false, static_cast<hipStream_t>(stream));

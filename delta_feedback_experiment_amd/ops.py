@@ -22,7 +22,8 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .chunk import CHUNK_SIZE, ChunkPlan, chunk_backward, chunk_forward, gate_backward, gate_forward
+from .chunk import (CHUNK_SIZE, ChunkPlan, chunk_backward, chunk_forward, gate_backward, gate_forward,
+                    wants_gcum_lo)
 from .pkda import _f32
 from . import precond as pre
 
@@ -40,6 +41,11 @@ SAVED_RETAINED = ("w", "v_new", "Aqk", "T", "h", "qg", "kg", "gcum")
 query-key products, the inverted WY matrix, the chunk-entry states, the
 gated query and write key, and the gate's chunk-local cumulative log-decay
 (FP32)."""
+
+SAVED_GCUM_LO = "gcum_lo"
+"""Saved after ``gcum`` for FP32 activations unless ``lean``: the remainder
+of the gate's FP64 cumsum, from which the chunk kernels form the decay
+between two tokens of a chunk (``chunk.wants_gcum_lo``)."""
 
 
 def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int, ...], torch.dtype], ...]:
@@ -64,13 +70,16 @@ def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int
             ((ntok, H, K), act),                  # kg
             ((ntok, H, K), torch.float32),        # gcum
         ]
+        if act == torch.float32:
+            meta.append(((ntok, H, K), torch.float32))  # gcum_lo
     return tuple(meta)
 
 
 def saved_names(q: Tensor, lean: bool) -> tuple[str, ...]:
     """Names of the saved intermediates, in the order of :func:`intermediate_meta`."""
     wide = (SAVED_WIDE_KEY,) if q.dtype != torch.float32 else ()
-    return SAVED_ALWAYS[:1] + wide + SAVED_ALWAYS[1:] + (() if lean else SAVED_RETAINED)
+    retained = () if lean else SAVED_RETAINED + ((SAVED_GCUM_LO,) if q.dtype == torch.float32 else ())
+    return SAVED_ALWAYS[:1] + wide + SAVED_ALWAYS[1:] + retained
 
 
 def _check_saved(saved: list[Tensor], q: Tensor, v: Tensor, lean: bool) -> None:
@@ -109,12 +118,21 @@ def _forward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, s
     if gf.dtype not in (torch.float32, torch.bfloat16):
         gf = gf.float()
     A32, dt32 = _f32(A_log), _f32(dt_bias)
-    gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)
+    gcum_lo = _gcum_lo(plan, qf)
+    gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gcum_lo=gcum_lo)
     pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, None,
                                  want_kw32=True)
     beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
-    o, _, fs = chunk_forward(plan, qf, kf, pstate.kw, vf, gcum, beta32, scale, None, False, save_states=save_all)
-    return plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs
+    o, _, fs = chunk_forward(plan, qf, kf, pstate.kw, vf, gcum, beta32, scale, None, False, save_states=save_all,
+                             gcum_lo=gcum_lo)
+    return plan, qf, kf, vf, gf, A32, dt32, gcum, gcum_lo, pstate, beta32, o, fs
+
+
+def _gcum_lo(plan: ChunkPlan, qf: Tensor) -> Tensor | None:
+    """The gate's FP64 remainder buffer for FP32 activations, else None."""
+    if not wants_gcum_lo(_lib.GATE_RAW_CHANNEL, qf.dtype):
+        return None
+    return torch.empty(plan.num_tokens, plan.heads, plan.head_dim, device=qf.device, dtype=torch.float32)
 
 
 @torch.library.custom_op("pkda_mi355x::pkda_recurrence", mutates_args=(), device_types="cuda")
@@ -131,12 +149,14 @@ def pkda_recurrence(
     """
     _check_inputs(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale)
     with torch.cuda.device(q.device):
-        (plan, qf, kf, vf, gf, A32, dt32, gcum, pstate, beta32, o, fs) = _forward(
+        (plan, qf, kf, vf, gf, A32, dt32, gcum, gcum_lo, pstate, beta32, o, fs) = _forward(
             q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, scale, squash_x, squash_eps,
             save_all=not lean)
     saved = [pstate.kw] + ([] if pstate.kw32 is None else [pstate.kw32]) + [pstate.a_chunk]
     if not lean:
         saved += [fs.w, fs.u, fs.aqk, fs.akk, fs.h, fs.qg, fs.kg, gcum]
+        if gcum_lo is not None:
+            saved.append(gcum_lo)
     _check_saved(saved, q, v, lean)
     return o.reshape(*q.shape[:3], v.shape[-1]).to(q.dtype), saved
 
@@ -170,17 +190,19 @@ def pkda_recurrence_backward(
         named = dict(zip(saved_names(q, lean), saved))
         kw, kw32, a_chunk = named["k_write"], named.get(SAVED_WIDE_KEY), named["a_chunk"]
         if lean:  # the gate and the chunk quantities again, as the forward ran them
-            gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32)
-            _, _, fs = chunk_forward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, False, save_states=True)
+            gcum_lo = _gcum_lo(plan, qf)
+            gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gcum_lo=gcum_lo)
+            _, _, fs = chunk_forward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, False, save_states=True,
+                                     gcum_lo=gcum_lo)
         else:
-            gcum = named["gcum"]
+            gcum, gcum_lo = named["gcum"], named.get(SAVED_GCUM_LO)
             fs = FwdSaved(*(named[n] for n in SAVED_RETAINED[:-1]))
         dof = flat(do.to(q.dtype))
         # every gradient leaves the kernel in the input dtype; the
         # preconditioner's reverse scan reads dk, dkw that way and writes the
         # final dk
         gr = chunk_backward(plan, qf, kf, kw, vf, gcum, beta32, scale, None, fs, dof, None, False,
-                            grad_dtype=qf.dtype, key_grad_dtype=qf.dtype, kw32=kw32)
+                            grad_dtype=qf.dtype, key_grad_dtype=qf.dtype, kw32=kw32, gcum_lo=gcum_lo)
         pstate = pre.PrecondState(kw, a_chunk, None, None)
         dk = torch.empty_like(kf)  # the preconditioner's scan writes the final dk in k's dtype
         dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(

@@ -34,7 +34,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .chunk import ChunkPlan, _flat, chunk_forward, gate_forward
+from .chunk import ChunkPlan, _flat, chunk_forward, gate_forward, wants_gcum_lo
 from .pkda import (_check_common, _dtype_code, _f32, _ptr, _require_cuda, _require_device, _stream,
                    check_slot_indices, gate_form)
 
@@ -156,7 +156,10 @@ def prefill_op(
         A_log32, dt32 = _f32(A_log), _f32(dt_bias)
         qf, kf, vf = (_flat(t.contiguous(), plan) for t in (q, k, v))
         beta32 = _f32(beta).reshape(plan.num_tokens, H)
-        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32)
+        gcum_lo = None
+        if wants_gcum_lo(kind, q.dtype):  # as chunk_pkda takes it
+            gcum_lo = torch.empty(plan.num_tokens, H, D, device=device, dtype=torch.float32)
+        gcum = gate_forward(plan, _flat(g_used, plan), kind, A_log32, dt32, gcum_lo=gcum_lo)
         kwf = kf
         if g_atk is not None:
             pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, x, eps,
@@ -164,7 +167,7 @@ def prefill_op(
             kwf = pstate.kw
         chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, float(scale),
                       state_pool if continue_state else None, True, False,
-                      slot_idx=idx, final_state=state_pool, out=_flat(o, plan))
+                      slot_idx=idx, final_state=state_pool, out=_flat(o, plan), gcum_lo=gcum_lo)
 
 
 @prefill_op.register_fake

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 10
+#define PKDA_ABI_VERSION 11
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -203,6 +203,15 @@ typedef struct pkda_gate_args {
   int32_t rank;
   int32_t g_stride;
   int32_t dg_dtype;         /* PKDA_F32 (0), or g_dtype for the per-channel forms */
+  /* Forward, optional (per-channel forms: PKDA_GATE_LOG_CHANNEL, RAW_CHANNEL,
+   * LOW_RANK): the cumsum is then formed in FP64 and split as gcum (its FP32
+   * rounding) + gcum_lo (the FP32 rounding of the remainder), [N_tok, H, K].
+   * Differences of cumsums (the decay between two tokens of a chunk) taken
+   * as (gcum[t] - gcum[s]) + (gcum_lo[t] - gcum_lo[s]) then carry only their
+   * own rounding, where gcum alone carries that of the larger cumsums
+   * (~1e-5 of the difference once |gcum| reaches a few hundred).  NULL: FP32
+   * cumsum, gcum only. */
+  float* gcum_lo;
 } pkda_gate_args;
 
 int pkda_gate_fwd(const pkda_gate_args* args, void* stream);
@@ -354,6 +363,11 @@ typedef struct pkda_chunk_fwd_args {
    * unique).  NULL: document n uses row n. */
   const int32_t* slot_idx;
   int64_t pool_size;
+  /* Optional, FP32 with a per-channel gate: the gate's gcum_lo
+   * (pkda_gate_args.gcum_lo).  The pair decays e^{G[t]-G[s]} inside a chunk
+   * are then formed from (gcum[t] - gcum[s]) + (gcum_lo[t] - gcum_lo[s]).
+   * Ignored for BF16.  NULL: gcum alone. */
+  const float* gcum_lo;
 } pkda_chunk_fwd_args;
 
 int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
@@ -403,6 +417,11 @@ typedef struct pkda_chunk_bwd_args {
    * write key they move dA_log (a sum of the gate gradient over a whole head)
    * by ~1e-2.  NULL: the BF16 kw serves. */
   const float* kw32;
+  /* Optional, FP32 with a per-channel gate: as pkda_chunk_fwd_args.gcum_lo.
+   * The gate gradient sums the pair terms of a chunk with the decays between
+   * the pair's tokens inside them; with gcum alone their FP32 rounding moves
+   * dA_log (a signed sum of that gradient over a whole head) by ~1e-5. */
+  const float* gcum_lo;
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);

@@ -14,15 +14,13 @@ the preconditioner, the output gate GEMM, RMSNorm with the sigmoid gate
   together, to the reference module (FP32, relative L2 <= 1e-6).
 * GPU (``gpu``): this package's operators composed -- conv, controls,
   ``chunk_pkda(decay_up=...)``, norm gate -- FP32, relative L2 <= 1e-5 on the
-  output, final S and A and the gradients of x and every parameter but the
-  decay's own.  ``A_log``, ``dt_bias`` and ``decay_up`` take the bound the
-  reference sets for FP32 summation-order drift in PKDA decay gradients
-  (tests/test_mtp.py:415-424): RMS error below 2e-6 + 5e-5 RMS(expected), and
-  every coordinate within 2e-6 + 2e-4 RMS(expected).  The chunked form's gate
-  gradient is a difference of three inner products (q.dq + k.dk - kw.dkw)
-  that ``dA_log`` then sums over B*T*K with signed weights: measured on these
-  inputs it sits at 7e-6 relative L2 in the recurrence alone, against 3e-7 for
-  q, k and v, with either gate form.
+  output, final S and A and the gradients of x and every parameter, the
+  decay's own (``A_log``, ``dt_bias``, ``decay_up``) included.  These inputs
+  drive the chunk-local cumulative gate to |G| ~ 340 (``A_log`` up to
+  log 16): the pair decays e^{G[t]-G[s]} are formed from the gate's FP64
+  cumsum carried as two floats, since from the FP32 cumsum alone each
+  difference carries ~2e-5 of rounding and ``dA_log`` (a signed sum of the
+  gate gradient over a head) ends near 1e-5.
 """
 
 from __future__ import annotations
@@ -35,7 +33,6 @@ from conftest import load_golden, rel_l2
 
 FP32_TOL = 1e-5
 H, D = 2, 64
-DECAY_PARAMS = ("A_log", "dt_bias", "decay_up__weight")
 
 
 def _params(gd, device):
@@ -61,14 +58,7 @@ def compose(P, x, conv, controls, recurrence, norm_gate):
     return F.linear(mixed.flatten(-2), P["o_proj__weight"]), S, A
 
 
-def _decay_drift_ok(got, want):
-    """tests/test_mtp.py:420-424's aggregate and per-coordinate drift bound."""
-    err = got.detach().double().cpu() - want.double()
-    scale = want.double().square().mean().sqrt()
-    return bool(err.square().mean().sqrt() < 2e-6 + 5e-5 * scale and err.abs().max() < 2e-6 + 2e-4 * scale)
-
-
-def _check(gd, out, S, A, x, P, tol, decay_drift=False):
+def _check(gd, out, S, A, x, P, tol):
     loss = ((out * torch.from_numpy(gd["cot_o"]).to(out.device)).sum()
             + (S * torch.from_numpy(gd["cot_S"]).to(S.device)).sum()
             + (A * torch.from_numpy(gd["cot_A"]).to(A.device)).sum())
@@ -77,18 +67,11 @@ def _check(gd, out, S, A, x, P, tol, decay_drift=False):
     res = {"out": rel_l2(out, torch.from_numpy(gd["out_o"])), "S": rel_l2(S, torch.from_numpy(gd["out_S"])),
            "A": rel_l2(A, torch.from_numpy(gd["out_A"])),
            "dx": rel_l2(grads[0], torch.from_numpy(gd["grad_x"]))}
-    drift = {}
     for n, gval in zip(names, grads[1:]):
-        want = torch.from_numpy(gd["grad_" + n])
-        res["d" + n] = rel_l2(gval, want)
-        if decay_drift and n in DECAY_PARAMS:
-            drift["d" + n] = _decay_drift_ok(gval, want)
+        res["d" + n] = rel_l2(gval, torch.from_numpy(gd["grad_" + n]))
     print("  " + " ".join(f"{k}={v:.2e}" for k, v in res.items()), flush=True)
     for name, val in res.items():
-        if name in drift:
-            assert drift[name], (name, val)
-        else:
-            assert val < tol, (name, val)
+        assert val < tol, (name, val)
 
 
 def test_oracle_composition_matches_the_reference_module():
@@ -130,4 +113,4 @@ def test_gpu_operators_compose_to_the_reference_module():
 
     out, S, A = compose(P, x, pkda_qkv_conv, pkda_controls, recurrence, pkda_norm_gate)
     torch.cuda.synchronize()
-    _check(gd, out, S, A, x, P, FP32_TOL, decay_drift=True)
+    _check(gd, out, S, A, x, P, FP32_TOL)
