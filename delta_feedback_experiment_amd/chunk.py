@@ -89,6 +89,17 @@ class ChunkPlan:
         )
 
 
+def validate_cu_seqlens(cu_seqlens: Tensor, num_tokens: int) -> None:
+    """Raise ``ValueError`` unless ``cu_seqlens`` rises from 0 to the packed
+    length ``num_tokens`` without decreasing (reads it back: synchronises).
+    Without this check a malformed array is clamped on the device and the
+    tokens it leaves outside every document keep unwritten outputs."""
+    cu = cu_seqlens.detach().to("cpu", torch.int64).reshape(-1)
+    if cu.numel() < 1 or int(cu[0]) != 0 or int(cu[-1]) != num_tokens or bool((cu[1:] < cu[:-1]).any()):
+        raise ValueError(f"cu_seqlens must rise from 0 to the packed length {num_tokens} without decreasing, "
+                         f"got {cu.tolist() if cu.numel() <= 16 else '[...]'}")
+
+
 def wants_gcum_lo(kind: int, dtype: torch.dtype) -> bool:
     """Whether the chunk kernels take the gate's FP64 remainder: FP32
     activations with a per-channel gate.  There the decay between two tokens
@@ -294,7 +305,8 @@ def low_rank_grads(draw: Tensor, hidden_rows: Tensor, up_weight: Tensor) -> tupl
     FP32 library GEMMs (the backward of the reference's ``F.linear``,
     delta_feedback_experiment/pkda.py:334-339)."""
     d2 = draw.reshape(draw.shape[0], -1)
-    return d2 @ up_weight.float(), d2.t() @ hidden_rows.float()
+    with torch.autocast("cuda", enabled=False):  # FP32 whatever autocast state the backward runs under
+        return d2 @ up_weight.float(), d2.t() @ hidden_rows.float()
 
 
 def _flat(t: Tensor, plan: ChunkPlan) -> Tensor:
@@ -310,7 +322,10 @@ class _ChunkPKDA(torch.autograd.Function):
     those of the same kernels on the same inputs.
     """
 
+    # the backward runs under the autocast state of the forward, as FLA's
+    # custom_fwd / custom_bwd pair does for chunk_precond_kda
     @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, q, k, v, g, beta, g_atk, beta_atk, A_log, dt_bias, log_atk_scale,
                 initial_state, initial_A_state, cu_seqlens, decay_up, opts):
         from .pkda import gate_form
@@ -370,6 +385,7 @@ class _ChunkPKDA(torch.autograd.Function):
         return o, S_T, A_T
 
     @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, do, dS_T, dA_T):
         from . import precond as pre
 
@@ -456,6 +472,7 @@ def chunk_pkda(
     lean: bool = False,
     use_qk_l2norm_in_kernel: bool = False,
     decay_up: Tensor | None = None,
+    check_cu_seqlens: bool = False,
     **_ignored,
 ) -> tuple[Tensor, Tensor | None, Tensor | None]:
     """Stateful, differentiable chunked PKDA: ``(o, S_T, A_T)``.
@@ -475,6 +492,11 @@ def chunk_pkda(
     ``g @ decay_up^T`` (pkda.py:334-339) is formed inside the gate kernel on
     MFMA instead of being materialised; ``use_gate_in_kernel`` must be set.
     ``decay_up`` receives its gradient too.
+
+    ``check_cu_seqlens`` verifies on the host (synchronising) that
+    ``cu_seqlens`` rises from 0 to the packed length; without it a malformed
+    array is clamped on the device, and tokens outside every document keep
+    unwritten outputs and gradients.
     """
     from .pkda import _check_common, _require_cuda
 
@@ -496,6 +518,8 @@ def chunk_pkda(
         if tuple(decay_up.shape) != (H * D, D) or tuple(g.shape) != (*q.shape[:2], D):
             raise ValueError(f"decay_up [{H * D}, {D}] with g the decay hidden {(*q.shape[:2], D)} expected, got "
                              f"{tuple(decay_up.shape)} and {tuple(g.shape)}")
+    if check_cu_seqlens and cu_seqlens is not None:
+        validate_cu_seqlens(cu_seqlens, q.shape[1])
     N = q.shape[0] if cu_seqlens is None else cu_seqlens.numel() - 1
     if initial_state is not None and tuple(initial_state.shape) != (N, q.shape[2], D, D):
         raise ValueError(f"initial_state must be {(N, q.shape[2], D, D)}")

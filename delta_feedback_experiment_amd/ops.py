@@ -173,13 +173,20 @@ def _pkda_recurrence_fake(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log
 def pkda_recurrence_backward(
     q: Tensor, k: Tensor, v: Tensor, g: Tensor, g_atk: Tensor, beta_atk: Tensor, beta: Tensor,
     A_log: Tensor, dt_bias: Tensor, log_atk_scale: Tensor, saved: list[Tensor], do: Tensor,
-    scale: float, squash_x: float, squash_eps: float, lean: bool,
+    scale: float, squash_x: float, squash_eps: float, autocast_dtype: torch.dtype | None, lean: bool,
 ) -> list[Tensor]:
     """Gradients of :func:`pkda_recurrence` for its ten tensor inputs, each in
-    that input's dtype (``delta_feedback_experiment/fla_ops.py:488-499``)."""
+    that input's dtype (``delta_feedback_experiment/fla_ops.py:488-499``).
+
+    ``autocast_dtype`` is the autocast state the forward ran under (None:
+    disabled); the backward runs under it, as the reference's does
+    (``fla_ops.py:433-437``), whatever state the caller's ``backward()`` is
+    in.  The gfx950 kernels take their dtypes from the tensors, so the
+    gradients do not depend on it."""
     from .chunk import FwdSaved
 
-    with torch.cuda.device(q.device):
+    with torch.cuda.device(q.device), torch.autocast(
+            "cuda", enabled=autocast_dtype is not None, dtype=autocast_dtype or torch.bfloat16):
         plan = ChunkPlan.make(q, None)
         flat = lambda t: t.contiguous().reshape(plan.num_tokens, plan.heads, *t.shape[3:])  # noqa: E731
         qf, kf, vf, gf = flat(q), flat(k), flat(v), flat(g)
@@ -222,7 +229,7 @@ def pkda_recurrence_backward(
 
 @pkda_recurrence_backward.register_fake
 def _pkda_recurrence_backward_fake(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, saved, do,
-                                   scale, squash_x, squash_eps, lean):
+                                   scale, squash_x, squash_eps, autocast_dtype, lean):
     return [torch.empty_like(t) for t in (q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale)]
 
 
@@ -231,6 +238,8 @@ def _setup_context(ctx, inputs, output) -> None:
     _o, saved = output
     ctx.save_for_backward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, *saved)
     ctx.scalars = tuple(scalars)
+    # the autocast state of the forward, for the backward (fla_ops.py:546-548)
+    ctx.autocast_dtype = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
     ctx.mark_non_differentiable(*saved)
     # the saved intermediates never receive gradients: do not fill zeros for them
     ctx.set_materialize_grads(False)
@@ -242,7 +251,7 @@ def _backward(ctx, do, _dsaved):
     tensors = ctx.saved_tensors
     inputs, saved = tensors[:10], list(tensors[10:])
     scale, squash_x, squash_eps, lean = ctx.scalars
-    grads = pkda_recurrence_backward(*inputs, saved, do, scale, squash_x, squash_eps, lean)
+    grads = pkda_recurrence_backward(*inputs, saved, do, scale, squash_x, squash_eps, ctx.autocast_dtype, lean)
     return (*grads, None, None, None, None)
 
 

@@ -110,6 +110,7 @@ def fused_recurrent_pkda(
     eps: float = 1e-6,
     log_atk_scale: Tensor | None = None,
     use_qk_l2norm_in_kernel: bool = False,
+    check_cu_seqlens: bool = False,
     **_ignored,
 ) -> tuple[Tensor, Tensor | None, Tensor | None]:
     """Token-recurrent PKDA forward (no autograd): ``(o, S_T, A_T)``.
@@ -118,7 +119,9 @@ def fused_recurrent_pkda(
     (``use_gate_in_kernel``) or log-decay ``[B,T,H]``/``[B,T,H,D]``, ``beta
     [B,T,H]``, ``g_atk, beta_atk [B,T,H]``, ``log_atk_scale [H]`` (the
     preconditioner's log-space center), states ``[N,H,D,D]`` / ``[N,H,D]``
-    FP32 where ``N = B`` or ``len(cu_seqlens) - 1``.
+    FP32 where ``N = B`` or ``len(cu_seqlens) - 1``.  ``check_cu_seqlens``
+    verifies ``cu_seqlens`` on the host first (synchronising); without it a
+    malformed array is clamped on the device.
     """
     if use_qk_l2norm_in_kernel:
         raise ValueError("q and k arrive L2-normalised (pkda.py:464-465); in-kernel norm is not provided")
@@ -133,8 +136,10 @@ def fused_recurrent_pkda(
     if cu_seqlens is not None:
         if B != 1:
             raise ValueError("cu_seqlens requires batch size 1")
-        from .chunk import ChunkPlan
+        from .chunk import ChunkPlan, validate_cu_seqlens
 
+        if check_cu_seqlens:
+            validate_cu_seqlens(cu_seqlens, T)
         # the kernel reads document bounds from the chunk table's sanitised
         # copy: a malformed cu_seqlens cannot send it past the token tensors
         with torch.cuda.device(device):

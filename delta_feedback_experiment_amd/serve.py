@@ -34,7 +34,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .chunk import ChunkPlan, _flat, chunk_forward, gate_forward, wants_gcum_lo
+from .chunk import ChunkPlan, _flat, chunk_forward, gate_forward, validate_cu_seqlens, wants_gcum_lo
 from .pkda import (_check_common, _dtype_code, _f32, _ptr, _require_cuda, _require_device, _stream,
                    check_slot_indices, gate_form)
 
@@ -90,6 +90,7 @@ def pkda_prefill_(
     x: float = 1.0,
     eps: float = 1e-6,
     check_slots: bool = False,
+    check_cu_seqlens: bool = False,
 ) -> Tensor:
     """Chunked prefill whose final states land in pool slots; returns ``o``.
 
@@ -102,7 +103,9 @@ def pkda_prefill_(
     ``continue_state=False`` starts every sequence from zero states (a new
     prompt); ``True`` continues from the states in its slot (a prompt
     extended in pieces).  ``check_slots`` verifies range and uniqueness on the
-    host first (synchronising).
+    host first (synchronising); ``check_cu_seqlens`` likewise that
+    ``cu_seqlens`` rises from 0 to the packed length (a malformed one is
+    otherwise clamped on the device).
     """
     _check_common(q, k, v, beta)
     _require_device(q, k, v, g, beta, state_pool, slot_idx, a_pool, cu_seqlens, g_atk, beta_atk,
@@ -121,6 +124,8 @@ def pkda_prefill_(
         raise ValueError(f"a_pool must be a contiguous float32 [{P}, {H}, {D}] tensor")
     if cu_seqlens is not None and B != 1:
         raise ValueError("cu_seqlens requires batch size 1")
+    if check_cu_seqlens and cu_seqlens is not None:
+        validate_cu_seqlens(cu_seqlens, T)
     gate_form(g, q.shape[:-1], D, use_gate_in_kernel, A_log, dt_bias)  # shape check
     N = B if cu_seqlens is None else cu_seqlens.numel() - 1
     _slots(slot_idx, N, P, check_slots)

@@ -71,3 +71,17 @@ def test_operators_refuse_cpu_tensors():
     q = torch.randn(1, 4, 1, 64)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         fused_recurrent_pkda(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1))
+
+
+def test_noalloc_gate_backward_refuses_past_its_scratch():
+    """pkda_gate_bwd_noalloc checks its size bound before any HIP call, so the
+    refusal runs here, without a device; the pointers are never read."""
+    from delta_feedback_experiment_amd import _lib
+
+    H, D = 64, 128
+    chunks = (1 << 22) // (H * (D + 1)) + 1  # one chunk past the 16 MiB array
+    args = _lib.GateArgs(num_seqs=chunks, seqlen=64, heads=H, head_dim=D, gate_kind=_lib.GATE_RAW_CHANNEL,
+                         g_dtype=_lib.PKDA_BF16, g=1, A_log=1, dt_bias=1, dgcum=1, dg=1, dA_log=1, ddt_bias=1,
+                         num_chunks=chunks, dg_dtype=_lib.PKDA_F32)
+    with pytest.raises(ValueError, match="exceeds its scratch"):
+        _lib.call("pkda_gate_bwd_noalloc", args, 0)

@@ -101,6 +101,14 @@ def test_chunk_table_sanitises_cu_seqlens(dev, cu, ok):
     if not ok:
         with pytest.raises(ValueError, match="cu_seqlens"):
             ChunkPlan.make(q, cu_t.to(dev), check=True)
+        # the public operators' opt-in check refuses it on the host, before any launch
+        from delta_feedback_experiment_amd import chunk_pkda, fused_recurrent_pkda
+
+        z = torch.zeros(1, T, 1, 64, device=dev, dtype=torch.bfloat16)
+        gb = torch.zeros(1, T, 1, device=dev)
+        for fn in (chunk_pkda, fused_recurrent_pkda):
+            with pytest.raises(ValueError, match="cu_seqlens"):
+                fn(z, z, z, gb, gb, cu_seqlens=cu_t.to(dev), check_cu_seqlens=True)
 
 def test_state_pass_forms_agree_bitwise(dev):
     """Every kernel works per head and the state passes per value column, so
@@ -500,3 +508,52 @@ def test_pkda_recurrence_op_matches_oracle(dev, lean, seed):
     print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
     for n, val in res.items():
         assert val < BF16_TOL, (n, val)
+
+
+def test_production_key_gradient_handoff(dev):
+    """The production backward hands the chunk kernel's key gradients (read
+    key dk and write key dkw) to the preconditioner's reverse scan in BF16,
+    rounded once (half the bytes to write and read).  Against the FP32
+    handoff of the same kernels at T = 1,024 (16 chunks per document): both
+    within the BF16 bar of the oracle, and the difference the rounding makes
+    to dk, dg_atk, dbeta_atk and dlog_atk_scale printed and bounded."""
+    from delta_feedback_experiment_amd import ops
+    from delta_feedback_experiment_amd import precond as pre
+    from delta_feedback_experiment_amd.chunk import chunk_backward
+
+    print("[gpu] production key-gradient handoff, BF16 vs FP32", flush=True)
+    B, T, H, D = 1, 1024, 4, 128
+    (q, k, v, g_raw, beta, A_log, dt_bias, g_atk, beta_atk, center) = _production_inputs(
+        B, T, H, D, torch.bfloat16, 8)
+    do = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    d = [x.to(dev) for x in (q, k, v, g_raw, g_atk, beta_atk, beta, A_log, dt_bias, center)]
+    scale = D ** -0.5
+    with torch.no_grad():
+        plan, qf, kf, vf, gf, A32, dt32, gcum, gcum_lo, pstate, beta32, o, fs = ops._forward(
+            *d, scale, 1.5, 1e-6, save_all=True)
+        dof = do.to(dev).reshape(plan.num_tokens, H, D)
+        out = {}
+        for name, kd in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+            gr = chunk_backward(plan, qf, kf, pstate.kw, vf, gcum, beta32, scale, None, fs, dof, None, False,
+                                grad_dtype=torch.bfloat16, key_grad_dtype=kd, kw32=pstate.kw32)
+            dk_final = torch.empty_like(kf) if kd == torch.bfloat16 else None
+            dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(plan, kf, d[4], d[5], d[9], 1.5, 1e-6, pstate,
+                                                                 gr.dkw, gr.dk, None, False, dk_final=dk_final)
+            dk = (dk_final if dk_final is not None else gr.dk).float().reshape(B, T, H, D)
+            out[name] = (dk, dg_atk.reshape(B, T, H), dbeta_atk.reshape(B, T, H), dcenter)
+    torch.cuda.synchronize()
+    leaves = [x.float().clone().requires_grad_() for x in (q, k, g_atk, beta_atk, center)]
+    o_r = oracle.pkda_reference(leaves[0], leaves[1], v.float(), g_raw.float(), beta, A_log=A_log, dt_bias=dt_bias,
+                                use_gate_in_kernel=True, g_atk=leaves[2], beta_atk=leaves[3],
+                                log_atk_scale=leaves[4], x=1.5, eps=1e-6, out_dtype=torch.float32)[0]
+    ref = torch.autograd.grad((o_r * do.float()).sum(), leaves)
+    ref = (ref[1], ref[2], ref[3], ref[4])
+    names = ("dk", "dg_atk", "dbeta_atk", "dlog_atk_scale")
+    res = {}
+    for n, a, b, r in zip(names, out["bf16"], out["fp32"], ref):
+        res[n] = (rel_l2(a, r), rel_l2(b, r), rel_l2(a, b))
+    print("  (bf16 handoff vs oracle, fp32 handoff vs oracle, bf16 vs fp32) "
+          + " ".join(f"{n}=({x:.2e}, {y:.2e}, {z:.2e})" for n, (x, y, z) in res.items()), flush=True)
+    for n, (x, y, z) in res.items():
+        assert x < BF16_TOL and y < BF16_TOL, (n, x, y)
+        assert z < 1e-2, (n, z)

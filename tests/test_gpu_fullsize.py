@@ -249,3 +249,77 @@ def test_c5_full_size_gradients_with_initial_state(dev):
     print("  row 0, tokens 0..255 and dS0: " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
     bad = {n: e for n, e in errs.items() if not e < BF16_TOL}
     assert not bad, bad
+
+
+def _production_inputs(dev, B, T, H, D, seed):
+    """The production operator's inputs as the reference's bench draws them
+    (scripts/pkda_bench.py:162-187): raw per-channel gate, A_log = log U(1, 16),
+    preconditioner with x = 1.5; BF16 activations."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*s):
+        return torch.randn(*s, generator=gen, device=dev)
+
+    q = _l2norm(rn(B, T, H, D)).to(torch.bfloat16)
+    k = _l2norm(rn(B, T, H, D)).to(torch.bfloat16)
+    v = rn(B, T, H, D).to(torch.bfloat16)
+    g_raw = (0.2 * rn(B, T, H, D)).to(torch.bfloat16)
+    beta = torch.sigmoid(0.2 * rn(B, T, H))
+    A_log = torch.empty(H, device=dev).uniform_(1, 16, generator=gen).log()
+    dt_bias = 0.1 * rn(H * D)
+    g_atk = -F.softplus(0.2 * rn(B, T, H) + 0.3)
+    beta_atk = torch.sigmoid(rn(B, T, H))
+    center = -0.2 + 0.1 * rn(H)
+    do = rn(B, T, H, D).to(torch.bfloat16)
+    return [q, k, v, g_raw, g_atk, beta_atk, beta, A_log, dt_bias, center], do
+
+
+PRODUCTION_NAMES = ("q", "k", "v", "g", "g_atk", "beta_atk", "beta", "A_log", "dt_bias", "log_atk_scale")
+
+
+def test_production_operator_full_length(dev):
+    """pkda_recurrence (the reference model's training operator: raw
+    per-channel gate, preconditioner x = 1.5, all ten gradients) at the c2
+    geometry B8 T4096 H16 d128 -- 64 chunks per document through the
+    per-channel state passes and the preconditioner's chunk scan.
+
+    * Independence, bitwise: row 2, heads 4..7 run alone give the full run's
+      output and per-token gradients of that row and those heads.
+    * That slice (all 4,096 tokens) against the CPU oracle's FP32 autograd on
+      the same BF16-rounded values, every gradient including dA_log,
+      ddt_bias and dlog_atk_scale (which the slice run sums over its own row
+      and heads)."""
+    from delta_feedback_experiment_amd import pkda_recurrence
+
+    B, T, H, D = 8, 4096, 16, 128
+    row, hs = 2, slice(4, 8)
+    inputs, do = _production_inputs(dev, B, T, H, D, seed=61)
+    print("[gpu] production operator c2 geometry: full run, row 2 heads 4-7 alone, oracle", flush=True)
+
+    def run(ins, d):
+        leaves = [x.detach().clone().requires_grad_() for x in ins]
+        o, _ = pkda_recurrence(*leaves, D ** -0.5, 1.5, 1e-6, False)
+        return (o, *torch.autograd.grad(o, leaves, d))
+
+    full = run(inputs, do)
+    tok = lambda t: t[row:row + 1, :, hs].contiguous()  # noqa: E731
+    q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, center = inputs
+    part_in = [tok(q), tok(k), tok(v), tok(g), tok(g_atk), tok(beta_atk), tok(beta), A_log[hs].contiguous(),
+               dt_bias.view(H, D)[hs].reshape(-1).contiguous(), center[hs].contiguous()]
+    part = run(part_in, tok(do))
+    torch.cuda.synchronize()
+    for name, x, y in zip(("o",) + PRODUCTION_NAMES[:7], full[:8], part[:8]):
+        assert torch.equal(tok(x), y), f"{name}: row {row} heads 4-7 differ from their own run"
+    del full
+    cl = [x.detach().float().cpu().clone().requires_grad_() for x in part_in]
+    o_r = oracle.pkda_reference(cl[0], cl[1], cl[2], cl[3], cl[6], A_log=cl[7], dt_bias=cl[8],
+                                use_gate_in_kernel=True, g_atk=cl[4], beta_atk=cl[5], log_atk_scale=cl[9],
+                                x=1.5, eps=1e-6, out_dtype=torch.float32)[0]
+    ref = torch.autograd.grad(o_r, cl, tok(do).float().cpu())
+    errs = {"o": rel_l2(part[0].float(), o_r)}
+    for n, a, b, x in zip(PRODUCTION_NAMES, part[1:], ref, part_in):
+        assert a.dtype == x.dtype, (n, a.dtype, x.dtype)
+        errs["d" + n] = rel_l2(a.float(), b)
+    print("  " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    bad = {n: e for n, e in errs.items() if not e < BF16_TOL}
+    assert not bad, bad
