@@ -1407,7 +1407,11 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
 #pragma unroll
   for (int j = 0; j < HCT; ++j) store_acc_global<OT>(dvo, gs, dv[j], r0, 16 * (ch * HCT + j), len, lane);
   // Each pass works on slot 0 of dq, dk and dkws, which hold column tile
-  // ch HCT + j at pass j.
+  // ch HCT + j at pass j.  dq, dk and dkw leave two adjacent column tiles of
+  // a row block together, so each BF16 row piece is a 64-byte span (one tile
+  // alone would write 32-byte pieces, half a cache line, one pass apart).
+  TileGroupStore<OT, 2> st_q;
+  TileGroupStore<OK, 2> st_k, st_w;
 #pragma unroll 1
   for (int j = 0; j < HCT; ++j) {
     const int ct = ch * HCT + j;
@@ -1677,12 +1681,12 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     }
     store_acc_global<float>(p.dgcum + row0 * D, gs, dg, r0, 16 * ct, len, lane);
     // this column tile's dq, dk and dkw are final
-    store_acc_global<OT>(dqo, gs, dq[0], r0, 16 * ct, len, lane);
+    st_q.put(dqo, gs, dq[0], r0, 16 * ct, len, lane, j & 1);
     if (p.kw_is_k) {
-      store_acc_global<OK>(dko, gs, dk[0] + dkwj, r0, 16 * ct, len, lane);
+      st_k.put(dko, gs, dk[0] + dkwj, r0, 16 * ct, len, lane, j & 1);
     } else {
-      store_acc_global<OK>(dko, gs, dk[0], r0, 16 * ct, len, lane);
-      store_acc_global<OK>(dkwo, gs, dkwj, r0, 16 * ct, len, lane);
+      st_k.put(dko, gs, dk[0], r0, 16 * ct, len, lane, j & 1);
+      st_w.put(dkwo, gs, dkwj, r0, 16 * ct, len, lane, j & 1);
     }
     // the next tile's accumulators move into slot 0 (fixed registers: a
     // runtime index into the arrays would go through indexed register moves)

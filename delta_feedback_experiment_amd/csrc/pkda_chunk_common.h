@@ -682,6 +682,56 @@ __device__ __forceinline__ void store_acc_global(T* g, int64_t gstride, const f3
   AccStore<T, FULL>::run(g, gstride, acc, m0, n0, nvalid, lane);
 }
 
+// Output tiles of a loop that produces one 16-column tile per pass with long
+// work in between.  A BF16 tile row is a 32-byte piece; stored alone, long
+// before the row's next piece, it reaches memory as a partial line (the
+// counters show ~1.7x the bytes).  put(.., pos) keeps the tiles of passes
+// pos = 0 .. NG - 2 in registers (packed and quad-transposed, shifted along so
+// every register stays fixed in a loop that is not unrolled) and stores the
+// NG tiles together at pos = NG - 1, so each row gets NG adjacent pieces at
+// once (tile pos at n0 - 16 (NG - 1 - pos)).  FP32 rows are 64-byte pieces
+// already and are stored as they come.
+template <typename T, int NG>
+struct TileGroupStore {
+  __device__ __forceinline__ void put(T* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid, int lane,
+                                      int pos) {
+    store_acc_global<T>(g, gstride, acc, m0, n0, nvalid, lane);
+  }
+};
+template <int NG>
+struct TileGroupStore<bf16_t, NG> {
+  static_assert(NG >= 2 && NG <= 4, "2 to 4 tiles per group");
+  uint32_t p0[NG - 1], p1[NG - 1];  // [i]: the tile NG - 1 - i passes back
+  __device__ __forceinline__ void put(bf16_t* g, int64_t gstride, const f32x4& acc, int m0, int n0, int nvalid,
+                                      int lane, int pos) {
+    bf16x2_t a, b;  // the same rounding as store_acc_global
+    a[0] = static_cast<__bf16>(acc[0]);
+    a[1] = static_cast<__bf16>(acc[1]);
+    b[0] = static_cast<__bf16>(acc[2]);
+    b[1] = static_cast<__bf16>(acc[3]);
+    uint32_t v0 = __builtin_bit_cast(uint32_t, a), v1 = __builtin_bit_cast(uint32_t, b);
+    quad_transpose_b16(v0, v1, lane);
+    if (pos == NG - 1) {  // uniform: the pass index
+      const int r = m0 + quad_row(lane);
+      if (r < nvalid) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        bf16_t* row = g + r * gstride + n0 + quad_col(lane);
+#pragma unroll
+        for (int i = NG - 2; i >= 0; --i) *reinterpret_cast<u32x2*>(row - 16 * (i + 1)) = u32x2{p0[i], p1[i]};
+        *reinterpret_cast<u32x2*>(row) = u32x2{v0, v1};
+      }
+    } else {
+#pragma unroll
+      for (int i = NG - 2; i > 0; --i) {
+        p0[i] = p0[i - 1];
+        p1[i] = p1[i - 1];
+      }
+      p0[0] = v0;
+      p1[0] = v1;
+    }
+  }
+};
+
 template <typename E>
 __device__ __forceinline__ void store_acc_lds(E* lds, int ld, const f32x4& acc, int m0, int n0, int lane) {
 #pragma unroll
