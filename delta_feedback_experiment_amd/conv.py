@@ -1,4 +1,5 @@
-"""The fused Q/K/V short convolution + SiLU + per-head L2 norm, as a custom op.
+"""Custom op over the gfx950 depthwise causal conv kernel: Q, K and V slabs
+out of one pass, each through SiLU, Q and K unit-normalised per head.
 
 Mirrors ``delta_feedback::pkda_qkv_conv`` and its backward op
 (``delta_feedback_experiment/fla_ops.py:134-249``): same arguments
@@ -6,8 +7,8 @@ Mirrors ``delta_feedback::pkda_qkv_conv`` and its backward op
 slabs ``[B, T, C / 3]`` in ``x.dtype``), gradients ``(dx, dw)`` in the dtypes
 of ``x`` and ``weight``.  ``PreconditionedKDA._project`` calls it on the
 concatenated projections with ``norm_channels = 2 * projection_size``
-(``delta_feedback_experiment/pkda.py:223-288``).  ``x`` is made contiguous
-here and in the backward, as the reference does.
+(``delta_feedback_experiment/pkda.py:223-288``).  The kernels index ``x`` by
+dense strides, so the forward and the backward both take ``x.contiguous()``.
 """
 
 from __future__ import annotations

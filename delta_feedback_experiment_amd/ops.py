@@ -49,7 +49,9 @@ between two tokens of a chunk (``chunk.wants_gcum_lo``)."""
 
 
 def intermediate_meta(q: Tensor, v: Tensor, lean: bool) -> tuple[tuple[tuple[int, ...], torch.dtype], ...]:
-    """Shape and dtype of every saved intermediate, from the input geometry."""
+    """What ``_setup_context`` saves, as (shape, dtype) pairs in save order:
+    a function of the shapes of ``q`` and ``v``, their dtype and ``lean`` only,
+    so the fake kernel and the real one agree without running either."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     chunks = -(-T // CHUNK_SIZE)
@@ -91,7 +93,7 @@ def _check_saved(saved: list[Tensor], q: Tensor, v: Tensor, lean: bool) -> None:
         if tuple(t.shape) != shape or t.dtype != dtype or t.device != q.device or not t.is_contiguous():
             raise RuntimeError(
                 f"pkda_recurrence intermediate {name} is {(tuple(t.shape), t.dtype, t.device)}, "
-                f"not {(shape, dtype, q.device)}; the fake implementation is stale"
+                f"not {(shape, dtype, q.device)}: the forward and intermediate_meta (the fake's shapes) disagree"
             )
 
 
