@@ -611,8 +611,8 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
 //     take S0 and dS_C rows of its own columns only: they come from the
 //     tile-major checkpoints straight into registers as MFMA B operands
 //     (never through LDS), and sum(S0 * dS_C) is formed there too.
-//   * dv = beta dBv and sum_c dBv V (the value part of dbeta) are formed on
-//     the loaded registers: V and dv never touch LDS.
+//   * dv = beta dBv and dbeta = sum_c dBv U / beta are formed on the loaded
+//     registers (V is not read: see below) and dv never touches LDS.
 //   * Two [64 x D] LDS regions hold U and dO, then U and dBv, then K and Q;
 //     the pair matrices (s dAqk E, dAkk E, beta dAkk E) have their own.
 // Passes: (1) dQg = dO S0^T, dAqk = dO U^T -> P2;  (2) dBw = -dBv S0^T,
@@ -635,8 +635,9 @@ struct FusedW4Layout {
   static constexpr int off_gam = off_P1 + CT;    // [64] G
   static constexpr int off_beta = off_gam + C * 4;
   static constexpr int off_p2d = off_beta + C * 4;   // [64] s dAqk[t,t], FP32, then 64 dummy slots
-  static constexpr int off_db1 = off_p2d + 2 * C * 4;  // [64] sum_c dBv V
-  static constexpr int off_rowg = off_db1 + C * 4;   // [4][64] per-wave row sums of the gate gradient
+  static constexpr int off_db1 = off_p2d + 2 * C * 4;  // [64] sum_c dBv U
+  static constexpr int off_dbv = off_db1 + C * 4;    // [64] sum_c dBv V (rows with |beta| < 1e-20 only)
+  static constexpr int off_rowg = off_dbv + C * 4;   // [4][64] per-wave row sums of the gate gradient
   static constexpr int off_rowb = off_rowg + 4 * C * 4;  // [4][64] per-wave row sums of dbeta
   static constexpr int off_wave = off_rowb + 4 * C * 4;  // [2][4] sum(S0 dS_C), sum(kw dKg) per wave
   // dq's last PARK tiles (row blocks 2-3) between passes 1 and 3 (FP32, one
@@ -682,6 +683,7 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
   float* sP2d = reinterpret_cast<float*>(smem + L::off_p2d);
   float* sDb1 = reinterpret_cast<float*>(smem + L::off_db1);
+  float* sDbV = reinterpret_cast<float*>(smem + L::off_dbv);
   float* sRowG = reinterpret_cast<float*>(smem + L::off_rowg);
   float* sRowB = reinterpret_cast<float*>(smem + L::off_rowb);
   float* sWave = reinterpret_cast<float*>(smem + L::off_wave);
@@ -693,7 +695,7 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
   const int64_t gidx = (int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + hh;
   const float gval = p.gcum[gidx];  // rows past the end repeat the last gate
   const float bval = p.beta[gidx];
-  RegTile<kW4, C, D, E> rU, rdO, rdBv, rV, rK, rQ;
+  RegTile<kW4, C, D, E> rU, rdO, rdBv, rK, rQ;
   s16x8_t S0f[NJ][KV], dSf[NJ][KV];  // B operands: rows of this wave's columns, k over the value index
   const E* hsrc = static_cast<const E*>(p.h) + ((int64_t)cid * H + hh) * D * D;
   const E* dhsrc = static_cast<const E*>(p.dh) + ((int64_t)cid * H + hh) * D * D;
@@ -709,7 +711,6 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
       S0f[j][kk] = *reinterpret_cast<const s16x8_t*>(hsrc + off);
     }
   rdBv.load(static_cast<const E*>(p.du) + row0 * D, gs, len);
-  rV.load(static_cast<const E*>(p.v) + row0 * D, gs, len);
   // every thread writes (the C rows' values, repeated): no branch
   sGam[tid & (C - 1)] = gval;
   sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? bval : 0.f;
@@ -717,8 +718,16 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
   rdO.store(sR1, L::LD);
   __syncthreads();
 
-  // dv = beta dBv (final) and sum_c dBv V on the registers: the 16 pieces of
-  // a row sit in 16 consecutive lanes
+  // dv = beta dBv (final) and sum_c dBv U on the registers: the 16 pieces of
+  // a row sit in 16 consecutive lanes.
+  // dbeta: every beta-dependent quantity of the chunk (Bv, Bw and the rows of
+  // Akk) is row t scaled by beta_t, so (I + Akk) U = Bv - Bw S0 reads
+  // U_t = beta_t r_t with r_t independent of beta_t, and the adjoint of the
+  // right-hand side being dBv = T^T dU, dL/dbeta_t = sum_c dBv[t,c] r_t[c]
+  // = sum_c dBv[t,c] U[t,c] / beta_t.  (The three-term form -- dBv V, the Bw
+  // part and the Akk part -- is the same sum; it needs V, which this kernel
+  // then does not read.)  A row with |beta_t| < 1e-20 (where U_t no longer
+  // carries r_t) takes the three-term form, with V loaded for that row only.
   {
     constexpr int V = Vec16<E>::N;
     constexpr int PER_ROW = D / V;
@@ -728,18 +737,29 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
     for (int i = 0; i < RegTile<kW4, C, D, E>::ITER; ++i) {
       const int idx = tid + i * kW4;
       const int r = idx / PER_ROW, c = (idx % PER_ROW) * V;
-      float b[V], v[V];
+      float b[V], u[V];
       Vec16<E>::unpack(rdBv.r[i], b);
-      Vec16<E>::unpack(rV.r[i], v);
-      float part = 0.f;
+      Vec16<E>::unpack(rU.r[i], u);
+      const float br = sBeta[r];
+      float part = 0.f, pv = 0.f;
 #pragma unroll
-      for (int e = 0; e < V; ++e) part += b[e] * v[e];
+      for (int e = 0; e < V; ++e) part += b[e] * u[e];
+      if (r < len && !(fabsf(br) >= 1e-20f)) {  // rare: the value part from V itself
+        float v[V];
+        Vec16<E>::load(static_cast<const E*>(p.v) + row0 * D + r * gs + c, v);
+#pragma unroll
+        for (int e = 0; e < V; ++e) pv += b[e] * v[e];
+      }
       part += __shfl_xor(part, 1);
       part += __shfl_xor(part, 2);
       part += __shfl_xor(part, 4);
       if constexpr (PER_ROW == 16) part += __shfl_xor(part, 8);
-      sDb1[r] = part;  // the row's lanes all hold the sum: unconditional, no branch
-      const float br = sBeta[r];
+      pv += __shfl_xor(pv, 1);
+      pv += __shfl_xor(pv, 2);
+      pv += __shfl_xor(pv, 4);
+      if constexpr (PER_ROW == 16) pv += __shfl_xor(pv, 8);
+      sDb1[r] = part;  // the row's lanes all hold the sums: unconditional, no branch
+      sDbV[r] = pv;
 #pragma unroll
       for (int e = 0; e < V; ++e) b[e] *= br;
       if (r < len) store_vec<V>(dvo + r * gs + c, b);
@@ -1019,12 +1039,14 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
   __syncthreads();
   if (tid < len) {
     const int64_t idx = (int64_t)(ci.start + tid) * H + hh;
-    float g = 0.f, b = sDb1[tid];
+    const float bt = sBeta[tid];
+    float g = 0.f, b3 = sDbV[tid];  // the three-term form (|beta| < 1e-20)
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       g += sRowG[w * C + tid];
-      b += sRowB[w * C + tid];
+      b3 += sRowB[w * C + tid];
     }
+    const float b = fabsf(bt) >= 1e-20f ? sDb1[tid] / bt : b3;
     if (tid == len - 1) {
       float hd_sum = 0.f, kg_sum = 0.f;
 #pragma unroll
@@ -1128,7 +1150,6 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   const int64_t row0 = (int64_t)ci.start * H + hh;
 
   E* sU = reinterpret_cast<E*>(smem + L::off_U);
-  E* sV = reinterpret_cast<E*>(smem + L::off_V);
   float* sG = reinterpret_cast<float*>(smem + L::off_U);
   E* sT = reinterpret_cast<E*>(smem + L::off_T);
   E* sdO = reinterpret_cast<E*>(smem + L::off_dO);
@@ -1179,13 +1200,12 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   // beta first: its LDS store below then waits for this load only
   const float bval = p.beta[(int64_t)(ci.start + min(tid & (C - 1), len - 1)) * H + hh];
   {
-    RegTile<kFW, C, D, T> rU, rdO, rdU, rV;
+    RegTile<kFW, C, D, T> rU, rdO, rdU;
     RegTile<kFW, C, C, T> rT;
     TiledTile<kFW, D, T> rH;
     rU.load(static_cast<const T*>(p.u) + row0 * D, gs, len);
     rdO.load(static_cast<const T*>(p.dO) + row0 * D, gs, len);
     rdU.load(static_cast<const T*>(p.du) + row0 * D, gs, len);
-    rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
     rT.load(static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, len);
     rH.load(hsrc);
     rK.load(kg_, gs, len);
@@ -1195,14 +1215,23 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     rU.store(sU, L::LD);
     rdO.store(sdO, L::LD);
     rdU.store(sdU, L::LD);
-    rV.store(sV, L::LD);
     rT.store(sT, L::LDC);
     rH.store(sH, L::LD);
   }
   __syncthreads();
 
   f32x4 dq[HCT], dk[HCT], dv[HCT], dkws[HCT];
-  float db[4] = {0.f, 0.f, 0.f, 0.f};
+  // dbeta_t = sum_c dBv[t,c] U[t,c] / beta_t (every beta-dependent quantity of
+  // the chunk is row t scaled by beta_t, so U_t = beta_t r_t and the adjoint
+  // of the row is dBv_t); db gathers the three-term form (dBv V, the Bw and
+  // the Akk parts), which rows with |beta_t| < 1e-20 take, their V alone read
+  float db[4] = {0.f, 0.f, 0.f, 0.f}, dbu[4] = {0.f, 0.f, 0.f, 0.f};
+  bool tiny[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = r0 + acc_row(lane, e);
+    tiny[e] = r < len && !(fabsf(sBeta[r]) >= 1e-20f);
+  }
   const int kbeg = kfloor<E>(r0);
   // ---- phase 1: dQg = dO S0^T, dAqk = dO U^T, dBv = T^T dU ------------------------
   // (dk's WY part goes through dBv too: with (Bv - Bw S0) = T^-1 U,
@@ -1225,7 +1254,11 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     mma_tile_range<E, COL, ROW>(acv, sT, L::LDC, r0, sdU, L::LD, 16 * ct, kbeg, C, lane);  // dBv = T^T dU
     dv[j] = acv;  // dBv until it is in LDS
 #pragma unroll
-    for (int e = 0; e < 4; ++e) db[e] += acv[e] * from_e<E>(sV[(r0 + acc_row(lane, e)) * L::LD + c]);
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + acc_row(lane, e);
+      dbu[e] += acv[e] * from_e<E>(sU[r * L::LD + c]);
+      if (tiny[e]) db[e] += acv[e] * io<T>::load(static_cast<const T*>(p.v) + row0 * D + (int64_t)r * gs + c);
+    }
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -1697,14 +1730,23 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       dkws[t] = dkws[t + 1];
     }
   }
-  float* sRowB = sRed;  // [2][64]
+  float* sRowB = sRed;          // [2][64] the three-term form
+  float* sRowU = sRed + 2 * C;  // [2][64] sum_c dBv U
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float b = group16_sum(db[e]);
-    if ((lane & 15) == 0) sRowB[ch * C + r0 + acc_row(lane, e)] = b;
+    const float bu = group16_sum(dbu[e]);
+    if ((lane & 15) == 0) {
+      sRowB[ch * C + r0 + acc_row(lane, e)] = b;
+      sRowU[ch * C + r0 + acc_row(lane, e)] = bu;
+    }
   }
   __syncthreads();
-  if (tid < len) p.dbeta[(int64_t)(ci.start + tid) * H + hh] = sRowB[tid] + sRowB[C + tid];
+  if (tid < len) {
+    const float bt = sBeta[tid];
+    p.dbeta[(int64_t)(ci.start + tid) * H + hh] =
+        fabsf(bt) >= 1e-20f ? (sRowU[tid] + sRowU[C + tid]) / bt : sRowB[tid] + sRowB[C + tid];
+  }
 }
 
 template <typename T, int D, typename OT, typename OK>

@@ -238,10 +238,20 @@ def test_chunk_forward_varlen(dev, dtype):
     assert torch.equal(S[1].cpu(), S0[1])
 
 
-def _grad_case(dev, B, T, H, D, dtype, seed, cu=None, S0_scale=0.02):
+def _vanishing_beta(beta):
+    """A tenth of the tokens with beta = 0 and another tenth with 1e-25."""
+    beta = beta.clone()
+    beta[:, 3::10] = 0.0
+    beta[:, 8::10] = 1e-25
+    return beta
+
+
+def _grad_case(dev, B, T, H, D, dtype, seed, cu=None, S0_scale=0.02, beta_fn=None):
     from delta_feedback_experiment_amd.chunk import chunk_pkda
 
     q, k, v, g, beta = make_inputs(B, T, H, D, dtype, seed=seed, strong=True)
+    if beta_fn is not None:
+        beta = beta_fn(beta)
     N = B if cu is None else cu.numel() - 1
     gen = torch.Generator().manual_seed(seed + 100)
     S0 = S0_scale * torch.randn(N, H, D, D, generator=gen)
@@ -272,6 +282,21 @@ def test_chunk_gradients_match_oracle(dev, D, dtype):
     tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
     for name, val in res.items():
         assert val < tol, (name, val)
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_chunk_dbeta_with_vanishing_beta(dev, per_channel):
+    """The BF16 chunk backward forms dbeta_t as sum_c dBv[t,c] U[t,c] / beta_t
+    (U_t is beta_t times a beta_t-free residual, and dBv_t is that row's
+    adjoint); rows with |beta_t| < 1e-20 -- here exact zeros and 1e-25, a
+    tenth of the tokens each -- take the three-term form from V instead.
+    Every gradient still matches the oracle, through the four-wave (per-head
+    gate) and the per-channel backward, at d = 128 with a partial chunk."""
+    print(f"[gpu] dbeta with vanishing beta, per_channel={per_channel}", flush=True)
+    case = _grad_case_pc if per_channel else _grad_case
+    res = case(dev, 2, 200, 2, 128, torch.bfloat16, seed=13, beta_fn=_vanishing_beta)
+    for name, val in res.items():
+        assert val < BF16_TOL, (name, val)
 
 
 def test_chunk_gradients_varlen(dev):
@@ -354,10 +379,12 @@ def test_chunk_per_channel_gate_matches_oracle(dev, D, dtype):
         assert val < tol, (name, val)
 
 
-def _grad_case_pc(dev, B, T, H, D, dtype, seed, cu=None, all_strong=False):
+def _grad_case_pc(dev, B, T, H, D, dtype, seed, cu=None, all_strong=False, beta_fn=None):
     from delta_feedback_experiment_amd.chunk import chunk_pkda
 
     q, k, v, g, beta = make_inputs(B, T, H, D, dtype, seed=seed, strong=True, per_channel=True)
+    if beta_fn is not None:
+        beta = beta_fn(beta)
     if all_strong:
         g = torch.full_like(g, -8.0)
     N = B if cu is None else cu.numel() - 1
