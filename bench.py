@@ -11,8 +11,13 @@ per-head log-decay, returning dq, dk, dv, dbeta, dg).  Inputs are resident in
 HBM before the timed region starts.
 
 Printed as ONE JSON line:
-  value           tokens/s of the whole fwd+bwd step (K steps between two
-                  synchronised events);
+  value           tokens/s of the whole fwd+bwd step: K steps between two
+                  synchronised events, as K replays of the step captured in a
+                  HIP graph or as K eager steps after W warm-up steps on the
+                  warm GPU, whichever is faster (``timing`` names it; on this
+                  ROCm a graph replay costs ~10 us per kernel over the same
+                  launches issued eagerly, and the eager step's host work
+                  stays behind the GPU's);
   roofline        the dominant kernel of the step, timed with HIP events on
                   the stream it runs on.  Both of its rates are measured --
                   algorithmic flops per launch (per token-head figures below)
@@ -824,9 +829,11 @@ def bench_production(dev: torch.device, steps: int = 10, warmup: int = 3) -> dic
     205-236): every output and gradient finite, and two backwards
     accumulated in FP32 and halved equal to one (deterministic kernels: FP32
     rounding only).  Agreement with the oracle on a slice runs in the CPU
-    leg.  Timing: eager, then one step captured in a HIP graph and replayed
-    (median and minimum replay).  Flops are reported on the same fixed
-    per-token-head convention as the headline step."""
+    leg.  Timing: one step captured in a HIP graph and replayed K times back
+    to back, then K eager steps after the warm-up; the faster K-step timing
+    is reported (the median and minimum replay beside it).  Flops are
+    reported on the same fixed per-token-head convention as the headline
+    step."""
     from delta_feedback_experiment_amd import pkda_recurrence
 
     B, T, H, D = 8, 4096, 16, 128
@@ -850,6 +857,9 @@ def bench_production(dev: torch.device, steps: int = 10, warmup: int = 3) -> dic
     del o, first, sinks
     print(f"[bench] production checks {json.dumps(checks)}", file=sys.stderr, flush=True)
 
+    # K graph replays back to back, then K eager steps after the warm-up, as
+    # for the headline step: the faster of the two K-step timings
+    graph = capture_replays(step, steps, warmup)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -860,8 +870,8 @@ def bench_production(dev: torch.device, steps: int = 10, warmup: int = 3) -> dic
     t1.record()
     torch.cuda.synchronize()
     ms_eager = t0.elapsed_time(t1) / steps
-    graph = capture_replays(step, steps, warmup)
-    ms = graph["median_ms"] if graph["agree"] else ms_eager
+    use_graph = graph["agree"] and graph["ms_per_step"] < ms_eager
+    ms = graph["ms_per_step"] if use_graph else ms_eager
     stage_ms = time_production_stages([x.detach() for x in leaves], do, D ** -0.5, steps)
     # dominant kernel: the per-channel fused backward, priced on the products
     # it shares with the per-head kernel (its pair terms come on top)
@@ -873,7 +883,8 @@ def bench_production(dev: torch.device, steps: int = 10, warmup: int = 3) -> dic
                     "preconditioner x=1.5, fwd+bwd of all ten inputs",
         "ms_per_step": ms, "ms_per_step_eager": ms_eager, "median_ms": graph["median_ms"], "min_ms": graph["min_ms"],
         "graph_ms_per_step": graph["ms_per_step"], "graph_replays_agree": graph["agree"],
-        "timing": "HIP graph replays, median" if graph["agree"] else "eager",
+        "timing": (f"HIP graph, {steps} replays back to back" if use_graph
+                   else f"eager, {steps} steps back to back after {warmup} warm-up steps"),
         "tokens_per_s": B * T / (ms / 1e3),
         "mfma_frac_step": B * T * H * step_flops_convention(D) / (ms / 1e3) / MFMA_BF16_PEAK,
         "checks": checks, "stage_ms": stage_ms, "stage_kernels": PRODUCTION_STAGE_KERNEL, "roofline": roofline,
@@ -1166,19 +1177,26 @@ def main() -> None:
         base, agreement = cpu_baseline(inp, D=w["D"], H=w["H"], T=args.cpu_tokens, budget_s=args.cpu_seconds)
     checks = step_checks(inp)
     print(f"[bench] checks {json.dumps(checks)}", file=sys.stderr, flush=True)
-    ms_eager = time_step(inp, args.steps, args.warmup)
-    print(f"[bench] fwd+bwd eager {ms_eager:.3f} ms/step", file=sys.stderr, flush=True)
-    ms, graph_ok, timing, graph = ms_eager, None, "eager", None
+    # Two timings of K whole steps: K replays of the step captured as a HIP
+    # graph, then W eager warm-up steps and K eager steps back to back (after
+    # the graph, so neither runs on a GPU still at its idle clocks).  A graph
+    # replay costs ~10 us per kernel on this ROCm beyond the same launches
+    # issued eagerly, and the eager step's host work (0.33 ms) stays behind
+    # the GPU's; `value` is the faster of the two and `timing` says which.
+    graph_ok, graph = None, None
     if not args.no_graph:
         try:
             graph = time_step_graph(inp, args.steps, args.warmup)
             graph_ok = graph["agree"]
             print(f"[bench] fwd+bwd graph {graph['ms_per_step']:.3f} ms/step, median {graph['median_ms']:.3f}, "
                   f"min {graph['min_ms']:.3f} (replays agree: {graph_ok})", file=sys.stderr, flush=True)
-            if graph_ok:
-                ms, timing = graph["ms_per_step"], f"HIP graph, {args.steps} replays back to back"
         except RuntimeError as exc:  # capture unsupported here: report eager
             print(f"[bench] graph capture failed ({exc}); reporting eager timing", file=sys.stderr, flush=True)
+    ms_eager = time_step(inp, args.steps, args.warmup)
+    print(f"[bench] fwd+bwd eager {ms_eager:.3f} ms/step", file=sys.stderr, flush=True)
+    ms, timing = ms_eager, f"eager, {args.steps} steps back to back after {args.warmup} warm-up steps"
+    if graph_ok and graph["ms_per_step"] < ms_eager:
+        ms, timing = graph["ms_per_step"], f"HIP graph, {args.steps} replays back to back"
     per_th = stage_flops(w["D"])
     token_heads = ntok * w["H"]
     step_flops = token_heads * step_flops_convention(w["D"])
@@ -1258,7 +1276,8 @@ def main() -> None:
         result["production"] = bench_production(dev, args.steps, args.warmup)
         c = result["production"]
         print(f"[bench] production operator {c['ms_per_step']:.3f} ms/step ({c['timing']}; eager "
-              f"{c['ms_per_step_eager']:.3f}, min {c['min_ms']:.3f}, replays agree {c['graph_replays_agree']}) "
+              f"{c['ms_per_step_eager']:.3f}, graph {c['graph_ms_per_step']:.3f}, replay median {c['median_ms']:.3f}, "
+              f"min {c['min_ms']:.3f}, replays agree {c['graph_replays_agree']}) "
               f"({c['tokens_per_s'] / 1e6:.2f} M tok/s); stages (ms): "
               f"{json.dumps({n: round(t, 4) for n, t in c['stage_ms'].items()})}", file=sys.stderr, flush=True)
         inp = None
