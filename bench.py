@@ -127,8 +127,8 @@ def step_flops_convention(D: int, C: int = CHUNK) -> int:
 # as rocprofv3 names it (template arguments with bf16 for unsigned short).
 STAGE_KERNEL = {
     "fwd_intra": "chunk_intra_fwd_kernel<bf16, 128, true, false>",
-    "fwd_state": "chunk_state_fwd_rr_kernel<128, 64, true>",
-    "bwd_state": "chunk_state_bwd_rr_kernel<128, 64, true>",
+    "fwd_state": "chunk_state_fwd_rr_kernel<128, 64, true, true>",
+    "bwd_state": "chunk_state_bwd_rr_kernel<128, 64, true, true>",
     "bwd_chunk": "chunk_fused_bwd_w4_kernel<128>",
     "decode": "decode_kernel<bf16, 128, 512>",
 }
@@ -442,7 +442,8 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
     bf = dict(device=dev, dtype=torch.bfloat16)
     f32 = dict(device=dev, dtype=torch.float32)
     o, wbuf, ubuf = torch.empty(ntok, H, D, **bf), torch.empty(ntok, H, D, **bf), torch.empty(ntok, H, D, **bf)
-    aqk, akk = torch.empty(ntok, H, CHUNK, **bf), torch.empty(ntok, H, CHUNK, **bf)
+    # Aqk and T packed (their ten lower blocks per chunk), as the step stores them
+    aqk, akk = torch.empty(plan.num_chunks, H, 10, 256, **bf), torch.empty(plan.num_chunks, H, 10, 256, **bf)
     h = torch.empty(plan.num_chunks, H, D, D, **bf)
     dh = torch.empty(plan.num_chunks, H, D, D, **bf)
     du = torch.empty(ntok, H, D, **bf)
@@ -453,7 +454,7 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
     fa = _lib.ChunkFwdArgs(
         dtype=_lib.PKDA_BF16, **plan.common(), q=_ptr(q), k=_ptr(k), kw=_ptr(k), v=_ptr(v), gcum=_ptr(gcum),
         gate_per_channel=0, beta=_ptr(beta), scale=scale, initial_state=_ptr(s0), final_state=None, o=_ptr(o),
-        w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h),
+        w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), tri_packed=1,
     )
     ba = _lib.ChunkBwdArgs(
         dtype=_lib.PKDA_BF16, **plan.common(), q=_ptr(q), k=_ptr(k), kw=_ptr(k), v=_ptr(v), gcum=_ptr(gcum),
@@ -461,6 +462,7 @@ def time_stages(inp: dict, w: dict, steps: int) -> dict[str, float]:
         w=_ptr(wbuf), u=_ptr(ubuf), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), do=_ptr(do), dht=None, dh=_ptr(dh),
         du=_ptr(du), dq=_ptr(dq), dk=_ptr(dk), dkw=None, dv=_ptr(dv),
         dbeta=_ptr(dbeta), dgcum=_ptr(dgcum), dh0=None, grad_dtype=_lib.PKDA_BF16, key_grad_dtype=_lib.PKDA_BF16,
+        tri_packed=1,
     )
     return _event_stages(fa, ba, _stream(dev), steps)
 

@@ -23,7 +23,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 class RecurrentArgs(ctypes.Structure):
@@ -88,7 +88,7 @@ class ChunkFwdArgs(ctypes.Structure):
         ("final_state", c_void_p), ("o", c_void_p),
         ("w", c_void_p), ("u", c_void_p), ("aqk", c_void_p), ("akk", c_void_p), ("h", c_void_p),
         ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p),
-        ("slot_idx", c_void_p), ("pool_size", c_int64), ("gcum_lo", c_void_p),
+        ("slot_idx", c_void_p), ("pool_size", c_int64), ("gcum_lo", c_void_p), ("tri_packed", c_int32),
     ]
 
 
@@ -99,7 +99,7 @@ class ChunkBwdArgs(ctypes.Structure):
         ("dq", c_void_p), ("dk", c_void_p), ("dkw", c_void_p), ("dv", c_void_p),
         ("dbeta", c_void_p), ("dgcum", c_void_p), ("dh0", c_void_p),
         ("stages", c_int32), ("qg", c_void_p), ("kg", c_void_p), ("grad_dtype", c_int32),
-        ("key_grad_dtype", c_int32), ("kw32", c_void_p), ("gcum_lo", c_void_p),
+        ("key_grad_dtype", c_int32), ("kw32", c_void_p), ("gcum_lo", c_void_p), ("tri_packed", c_int32),
     ]
 
 

@@ -157,20 +157,31 @@ class FwdSaved:
     h: Tensor | None
     qg: Tensor | None = None   # per-channel gates: scale e^G q
     kg: Tensor | None = None   # per-channel gates: e^{G_last - G} kw
+    tri_packed: bool = False   # aqk, akk as each chunk's ten lower 16 x 16 blocks (:func:`tri_packed`)
+
+
+def tri_packed(q: Tensor, k: Tensor, kw: Tensor, gcum: Tensor) -> bool:
+    """Whether Aqk and T are stored packed -- only the ten 16 x 16 blocks on
+    and below each chunk's diagonal, ``[num_chunks, H, 10, 256]`` -- which
+    the kernels do for BF16 with a per-head gate and no separate write key
+    (3/8 fewer bytes to write and to read back twice)."""
+    return q.dtype == torch.bfloat16 and gcum.dim() == 2 and kw.data_ptr() == k.data_ptr()
 
 
 def chunk_forward(
     plan: ChunkPlan, q: Tensor, k: Tensor, kw: Tensor, v: Tensor, gcum: Tensor, beta32: Tensor,
     scale: float, initial_state: Tensor | None, output_final_state: bool, save_states: bool,
     *, slot_idx: Tensor | None = None, final_state: Tensor | None = None, out: Tensor | None = None,
-    gcum_lo: Tensor | None = None,
+    gcum_lo: Tensor | None = None, pack_triangular: bool | None = None,
 ) -> tuple[Tensor, Tensor | None, FwdSaved]:
     """Run the chunk forward on flat ``[N_tok, H, D]`` operands.
 
     With ``slot_idx`` (int32 ``[N]``) the states are rows of a pool:
     ``initial_state`` (or zero when ``None``) and ``final_state`` are
     ``[P, H, D, D]`` and document ``n`` uses row ``slot_idx[n]`` of each.
-    ``gcum_lo``: the gate's FP64 remainder (:func:`wants_gcum_lo`)."""
+    ``gcum_lo``: the gate's FP64 remainder (:func:`wants_gcum_lo`).
+    ``pack_triangular``: None stores Aqk and T packed where :func:`tri_packed`
+    allows it; False keeps them ``[N_tok, H, 64]`` (the same values)."""
     dev = q.device
     N, H, D = plan.num_seqs, plan.heads, plan.head_dim
     o = torch.empty_like(v) if out is None else out
@@ -178,8 +189,12 @@ def chunk_forward(
     # BF16 with a per-head gate: the state passes form W S and W^T dU from T and k
     w = None if (q.dtype == torch.bfloat16 and not per_channel) else torch.empty_like(k)
     u = torch.empty_like(v)
-    aqk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
-    akk = torch.empty(plan.num_tokens, H, CHUNK_SIZE, device=dev, dtype=q.dtype)
+    tri = tri_packed(q, k, kw, gcum) if pack_triangular is None else bool(pack_triangular)
+    if tri and not tri_packed(q, k, kw, gcum):
+        raise ValueError("Aqk and T are stored packed only for BF16, a per-head gate and kw is k")
+    tshape = (plan.num_chunks, H, 10, 256) if tri else (plan.num_tokens, H, CHUNK_SIZE)
+    aqk = torch.empty(tshape, device=dev, dtype=q.dtype)
+    akk = torch.empty(tshape, device=dev, dtype=q.dtype)
     h = torch.empty(plan.num_chunks, H, D, D, device=dev, dtype=q.dtype) if save_states else None
     if slot_idx is not None:
         S_T = final_state
@@ -194,9 +209,10 @@ def chunk_forward(
         initial_state=_ptr(initial_state), final_state=_ptr(S_T), o=_ptr(o),
         w=_ptr(w), u=_ptr(u), aqk=_ptr(aqk), akk=_ptr(akk), h=_ptr(h), qg=_ptr(qg), kg=_ptr(kg),
         slot_idx=_ptr(slot_idx), pool_size=0 if S_T is None else S_T.shape[0], gcum_lo=_ptr(gcum_lo),
+        tri_packed=int(tri),
     )
     _lib.call("pkda_chunk_fwd", args, _stream(dev))
-    return o, S_T, FwdSaved(w, u, aqk, akk, h, qg, kg)
+    return o, S_T, FwdSaved(w, u, aqk, akk, h, qg, kg, tri)
 
 
 @dataclass
@@ -257,7 +273,7 @@ def chunk_backward(
         dh0=_ptr(dh0), qg=_ptr(saved.qg), kg=_ptr(saved.kg),
         grad_dtype=_lib.PKDA_F32 if grad_dtype == torch.float32 else _dtype_code(q),
         key_grad_dtype=_lib.PKDA_F32 if key_grad_dtype == torch.float32 else _dtype_code(q),
-        kw32=_ptr(kw32), gcum_lo=_ptr(gcum_lo),
+        kw32=_ptr(kw32), gcum_lo=_ptr(gcum_lo), tri_packed=int(saved.tri_packed),
     )
     if kw32 is not None and (kw32.dtype != torch.float32 or kw32.shape != kw.shape or not kw32.is_contiguous()):
         raise ValueError("kw32 must be a contiguous float32 tensor of kw's shape")
@@ -373,6 +389,7 @@ class _ChunkPKDA(torch.autograd.Function):
             # (none through ctx attributes: A_T is an output, and keeping the
             # scan state on ctx would tie output -> grad_fn -> ctx -> output)
             fwd = (None,) * 7 if lean else (saved.w, saved.u, saved.aqk, saved.akk, saved.h, saved.qg, saved.kg)
+            ctx.tri_packed = saved.tri_packed
             ctx.save_for_backward(qf, kf, kwf, vf, gcum, beta32, s0, g_used, A_log32, dt32,
                                   None if g_atk is None else _f32(g_atk),
                                   None if beta_atk is None else _f32(beta_atk),
@@ -396,7 +413,7 @@ class _ChunkPKDA(torch.autograd.Function):
             _, _, saved = chunk_forward(plan, qf, kf, kwf, vf, gcum, beta32, ctx.scale, s0, False, True,
                                         gcum_lo=gcum_lo)
         else:
-            saved = FwdSaved(*fwd)
+            saved = FwdSaved(*fwd, tri_packed=ctx.tri_packed)
         pstate = pre.PrecondState(kwf, a_chunk, None, None, kw32) if ctx.precond else None
         dof = _flat(do.to(qf.dtype).contiguous(), plan)
         dht = None if dS_T is None else dS_T.float().contiguous()

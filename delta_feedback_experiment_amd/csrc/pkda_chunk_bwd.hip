@@ -71,6 +71,7 @@ struct BwdParams {
   const void* kg;  // per-channel gates: e^{G_last - G} kw
   const float* kw32;  // per-channel gates: kw in FP32 (BF16 kw otherwise), or null
   const float* gcum_lo;  // FP32 per-channel gates, optional: gcum's FP64 remainder
+  bool tri_packed;       // BF16, per-head gate, kw = k: Aqk and T as their ten lower blocks
 };
 
 // Deterministic sum of one value per thread over an NT-thread workgroup.
@@ -650,12 +651,6 @@ struct FusedW4Layout {
   static_assert(2 * bytes <= 160 * 1024, "two workgroups per compute unit");
 };
 
-// The lower 16 x 16 tiles (tb >= sb) of a [64 x 64] chunk matrix, numbered
-// 0..9, dealt to the four waves as w, w + 4, w + 8.
-__device__ __forceinline__ void lower_tile(int i, int& tb, int& sb) {
-  tb = i < 1 ? 0 : i < 3 ? 1 : i < 6 ? 2 : 3;
-  sb = i - tb * (tb + 1) / 2;
-}
 
 // The body for one chunk; `len` is a literal C for whole chunks (every chunk
 // of a document but its last), so every row test folds away and no branch
@@ -809,7 +804,7 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
     const int i = wave + 4 * u;
     if (i < 10) {
       int tb, sb;
-      lower_tile(i, tb, sb);
+      lower_block(i, tb, sb);
       f32x4 acc = zero4();
 #pragma unroll
       for (int kk = 0; kk < KV; ++kk)
@@ -904,7 +899,7 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
     const int i = wave + 4 * u;
     if (i < 10) {
       int tb, sb;
-      lower_tile(i, tb, sb);
+      lower_block(i, tb, sb);
       f32x4 acc = zero4();
 #pragma unroll
       for (int kk = 0; kk < KV; ++kk)
@@ -1808,7 +1803,7 @@ struct RrBwdLayout {
 
 constexpr int kRrLoadersBwd = 4;  // two groups of two waves
 
-template <int D, int BV, bool ALIAS>
+template <int D, int BV, bool ALIAS, bool PACK>
 __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bwd_rr_kernel(BwdParams p) {
   using L = RrBwdLayout<D, BV, ALIAS>;
   using T = bf16_t;
@@ -1830,9 +1825,17 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
     const int lgroup = (tid - 64 * NC) / NGT;  // takes visits s with s % 2 == lgroup
     const int lt = (tid - 64 * NC) % NGT;
     RegTile<NGT, C, D, T> rQ, rKW, rK;
-    RegTile<NGT, C, C, T> rA, rT;
+    std::conditional_t<PACK, TriRegTile<NGT>, RegTile<NGT, C, C, T>> rA, rT;
     RegTile<NGT, C, BV, T> rdO;
     float rg = 0.f, rb = 0.f;
+    if constexpr (PACK) {  // the stages' blocks above the diagonal: zero once
+      const int lt2 = tid - 64 * NC;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        zero_upper_blocks<2 * NGT>(lt2, reinterpret_cast<T*>(smem + b * L::BUF + L::off_A), L::LDC);
+        zero_upper_blocks<2 * NGT>(lt2, reinterpret_cast<T*>(smem + b * L::BUF + L::off_T), L::LDC);
+      }
+    }
     auto load = [&](int s) {
       const int jc = count - 1 - s;
       const int cstart = dstart + jc * C;
@@ -1841,8 +1844,14 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       rQ.load_as(lt, static_cast<const T*>(p.q) + row0 * D, gs, clen);
       rKW.load_as(lt, static_cast<const T*>(p.kw) + row0 * D, gs, clen);
       if (!ALIAS) rK.load_as(lt, static_cast<const T*>(p.k) + row0 * D, gs, clen);
-      rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
-      rT.load_as(lt, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, clen);
+      if constexpr (PACK) {
+        const int64_t tri0 = ((int64_t)(first + jc) * H + h) * kTriElems;
+        rA.load_as(lt, static_cast<const T*>(p.aqk) + tri0);
+        rT.load_as(lt, static_cast<const T*>(p.akk) + tri0);
+      } else {
+        rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+        rT.load_as(lt, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, clen);
+      }
       rdO.load_as(lt, static_cast<const T*>(p.dO) + row0 * D + v0, gs, clen);
       if (lt < C) {
         const int64_t gi = (int64_t)(cstart + min(lt, clen - 1)) * H + h;
@@ -2059,9 +2068,9 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
   }
 }
 
-template <int D, int BV, bool ALIAS>
+template <int D, int BV, bool ALIAS, bool PACK = false>
 int launch_state_bwd_rr_as(const BwdParams& p, hipStream_t s) {
-  auto kern = chunk_state_bwd_rr_kernel<D, BV, ALIAS>;
+  auto kern = chunk_state_bwd_rr_kernel<D, BV, ALIAS, PACK>;
   constexpr int bytes = RrBwdLayout<D, BV, ALIAS>::bytes;
   if (int st = set_smem(kern, bytes)) return st;
   hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoadersBwd)), bytes, s, p);
@@ -2075,6 +2084,9 @@ int launch_state_bwd_rr(const BwdParams& p, hipStream_t s) {
   const int N = p.geom.num_seqs;
   if (N <= 0) return 0;
   const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
+  if (p.tri_packed) {  // kw = k (checked at the entry point)
+    return narrow ? launch_state_bwd_rr_as<D, 32, true, true>(p, s) : launch_state_bwd_rr_as<D, 64, true, true>(p, s);
+  }
   if (narrow) return p.kw_is_k ? launch_state_bwd_rr_as<D, 32, true>(p, s) : launch_state_bwd_rr_as<D, 32, false>(p, s);
   return p.kw_is_k ? launch_state_bwd_rr_as<D, 64, true>(p, s) : launch_state_bwd_rr_as<D, 64, false>(p, s);
 }
@@ -2404,6 +2416,9 @@ extern "C" int pkda_chunk_bwd(const pkda_chunk_bwd_args* a, void* stream) {
   p.qg = a->gate_per_channel ? a->qg : nullptr;
   p.kg = a->gate_per_channel ? a->kg : nullptr;
   p.kw32 = a->gate_per_channel && !kw_is_k && a->dtype == PKDA_BF16 ? a->kw32 : nullptr;
+  p.tri_packed = a->tri_packed != 0;
+  PKDA_REQUIRE(!p.tri_packed || (a->dtype == PKDA_BF16 && !a->gate_per_channel && kw_is_k), PKDA_EUNSUPPORTED,
+               "packed aqk / akk (tri_packed) are built for BF16 with a per-head gate and kw == k");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   if (a->dtype == PKDA_BF16) {

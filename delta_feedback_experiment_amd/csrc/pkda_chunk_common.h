@@ -682,6 +682,86 @@ __device__ __forceinline__ void store_acc_global(T* g, int64_t gstride, const f3
   AccStore<T, FULL>::run(g, gstride, acc, m0, n0, nvalid, lane);
 }
 
+// ----------------------------------------------------------------------------
+// Lower-triangular chunk matrices stored packed (T and Aqk of the BF16 per-head
+// path with kw = k): per (chunk, head) the ten 16 x 16 blocks on and below the
+// diagonal, block by block in lower_block order, each row-major -- 10 x 256
+// BF16, 5 KB instead of 8 KB.  Rows past a chunk's end hold zeros; the six
+// blocks above the diagonal are not stored (their LDS copies are zeroed once).
+// ----------------------------------------------------------------------------
+constexpr int kTriBlocks = 10;
+constexpr int kTriElems = kTriBlocks * 256;
+
+// Row and column block of lower block i (0..9) of a 64 x 64 chunk matrix,
+// row-block-major, and of upper block u (0..5).
+__device__ __forceinline__ void lower_block(int i, int& tb, int& sb) {
+  tb = i < 1 ? 0 : i < 3 ? 1 : i < 6 ? 2 : 3;
+  sb = i - tb * (tb + 1) / 2;
+}
+__device__ __forceinline__ void upper_block(int u, int& tb, int& sb) {
+  tb = u < 3 ? 0 : u < 5 ? 1 : 2;
+  sb = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
+}
+
+// A packed lower-triangular tile in registers, 16-byte pieces shared by NT
+// threads (piece p: block p / 32, row (p % 32) / 2, columns 8 (p % 2) ..).
+template <int NT>
+struct TriRegTile {
+  static constexpr int TOTAL = kTriBlocks * 32;
+  static constexpr int ITER = (TOTAL + NT - 1) / NT;
+  uint4 r[ITER];
+  __device__ __forceinline__ void load_as(int t, const bf16_t* g) {
+    __builtin_assume(t >= 0 && t < NT);
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int idx = t + i * NT;
+      r[i] = (TOTAL % NT == 0 || idx < TOTAL) ? *reinterpret_cast<const uint4*>(g + 8 * idx) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  // into a [64][ld] LDS tile (its upper blocks are left as they are)
+  __device__ __forceinline__ void store_as(int t, bf16_t* lds, int ld) const {
+    __builtin_assume(t >= 0 && t < NT);
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int idx = t + i * NT;
+      if (TOTAL % NT != 0 && idx >= TOTAL) break;
+      int tb, sb;
+      lower_block(idx >> 5, tb, sb);
+      const int row = (idx & 31) >> 1, half = idx & 1;
+      *reinterpret_cast<uint4*>(lds + (16 * tb + row) * ld + 16 * sb + 8 * half) = r[i];
+    }
+  }
+};
+
+// Zeros into the six blocks above the diagonal of a [64][ld] BF16 LDS tile,
+// pieces t, t + NT, ... of the 192.
+template <int NT>
+__device__ __forceinline__ void zero_upper_blocks(int t, bf16_t* lds, int ld) {
+  for (int idx = t; idx < 6 * 32; idx += NT) {
+    int tb, sb;
+    upper_block(idx >> 5, tb, sb);
+    const int row = (idx & 31) >> 1, half = idx & 1;
+    *reinterpret_cast<uint4*>(lds + (16 * tb + row) * ld + 16 * sb + 8 * half) = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// The ten lower blocks of an FP32 [64][ldf] LDS tile to packed BF16 in
+// global memory, rows >= nvalid as zeros (NT threads, one 16-byte piece each).
+template <int NT>
+__device__ __forceinline__ void store_tri_from_f32(bf16_t* g, const float* lds, int ldf, int nvalid) {
+  for (int idx = threadIdx.x; idx < kTriBlocks * 32; idx += NT) {
+    int tb, sb;
+    lower_block(idx >> 5, tb, sb);
+    const int r = 16 * tb + ((idx & 31) >> 1), c = 16 * sb + 8 * (idx & 1);
+    const float4 a = *reinterpret_cast<const float4*>(lds + r * ldf + c);
+    const float4 b = *reinterpret_cast<const float4*>(lds + r * ldf + c + 4);
+    const uint4 w = r < nvalid ? make_uint4(pack_bf16x2_(a.x, a.y), pack_bf16x2_(a.z, a.w), pack_bf16x2_(b.x, b.y),
+                                            pack_bf16x2_(b.z, b.w))
+                               : make_uint4(0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4*>(g + 8 * idx) = w;
+  }
+}
+
 // Output tiles of a loop that produces one 16-column tile per pass with long
 // work in between.  A BF16 tile row is a 32-byte piece; stored alone, long
 // before the row's next piece, it reaches memory as a partial line (the

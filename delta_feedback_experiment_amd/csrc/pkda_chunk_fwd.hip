@@ -52,6 +52,7 @@ struct FwdParams {
   void* kg;   // per-channel gates: e^{G_last - G} kw
   const int32_t* slot;  // document -> state row (slot-indexed pools), or null
   const float* gcum_lo;  // FP32 per-channel gates, optional: gcum's FP64 remainder
+  bool tri_packed;       // BF16, per-head gate, kw = k: Aqk and T as their ten lower blocks
 };
 
 // Row of the initial/final state of document n.
@@ -236,6 +237,11 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
   // (block blk = wave + 8 u of this wave; without W and u the Akk values wait
   // in registers until every wave is done with K, whose region they take)
   T* aqk_out = static_cast<T*>(p.aqk) + row0 * C;
+  // packed (BF16, per-head gate, kw = k): the chunk's ten lower blocks, rows
+  // past its end zero
+  constexpr bool TRI_OK = std::is_same<T, bf16_t>::value && !WU;
+  const bool tri = TRI_OK && p.tri_packed;
+  T* aqk_tri = static_cast<T*>(p.aqk) + ((int64_t)blockIdx.x * H + h) * kTriElems;
   f32x4 akk_keep[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -254,13 +260,20 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
         akk[j] = (s < t) ? sBeta[t] * dec * akk[j] : 0.f;
         aqk[j] = p.scale * dec * aqk[j];
       }
-      store_acc_global<T>(aqk_out, (int64_t)H * C, aqk, 16 * tb, 16 * sb, len, lane);
+      if (tri) {
+        f32x4 a = aqk;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = 16 * tb + acc_row(lane, j) < len ? a[j] : 0.f;
+        store_acc_global<T, true>(aqk_tri + blk * 256, 16, a, 0, 0, 16, lane);
+      } else {
+        store_acc_global<T>(aqk_out, (int64_t)H * C, aqk, 16 * tb, 16 * sb, len, lane);
+      }
       akk_keep[u] = akk;
     } else {  // (tb, sb) above the diagonal
       const int v = blk - 10;  // 0..5: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
       const int tb = v < 3 ? 0 : v < 5 ? 1 : 2;
       const int sb = v < 3 ? v + 1 : v < 5 ? v - 1 : 3;
-      store_acc_global<T>(aqk_out, (int64_t)H * C, zero4(), 16 * tb, 16 * sb, len, lane);
+      if (!tri) store_acc_global<T>(aqk_out, (int64_t)H * C, zero4(), 16 * tb, 16 * sb, len, lane);
       akk_keep[u] = zero4();
     }
     if (!LEAN) {  // Akk has a region of its own
@@ -301,6 +314,13 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
   // ---- T = (I + Akk)^-1 in place (scratch over Q, dead since Aqk) -------------
   solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
   if (!WU) {
+    if constexpr (TRI_OK) {
+      if (tri) {
+        store_tri_from_f32<kIW>(static_cast<bf16_t*>(p.akk) + ((int64_t)blockIdx.x * H + h) * kTriElems, sA, L::LDF,
+                                len);
+        return;
+      }
+    }
     store_tile_from_f32<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sA, L::LDF, len);
     return;
   }
@@ -1103,7 +1123,7 @@ __global__ __launch_bounds__(state_threads(D, BV)) void chunk_state_fwd_kernel(F
 constexpr int kRrLoaders = 4;  // two groups of two waves
 
 template <int D, int BV, bool ALIAS>
-struct RrFwdLayout {
+struct RrFwdLayout {  // (PACK kernels: Aqk and T come packed, see TriRegTile)
   static constexpr int LD = D + Pad<bf16_t>::v;
   static constexpr int LDV = BV + Pad<bf16_t>::v;
   static constexpr int LDC = C + Pad<bf16_t>::v;
@@ -1128,7 +1148,7 @@ struct RrFwdLayout {
   static_assert(bytes <= 160 * 1024, "LDS of one compute unit");
 };
 
-template <int D, int BV, bool ALIAS>
+template <int D, int BV, bool ALIAS, bool PACK>
 __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_rr_kernel(FwdParams p) {
   using L = RrFwdLayout<D, BV, ALIAS>;
   using T = bf16_t;
@@ -1151,9 +1171,17 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
     // The two roles run separate loops with the same barriers, so neither
     // keeps the other's registers live.
     RegTile<NGT, C, D, T> rQ, rKW, rK;
-    RegTile<NGT, C, C, T> rA, rT;
+    std::conditional_t<PACK, TriRegTile<NGT>, RegTile<NGT, C, C, T>> rA, rT;
     RegTile<NGT, C, BV, T> rV;
     float rg = 0.f, rb = 0.f;
+    if constexpr (PACK) {  // the stages' blocks above the diagonal: zero once
+      const int lt2 = tid - 64 * NC;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        zero_upper_blocks<2 * NGT>(lt2, reinterpret_cast<T*>(smem + b * L::BUF + L::off_A), L::LDC);
+        zero_upper_blocks<2 * NGT>(lt2, reinterpret_cast<T*>(smem + b * L::BUF + L::off_T), L::LDC);
+      }
+    }
     auto load = [&](int jc) {
       const int cstart = dstart + jc * C;
       const int clen = min(C, dlen - jc * C);
@@ -1161,8 +1189,14 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
       rQ.load_as(lt, static_cast<const T*>(p.q) + row0 * D, gs, clen);
       rKW.load_as(lt, static_cast<const T*>(p.kw) + row0 * D, gs, clen);
       if (!ALIAS) rK.load_as(lt, static_cast<const T*>(p.k) + row0 * D, gs, clen);
-      rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
-      rT.load_as(lt, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, clen);
+      if constexpr (PACK) {
+        const int64_t tri0 = ((int64_t)(first + jc) * H + h) * kTriElems;
+        rA.load_as(lt, static_cast<const T*>(p.aqk) + tri0);
+        rT.load_as(lt, static_cast<const T*>(p.akk) + tri0);
+      } else {
+        rA.load_as(lt, static_cast<const T*>(p.aqk) + row0 * C, (int64_t)H * C, clen);
+        rT.load_as(lt, static_cast<const T*>(p.akk) + row0 * C, (int64_t)H * C, clen);
+      }
       rV.load_as(lt, static_cast<const T*>(p.v) + row0 * D + v0, gs, clen);
       if (lt < C) {
         const int64_t gi = (int64_t)(cstart + min(lt, clen - 1)) * H + h;
@@ -1644,9 +1678,9 @@ int set_smem(K kernel, int bytes) {
   return 0;
 }
 
-template <int D, int BV, bool ALIAS>
+template <int D, int BV, bool ALIAS, bool PACK = false>
 int launch_state_fwd_rr_as(const FwdParams& p, hipStream_t s) {
-  auto kern = chunk_state_fwd_rr_kernel<D, BV, ALIAS>;
+  auto kern = chunk_state_fwd_rr_kernel<D, BV, ALIAS, PACK>;
   constexpr int bytes = RrFwdLayout<D, BV, ALIAS>::bytes;
   if (int st = set_smem(kern, bytes)) return st;
   hipLaunchKernelGGL(kern, doc_grid(p.geom.num_seqs, p.H, D / BV), dim3(64 * (BV / 16 + kRrLoaders)), bytes, s, p);
@@ -1661,6 +1695,9 @@ int launch_state_fwd_rr(const FwdParams& p, hipStream_t s) {
   if (N <= 0) return 0;
   const bool narrow = (int64_t)N * p.H * (D / 64) < 256;
   const bool alias = p.kw == p.k;
+  if (p.tri_packed) {  // kw = k (checked at the entry point)
+    return narrow ? launch_state_fwd_rr_as<D, 32, true, true>(p, s) : launch_state_fwd_rr_as<D, 64, true, true>(p, s);
+  }
   if (narrow) return alias ? launch_state_fwd_rr_as<D, 32, true>(p, s) : launch_state_fwd_rr_as<D, 32, false>(p, s);
   return alias ? launch_state_fwd_rr_as<D, 64, true>(p, s) : launch_state_fwd_rr_as<D, 64, false>(p, s);
 }
@@ -1773,6 +1810,9 @@ extern "C" int pkda_chunk_fwd(const pkda_chunk_fwd_args* a, void* stream) {
   p.kg = a->gate_per_channel ? a->kg : nullptr;
   p.slot = a->slot_idx;
   PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed states need pool_size > 0");
+  p.tri_packed = a->tri_packed != 0;
+  PKDA_REQUIRE(!p.tri_packed || (a->dtype == PKDA_BF16 && !a->gate_per_channel && p.kw == p.k), PKDA_EUNSUPPORTED,
+               "packed aqk / akk (tri_packed) are built for BF16 with a per-head gate and kw == k");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = a->num_chunks;
   const int st = a->stages;

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 11
+#define PKDA_ABI_VERSION 12
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -368,6 +368,13 @@ typedef struct pkda_chunk_fwd_args {
    * are then formed from (gcum[t] - gcum[s]) + (gcum_lo[t] - gcum_lo[s]).
    * Ignored for BF16.  NULL: gcum alone. */
   const float* gcum_lo;
+  /* Nonzero (BF16, per-head gate, kw == k or NULL only): aqk and akk hold
+   * each chunk's ten 16 x 16 blocks on and below the diagonal, packed
+   * [num_chunks, H, 10, 16, 16] (blocks in the order (0,0) (1,0) (1,1) (2,0)
+   * (2,1) (2,2) (3,0) .. (3,3), each row-major; rows past a chunk's end zero)
+   * instead of [N_tok, H, 64]: 5 KB instead of 8 KB per chunk and head to
+   * write and to read back.  The backward takes the same flag. */
+  int32_t tri_packed;
 } pkda_chunk_fwd_args;
 
 int pkda_chunk_fwd(const pkda_chunk_fwd_args* args, void* stream);
@@ -422,6 +429,7 @@ typedef struct pkda_chunk_bwd_args {
    * the pair's tokens inside them; with gcum alone their FP32 rounding moves
    * dA_log (a signed sum of that gradient over a whole head) by ~1e-5. */
   const float* gcum_lo;
+  int32_t tri_packed;          /* as pkda_chunk_fwd_args.tri_packed: how the forward stored aqk, akk */
 } pkda_chunk_bwd_args;
 
 int pkda_chunk_bwd(const pkda_chunk_bwd_args* args, void* stream);

@@ -159,6 +159,73 @@ def test_state_pass_forms_agree_bitwise(dev):
         assert torch.equal(w, joined), name
 
 
+@pytest.mark.parametrize("B,T,H,D,varlen", [
+    (2, 200, 3, 64, False),     # 32 value columns per state-pass workgroup, a partial last chunk
+    (1, 333, 3, 128, True),     # packed documents of 70, 130 and 133 tokens
+    (4, 256, 32, 128, False),   # 64 value columns per workgroup (the c2 form)
+    (1, 1000, 32, 64, True),    # 64 columns at d = 64, documents 1, 63, 64, 65 and 807 tokens long
+])
+def test_packed_triangular_aqk_and_t_bitwise(dev, B, T, H, D, varlen):
+    """BF16, per-head gate, kw = k: Aqk and T stored as each chunk's ten lower
+    16 x 16 blocks hold the row layout's values (rows past a chunk's end zero,
+    as the row layout's readers see them), and the forward's o, final state,
+    chunk states and U and the backward's every gradient (dS0 with a
+    final-state gradient in) are the same bits either way."""
+    from delta_feedback_experiment_amd import _lib
+    from delta_feedback_experiment_amd.chunk import ChunkPlan, chunk_backward, chunk_forward, gate_forward
+
+    print(f"[gpu] packed Aqk/T vs row layout: B{B} T{T} H{H} D{D} varlen={varlen}", flush=True)
+    q, k, v, g, beta = make_inputs(B, T, H, D, torch.bfloat16, seed=D + T, strong=True)
+    cu = torch.tensor([0, 70, 200, 333] if T == 333 else [0, 1, 64, 128, 193, 1000], dtype=torch.int32) \
+        if varlen else None
+    N = B if cu is None else cu.numel() - 1
+    gen = torch.Generator().manual_seed(T)
+    S0 = (0.02 * torch.randn(N, H, D, D, generator=gen)).to(dev)
+    dht = torch.randn(N, H, D, D, generator=gen).to(dev)
+    do = torch.randn(B, T, H, D, generator=gen).to(torch.bfloat16).to(dev)
+    qd, kd, vd = (t.to(dev).contiguous() for t in (q, k, v))
+    plan = ChunkPlan.make(qd, None if cu is None else cu.to(dev))
+    gcum = gate_forward(plan, g.to(dev).float().contiguous(), _lib.GATE_LOG_HEAD, None, None)
+    flat = lambda t: t.reshape(plan.num_tokens, plan.heads, plan.head_dim)  # noqa: E731
+    qf, kf, vf, dof = flat(qd), flat(kd), flat(vd), flat(do)
+    beta32 = beta.to(dev).float().contiguous()
+    scale = D ** -0.5
+    runs, saves = [], []
+    for pack in (False, True):
+        o, S, saved = chunk_forward(plan, qf, kf, kf, vf, gcum, beta32, scale, S0, True, True, pack_triangular=pack)
+        assert saved.tri_packed == pack
+        gr = chunk_backward(plan, qf, kf, kf, vf, gcum, beta32, scale, S0, saved, dof, dht, True,
+                            grad_dtype=torch.bfloat16)
+        runs.append(dict(o=o, S=S, h=saved.h, U=saved.u, dq=gr.dq, dk=gr.dk, dv=gr.dv, dbeta=gr.dbeta,
+                         dgcum=gr.dgcum, dS0=gr.dh0))
+        saves.append(saved)
+    torch.cuda.synchronize()
+    # the packed blocks against the row layout's chunk matrices, chunk by chunk
+    lens = [T] * B if cu is None else (cu[1:] - cu[:-1]).tolist()
+    starts = [b * T for b in range(B)] if cu is None else cu[:-1].tolist()
+    blocks = [(tb, sb) for tb in range(4) for sb in range(tb + 1)]
+    cid = 0
+    for start, n in zip(starts, lens):
+        for c0 in range(0, n, 64):
+            ln = min(64, n - c0)
+            for name in ("aqk", "akk"):
+                rows = getattr(saves[0], name)[start + c0:start + c0 + ln].float()  # [ln, H, 64]
+                packed = getattr(saves[1], name)[cid].float().reshape(H, 10, 16, 16)
+                full = torch.zeros(H, 64, 64, device=dev)
+                for i, (tb, sb) in enumerate(blocks):
+                    full[:, 16 * tb:16 * tb + 16, 16 * sb:16 * sb + 16] = packed[:, i]
+                assert torch.equal(full[:, :ln], rows.transpose(0, 1)), (name, cid)
+                assert not full[:, ln:].any(), (name, cid)
+            cid += 1
+    real = cid  # h has a slot per chunk of the launch bound; the documents' chunks come first
+    for r in runs:
+        r["h"] = r["h"][:real]
+    for name, a in runs[0].items():
+        b = runs[1][name]
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(a, b), (name, (a.float() - b.float()).abs().max().item())
+
+
 def make_inputs(B, T, H, D, dtype, seed=0, strong=False, per_channel=False):
     gen = torch.Generator().manual_seed(seed)
 
