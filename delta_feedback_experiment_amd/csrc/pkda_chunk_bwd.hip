@@ -72,6 +72,11 @@ struct BwdParams {
   const float* kw32;  // per-channel gates: kw in FP32 (BF16 kw otherwise), or null
   const float* gcum_lo;  // FP32 per-channel gates, optional: gcum's FP64 remainder
   bool tri_packed;       // BF16, per-head gate, kw = k: Aqk and T as their ten lower blocks
+  // BF16, per-head gate, kw = k, BF16 dq, dk, dv (the four-wave backward): the
+  // reverse pass writes dv = beta dBv, the final output, instead of dBv, and
+  // dBv only for rows with |beta| < 1e-20 (into du); the per-chunk kernel
+  // takes dBv = dv / beta.
+  bool dv_handoff;
 };
 
 // Deterministic sum of one value per thread over an NT-thread workgroup.
@@ -705,7 +710,7 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
       const int64_t off = tile_offset(D, ct, 2 * kk + (q >> 1)) + il * 16 + 8 * (q & 1);
       S0f[j][kk] = *reinterpret_cast<const s16x8_t*>(hsrc + off);
     }
-  rdBv.load(static_cast<const E*>(p.du) + row0 * D, gs, len);
+  rdBv.load(static_cast<const E*>(p.dv_handoff ? p.dv : p.du) + row0 * D, gs, len);  // dBv, or dv (final)
   // every thread writes (the C rows' values, repeated): no branch
   sGam[tid & (C - 1)] = gval;
   sBeta[tid & (C - 1)] = (tid & (C - 1)) < len ? bval : 0.f;
@@ -736,6 +741,17 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
       Vec16<E>::unpack(rdBv.r[i], b);
       Vec16<E>::unpack(rU.r[i], u);
       const float br = sBeta[r];
+      const bool tiny_row = !(fabsf(br) >= 1e-20f);
+      if (p.dv_handoff) {  // b holds dv (already written): dBv = dv / beta, or dBv itself for a tiny beta
+        if (tiny_row && r < len) {
+          Vec16<E>::load(static_cast<const E*>(p.du) + row0 * D + r * gs + c, b);
+        } else {
+          const float rb = 1.f / br;
+#pragma unroll
+          for (int e = 0; e < V; ++e) b[e] = tiny_row ? 0.f : b[e] * rb;
+        }
+        rdBv.r[i] = pack_vec16<E>(b);  // the dBv operand of passes 2-3
+      }
       float part = 0.f, pv = 0.f;
 #pragma unroll
       for (int e = 0; e < V; ++e) part += b[e] * u[e];
@@ -755,9 +771,11 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
       if constexpr (PER_ROW == 16) pv += __shfl_xor(pv, 8);
       sDb1[r] = part;  // the row's lanes all hold the sums: unconditional, no branch
       sDbV[r] = pv;
+      if (!p.dv_handoff) {
 #pragma unroll
-      for (int e = 0; e < V; ++e) b[e] *= br;
-      if (r < len) store_vec<V>(dvo + r * gs + c, b);
+        for (int e = 0; e < V; ++e) b[e] *= br;
+        if (r < len) store_vec<V>(dvo + r * gs + c, b);
+      }
     }
   }
 
@@ -1886,7 +1904,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
         const int r = i / SEG, sg = i % SEG;
         if (r < clen) {
           const uint4 x = *reinterpret_cast<const uint4*>(so + r * L::LDV + 8 * sg);
-          *reinterpret_cast<uint4*>(static_cast<T*>(p.du) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg) = x;
+          *reinterpret_cast<uint4*>(static_cast<T*>(p.dv_handoff ? p.dv : p.du) + (row0 + (int64_t)r * H) * D + v0 +
+                                    8 * sg) = x;
         }
       }
     };
@@ -2019,15 +2038,44 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
       mfma_bf16(Z[2], at[4], dUnB[1]);
       mfma_bf16(Z[3], at[5], dUnB[1]);
     }
-    // the per-chunk kernel needs dU only through dBv = T^T dU = -Z: hand it that
-    if constexpr (L::STAGE_OUT) {
-      T* so = reinterpret_cast<T*>(smem + L::off_Out + (s & 1) * L::OUT) + 16 * wave;
+    // the per-chunk kernel needs dU only through dBv = T^T dU = -Z: hand it
+    // that, or (dv_handoff) dv = beta dBv with dBv itself for the rows whose
+    // beta is too small to divide by
+    {
+      f32x4 hz[4];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) store_acc_global<T, true>(so, L::LDV, -Z[rb], 16 * rb, 0, C, lane);
-    } else {
-      T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
+      for (int rb = 0; rb < 4; ++rb) hz[rb] = -Z[rb];
+      if (p.dv_handoff) {
+        // one test per chunk (lane r looks at row r; the ballot is uniform):
+        // rows whose beta is too small to divide by also leave dBv itself
+        const float bl = sB[lane];
+        if (__builtin_expect(__ballot(lane < clen && !(fabsf(bl) >= 1e-20f)) != 0, 0)) {
+          T* du_out = static_cast<T*>(p.du) + row0 * D + col0;
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(du_out, gs, -Z[rb], 16 * rb, 0, clen, lane);
+          for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 16 * rb + q4 + j;
+              if (r < clen && !(fabsf(sB[r]) >= 1e-20f)) du_out[(int64_t)r * gs + il] = to_e<T>(hz[rb][j]);
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          float b4[4];
+          lds4(sB + 16 * rb + q4, b4);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) hz[rb][j] *= b4[j];
+        }
+      }
+      if constexpr (L::STAGE_OUT) {
+        T* so = reinterpret_cast<T*>(smem + L::off_Out + (s & 1) * L::OUT) + 16 * wave;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) store_acc_global<T, true>(so, L::LDV, hz[rb], 16 * rb, 0, C, lane);
+      } else {
+        T* du_out = static_cast<T*>(p.dv_handoff ? p.dv : p.du) + row0 * D + col0;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) store_acc_global<T>(du_out, gs, hz[rb], 16 * rb, 0, clen, lane);
+      }
     }
     // dS <- e^{G_C} dS + Q^T (s e^G dO) + K^T diag(beta e^G) Z
     s16x8_t ZB[2];
@@ -2331,7 +2379,11 @@ int launch_state_bwd_rr_pc(const BwdParams& p, hipStream_t s) {
 }
 
 template <typename T, int D, int BV, typename OT, typename OK>
-int launch_bwd(const BwdParams& p, int num_chunks, int stages, hipStream_t s) {
+int launch_bwd(const BwdParams& p_in, int num_chunks, int stages, hipStream_t s) {
+  BwdParams p = p_in;
+  // the four-wave per-chunk kernel runs: the reverse pass hands it dv
+  p.dv_handoff = implicit_w<T>() && std::is_same<OT, bf16_t>::value && std::is_same<OK, bf16_t>::value && !p.qg &&
+                 p.kw_is_k;
   const int N = p.geom.num_seqs;
   const bool all = stages == 0;
   if (all || (stages & PKDA_STAGE_BWD_STATE)) {

@@ -341,6 +341,16 @@ template <int N> __device__ __forceinline__ void store_vec(bf16_t* dst, const fl
   }
 }
 
+// V floats rounded to T (nearest even) and packed into one 16-byte piece.
+template <typename T> __device__ __forceinline__ uint4 pack_vec16(const float* x);
+template <> __device__ __forceinline__ uint4 pack_vec16<bf16_t>(const float* x) {
+  return make_uint4(pack_bf16x2_(x[0], x[1]), pack_bf16x2_(x[2], x[3]), pack_bf16x2_(x[4], x[5]),
+                    pack_bf16x2_(x[6], x[7]));
+}
+template <> __device__ __forceinline__ uint4 pack_vec16<float>(const float* x) {
+  return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+}
+
 template <int NT, int ROWS, int NC, typename T, typename E, typename F>
 __device__ __forceinline__ void load_tile(E* lds, int ld, const T* g, int64_t gstride, int nvalid, F f) {
   constexpr int V = Vec16<T>::N;
