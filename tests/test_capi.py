@@ -85,3 +85,23 @@ def test_noalloc_gate_backward_refuses_past_its_scratch():
                          num_chunks=chunks, dg_dtype=_lib.PKDA_F32)
     with pytest.raises(ValueError, match="exceeds its scratch"):
         _lib.call("pkda_gate_bwd_noalloc", args, 0)
+
+
+def test_packed_triangular_refused_outside_its_configuration():
+    """``tri_packed`` (Aqk and T as each chunk's ten lower blocks) is built for
+    BF16 with a per-head gate and kw == k; both chunk entry points refuse any
+    other combination before any HIP call, so this runs without a device
+    (the pointers, nonzero stand-ins, are never read)."""
+    from delta_feedback_experiment_amd import _lib
+
+    geo = dict(num_seqs=1, seqlen=64, heads=1, head_dim=64, num_chunks=1)
+    fake = dict(q=16, k=16, v=32, gcum=48, beta=64, u=96, aqk=112, akk=128, w=144, h=160)
+    for dtype, kw in ((_lib.PKDA_F32, 16), (_lib.PKDA_BF16, 176)):  # FP32; a separate write key
+        args = _lib.ChunkFwdArgs(dtype=dtype, **geo, kw=kw, o=80, tri_packed=1, **fake)
+        with pytest.raises(ValueError, match="tri_packed"):
+            _lib.call("pkda_chunk_fwd", args, 0)
+    grads = dict(do=192, dh=208, du=224, dq=240, dk=256, dkw=272, dv=288, dbeta=304, dgcum=320)
+    for dtype, kw in ((_lib.PKDA_F32, 16), (_lib.PKDA_BF16, 176)):
+        args = _lib.ChunkBwdArgs(dtype=dtype, **geo, kw=kw, tri_packed=1, **fake, **grads)
+        with pytest.raises(ValueError, match="tri_packed"):
+            _lib.call("pkda_chunk_bwd", args, 0)
