@@ -99,8 +99,9 @@ def _serving_args(N=3, P=8, H=2, D=64, T=40):
 
 def test_serving_ops_trace_as_mutating_custom_ops():
     """Prefill into pool slots, then a decode step: both trace as opaque
-    custom ops whose schema marks the pools as mutated (SURVEY's drop-in
-    boundary asks for mutates_args on the in-place serving operators)."""
+    custom ops whose schema marks the pools as mutated (``mutates_args``:
+    an in-place serving operator must declare what it writes, or a compiled
+    caller would reorder or drop its writes)."""
     from delta_feedback_experiment_amd import pkda_decode_step_, pkda_prefill_
 
     (q, k, v, g, beta, pool, idx), (pq, pk, pv, pg, pb) = _serving_args()
