@@ -627,9 +627,10 @@ __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
 // workgroup's loads then overlap the other's products).  Every contraction
 // over the channels (the pair sums of Akk and Aqk) accumulates in registers
 // across the halves; qg, kg and the column blocks of W = T Bw and u = T Bv
-// are per half.  Both halves' tiles are loaded up front: the second half
-// waits in registers while the first computes, and the first half's K and G
-// stay there until W needs them again.
+// are per half.  The second half's tiles are loaded while the first half
+// computes, and W's first column block takes Bw = diag(beta) (e^G * K) of
+// the first half, formed while that half's K and G are in LDS and kept in a
+// region of its own (not loaded a second time).
 // ---------------------------------------------------------------------------
 template <bool ALIAS>
 struct IntraPc2Layout {
@@ -648,7 +649,8 @@ struct IntraPc2Layout {
   static constexpr int off_A = off_G + C * LDG * 4;        // fp32 [64][LDF]: Akk, then T
   static constexpr int off_Aqk = off_A + C * LDF * 4;      // bf16 Aqk, then T
   static constexpr int off_beta = off_Aqk + C * LDC * 2;
-  static constexpr int bytes = off_beta + C * 4;
+  static constexpr int off_Bw0 = off_beta + C * 4;         // bf16 Bw of the first half (W's first block)
+  static constexpr int bytes = off_Bw0 + RT;
   static_assert(ALIAS || QR + RT >= SCR, "the solve's scratch fits the Q and KW regions");
   static_assert(2 * bytes <= 160 * 1024, "two workgroups per compute unit");
 };
@@ -675,6 +677,7 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
   E* sAqk = reinterpret_cast<E*>(smem + L::off_Aqk);
   E* sTe = sAqk;
   float* sBeta = reinterpret_cast<float*>(smem + L::off_beta);
+  E* sBw0 = reinterpret_cast<E*>(smem + L::off_Bw0);
 
   const T* k = static_cast<const T*>(p.k) + row0 * D;
   const T* q = static_cast<const T*>(p.q) + row0 * D;
@@ -806,6 +809,13 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
     Q1.load(q + DH, gs, len);
     if (!ALIAS) KW1.load(kw + DH, gs, len);
     G1.load_clamped(g + DH, gs, len);
+    // W's first column block takes Bw = beta e^G K of this half: formed while
+    // its K and G are in LDS (the second half's tiles replace them next)
+#pragma unroll 1
+    for (int i = tid; i < C * DH; i += kIW) {
+      const int r = i / DH, c = i - r * DH;
+      sBw0[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+    }
     __syncthreads();
     // ---- second half -----------------------------------------------------------
     K1.store(sK, L::LD);
@@ -843,13 +853,9 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
   // ---- T = (I + Akk)^-1 in place (scratch over Q and KW); Aqk leaves first ------
   store_tile<kIW, C, C>(static_cast<T*>(p.aqk) + row0 * C, (int64_t)H * C, sAqk, L::LDC, len);
   solve_unit_lower_64(sA, L::LDF, reinterpret_cast<float*>(sQ));
-  // W's operands: V, and the first half's K and G again
+  // u's operand V (both halves)
   RegTile<kIW, C, D, T> rV;
-  RegTile<kIW, C, DH, T> K0;
-  RegTile<kIW, C, DH, float> G0;
   rV.load(static_cast<const T*>(p.v) + row0 * D, gs, len);
-  K0.load(k, gs, len);
-  G0.load_clamped(g, gs, len);
   // (loops over the tile not unrolled: hoisted addresses would be held, and
   // spilled, across the phases)
 #pragma unroll 1
@@ -858,17 +864,19 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
     sTe[r * L::LDC + c] = to_e<E>(sA[r * L::LDF + c]);
   }
   // ---- W = T Bw and u = T Bv, column half by column half -------------------------
-  // Bw = diag(beta) (e^G * K), Bv = diag(beta) V; the second half's K and G
-  // are still in LDS, the first half's come back from the registers
+  // Bw = diag(beta) (e^G * K), Bv = diag(beta) V; the second half's Bw is
+  // formed in place over its K (still in LDS), the first half's is sBw0
   const int rb = wave & 3, ch = wave >> 2;
   const int kend = kceil<E>(16 * rb + 16);
   T* w_out = static_cast<T*>(p.w) + row0 * D;
   T* u_out = static_cast<T*>(p.u) + row0 * D;
-  auto wu_half = [&](int hc) {
+  auto wu_half = [&](int hc, E* sBw) {
+    if (hc == DH) {
 #pragma unroll 1
-    for (int i = tid; i < C * DH; i += kIW) {
-      const int r = i / DH, c = i - r * DH;
-      sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+      for (int i = tid; i < C * DH; i += kIW) {
+        const int r = i / DH, c = i - r * DH;
+        sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+      }
     }
     // this half's V columns from the register tile (pieces of 8 columns)
 #pragma unroll
@@ -888,18 +896,15 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
     for (int j = 0; j < DH / 32; ++j) {
       const int ct = ch * (DH / 32) + j;  // column tile within the half
       f32x4 aw = zero4(), au = zero4();
-      mma_tile_range<E, ROW, ROW>(aw, sTe, L::LDC, 16 * rb, sK, L::LD, 16 * ct, 0, kend, lane);
+      mma_tile_range<E, ROW, ROW>(aw, sTe, L::LDC, 16 * rb, sBw, L::LD, 16 * ct, 0, kend, lane);
       mma_tile_range<E, ROW, ROW>(au, sTe, L::LDC, 16 * rb, sQ, L::LD, 16 * ct, 0, kend, lane);
       store_acc_global<T>(w_out, gs, aw, 16 * rb, hc + 16 * ct, len, lane);
       store_acc_global<T>(u_out, gs, au, 16 * rb, hc + 16 * ct, len, lane);
     }
   };
-  wu_half(DH);
-  __syncthreads();  // every wave is done with the second half's Bw and Bv
-  K0.store(sK, L::LD);
-  G0.store(sG, L::LDG);
-  __syncthreads();
-  wu_half(0);
+  wu_half(DH, sK);
+  __syncthreads();  // every wave is done with the second half's Bv
+  wu_half(0, sBw0);
   store_tile<kIW, C, C>(static_cast<T*>(p.akk) + row0 * C, (int64_t)H * C, sTe, L::LDC, len);
 }
 
