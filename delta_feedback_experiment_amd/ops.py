@@ -112,6 +112,21 @@ def _check_inputs(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_sca
         raise RuntimeError("pkda_recurrence needs tensors on a HIP device; there is no CPU fallback")
 
 
+_GATE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _gate_stream(dev: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for the per-channel
+    gate, which neither reads nor writes anything of the preconditioner's:
+    the two run side by side, joined before the first kernel that needs
+    both (the chunk forward; the end of the backward)."""
+    i = dev.index if dev.index is not None else torch.cuda.current_device()
+    s = _GATE_STREAMS.get(i)
+    if s is None:
+        s = _GATE_STREAMS[i] = torch.cuda.Stream(device=i)
+    return s
+
+
 def _forward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, scale, squash_x, squash_eps,
              save_all: bool):
     plan = ChunkPlan.make(q, None)
@@ -121,9 +136,16 @@ def _forward(q, k, v, g, g_atk, beta_atk, beta, A_log, dt_bias, log_atk_scale, s
         gf = gf.float()
     A32, dt32 = _f32(A_log), _f32(dt_bias)
     gcum_lo = _gcum_lo(plan, qf)
-    gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gcum_lo=gcum_lo)
+    # the gate on its own stream beside the preconditioner (both read only
+    # the inputs); gcum is allocated there and recorded as used by this one
+    cur, side = torch.cuda.current_stream(q.device), _gate_stream(q.device)
+    side.wait_stream(cur)
+    with torch.cuda.stream(side):
+        gcum = gate_forward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gcum_lo=gcum_lo)
     pstate = pre.precond_forward(plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, None,
                                  want_kw32=True)
+    cur.wait_stream(side)
+    gcum.record_stream(cur)
     beta32 = _f32(beta).reshape(plan.num_tokens, plan.heads)
     o, _, fs = chunk_forward(plan, qf, kf, pstate.kw, vf, gcum, beta32, scale, None, False, save_states=save_all,
                              gcum_lo=gcum_lo)
@@ -214,10 +236,18 @@ def pkda_recurrence_backward(
                             grad_dtype=qf.dtype, key_grad_dtype=qf.dtype, kw32=kw32, gcum_lo=gcum_lo)
         pstate = pre.PrecondState(kw, a_chunk, None, None)
         dk = torch.empty_like(kf)  # the preconditioner's scan writes the final dk in k's dtype
+        # the gate's backward (dgcum only) beside the preconditioner's (dk, dkw)
+        cur, side = torch.cuda.current_stream(q.device), _gate_stream(q.device)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            dg, dA_log, ddt_bias = gate_backward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gr.dgcum,
+                                                 dg_dtype=gf.dtype)
         dg_atk, dbeta_atk, dcenter, _ = pre.precond_backward(
             plan, kf, g_atk, beta_atk, log_atk_scale, squash_x, squash_eps, pstate, gr.dkw, gr.dk, None, False,
             dk_final=dk)
-        dg, dA_log, ddt_bias = gate_backward(plan, gf, _lib.GATE_RAW_CHANNEL, A32, dt32, gr.dgcum, dg_dtype=gf.dtype)
+        cur.wait_stream(side)
+        for t in (dg, dA_log, ddt_bias):
+            t.record_stream(cur)
     shape = tuple(q.shape)
     lead = shape[:3]
     return [

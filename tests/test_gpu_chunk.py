@@ -604,6 +604,50 @@ def test_pkda_recurrence_op_matches_oracle(dev, lean, seed):
         assert val < BF16_TOL, (n, val)
 
 
+@pytest.mark.parametrize("lean", [False, True])
+def test_pkda_recurrence_graph_replays_match_eager(dev, lean):
+    """The production op runs the per-channel gate on a second stream beside
+    the preconditioner and joins it, in the forward and in the backward.
+    Captured in a HIP graph (after warm-up on a side stream, as torch's
+    capture requires) the fork and the join become graph dependencies: each
+    of three replays, with eager steps and synchronisations between them,
+    gives the eager call's output and ten gradients bit for bit, and so does
+    every eager step in between."""
+    from delta_feedback_experiment_amd import pkda_recurrence
+
+    print(f"[gpu] pkda_recurrence graph replays lean={lean}", flush=True)
+    B, T, H, D = 2, 256, 4, 128
+    (q, k, v, g_raw, beta, A_log, dt_bias, g_atk, beta_atk, center) = _production_inputs(
+        B, T, H, D, torch.bfloat16, 13)
+    leaves = [x.to(dev).clone().requires_grad_()
+              for x in (q, k, v, g_raw, g_atk, beta_atk, beta, A_log, dt_bias, center)]
+    do = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(5)).to(dev, torch.bfloat16)
+    names = ("o", "dq", "dk", "dv", "dg", "dg_atk", "dbeta_atk", "dbeta", "dA_log", "ddt_bias", "dlog_atk_scale")
+
+    def step():
+        o, _ = pkda_recurrence(*leaves, D ** -0.5, 1.5, 1e-6, lean)
+        return [o.detach()] + list(torch.autograd.grad(o, leaves, do))
+
+    eager = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for n, a, b in zip(names, static, eager):
+            assert torch.equal(a, b), ("replay", i, n)
+        for n, a, b in zip(names, step(), eager):
+            assert torch.equal(a, b), ("eager", i, n)
+        torch.cuda.synchronize()
+
+
 def test_production_key_gradient_handoff(dev):
     """The production backward hands the chunk kernel's key gradients (read
     key dk and write key dkw) to the preconditioner's reverse scan in BF16,
