@@ -94,13 +94,7 @@ __device__ __forceinline__ float block_sum(float x, float* s_red) {
 }
 
 // Sum over the 16 lanes that share lane >> 4 (one accumulator row), fixed order.
-__device__ __forceinline__ float group16_sum(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 8);
-  return x;
-}
+__device__ __forceinline__ float group16_sum(float x) { return lane_group_sum<16>(x); }
 
 // Sum over the 64 lanes of a wave, fixed order; every lane gets the result.
 __device__ __forceinline__ float wave_sum(float x) {
@@ -761,14 +755,10 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
 #pragma unroll
         for (int e = 0; e < V; ++e) pv += b[e] * v[e];
       }
-      part += __shfl_xor(part, 1);
-      part += __shfl_xor(part, 2);
-      part += __shfl_xor(part, 4);
-      if constexpr (PER_ROW == 16) part += __shfl_xor(part, 8);
-      pv += __shfl_xor(pv, 1);
-      pv += __shfl_xor(pv, 2);
-      pv += __shfl_xor(pv, 4);
-      if constexpr (PER_ROW == 16) pv += __shfl_xor(pv, 8);
+      part = lane_group_sum<PER_ROW>(part);
+      // pv is zero on every lane unless a row of this wave's pieces has a
+      // vanishing beta (one wave-uniform test)
+      if (__builtin_expect(__ballot(r < len && !(fabsf(br) >= 1e-20f)) != 0, 0)) pv = lane_group_sum<PER_ROW>(pv);
       sDb1[r] = part;  // the row's lanes all hold the sums: unconditional, no branch
       sDbV[r] = pv;
       if (!p.dv_handoff) {

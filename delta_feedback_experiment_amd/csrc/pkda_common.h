@@ -125,4 +125,26 @@ __device__ __forceinline__ SeqBounds seq_bounds(const int32_t* cu, int n, int se
   return b;
 }
 
+// Sum over each aligned group of N = 2, 4, 8 or 16 consecutive lanes (a
+// pair, a quad, a DPP half-row or row), every lane of the group getting it:
+// the butterfly over lane ^ 1, lane ^ 2, lane ^ 4 and lane ^ 8, each step
+// own + moved, with DPP lane moves (VALU) instead of permutes through the LDS
+// crossbar.  After the two quad steps every lane of a quad holds the quad's
+// sum, so the half-row and row mirrors bring the same partner values as
+// lane ^ 4 and lane ^ 8: the same additions in the same order as the
+// shuffle butterfly.  Every lane of each group must be active (lanes of
+// other groups need not be).
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "2, 4, 8 or 16 lanes");
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+  if constexpr (N >= 4)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+  if constexpr (N >= 8)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half-row mirror
+  if constexpr (N == 16)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+
 }  // namespace pkda

@@ -126,12 +126,17 @@ struct Raw8 {
   }
 };
 
-// Sum over the G lanes of one head (G a power of two, lanes aligned to G).
+// Sum over the G lanes of one head (G a power of two, lanes aligned to G;
+// the lanes of a head are active together).
 template <int G>
 __device__ __forceinline__ float head_sum(float x) {
+  if constexpr (G <= 16) {
+    return lane_group_sum<G>(x);
+  } else {
 #pragma unroll
-  for (int off = 1; off < G; off <<= 1) x += __shfl_xor(x, off);
-  return x;
+    for (int off = 1; off < G; off <<= 1) x += __shfl_xor(x, off);
+    return x;
+  }
 }
 
 __device__ __forceinline__ float sigmoid_fast(float a) { return 1.f / (1.f + __expf(-a)); }

@@ -79,11 +79,17 @@ template <> struct V8<float> {
   }
 };
 
+// Sum over the L lanes of one row (L a power of two, lanes aligned to L; the
+// lanes of a row are active together).
 template <int L>
 __device__ __forceinline__ float row_sum(float x) {
+  if constexpr (L <= 16) {
+    return lane_group_sum<L>(x);
+  } else {
 #pragma unroll
-  for (int off = 1; off < L; off <<= 1) x += __shfl_xor(x, off);
-  return x;
+    for (int off = 1; off < L; off <<= 1) x += __shfl_xor(x, off);
+    return x;
+  }
 }
 
 __device__ __forceinline__ float sigm(float a) { return 1.f / (1.f + __expf(-a)); }
