@@ -120,23 +120,21 @@ __device__ __forceinline__ ChunkHead chunk_head(int H) {
 
 // exp(sum of g_atk over the chunk) for chunks j0 .. j0 + nb - 1 of a document
 // (first token dstart, dlen tokens), chunk j0 + i at s[i]; thread i sums its
-// chunk's tokens in order.
+// chunk's tokens in order.  The chunk's C loads go out together (rows
+// clamped to its last token, masked in the sum -- adding 0 changes no
+// nonzero sum), so the sum waits for one memory round trip.
 __device__ __forceinline__ void chunk_decays(const PrecondParams& p, int h, int dstart, int dlen, int j0, int nb,
                                              float* s) {
   const int i = threadIdx.x;
   if (i < nb) {
     const int t0 = dstart + (j0 + i) * C;
     const int len = min(C, dlen - (j0 + i) * C);
-    // 16 tokens' loads go out together (clamped rows, masked in the sum); the
-    // sum still runs token by token in order
+    float v[C];
+#pragma unroll
+    for (int u = 0; u < C; ++u) v[u] = p.g_atk[(int64_t)(t0 + min(u, len - 1)) * p.H + h];
     float g = 0.f;
-    for (int tb = 0; tb < len; tb += 16) {
-      float v[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = p.g_atk[(int64_t)(t0 + min(tb + u, len - 1)) * p.H + h];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) g += tb + u < len ? v[u] : 0.f;
-    }
+    for (int u = 0; u < C; ++u) g += u < len ? v[u] : 0.f;
     s[i] = exp_fast(g);
   }
 }
@@ -155,25 +153,23 @@ __device__ __forceinline__ float chunk_scan(const PrecondParams& p, float* buf, 
   for (int b = 0; b < count; b += NT) {
     const int nb = min(NT, count - b);
     const int j0 = REVERSE ? count - b - nb : b;  // first chunk of this block
+    // the block's local ends go out first (indices clamped into the block),
+    // then the decays' loads: both wait together, one round trip, and the
+    // chain below runs on registers in the walk's order
+    float* base = buf + ((int64_t)(first + j0) * p.H + h) * D + (c < D ? c : 0);
+    float l[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) l[u] = base[(REVERSE ? max(nb - 1 - u, 0) : min(u, nb - 1)) * step];
     __syncthreads();
     chunk_decays(p, h, dstart, dlen, j0, nb, sDecay);
     __syncthreads();
     if (c < D) {
-      float* base = buf + ((int64_t)(first + j0) * p.H + h) * D + c;
-      for (int i0 = 0; i0 < nb; i0 += 8) {
-        float l[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int i = REVERSE ? nb - 1 - (i0 + u) : i0 + u;
-          l[u] = i0 + u < nb ? base[i * step] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (i0 + u < nb) {
-            const int i = REVERSE ? nb - 1 - (i0 + u) : i0 + u;
-            base[i * step] = x;
-            x = sDecay[i] * x + l[u];
-          }
+      for (int u = 0; u < NT; ++u) {
+        if (u < nb) {
+          const int i = REVERSE ? nb - 1 - u : u;
+          base[i * step] = x;
+          x = sDecay[i] * x + l[u];
         }
       }
     }
