@@ -374,6 +374,25 @@ def test_chunk_gradients_varlen(dev):
         assert val < BF16_TOL, (name, val)
 
 
+@pytest.mark.parametrize("case", ["ragged documents", "one partial chunk per row"])
+def test_chunk_gradients_ragged_d128(dev, case):
+    """The c2 kernels (BF16, d = 128, per-head gate, kw = k: packed T and
+    Aqk, the register-resident state passes, the reverse pass's dv hand-off,
+    the four-wave backward) on chunks of every fill: packed documents of 1,
+    64, 65, 0, 130, 17, 63, 3 and 128 tokens, or rows of 17 tokens (one
+    partial chunk each); output, final state and every gradient against the
+    oracle."""
+    print(f"[gpu] chunk grads d=128 bf16, {case}", flush=True)
+    if case == "ragged documents":
+        lens = [1, 64, 65, 0, 130, 17, 63, 3, 128]
+        cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+        res = _grad_case(dev, 1, int(cu[-1]), 2, 128, torch.bfloat16, seed=19, cu=cu)
+    else:
+        res = _grad_case(dev, 3, 17, 2, 128, torch.bfloat16, seed=23)
+    for name, val in res.items():
+        assert val < BF16_TOL, (name, val)
+
+
 def _precond_inputs(B, T, H, gen):
     """Preconditioner controls drawn as the reference's bench draws them
     (scripts/pkda_bench.py:162-187): g_atk = -A softplus(0.2 n + bias)."""
