@@ -23,7 +23,7 @@ STAGE_FWD_INTRA = 1
 STAGE_FWD_STATE = 2
 STAGE_BWD_STATE = 1
 STAGE_BWD_CHUNK = 2
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 
 class RecurrentArgs(ctypes.Structure):
@@ -69,7 +69,7 @@ class PrecondArgs(ctypes.Structure):
         ("dkw", c_void_p), ("dk", c_void_p), ("dg_atk", c_void_p), ("dbeta_atk", c_void_p),
         ("dcenter_part", c_void_p), ("dcenter", c_void_p), ("dA0", c_void_p), ("dA_T", c_void_p),
         ("table", c_void_p), ("slot_idx", c_void_p), ("pool_size", c_int64), ("lam_chunk", c_void_p),
-        ("dk_final", c_void_p), ("kw32", c_void_p), ("grad_dtype", c_int32),
+        ("dk_final", c_void_p), ("kw32", c_void_p), ("grad_dtype", c_int32), ("chunk_decay", c_void_p),
     ]
 
 

@@ -68,6 +68,7 @@ struct PrecondParams {
   void* dk_final;  // backward: dk + the terms here in k's dtype (dk untouched), or null
   float* kw32;     // forward: kw also in FP32, or null
   bool narrow_grads;  // backward: dkw and dk in k's dtype (dk read only, dk_final written)
+  float* chunk_decay;  // [num_chunks][H] exp(sum of the chunk's g_atk) from the local pass, or null
 };
 
 template <int D> struct PrecondThreads { static constexpr int v = D < 64 ? 64 : D; };
@@ -119,14 +120,18 @@ __device__ __forceinline__ ChunkHead chunk_head(int H) {
 }
 
 // exp(sum of g_atk over the chunk) for chunks j0 .. j0 + nb - 1 of a document
-// (first token dstart, dlen tokens), chunk j0 + i at s[i]; thread i sums its
-// chunk's tokens in order.  The chunk's C loads go out together (rows
-// clamped to its last token, masked in the sum -- adding 0 changes no
-// nonzero sum), so the sum waits for one memory round trip.
-__device__ __forceinline__ void chunk_decays(const PrecondParams& p, int h, int dstart, int dlen, int j0, int nb,
-                                             float* s) {
+// (first chunk id first, first token dstart, dlen tokens), chunk j0 + i at
+// s[i]: read from chunk_decay when the local pass wrote it there, else
+// thread i sums its chunk's tokens in order, as the local passes do.  The
+// chunk's C loads go out together (rows clamped to its last token, masked in
+// the sum -- adding 0 changes no nonzero sum), so the sum waits for one
+// memory round trip.
+__device__ __forceinline__ void chunk_decays(const PrecondParams& p, int h, int first, int dstart, int dlen, int j0,
+                                             int nb, float* s) {
   const int i = threadIdx.x;
-  if (i < nb) {
+  if (i < nb && p.chunk_decay) {
+    s[i] = p.chunk_decay[(int64_t)(first + j0 + i) * p.H + h];  // the local pass's sum, bit for bit
+  } else if (i < nb) {
     const int t0 = dstart + (j0 + i) * C;
     const int len = min(C, dlen - (j0 + i) * C);
     float v[C];
@@ -147,29 +152,30 @@ __device__ __forceinline__ void chunk_decays(const PrecondParams& p, int h, int 
 template <int D, bool REVERSE>
 __device__ __forceinline__ float chunk_scan(const PrecondParams& p, float* buf, int h, int first, int count,
                                             int dstart, int dlen, float x, float* sDecay) {
-  constexpr int NT = PrecondThreads<D>::v;
+  constexpr int NB = C;  // chunks per block (<= the workgroup's threads)
+  static_assert(NB <= PrecondThreads<D>::v, "one decay per thread");
   const int c = threadIdx.x;
   const int64_t step = (int64_t)p.H * D;
-  for (int b = 0; b < count; b += NT) {
-    const int nb = min(NT, count - b);
+  for (int b = 0; b < count; b += NB) {
+    const int nb = min(NB, count - b);
     const int j0 = REVERSE ? count - b - nb : b;  // first chunk of this block
     // the block's local ends go out first (indices clamped into the block),
     // then the decays' loads: both wait together, one round trip, and the
     // chain below runs on registers in the walk's order
     float* base = buf + ((int64_t)(first + j0) * p.H + h) * D + (c < D ? c : 0);
-    float l[NT];
+    float l[NB];
 #pragma unroll
-    for (int u = 0; u < NT; ++u) l[u] = base[(REVERSE ? max(nb - 1 - u, 0) : min(u, nb - 1)) * step];
+    for (int u = 0; u < NB; ++u) l[u] = base[(REVERSE ? max(nb - 1 - u, 0) : min(u, nb - 1)) * step];
     __syncthreads();
-    chunk_decays(p, h, dstart, dlen, j0, nb, sDecay);
+    chunk_decays(p, h, first, dstart, dlen, j0, nb, sDecay);
     __syncthreads();
     if (c < D) {
 #pragma unroll
-      for (int u = 0; u < NT; ++u) {
+      for (int u = 0; u < NB; ++u) {
         if (u < nb) {
           const int i = REVERSE ? nb - 1 - u : u;
           base[i * step] = x;
-          x = sDecay[i] * x + l[u];
+          x = __builtin_fmaf(sDecay[i], x, l[u]);
         }
       }
     }
@@ -198,6 +204,7 @@ __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j,
   for (int q = 0; q < CH; ++q) a[q] = 0.f;
   if (APPLY) FIO::load(slot, a);
   const float center = APPLY ? p.center[h] : 0.f;
+  float gs = 0.f;  // local pass: the chunk's g_atk summed in token order (masked rows add 0)
   auto tok = [&](int t) -> int64_t { return (int64_t)(start + (FULL ? t : min(t, len - 1))) * H + h; };
 #pragma unroll 1
   for (int g0 = 0; g0 < C; g0 += G) {
@@ -215,6 +222,7 @@ __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j,
       const int t = g0 + u;
       const int64_t th = tok(t);
       const float eg = exp_fast(lg[u]), bt = bg[u];
+      if (!APPLY) gs += (FULL || t < len) ? lg[u] : 0.f;
       float w[CH];
 #pragma unroll
       for (int q = 0; q < CH; ++q) {
@@ -231,7 +239,10 @@ __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j,
       }
     }
   }
-  if (!APPLY) FIO::store(slot, a);
+  if (!APPLY) {
+    FIO::store(slot, a);
+    if (p.chunk_decay && threadIdx.x == 0) p.chunk_decay[(int64_t)j * H + h] = exp_fast(gs);
+  }
 }
 
 template <typename T, int D, bool APPLY>
@@ -270,11 +281,12 @@ __device__ __forceinline__ float row_sum16(float v) {
 }
 
 // Backward launches 1 (APPLY = false: lambda's local value before the chunk
-// from a zero start after it, into lam_chunk) and 3 (APPLY: from the lambda
-// entering the chunk, the gradients).  The chunk is walked in reverse in
-// sub-blocks of 4 (apply) or 8 (local) tokens: a first forward pass keeps A at each sub-block's
-// start, and each sub-block recomputes its A_t from there (the same
-// arithmetic, so the same values) with its k, dkw and dk rows in registers.
+// from a zero start after it, into lam_chunk, and the chunk's decay into
+// chunk_decay) and 3 (APPLY: from the lambda entering the chunk, the
+// gradients).  The chunk is walked in reverse in sub-blocks of 8 tokens: a
+// first forward pass keeps A at each sub-block's start, and each sub-block
+// recomputes its A_t from there (the same arithmetic, so the same values)
+// with its k, dkw and dk rows in registers.
 // Loads clamp as in the forward.  The per-token channel sums leave each
 // 16-lane row in lane (t mod 16) of that row (register t / 16), then cross
 // the rows through LDS.
@@ -283,7 +295,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
                                                   float (*sRow)[C][PrecondChunk<D>::NT / 16 + 1], float* sCen) {
   constexpr int CH = PrecondChunk<D>::CH;
   constexpr int NR = PrecondChunk<D>::NT / 16;  // 16-lane rows
-  constexpr int G = APPLY ? 4 : 8;               // tokens per sub-block (measured best for each pass)
+  constexpr int G = 8;                           // tokens per sub-block (measured best for both passes)
   constexpr int NB = C / G;
   constexpr int NQ = C / 16;                     // per-token sum registers
   using IO = ChanIO<T, CH>;
@@ -318,30 +330,38 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
   };
   // Register arrays indexed by the (rolled) sub-block number go through
   // compile-time selects so they stay in registers.
+  // The forward walk that records them loads GL tokens per memory round
+  // trip (their gate values one per lane, taken back by lane reads), so the
+  // A recomputation waits C / GL times rather than NB times.
+  constexpr int GL = 16;
+  static_assert(GL % G == 0 && C % GL == 0 && GL <= 64, "load rounds hold whole sub-blocks");
   float a_blk[NB][CH];  // A entering each sub-block
+  float gs = 0.f;       // local pass: the chunk's g_atk summed in token order (masked rows add 0)
   {
     float a[CH];
 #pragma unroll
     for (int q = 0; q < CH; ++q) a[q] = a_in[q];
+    const int lt = threadIdx.x & (GL - 1);  // the token whose gate values this lane loads
 #pragma unroll 1
-    for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < C / GL; ++b) {
+      float kb[GL][CH];  // k rows of the round, loaded together
 #pragma unroll
-      for (int r = 0; r < NB; ++r)
+      for (int u = 0; u < GL; ++u) IO::load(k + tok(b * GL + u) * D + c0, kb[u]);
+      const float lgl = g_atk[tok(b * GL + lt)], bgl = beta_atk[tok(b * GL + lt)];
 #pragma unroll
-        for (int q = 0; q < CH; ++q) a_blk[r][q] = r == b ? a[q] : a_blk[r][q];
-      float kb[G][CH], lg[G], bg[G];  // k rows and gate values of the sub-block, loaded together
+      for (int u = 0; u < GL; ++u) {
+        if (u % G == 0) {
+          const int sb = b * (GL / G) + u / G;
 #pragma unroll
-      for (int u = 0; u < G; ++u) {
-        const int64_t th = tok(b * G + u);
-        IO::load(k + th * D + c0, kb[u]);
-        lg[u] = g_atk[th];
-        bg[u] = beta_atk[th];
-      }
+          for (int r = 0; r < NB; ++r)
 #pragma unroll
-      for (int u = 0; u < G; ++u) {
+            for (int q = 0; q < CH; ++q) a_blk[r][q] = r == sb ? a[q] : a_blk[r][q];
+        }
 #pragma unroll
         for (int q = 0; q < CH; ++q) kb[u][q] = active ? kb[u][q] : 0.f;
-        step(b * G + u, a, kb[u], lg[u], bg[u]);
+        const float lgu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lgl), u));
+        step(b * GL + u, a, kb[u], lgu, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bgl), u)));
+        if (!APPLY) gs += (FULL || b * GL + u < len) ? lgu : 0.f;
       }
     }
   }
@@ -366,8 +386,14 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
       IO::load(k + th * D + c0, rk[u]);
       GIO::load(dkw_p + th * D + c0, rdkw[u]);
       if (APPLY) GIO::load(dk_p + th * D + c0, rdk[u]);
-      lg[u] = g_atk[th];
-      bg[u] = beta_atk[th];
+    }
+    {  // the sub-block's gate values, one per lane, read back lane by lane
+      const float lgl = g_atk[tok(g0 + (threadIdx.x & (G - 1)))], bgl = beta_atk[tok(g0 + (threadIdx.x & (G - 1)))];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        lg[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lgl), u));
+        bg[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bgl), u));
+      }
     }
     {
       float a[CH];
@@ -430,6 +456,7 @@ __device__ __forceinline__ void precond_bwd_chunk(const PrecondParams& p, int j,
   }
   if (!APPLY) {
     if (active) FIO::store(p.lam_chunk + row, lam);
+    if (p.chunk_decay && c == 0) p.chunk_decay[(int64_t)j * H + h] = exp_fast(gs);
     return;
   }
 #pragma unroll
@@ -538,6 +565,7 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
   p.dk_final = a->dk_final;
   p.kw32 = a->kw32;
   p.narrow_grads = a->grad_dtype != PKDA_F32;
+  p.chunk_decay = a->chunk_decay;
   PKDA_REQUIRE(!a->slot_idx || a->pool_size > 0, PKDA_EINVAL, "slot-indexed A states need pool_size > 0");
   return 0;
 }

@@ -6,8 +6,9 @@ The forward turns the raw key into the write key
 (``delta_feedback_experiment/pkda.py:392-398``), checkpointing ``A`` at every
 chunk start; the backward is its reverse scan.  Both run in
 ``libpkda_gfx950.so`` (``pkda_precond_fwd`` / ``pkda_precond_bwd``),
-chunk-parallel: local chunk ends, a scan over each document's chunks, then
-the chunks again from their entering values.
+chunk-parallel: local chunk ends (and each chunk's decay, handed to the
+scan in a small workspace), a scan over each document's chunks, then the
+chunks again from their entering values.
 """
 
 from __future__ import annotations
@@ -36,7 +37,8 @@ def _flat2(t: Tensor, plan) -> Tensor:
 
 def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
                     initial_A_state: Tensor | None, *, slot_idx: Tensor | None = None,
-                    final_A: Tensor | None = None, want_kw32: bool = False) -> PrecondState:
+                    final_A: Tensor | None = None, want_kw32: bool = False,
+                    handoff: bool = True) -> PrecondState:
     """Write keys for flat ``kf [N_tok, H, K]``; returns the scan's state.
 
     With ``slot_idx`` the A states are rows of a pool: ``initial_A_state``
@@ -44,7 +46,8 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
     used in place (no conversion copy), document ``n`` at row ``slot_idx[n]``.
     ``want_kw32`` also returns the write keys in FP32 when ``kf`` is narrower
     (the chunk backward with per-channel gates sums its in-block pairs from
-    them)."""
+    them).  ``handoff=False`` passes no chunk-decay workspace: the document
+    scan then sums every chunk's g_atk itself (the same bits, more loads)."""
     dev = kf.device
     H, K, N = plan.heads, plan.head_dim, plan.num_seqs
     ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
@@ -59,6 +62,7 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
     kw = torch.empty_like(kf)
     kw32 = torch.empty(kf.shape, device=dev, dtype=torch.float32) if want_kw32 and kf.dtype != torch.float32 else None
     a_chunk = torch.empty(plan.num_chunks, H, K, device=dev, dtype=torch.float32)
+    decay = torch.empty(plan.num_chunks, H, device=dev, dtype=torch.float32) if handoff else None
     if final_A is None:
         final_A = torch.empty(N, H, K, device=dev, dtype=torch.float32)
     args = _lib.PrecondArgs(
@@ -67,6 +71,7 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
         squash_x=float(x), squash_eps=float(eps), initial_A_state=_ptr(a0), final_A_state=_ptr(final_A),
         kw=_ptr(kw), a_chunk=_ptr(a_chunk), num_chunks=plan.num_chunks, table=_ptr(plan.table),
         slot_idx=_ptr(slot_idx), pool_size=final_A.shape[0] if slot_idx is not None else 0, kw32=_ptr(kw32),
+        chunk_decay=_ptr(decay),
     )
     _lib.call("pkda_precond_fwd", args, _stream(dev))
     return PrecondState(kw, a_chunk, final_A, a0, kw32)
@@ -74,7 +79,7 @@ def precond_forward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: T
 
 def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: Tensor, x: float, eps: float,
                      state: PrecondState, dkw: Tensor, dk: Tensor, dA_T: Tensor | None, want_dA0: bool,
-                     dk_final: Tensor | None = None):
+                     dk_final: Tensor | None = None, handoff: bool = True):
     """Reverse scan: adds the preconditioner's terms into ``dk`` (FP32, in
     place) -- or, with ``dk_final`` (``kf``'s shape and dtype), writes the
     sum there and leaves ``dk`` alone -- and returns ``(dg_atk [N_tok,H],
@@ -82,7 +87,7 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
 
     ``dkw`` and ``dk`` come in FP32, or both in ``kf``'s dtype (the chunk
     backward's key gradients as it rounds them once); the narrow form needs
-    ``dk_final``."""
+    ``dk_final``.  ``handoff`` as in ``precond_forward``."""
     dev = kf.device
     H, K, N = plan.heads, plan.head_dim, plan.num_seqs
     ga, ba, cen = _flat2(g_atk, plan), _flat2(beta_atk, plan), _f32(center)
@@ -91,6 +96,7 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
     dbeta_atk = torch.empty(plan.num_tokens, H, **f32)
     dcenter_part = torch.empty(max(plan.num_chunks, 1), H, **f32)
     lam_chunk = torch.empty(plan.num_chunks, H, K, **f32)
+    decay = torch.empty(plan.num_chunks, H, **f32) if handoff else None
     dcenter = torch.empty(H, **f32)
     dA0 = torch.empty(N, H, K, **f32) if want_dA0 else None
     dAT = None if dA_T is None else _f32(dA_T)
@@ -106,7 +112,7 @@ def precond_backward(plan, kf: Tensor, g_atk: Tensor, beta_atk: Tensor, center: 
         dkw=_ptr(dkw), dk=_ptr(dk), dg_atk=_ptr(dg_atk), dbeta_atk=_ptr(dbeta_atk),
         dcenter_part=_ptr(dcenter_part), dcenter=_ptr(dcenter), dA0=_ptr(dA0), dA_T=_ptr(dAT),
         table=_ptr(plan.table), lam_chunk=_ptr(lam_chunk), dk_final=_ptr(dk_final),
-        grad_dtype=_dtype_code(dkw) if narrow else _lib.PKDA_F32,
+        grad_dtype=_dtype_code(dkw) if narrow else _lib.PKDA_F32, chunk_decay=_ptr(decay),
     )
     if dk_final is not None and (dk_final.shape != kf.shape or dk_final.dtype != kf.dtype
                                  or not dk_final.is_contiguous()):

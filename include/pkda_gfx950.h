@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PKDA_ABI_VERSION 12
+#define PKDA_ABI_VERSION 13
 #define PKDA_CHUNK 64
 
 enum pkda_dtype { PKDA_F32 = 0, PKDA_BF16 = 1 };
@@ -292,6 +292,10 @@ typedef struct pkda_precond_args {
                                     narrow form needs dk_final (the chunk backward hands its
                                     key gradients over in the activation dtype: half the bytes
                                     for it to write and for both reverse-scan passes to read) */
+  float* chunk_decay;            /* optional workspace [num_chunks, H] FP32: each chunk's
+                                    exp(sum of g_atk), written by the local chunk pass and read
+                                    by the document scan (which otherwise sums every chunk's
+                                    g_atk again); the same bits either way */
 } pkda_precond_args;
 
 int pkda_precond_fwd(const pkda_precond_args* args, void* stream);
