@@ -205,6 +205,14 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(RecParams p) {
 // ---------------------------------------------------------------------------
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// A read, through the scalar unit (s_load), of an input the kernel never
+// writes, at an address the same for the whole workgroup: its wait counts
+// apart from the vector memory operations in flight.
+template <typename U>
+__device__ __forceinline__ U scalar_load(const U* ptr) {
+  return *(const __attribute__((address_space(4))) U*)ptr;
+}
+
 template <typename T, int D, int NTH>
 __global__ __launch_bounds__(NTH) void decode_kernel(RecParams p) {
   constexpr int NCG = D / 4;
@@ -222,72 +230,92 @@ __global__ __launch_bounds__(NTH) void decode_kernel(RecParams p) {
   const int rg = tid / NCG;
   const int total = p.num_seqs * H;
   const bool precond = p.g_atk != nullptr;
-  auto state_of = [&](int it) {
-    const int n = it / H, h = it - n * H;
-    const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
-    return p.state_pool + (slot * H + h) * (int64_t)D * D;
+  // Every input of an item is requested one item ahead, and an iteration
+  // runs the current item's channel phase before it sends the next item's
+  // requests: a wait on the vector memory counter (which counts in order)
+  // then never waits for the next item's 64 KiB, which stays in flight
+  // through the current item's reductions and write-back.  The per-channel
+  // inputs (q, k, v, g as raw bits, widened where they are used; dt_bias, A)
+  // come through vector loads behind the state's, the item's uniform values
+  // (its slot, beta, the preconditioner's decay and strength, A_log and
+  // center of its head) through scalar loads, which count apart.
+  struct ItemIn {
+    int64_t slot;
+    float beta, g_atk, beta_atk, A_log, center;
   };
-  // One item's per-channel inputs (thread c < D holds channel c).
   struct ChanIn {
-    float q, k, v, g, beta, a, g_atk, beta_atk;
+    uint32_t q, k, v, g;  // T's (and g's) bits
+    float dtb, a;
   };
-  auto load_chan = [&](int it, ChanIn& x) {
-    if (tid >= D) return;
+  auto widen = [&](uint32_t bits, bool narrow) { return __uint_as_float(narrow ? bits << 16 : bits); };
+  constexpr bool TN = sizeof(T) == 2;
+  auto load_item = [&](int it, ItemIn& x) {
     const int n = it / H, h = it - n * H;
     const int64_t th = (int64_t)n * H + h;
-    const int c = tid;
-    x.q = io<T>::load(static_cast<const T*>(p.q) + th * D + c);
-    x.k = io<T>::load(static_cast<const T*>(p.k) + th * D + c);
-    x.v = io<T>::load(static_cast<const T*>(p.v) + th * D + c);
-    x.g = load_any(p.g, p.gate_kind == PKDA_GATE_LOG_HEAD ? th : th * D + c, p.g_dtype);
-    x.beta = p.beta[th];
+    x.slot = p.slot_idx ? scalar_load(p.slot_idx + n) : n;
+    x.beta = scalar_load(p.beta + th);
+    x.A_log = p.gate_kind == PKDA_GATE_RAW_CHANNEL ? scalar_load(p.A_log + h) : 0.f;
     if (precond) {
-      const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
-      x.a = p.a_pool[(slot * H + h) * (int64_t)D + c];
-      x.g_atk = p.g_atk[th];
-      x.beta_atk = p.beta_atk[th];
+      x.g_atk = scalar_load(p.g_atk + th);
+      x.beta_atk = scalar_load(p.beta_atk + th);
+      x.center = scalar_load(p.center + h);
     }
   };
+  // (every lane loads -- the lanes past D a copy of channel D - 1, unused --
+  // so the loaded registers join no divergent branch and wait for nothing)
+  auto load_chan = [&](int it, const ItemIn& xi, ChanIn& x) {
+    const int n = it / H, h = it - n * H;
+    const int64_t th = (int64_t)n * H + h;
+    const int c = min(tid, D - 1);
+    using R = std::conditional_t<TN, uint16_t, uint32_t>;
+    x.q = reinterpret_cast<const R*>(p.q)[th * D + c];
+    x.k = reinterpret_cast<const R*>(p.k)[th * D + c];
+    x.v = reinterpret_cast<const R*>(p.v)[th * D + c];
+    const int64_t gi = p.gate_kind == PKDA_GATE_LOG_HEAD ? th : th * D + c;
+    if (p.g_dtype == PKDA_BF16) x.g = static_cast<const uint16_t*>(p.g)[gi];
+    else x.g = static_cast<const uint32_t*>(p.g)[gi];
+    if (p.gate_kind == PKDA_GATE_RAW_CHANNEL) x.dtb = p.dt_bias[h * D + c];
+    if (precond) x.a = p.a_pool[(xi.slot * H + h) * (int64_t)D + c];
+  };
+  auto state_of = [&](int it, int64_t slot) {
+    const int h = it - (it / H) * H;
+    return p.state_pool + (slot * H + h) * (int64_t)D * D;
+  };
   f4v S[RPT], Sn[RPT];
+  ItemIn ci{}, ni{};
   ChanIn cur{}, nxt_in{};
   int item = blockIdx.x;
   if (item < total) {
-    const float* src = state_of(item);
+    load_item(item, ci);
+    const float* src = state_of(item, ci.slot);
 #pragma unroll
     for (int j = 0; j < RPT; ++j)
       S[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src + (rg + NRG * j) * D + 4 * cg));
-    load_chan(item, cur);
+    load_chan(item, ci, cur);
   }
   for (; item < total; item += gridDim.x) {
     const int nxt = item + gridDim.x;
-    if (nxt < total) {
-      const float* src = state_of(nxt);
-#pragma unroll
-      for (int j = 0; j < RPT; ++j)
-        Sn[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src + (rg + NRG * j) * D + 4 * cg));
-      load_chan(nxt, nxt_in);
-    }
     const int n = item / H, h = item - n * H;
-    const int64_t slot = p.slot_idx ? p.slot_idx[n] : n;
+    const int64_t slot = ci.slot;
     const int64_t th = (int64_t)n * H + h;
     // ---- channel phase ------------------------------------------------------
     float qk_part = 0.f;
     if (tid < D) {
       const int c = tid;
-      const float qc = cur.q * p.scale;
-      const float kc = cur.k;
-      const float vc = cur.v;
-      float gl = cur.g;
-      if (p.gate_kind == PKDA_GATE_RAW_CHANNEL) gl = -expf(p.A_log[h]) * softplus_sigmoid_fast(gl + p.dt_bias[h * D + c]).softplus;
+      const float qc = widen(cur.q, TN) * p.scale;
+      const float kc = widen(cur.k, TN);
+      const float vc = widen(cur.v, TN);
+      float gl = widen(cur.g, p.g_dtype == PKDA_BF16);
+      if (p.gate_kind == PKDA_GATE_RAW_CHANNEL) gl = -expf(ci.A_log) * softplus_sigmoid_fast(gl + cur.dtb).softplus;
       const float al = expf(gl);
       float kw = kc;
       if (precond) {
-        const float a_c = expf(cur.g_atk) * cur.a + cur.beta_atk * (kc * kc);
+        const float a_c = expf(ci.g_atk) * cur.a + ci.beta_atk * (kc * kc);
         p.a_pool[(slot * H + h) * (int64_t)D + c] = a_c;
-        const float r = logf(a_c + p.squash_eps) - p.center[h];
+        const float r = logf(a_c + p.squash_eps) - ci.center;
         kw = kc * expf(-p.log_x * (r / (1.f + fabsf(r))));
       }
-      const float bt = cur.beta;
+      const float bt = ci.beta;
       s_ak[c] = al * kc;
       s_aq[c] = al * qc;
       s_al[c] = al;
@@ -298,6 +326,18 @@ __global__ __launch_bounds__(NTH) void decode_kernel(RecParams p) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) qk_part += __shfl_xor(qk_part, off);
     if ((tid & 63) == 0) s_qk[tid >> 6] = qk_part;
+    // ---- the next item's requests -------------------------------------------
+    // (its few per-channel bytes unconditionally, for this item again when
+    // there is no next one: loads behind no branch join nothing)
+    const int nl = nxt < total ? nxt : item;
+    load_item(nl, ni);
+    if (nxt < total) {
+      const float* src = state_of(nxt, ni.slot);
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        Sn[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(src + (rg + NRG * j) * D + 4 * cg));
+    }
+    load_chan(nl, ni, nxt_in);
     __syncthreads();
     // ---- column reductions of the old state ---------------------------------
     float4 pe = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -339,6 +379,7 @@ __global__ __launch_bounds__(NTH) void decode_kernel(RecParams p) {
     __syncthreads();  // LDS is reused by the next item
 #pragma unroll
     for (int j = 0; j < RPT; ++j) S[j] = Sn[j];
+    ci = ni;
     cur = nxt_in;
   }
 }
