@@ -151,6 +151,55 @@ def test_decode_step_pool_matches_oracle(dev, precond):
         assert torch.equal(a_d.cpu()[untouched], a_pool[untouched])
 
 
+@pytest.mark.parametrize("D,dtype,g_form,slots_given", [
+    (32, torch.float32, "channel", True),    # 256-thread items, half a wave of channels
+    (64, torch.bfloat16, "channel_bf16", False),  # slots 0..N-1 (slot_idx None), g in BF16
+    (128, torch.bfloat16, "head", False),
+])
+def test_decode_step_input_forms_match_oracle(dev, D, dtype, g_form, slots_given):
+    """The decode step reads each item's inputs one item ahead: the uniform
+    ones (slot, beta, the preconditioner's per-token and per-head values) by
+    scalar loads, the per-channel ones as raw bits widened where used.  Every
+    form of those inputs against the oracle: FP32 and BF16 activations, a
+    per-head or per-channel log decay in FP32 or BF16, with and without
+    slot indices, d = 32 / 64 / 128, the preconditioner on, over enough
+    items that every workgroup walks several."""
+    from delta_feedback_experiment_amd import pkda_decode_step_
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    H = 16
+    N = -(-3 * 12 * cus // H)  # about three items per workgroup
+    P = N + 7 if slots_given else N
+    assert N * H > 12 * cus
+    print(f"[gpu] decode input forms D={D} {dtype} g={g_form} slots={slots_given} items={N * H}", flush=True)
+    gen = torch.Generator().manual_seed(300 + D)
+    pool = 0.02 * torch.randn(P, H, D, D, generator=gen)
+    a_pool = 0.1 * torch.randn(P, H, D, generator=gen).abs()
+    slots = torch.randperm(P, generator=gen)[:N].to(torch.int32) if slots_given else torch.arange(N, dtype=torch.int32)
+    q, k, v, g, beta = _inputs(N, 1, H, D, dtype, seed=301, per_channel=g_form != "head")
+    q, k, v, g, beta = q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0]
+    if g_form == "channel_bf16":
+        g = g.to(torch.bfloat16)
+    extra = dict(g_atk=-F.softplus(torch.randn(N, H, generator=gen)),
+                 beta_atk=torch.sigmoid(torch.randn(N, H, generator=gen)),
+                 log_atk_scale=-0.2 + 0.1 * torch.randn(H, generator=gen), x=1.5)
+    pool_ref, a_ref = pool.clone(), a_pool.clone()
+    o_ref = oracle.decode_step_reference(q, k, v, g.float(), beta, pool_ref, slots, a_pool=a_ref, **extra)
+    pool_d, a_d = pool.to(dev), a_pool.to(dev)
+    o = pkda_decode_step_(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), pool_d,
+                          slots.to(dev) if slots_given else None, a_pool=a_d,
+                          **{kk: (vv.to(dev) if torch.is_tensor(vv) else vv) for kk, vv in extra.items()})
+    torch.cuda.synchronize()
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    sl = slots.long()
+    assert rel_l2(o.float(), o_ref.float()) < tol
+    assert rel_l2(pool_d.cpu()[sl], pool_ref[sl]) < FP32_TOL
+    assert rel_l2(a_d.cpu()[sl], a_ref[sl]) < FP32_TOL
+    untouched = torch.ones(P, dtype=torch.bool)
+    untouched[sl] = False
+    assert torch.equal(pool_d.cpu()[untouched], pool[untouched])
+
+
 @pytest.mark.parametrize("P,N,H,D,precond", [
     (512, 256, 32, 128, False),   # BASELINE config 4: 8,192 (slot, head) items
     (512, 256, 32, 128, True),
