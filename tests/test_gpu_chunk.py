@@ -584,6 +584,41 @@ def test_chunk_production_gate_matches_oracle(dev, D, dtype):
         assert val < tol, (n, val)
 
 
+@pytest.mark.parametrize("lean", [False, True])
+def test_pkda_recurrence_fp32_long_matches_fp64_oracle(dev, lean):
+    """The training op with FP32 activations over sixteen chunks per row
+    (T = 1,024): the per-channel state passes carry the state across every
+    chunk, the preconditioner's document scans walk sixteen chunk ends each
+    way, and the per-channel backward forms every decay inside a chunk from
+    the gate's cumsum and its FP64 remainder.  Output and all ten gradients
+    against the oracle run in FP64, at the FP32 bar."""
+    from delta_feedback_experiment_amd import pkda_recurrence
+
+    print(f"[gpu] pkda_recurrence FP32 T=1024 lean={lean}", flush=True)
+    B, T, H, D = 1, 1024, 2, 64
+    base = _production_inputs(B, T, H, D, torch.float32, 23)
+    q, k, v, g_raw, beta, A_log, dt_bias, g_atk, beta_atk, center = base
+    base = (q, k, v, g_raw, g_atk, beta_atk, beta, A_log, dt_bias, center)
+    names = ("q", "k", "v", "g", "g_atk", "beta_atk", "beta", "A_log", "dt_bias", "log_atk_scale")
+    do = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(3))
+    t = [x.double().clone().requires_grad_() for x in base]
+    o_r = oracle.pkda_reference(t[0], t[1], t[2], t[3], t[6], A_log=t[7], dt_bias=t[8], use_gate_in_kernel=True,
+                                g_atk=t[4], beta_atk=t[5], log_atk_scale=t[9], x=1.5, eps=1e-6,
+                                dtype=torch.float64, out_dtype=torch.float64)[0]
+    g_r = torch.autograd.grad((o_r * do.double()).sum(), t)
+    leaves = [x.to(dev).clone().requires_grad_() for x in base]
+    o, _ = pkda_recurrence(*leaves, D ** -0.5, 1.5, 1e-6, lean)
+    g_d = torch.autograd.grad((o * do.to(dev)).sum(), leaves)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float32
+    res = {"o": rel_l2(o.double(), o_r)}
+    for n, a, b in zip(names, g_d, g_r):
+        res["d" + n] = rel_l2(a.double(), b)
+    print("  " + " ".join(f"{k_}={v_:.2e}" for k_, v_ in res.items()), flush=True)
+    for n, val in res.items():
+        assert val < FP32_TOL, (n, val)
+
+
 @pytest.mark.parametrize("lean,seed", [(False, 41), (True, 41), (False, 2), (False, 6)])
 def test_pkda_recurrence_op_matches_oracle(dev, lean, seed):
     """The training custom op exactly as PreconditionedKDA._cuda_recurrence
