@@ -492,6 +492,17 @@ struct RegTile {
     }
   }
   __device__ __forceinline__ void store(T* lds, int ld) const { store_as(threadIdx.x, lds, ld); }
+  // every value times a, in the registers (a float tile)
+  __device__ __forceinline__ void scale(float a) {
+    static_assert(sizeof(T) == 4, "scale() is for float tiles");
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      r[i].x = __float_as_uint(__uint_as_float(r[i].x) * a);
+      r[i].y = __float_as_uint(__uint_as_float(r[i].y) * a);
+      r[i].z = __float_as_uint(__uint_as_float(r[i].z) * a);
+      r[i].w = __float_as_uint(__uint_as_float(r[i].w) * a);
+    }
+  }
   __device__ __forceinline__ void store_as(int t, T* lds, int ld) const {
     __builtin_assume(t >= 0 && t < NT);
 #pragma unroll

@@ -645,7 +645,7 @@ struct IntraPc2Layout {
   static constexpr int off_K = 0;                          // K half, then Bw half
   static constexpr int off_Q = off_K + RT;                 // Q half, then solve scratch (with KW), then Bv half
   static constexpr int off_KW = off_Q + QR;                // KW half (when not aliased to K)
-  static constexpr int off_G = off_KW + (ALIAS ? 0 : RT);  // fp32 [64][LDG] half of G
+  static constexpr int off_G = off_KW + (ALIAS ? 0 : RT);  // fp32 [64][LDG] half of G, times log2 e
   static constexpr int off_A = off_G + C * LDG * 4;        // fp32 [64][LDF]: Akk, then T
   static constexpr int off_Aqk = off_A + C * LDF * 4;      // bf16 Aqk, then T
   static constexpr int off_beta = off_Aqk + C * LDC * 2;
@@ -701,6 +701,7 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
     K0.store(sK, L::LD);
     Q0.store(sQ, L::LD);
     if (!ALIAS) KW0.store(sKW, L::LD);
+    G0.scale(kLog2e);
     G0.store(sG, L::LDG);
   }
 #pragma unroll 1
@@ -726,7 +727,12 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
     t = 16 * tb + tl;
     s = 16 * tb + rest;
   };
+  // (eight VALU operations per pair and channel: three widenings, the
+  // difference, exp2 of it (G is staged times log2 e), w e^(G_t - G_s) once for
+  // both sums, two FMAs; unrolled four pieces deep: fully unrolled, the loads
+  // hoisted ahead take every register and spill)
   auto pair_sums = [&](int t, int s, int c0, int c1, float& akk, float& aqk) {
+#pragma unroll 4
     for (int c = c0; c < c1; c += V) {
       float kx[V], qx[V], wx[V];
       lds_vec<V>(sK + t * L::LD + c, kx);
@@ -734,9 +740,9 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
       lds_vec<V>(sKW + s * L::LD + c, wx);
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float e = exp_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
-        akk += kx[j] * wx[j] * e;
-        aqk += qx[j] * wx[j] * e;
+        const float we = wx[j] * exp2_fast(sG[t * L::LDG + c + j] - sG[s * L::LDG + c + j]);
+        akk = __builtin_fmaf(kx[j], we, akk);
+        aqk = __builtin_fmaf(qx[j], we, aqk);
       }
     }
   };
@@ -769,8 +775,8 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
 #pragma unroll
         for (int j = 0; j < F::N; ++j) {
           const float gr = sG[r * L::LDG + kk + j];
-          const float fa = exp_fast(sG[t * L::LDG + kk + j] - gr);
-          const float fb = exp_fast(gr - sG[s * L::LDG + kk + j]);
+          const float fa = exp2_fast(sG[t * L::LDG + kk + j] - gr);
+          const float fb = exp2_fast(gr - sG[s * L::LDG + kk + j]);
           ak[j] = from_e<E>(sK[t * L::LD + kk + j]) * fa;
           aq[j] = from_e<E>(sQ[t * L::LD + kk + j]) * fa;
           bw[j] = from_e<E>(sKW[s * L::LD + kk + j]) * fb;
@@ -789,8 +795,8 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
 #pragma unroll
         for (int j = 0; j < V; ++j) {
           const float gv = sG[r * L::LDG + c + j];
-          qx[j] *= p.scale * exp_fast(gv);
-          wx[j] *= exp_fast(sG[(C - 1) * L::LDG + c + j] - gv);
+          qx[j] *= p.scale * exp2_fast(gv);
+          wx[j] *= exp2_fast(sG[(C - 1) * L::LDG + c + j] - gv);
         }
         store_vec<V>(qg_out + r * gs + hc + c, qx);
         store_vec<V>(kg_out + r * gs + hc + c, wx);
@@ -814,13 +820,14 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
 #pragma unroll 1
     for (int i = tid; i < C * DH; i += kIW) {
       const int r = i / DH, c = i - r * DH;
-      sBw0[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+      sBw0[r * L::LD + c] = to_e<E>(sBeta[r] * exp2_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
     }
     __syncthreads();
     // ---- second half -----------------------------------------------------------
     K1.store(sK, L::LD);
     Q1.store(sQ, L::LD);
     if (!ALIAS) KW1.store(sKW, L::LD);
+    G1.scale(kLog2e);
     G1.store(sG, L::LDG);
   }
   __syncthreads();
@@ -875,7 +882,7 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
 #pragma unroll 1
       for (int i = tid; i < C * DH; i += kIW) {
         const int r = i / DH, c = i - r * DH;
-        sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
+        sK[r * L::LD + c] = to_e<E>(sBeta[r] * exp2_fast(sG[r * L::LDG + c]) * from_e<E>(sK[r * L::LD + c]));
       }
     }
     // this half's V columns from the register tile (pieces of 8 columns)

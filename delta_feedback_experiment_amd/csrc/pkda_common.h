@@ -48,7 +48,12 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
 // e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32).  The rounding of the
 // scaled argument costs a relative error of about |x| 6e-8; the chunk
 // kernels take it on decay factors e^(G_t - G_s) <= 1.
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+constexpr float kLog2e = 1.44269504088896341f;
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+// 2^x on the hardware exp2: e^y for an argument already scaled, x = y log2 e
+// (a cumulative log decay staged once as G log2 e saves the multiply on every
+// pair that differences it)
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ln x as log2(x) ln 2 on the hardware log2 (v_log_f32), for x > 0 normal.
 __device__ __forceinline__ float log_fast(float x) { return __builtin_amdgcn_logf(x) * 0.693147180559945309f; }
