@@ -1411,7 +1411,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
     const int c = 16 * (ch * HCT + j) + (lane & 15);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      sG[(r0 + rq + e) * L::LDG + c] = Gl[j][e];
+      sG[(r0 + rq + e) * L::LDG + c] = L::GLO ? Gl[j][e] : Gl[j][e] * kLog2e;
       if constexpr (L::GLO) sGlo[(r0 + rq + e) * L::LDG + c] = Gll[j][e];
       sKWf[(r0 + rq + e) * L::LDW + c] = r0 + rq + e < len ? Wl[j][e] : 0.f;
     }
@@ -1460,6 +1460,13 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       if constexpr (L::GLO) return (a - b) + (al - bl);
       else return a - b;
     };
+    // e^d for a difference d of staged G values: without the FP32 remainders
+    // G is staged times log2 e, so each exponential is one exp2 (the multiply
+    // by log2 e done once per element at staging, not once per pair)
+    auto exg = [](float d) -> float {
+      if constexpr (L::GLO) return exp_fast(d);
+      else return exp2_fast(d);
+    };
     {
       float kgc = 0.f;
 #pragma unroll
@@ -1478,7 +1485,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
         // enter two of q dq, kw dkw and sum(kg dkg) with opposite signs and
         // are left out of the gate gradient
         dg[e] = qv[e] * dq[0][e] + kv[e] * dk[0][e] - (r == len - 1 ? 0.f : wv[e] * dkws[0][e]);
-        if (r == len - 1) dg[e] += exp_fast(sG[(C - 1) * L::LDG + c]) * sHD[c] + kgc;
+        if (r == len - 1) dg[e] += exg(sG[(C - 1) * L::LDG + c]) * sHD[c] + kgc;
         dq[0][e] += pd * wv[e];
         dkwj[e] = dkws[0][e] + pd * qv[e];
       }
@@ -1500,7 +1507,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
         else lds4(sP2T + (16 * rb + rq + u) * 16 + rq, p2);
 #pragma unroll
         for (int e = u + 1; e < 4; ++e) {
-          const float w = wv[u] * exp_fast(gdv(gr[e], grl[e], gr[u], grl[u]));
+          const float w = wv[u] * exg(gdv(gr[e], grl[e], gr[u], grl[u]));
           ak[e] += p1[e] * w;
           aq[e] += p2[e] * w;
         }
@@ -1541,7 +1548,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           else a2 = from_e<E>(sP2[(r0 + mrow) * L::LDC + x]);
 #pragma unroll
           for (int g = j + 1; g < 4; ++g) {
-            const float bx = kwx * exp_fast(gdv(g0[g], g0l[g], gx, gxl));
+            const float bx = kwx * exg(gdv(g0[g], g0l[g], gx, gxl));
             Mma<float>::mfma(mk, ag == g ? a1 : 0.f, bx);
             Mma<float>::mfma(mq, ag == g ? a2 : 0.f, bx);
           }
@@ -1554,7 +1561,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float R = e == 0 ? 1.f : exp_fast(gdv(gr[e], grl[e], gr[0], grl[0]));
+        const float R = e == 0 ? 1.f : exg(gdv(gr[e], grl[e], gr[0], grl[0]));
         ak[e] += R * ak0[e];
         aq[e] += R * aq0[e];
         const float bk = sBeta[r0 + rq + e] * ak[e];
@@ -1579,7 +1586,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
             const int x = kk + jj;
-            bx[jj] = sKWf[x * L::LDW + nn] * exp_fast(grlo - sG[x * L::LDG + nn]);
+            bx[jj] = sKWf[x * L::LDW + nn] * exg(grlo - sG[x * L::LDG + nn]);
           }
           const s16x4_t b = pack_bf16x4(bx);
           mfma16_bf16(akX, a1, b);
@@ -1593,7 +1600,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           const int x = kk + jj;
           a1[jj] = from_e<E>(sP1r[(r0 + (lane & 15)) * L::LDC + x]);
           a2[jj] = from_e<E>(sP2[(r0 + (lane & 15)) * L::LDC + x]);
-          bx[jj] = x <= rlo ? sKWf[x * L::LDW + nn] * exp_fast(gdv(grlo, grlo_l, sG[x * L::LDG + nn], glo(x, nn)))
+          bx[jj] = x <= rlo ? sKWf[x * L::LDW + nn] * exg(gdv(grlo, grlo_l, sG[x * L::LDG + nn], glo(x, nn)))
                             : 0.f;
         }
         F::mfma(akX, a1, bx);
@@ -1603,7 +1610,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float sb = sBeta[r0 + rq + e];
-        const float dlo = exp_fast(gdv(gr[e], grl[e], grlo_c, grlo_cl));  // e^{G[t]-G[R]}
+        const float dlo = exg(gdv(gr[e], grl[e], grlo_c, grlo_cl));  // e^{G[t]-G[R]}
         dk[0][e] += sb * dlo * akX[e];
         db[e] += kv[e] * dlo * akX[e];
         dq[0][e] += dlo * aqX[e];
@@ -1626,7 +1633,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
         else lds4(sP2 + t * L::LDC + r0 + rq, p2);
         const float kx = sBeta[t] * kv[u], qx = qv[u];
 #pragma unroll
-        for (int e = 0; e < u; ++e) aw[e] += (p1[e] * kx + p2[e] * qx) * exp_fast(gdv(gr[u], grl[u], gr[e], grl[e]));
+        for (int e = 0; e < u; ++e) aw[e] += (p1[e] * kx + p2[e] * qx) * exg(gdv(gr[u], grl[u], gr[e], grl[e]));
       }
       // t in the block's later 4-row groups (t > t_3): FP32 MFMA steps, one per
       // (key group g, row group i > g), the decay split at t_3 of group g:
@@ -1654,7 +1661,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           else a2 = from_e<E>(sP2[t * L::LDC + r0 + mrow]);
 #pragma unroll
           for (int g = 0; g < i; ++g) {
-            const float f = exp_fast(gdv(gt, gtl, g3[g], g3l[g]));
+            const float f = exg(gdv(gt, gtl, g3[g], g3l[g]));
             Mma<float>::mfma(mw, ag == g ? a1 : 0.f, kt * f);
             Mma<float>::mfma(mw, ag == g ? a2 : 0.f, qt * f);
           }
@@ -1664,7 +1671,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        aw[e] += (e == 3 ? 1.f : exp_fast(gdv(gr[3], grl[3], gr[e], grl[e]))) * aw0[e];
+        aw[e] += (e == 3 ? 1.f : exg(gdv(gr[3], grl[3], gr[e], grl[e]))) * aw0[e];
         dkwj[e] += aw[e];
         dg[e] -= wv[e] * aw[e];
       }
@@ -1686,7 +1693,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int t = 16 * bi + 4 * (lane >> 4) + jj;
-          const float f = exp_fast(sG[t * L::LDG + nn] - gR);
+          const float f = exg(sG[t * L::LDG + nn] - gR);
           b1[jj] = sBeta[t] * bf16_to_f32(static_cast<bf16_t>(kt[jj])) * f;  // beta_t on the key, dAkk unscaled
           b2[jj] = bf16_to_f32(static_cast<bf16_t>(qt[jj])) * f;
         }
@@ -1700,7 +1707,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
           const int t = kk + jj;
           a1[jj] = from_e<E>(sP1r[t * L::LDC + r0 + (lane & 15)]);
           a2[jj] = from_e<E>(sP2[t * L::LDC + r0 + (lane & 15)]);
-          const float f = t > R && t <= R + 16 ? exp_fast(gdv(sG[t * L::LDG + nn], glo(t, nn), gR, gRl)) : 0.f;
+          const float f = t > R && t <= R + 16 ? exg(gdv(sG[t * L::LDG + nn], glo(t, nn), gR, gRl)) : 0.f;
           b1[jj] = sBeta[t] * from_e<E>(sK[t * L::LD + nn]) * f;  // beta_t on the key, dAkk unscaled
           b2[jj] = from_e<E>(sQ[t * L::LD + nn]) * f;
         }
@@ -1710,7 +1717,7 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
       const float gRc = sG[R * L::LDG + c], gRcl = glo(R, c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float dec = exp_fast(gdv(gRc, gRcl, gr[e], grl[e]));  // e^{G[R]-G[x]}
+        const float dec = exg(gdv(gRc, gRcl, gr[e], grl[e]));  // e^{G[R]-G[x]}
         dkwj[e] += dec * aw[e];
         dg[e] -= rnd(wv[e] * dec) * aw[e];  // the row side's B operand kw e^{G[R]-G[x]}
       }
