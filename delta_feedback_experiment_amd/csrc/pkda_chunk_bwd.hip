@@ -322,9 +322,12 @@ __global__ __launch_bounds__(kFW) void chunk_fused_bwd_kernel(BwdParams p) {
   constexpr bool kDbv = implicit_w<T>();
   constexpr int HCT = D / 32;  // column tiles per wave of a [64 x D] output
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const int H = p.H;
+  const ChunkHead wg = chunk_head<true>(H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
   if (ci.len <= 0) return;
-  const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
+  const int cid = wg.cid, hh = wg.h;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int rb = wave & 3, ch = wave >> 2;
   const int r0 = 16 * rb;
@@ -661,7 +664,9 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
   using M = Mma<bf16_t>;
   constexpr int NJ = D / 64;  // column tiles per wave
   constexpr int KV = D / 32;  // k steps over the value index
-  const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
+  const int H = p.H;
+  const ChunkHead wg = chunk_head<true>(H);
+  const int cid = wg.cid, hh = wg.h;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int q = lane >> 4, il = lane & 15;
   const int64_t gs = (int64_t)H * D;
@@ -1067,7 +1072,9 @@ __device__ __forceinline__ void fused_bwd_w4(const BwdParams& p, const ChunkInfo
 template <int D>
 __global__ __launch_bounds__(kW4, 2) void chunk_fused_bwd_w4_kernel(BwdParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const ChunkHead wg = chunk_head<true>(p.H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
   if (ci.len == C) fused_bwd_w4<D>(p, ci, C, smem);
   else if (ci.len > 0) fused_bwd_w4<D>(p, ci, ci.len, smem);
 }
@@ -1142,7 +1149,9 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
   using E = T;
   using F = FragK<E>;
   constexpr int HCT = D / 32;
-  const int cid = blockIdx.x, hh = blockIdx.y, H = p.H;
+  const int H = p.H;
+  const ChunkHead wg = chunk_head<false>(H);
+  const int cid = wg.cid, hh = wg.h;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // waves w and w + 4 share a SIMD: they take row blocks rb and 3 - rb, whose
   // cross-block pair work (later blocks for small rb, earlier ones for large)
@@ -1762,7 +1771,9 @@ __device__ __forceinline__ void fused_bwd_pc(const BwdParams& p, const ChunkInfo
 template <typename T, int D, typename OT, typename OK>
 __global__ __launch_bounds__(kFW) void chunk_fused_bwd_pc_kernel(BwdParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const ChunkHead wg = chunk_head<false>(p.H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
   if (ci.len == C) fused_bwd_pc<T, D, OT, OK>(p, ci, C, smem);
   else if (ci.len > 0) fused_bwd_pc<T, D, OT, OK>(p, ci, ci.len, smem);
 }
@@ -2408,7 +2419,7 @@ int launch_bwd(const BwdParams& p_in, int num_chunks, int stages, hipStream_t s)
         auto kern = chunk_fused_bwd_w4_kernel<D>;
         constexpr int bytes = FusedW4Layout<D>::bytes;
         if (int st = set_smem(kern, bytes)) return st;
-        hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kW4), bytes, s, p);
+        hipLaunchKernelGGL(kern, dim3(chunk_grid<true>(num_chunks, p.H)), dim3(kW4), bytes, s, p);
         return launch_status("pkda_chunk_bwd(chunk)");
       }
     }
@@ -2417,7 +2428,7 @@ int launch_bwd(const BwdParams& p_in, int num_chunks, int stages, hipStream_t s)
                                   : chunk_fused_bwd_kernel<T, D, OT, OK, false>);
     const int bytes = p.qg ? FusedBwdPcLayout<T, D>::bytes : FusedBwdLayout<T, D>::bytes;
     if (int st = set_smem(kern, bytes)) return st;
-    hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kFW), bytes, s, p);
+    hipLaunchKernelGGL(kern, p.qg ? dim3(chunk_grid<false>(num_chunks, p.H)) : dim3(chunk_grid<true>(num_chunks, p.H)), dim3(kFW), bytes, s, p);
     if (int st = launch_status("pkda_chunk_bwd(chunk)")) return st;
   }
   return 0;

@@ -50,6 +50,41 @@ struct ChunkInfo {
 // Host: fill a ChunkGeom from the entry-point arguments (validates them).
 int chunk_geom_from(const int32_t* cu, int num_seqs, int seqlen, int num_chunks, const int32_t* table, ChunkGeom& g);
 
+// (chunk, head) of a workgroup on the 1-D grid of chunk_grid<XCD>(num_chunks,
+// H) workgroups, heads fastest: the workgroups resident together read the H
+// heads' adjacent pieces of the same token rows of a [token][head][channel]
+// tensor (4 KB spans at H D = 2048 BF16), not one head's pieces of rows that
+// far apart.  Workgroup b runs on XCD b % 8.  With XCD, slot l = b / 8 of
+// XCD x is head l % H of chunk 8 (l / H) + x: an XCD takes whole chunks, all
+// H heads in a row, so the per-token lines of [token][head] values (the
+// per-head gate, beta: 16 heads share a line) come through one L2 instead of
+// eight, and the eight XCDs work on eight adjacent chunks at a time; the
+// chunk count is padded to a multiple of 8, and a workgroup with
+// cid >= num_chunks has no work.  Without XCD, b = cid H + h.  (The per-head
+// kernels take the XCD order; the per-channel kernels, whose per-token lines
+// belong to one head, measured faster without it.)
+constexpr int kXcds = 8;
+struct ChunkHead {
+  int cid, h;
+};
+template <bool XCD>
+__host__ __device__ inline unsigned chunk_grid(int num_chunks, int H) {
+  const int64_t nc = XCD ? (int64_t)(num_chunks + kXcds - 1) / kXcds * kXcds : num_chunks;
+  return (unsigned)(nc * H);
+}
+template <bool XCD>
+__device__ __forceinline__ ChunkHead chunk_head(int H) {
+  const int b = blockIdx.x;
+  if constexpr (XCD) {
+    const int l = b / kXcds;
+    const int cl = l / H;
+    return {cl * kXcds + (b - l * kXcds), l - cl * H};
+  } else {
+    const int c = b / H;
+    return {c, b - c * H};
+  }
+}
+
 __device__ __forceinline__ ChunkInfo chunk_info(const ChunkGeom& g, int c) {
   ChunkInfo ci;
   if (g.cu) {

@@ -190,8 +190,9 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
   constexpr bool LEAN = !WU && L::lean_fits;  // Akk over K's region
   using E = T;
   constexpr int HCT = D / 32;  // column tiles per wave of W / u
-  const int h = blockIdx.y;
   const int H = p.H;
+  const ChunkHead wg = chunk_head<true>(H);
+  const int h = wg.h;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t row0 = (int64_t)ci.start * H + h;  // token-row index of the chunk's first token
   const int64_t gs = (int64_t)H * D;               // token stride in elements
@@ -241,7 +242,7 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
   // past its end zero
   constexpr bool TRI_OK = std::is_same<T, bf16_t>::value && !WU;
   const bool tri = TRI_OK && p.tri_packed;
-  T* aqk_tri = static_cast<T*>(p.aqk) + ((int64_t)blockIdx.x * H + h) * kTriElems;
+  T* aqk_tri = static_cast<T*>(p.aqk) + ((int64_t)wg.cid * H + h) * kTriElems;
   f32x4 akk_keep[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -316,7 +317,7 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
   if (!WU) {
     if constexpr (TRI_OK) {
       if (tri) {
-        store_tri_from_f32<kIW>(static_cast<bf16_t*>(p.akk) + ((int64_t)blockIdx.x * H + h) * kTriElems, sA, L::LDF,
+        store_tri_from_f32<kIW>(static_cast<bf16_t*>(p.akk) + ((int64_t)wg.cid * H + h) * kTriElems, sA, L::LDF,
                                 len);
         return;
       }
@@ -354,7 +355,9 @@ __device__ __forceinline__ void intra_fwd_chunk(const FwdParams& p, const ChunkI
 template <typename T, int D, bool ALIAS, bool WU>
 __global__ __launch_bounds__(kIW) void chunk_intra_fwd_kernel(FwdParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const ChunkHead wg = chunk_head<true>(p.H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
   if (ci.len == C) intra_fwd_chunk<T, D, ALIAS, WU>(p, ci, C, smem);
   else if (ci.len > 0) intra_fwd_chunk<T, D, ALIAS, WU>(p, ci, ci.len, smem);
 }
@@ -616,9 +619,11 @@ __device__ __forceinline__ void intra_pc_run(const FwdParams& p, const ChunkInfo
 template <typename T, int D, bool ALIAS>
 __global__ __launch_bounds__(kIW) void chunk_intra_fwd_pc_kernel(FwdParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len == C) intra_pc_run<T, D, ALIAS>(p, ci, blockIdx.y, C, smem);
-  else if (ci.len > 0) intra_pc_run<T, D, ALIAS>(p, ci, blockIdx.y, ci.len, smem);
+  const ChunkHead wg = chunk_head<false>(p.H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
+  if (ci.len == C) intra_pc_run<T, D, ALIAS>(p, ci, wg.h, C, smem);
+  else if (ci.len > 0) intra_pc_run<T, D, ALIAS>(p, ci, wg.h, ci.len, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -918,9 +923,11 @@ __device__ __forceinline__ void intra_pc2_chunk(const FwdParams& p, const ChunkI
 template <bool ALIAS>
 __global__ __launch_bounds__(kIW, 4) void chunk_intra_fwd_pc2_kernel(FwdParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len == C) intra_pc2_chunk<ALIAS>(p, ci, blockIdx.y, C, smem);
-  else if (ci.len > 0) intra_pc2_chunk<ALIAS>(p, ci, blockIdx.y, ci.len, smem);
+  const ChunkHead wg = chunk_head<false>(p.H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
+  if (ci.len == C) intra_pc2_chunk<ALIAS>(p, ci, wg.h, C, smem);
+  else if (ci.len > 0) intra_pc2_chunk<ALIAS>(p, ci, wg.h, ci.len, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1748,13 +1755,13 @@ int launch_fwd(const FwdParams& p, int num_chunks, int stages, hipStream_t s) {
         auto kern2 = alias ? chunk_intra_fwd_pc2_kernel<true> : chunk_intra_fwd_pc2_kernel<false>;
         const int bytes2 = alias ? IntraPc2Layout<true>::bytes : IntraPc2Layout<false>::bytes;
         if (int st = set_smem(kern2, bytes2)) return st;
-        if (num_chunks > 0) hipLaunchKernelGGL(kern2, dim3(num_chunks, p.H), dim3(kIW), bytes2, s, p);
+        if (num_chunks > 0) hipLaunchKernelGGL(kern2, dim3(chunk_grid<false>(num_chunks, p.H)), dim3(kIW), bytes2, s, p);
         kern = nullptr;
       }
     }
     if (kern) {
       if (int st = set_smem(kern, bytes)) return st;
-      if (num_chunks > 0) hipLaunchKernelGGL(kern, dim3(num_chunks, p.H), dim3(kIW), bytes, s, p);
+      if (num_chunks > 0) hipLaunchKernelGGL(kern, p.qg ? dim3(chunk_grid<false>(num_chunks, p.H)) : dim3(chunk_grid<true>(num_chunks, p.H)), dim3(kIW), bytes, s, p);
     }
     if (int st = launch_status("pkda_chunk_fwd(intra)")) return st;
   }

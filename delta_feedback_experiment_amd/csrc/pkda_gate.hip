@@ -139,10 +139,12 @@ struct GateParams {
 
 // Per-head form: one wave, lane t scans the chunk.
 __global__ __launch_bounds__(64) void gate_fwd_kernel(GateParams p) {
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
-  const int h = blockIdx.y;
   const int H = p.heads;
+  const ChunkHead wg = chunk_head<true>(H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
+  if (ci.len <= 0) return;
+  const int h = wg.h;
   const int t = threadIdx.x;
   const int64_t idx = (int64_t)(ci.start + t) * H + h;
   float x = t < ci.len ? load_any(p.g, idx, p.g_dtype) : 0.f;
@@ -161,10 +163,12 @@ __global__ __launch_bounds__(64) void gate_fwd_kernel(GateParams p) {
 // a plain sequential scan.
 template <typename G, bool RAW, int NT>
 __global__ __launch_bounds__(NT) void gate_channel_fwd_kernel(GateParams p) {
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const ChunkHead wg = chunk_head<false>(p.heads);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
   const int len = ci.len;
   if (len <= 0) return;
-  const int h = blockIdx.y, H = p.heads, D = p.D;
+  const int h = wg.h, H = p.heads, D = p.D;
   const G* __restrict__ g = static_cast<const G*>(p.g);
   float* __restrict__ out = p.gcum;
   const float a_scale = RAW ? -expf(p.A_log[h]) : 0.f;
@@ -209,10 +213,12 @@ __global__ __launch_bounds__(NT) void gate_channel_fwd_kernel(GateParams p) {
 // dg = dglog * (-exp(A_log)) * sigmoid(g + dt_bias), dA_log += dglog * glog,
 // ddt_bias += dg.  Per-chunk partials, reduced by gate_reduce_kernel.
 __global__ __launch_bounds__(64) void gate_bwd_kernel(GateParams p) {
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
-  if (ci.len <= 0) return;
-  const int h = blockIdx.y;
   const int H = p.heads;
+  const ChunkHead wg = chunk_head<true>(H);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
+  if (ci.len <= 0) return;
+  const int h = wg.h;
   const int t = threadIdx.x;
   const int64_t idx = (int64_t)(ci.start + t) * H + h;
   float x = t < ci.len ? p.dgcum[idx] : 0.f;
@@ -231,9 +237,11 @@ __global__ __launch_bounds__(64) void gate_bwd_kernel(GateParams p) {
 template <typename G, bool RAW, int NT, typename DG>
 __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
   __shared__ float s_red[NT];
-  const ChunkInfo ci = chunk_info(p.geom, blockIdx.x);
+  const ChunkHead wg = chunk_head<false>(p.heads);
+  if (wg.cid >= p.geom.num_chunks) return;
+  const ChunkInfo ci = chunk_info(p.geom, wg.cid);
   const int len = ci.len;
-  const int h = blockIdx.y, H = p.heads, D = p.D;
+  const int h = wg.h, H = p.heads, D = p.D;
   const G* __restrict__ g = static_cast<const G*>(p.g);
   const float* __restrict__ dgcum = p.dgcum;
   DG* __restrict__ dg = reinterpret_cast<DG*>(p.dg);
@@ -270,7 +278,7 @@ __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
         }
       }
     }
-    if (RAW) p.ddt_bias_part[((int64_t)blockIdx.x * H + h) * D + c] = len > 0 ? ddt : 0.f;
+    if (RAW) p.ddt_bias_part[((int64_t)wg.cid * H + h) * D + c] = len > 0 ? ddt : 0.f;
   }
   if (!RAW) return;
   s_red[threadIdx.x] = dA_acc;
@@ -279,12 +287,12 @@ __global__ __launch_bounds__(NT) void gate_channel_bwd_kernel(GateParams p) {
     if (threadIdx.x < off) s_red[threadIdx.x] += s_red[threadIdx.x + off];
     __syncthreads();
   }
-  if (threadIdx.x == 0) p.dA_log_part[(int64_t)blockIdx.x * H + h] = s_red[0];
+  if (threadIdx.x == 0) p.dA_log_part[(int64_t)wg.cid * H + h] = s_red[0];
 }
 
 template <bool BWD, typename G, bool RAW>
 void launch_gate_channel_nt(const GateParams& p, int num_chunks, hipStream_t s) {
-  const dim3 grid(num_chunks, p.heads);
+  const dim3 grid(chunk_grid<false>(num_chunks, p.heads));
   const bool narrow = p.dg_dtype != PKDA_F32;  // backward: dg in G
   if (p.D <= 64) {
     if (!BWD) hipLaunchKernelGGL((gate_channel_fwd_kernel<G, RAW, 64>), grid, dim3(64), 0, s, p);
@@ -694,7 +702,8 @@ extern "C" int pkda_gate_fwd(const pkda_gate_args* a, void* stream) {
   if (a->gate_kind == PKDA_GATE_LOW_RANK)
     return dispatch_low_rank(p, a->num_chunks, false, static_cast<hipStream_t>(stream));
   if (a->gate_kind == PKDA_GATE_LOG_HEAD)
-    hipLaunchKernelGGL(gate_fwd_kernel, dim3(a->num_chunks, a->heads), dim3(64), 0, static_cast<hipStream_t>(stream), p);
+    hipLaunchKernelGGL(gate_fwd_kernel, dim3(chunk_grid<true>(a->num_chunks, a->heads)), dim3(64), 0,
+                       static_cast<hipStream_t>(stream), p);
   else
     launch_gate_channel<false>(p, a->num_chunks, static_cast<hipStream_t>(stream));
   return launch_status("pkda_gate_fwd");
@@ -725,7 +734,7 @@ int gate_bwd_impl(const pkda_gate_args* a, float* dA_part, float* ddt_part, hipS
     if (a->gate_kind == PKDA_GATE_LOW_RANK) {
       if (int e = dispatch_low_rank(p, a->num_chunks, true, s)) return e;
     } else if (a->gate_kind == PKDA_GATE_LOG_HEAD) {
-      hipLaunchKernelGGL(gate_bwd_kernel, dim3(a->num_chunks, a->heads), dim3(64), 0, s, p);
+      hipLaunchKernelGGL(gate_bwd_kernel, dim3(chunk_grid<true>(a->num_chunks, a->heads)), dim3(64), 0, s, p);
     } else {
       launch_gate_channel<true>(p, a->num_chunks, s);
     }

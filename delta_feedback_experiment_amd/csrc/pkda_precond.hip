@@ -107,17 +107,8 @@ template <> struct ChanIO<bf16_t, 2> {
   }
 };
 
-// Per-(chunk, head) launches: workgroup b takes chunk b / H of head b % H, so
-// neighbouring workgroups read neighbouring head slices of the same tokens.
-struct ChunkHead {
-  int j, h;
-};
-__device__ __forceinline__ ChunkHead chunk_head(int H) {
-  ChunkHead ch;
-  ch.j = blockIdx.x / H;
-  ch.h = blockIdx.x - ch.j * H;
-  return ch;
-}
+// Per-(chunk, head) launches on chunk_grid<false>: workgroup b takes chunk
+// b / H of head b % H (chunk_head<false>).
 
 // exp(sum of g_atk over the chunk) for chunks j0 .. j0 + nb - 1 of a document
 // (first chunk id first, first token dstart, dlen tokens), chunk j0 + i at
@@ -247,13 +238,13 @@ __device__ __forceinline__ void precond_fwd_chunk(const PrecondParams& p, int j,
 
 template <typename T, int D, bool APPLY>
 __global__ __launch_bounds__(PrecondChunk<D>::NT) void precond_fwd_chunk_kernel(PrecondParams p) {
-  const ChunkHead ch = chunk_head(p.H);
+  const ChunkHead ch = chunk_head<false>(p.H);
   if (threadIdx.x * PrecondChunk<D>::CH >= D) return;
-  const ChunkInfo ci = chunk_info(p.geom, ch.j);
+  const ChunkInfo ci = chunk_info(p.geom, ch.cid);
   if (ci.len == C)
-    precond_fwd_chunk<T, D, APPLY, true>(p, ch.j, ch.h, ci.start, C);
+    precond_fwd_chunk<T, D, APPLY, true>(p, ch.cid, ch.h, ci.start, C);
   else if (ci.len > 0)
-    precond_fwd_chunk<T, D, APPLY, false>(p, ch.j, ch.h, ci.start, ci.len);
+    precond_fwd_chunk<T, D, APPLY, false>(p, ch.cid, ch.h, ci.start, ci.len);
 }
 
 // Forward launch 2: per (document, head), A entering every chunk and the
@@ -490,14 +481,14 @@ template <typename T, int D, bool APPLY, typename GT>
 __global__ __launch_bounds__(PrecondChunk<D>::NT) void precond_bwd_chunk_kernel(PrecondParams p) {
   __shared__ float sRow[2][C][PrecondChunk<D>::NT / 16 + 1];
   __shared__ float sCen[PrecondChunk<D>::NT / 16];
-  const ChunkHead ch = chunk_head(p.H);
-  const ChunkInfo ci = chunk_info(p.geom, ch.j);
+  const ChunkHead ch = chunk_head<false>(p.H);
+  const ChunkInfo ci = chunk_info(p.geom, ch.cid);
   if (ci.len == C)
-    precond_bwd_chunk<T, D, APPLY, true, GT>(p, ch.j, ch.h, ci.start, C, sRow, sCen);
+    precond_bwd_chunk<T, D, APPLY, true, GT>(p, ch.cid, ch.h, ci.start, C, sRow, sCen);
   else if (ci.len > 0)
-    precond_bwd_chunk<T, D, APPLY, false, GT>(p, ch.j, ch.h, ci.start, ci.len, sRow, sCen);
+    precond_bwd_chunk<T, D, APPLY, false, GT>(p, ch.cid, ch.h, ci.start, ci.len, sRow, sCen);
   else if (APPLY && threadIdx.x == 0)
-    p.dcenter_part[(int64_t)ch.j * p.H + ch.h] = 0.f;
+    p.dcenter_part[(int64_t)ch.cid * p.H + ch.h] = 0.f;
 }
 
 // Backward launch 2: per (document, head), lambda entering every chunk from
@@ -573,7 +564,7 @@ int precond_common(const pkda_precond_args* a, PrecondParams& p) {
 template <typename T, int D, typename GT>
 void launch_precond_bwd_chunks(const PrecondParams& p, hipStream_t s) {
   constexpr int NT = PrecondThreads<D>::v, NTC = PrecondChunk<D>::NT;
-  const dim3 chunks((unsigned)((int64_t)p.geom.num_chunks * p.H));
+  const dim3 chunks(chunk_grid<false>(p.geom.num_chunks, p.H));
   const dim3 docs = doc_grid(p.geom.num_seqs, p.H, 1);
   const bool any = p.geom.num_chunks > 0;
   if (any) hipLaunchKernelGGL((precond_bwd_chunk_kernel<T, D, false, GT>), chunks, dim3(NTC), 0, s, p);
@@ -584,7 +575,7 @@ void launch_precond_bwd_chunks(const PrecondParams& p, hipStream_t s) {
 template <typename T, int D>
 int launch_precond(const PrecondParams& p, bool backward, hipStream_t s) {
   constexpr int NT = PrecondThreads<D>::v, NTC = PrecondChunk<D>::NT;
-  const dim3 chunks((unsigned)((int64_t)p.geom.num_chunks * p.H));
+  const dim3 chunks(chunk_grid<false>(p.geom.num_chunks, p.H));
   const dim3 docs = doc_grid(p.geom.num_seqs, p.H, 1);
   const bool any = p.geom.num_chunks > 0;
   if (backward) {
