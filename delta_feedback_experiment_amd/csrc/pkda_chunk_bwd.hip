@@ -1912,8 +1912,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
         const int r = i / SEG, sg = i % SEG;
         if (r < clen) {
           const uint4 x = *reinterpret_cast<const uint4*>(so + r * L::LDV + 8 * sg);
-          *reinterpret_cast<uint4*>(static_cast<T*>(p.dv_handoff ? p.dv : p.du) + (row0 + (int64_t)r * H) * D + v0 +
-                                    8 * sg) = x;
+          store16_nt(static_cast<T*>(p.dv_handoff ? p.dv : p.du) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg, x);
         }
       }
     };
@@ -1975,8 +1974,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
 #pragma unroll
       for (int kk = 0; kk < NKT / 2; ++kk) {
         const uint4 w = __builtin_bit_cast(uint4, dSB[kk]);
-        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
-        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+        store_packed_tile_nt(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile_nt(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
       }
     }
     // KW dS (eight independent accumulators per k step)
@@ -2237,7 +2236,7 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
         const int r = i / SEG, sg = i % SEG;
         if (r < clen) {
           const uint4 x = *reinterpret_cast<const uint4*>(so + r * L::LDV + 8 * sg);
-          *reinterpret_cast<uint4*>(static_cast<T*>(p.du) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg) = x;
+          store16_nt(static_cast<T*>(p.du) + (row0 + (int64_t)r * H) * D + v0 + 8 * sg, x);
         }
       }
     };
@@ -2296,8 +2295,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoadersBwd)) void chunk_state_bw
 #pragma unroll
       for (int kk = 0; kk < NKT / 2; ++kk) {
         const uint4 w = __builtin_bit_cast(uint4, dSB[kk]);
-        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
-        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+        store_packed_tile_nt(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile_nt(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
       }
     }
     // kg dS (eight independent accumulators per k step)

@@ -695,6 +695,19 @@ __device__ __forceinline__ void store_packed_tile(bf16_t* tile, uint32_t v0, uin
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   *reinterpret_cast<u32x2*>(tile + quad_row(lane) * 16 + quad_col(lane)) = u32x2{v0, v1};
 }
+// The same with a non-temporal hint: for the chunk-state checkpoints h and
+// dh, which are read back only by a later kernel.
+__device__ __forceinline__ void store_packed_tile_nt(bf16_t* tile, uint32_t v0, uint32_t v1, int lane) {
+  quad_transpose_b16(v0, v1, lane);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store(u32x2{v0, v1}, reinterpret_cast<u32x2*>(tile + quad_row(lane) * 16 + quad_col(lane)));
+}
+// A 16-byte piece of a streamed output (the reverse state passes' dU / dv
+// rows, read only by a later kernel) with a non-temporal hint.
+__device__ __forceinline__ void store16_nt(void* dst, const uint4 x) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(u32x4{x.x, x.y, x.z, x.w}, reinterpret_cast<u32x4*>(dst));
+}
 __device__ __forceinline__ void store_acc_tile(bf16_t* tile, const f32x4& acc, int lane) {
   store_packed_tile(tile, pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), lane);
 }

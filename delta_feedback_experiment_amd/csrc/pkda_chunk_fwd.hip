@@ -1318,8 +1318,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
 #pragma unroll
         for (int kk = 0; kk < NKT / 2; ++kk) {
           const uint4 w = __builtin_bit_cast(uint4, SB[kk]);
-          store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
-          store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+          store_packed_tile_nt(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+          store_packed_tile_nt(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
         }
       }
       // K S and Q S: for each k step the eight tiles are independent accumulators
@@ -1598,8 +1598,8 @@ __global__ __launch_bounds__(64 * (BV / 16 + kRrLoaders)) void chunk_state_fwd_r
 #pragma unroll
       for (int kk = 0; kk < NKT / 2; ++kk) {
         const uint4 w = __builtin_bit_cast(uint4, SB[kk]);
-        store_packed_tile(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
-        store_packed_tile(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
+        store_packed_tile_nt(hb + tile_offset(D, 2 * kk, col0 / 16), w.x, w.y, lane);
+        store_packed_tile_nt(hb + tile_offset(D, 2 * kk + 1, col0 / 16), w.z, w.w, lane);
       }
     }
     // W S and qg S: for each k step the eight tiles are independent accumulators
